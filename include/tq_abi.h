@@ -1,0 +1,172 @@
+/*
+ * tq_abi.h — C ABI of the MI355X (gfx950) TurboQuant KV-cache library.
+ *
+ * The reference (alex-rentel/mlx-turboquant) has no C ABI: its native code is
+ * Metal source dispatched through mx.fast.metal_kernel. Each entry point below
+ * replaces one reference operation on the compress / compressed-attention path;
+ * the comment above it names the reference interface it stands in for.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless stated otherwise; the caller owns
+ *     every buffer (including the attention workspace).
+ *   - fp16 tensors are passed as `const void*` holding IEEE binary16 values.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and
+ *     is stream-ordered; the functions do not synchronise.
+ *   - Return value: TQ_OK (0) or a negative TQ_ERR_* code; tq_last_error()
+ *     returns the message of the most recent failure on the calling thread.
+ *   - Stores are rows of (batch b, head h) = row r = b*heads + h. Within a row,
+ *     token t of a packed array starts at byte t*row_bytes; norms / gamma are
+ *     one float per token.
+ */
+#ifndef TQ_ABI_H
+#define TQ_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TQ_ABI_VERSION 1
+
+/* Element types of floating-point inputs. */
+enum { TQ_F16 = 0, TQ_BF16 = 1, TQ_F32 = 2 };
+
+enum {
+  TQ_OK = 0,
+  TQ_ERR_INVALID = -1,     /* bad argument: reference raises ValueError / AssertionError */
+  TQ_ERR_UNSUPPORTED = -2, /* width / head_dim not supported: reference ValueError */
+  TQ_ERR_LAUNCH = -3,      /* HIP launch or runtime failure */
+  TQ_ERR_WORKSPACE = -4    /* workspace too small */
+};
+
+/* Quantizer description shared by compress / dequantize / attention.
+ * Integer widths: bits_hi == bits_lo == bits, split == d.
+ * Fractional widths (e.g. 3.5): rotated dims [0, split) use bits_hi and
+ * [split, d) use bits_lo with split == d/2 (mlx_turboquant/cache.py:63-84).
+ * Both codebooks are the d-dimensional Lloyd-Max tables (codebook.py:146-174). */
+typedef struct tq_codec {
+  int32_t d;                   /* head_dim: 64, 128 or 256 */
+  int32_t bits_hi;             /* 1..4 */
+  int32_t bits_lo;             /* 1..4 */
+  int32_t split;               /* multiple of 32 */
+  const float* rotation;       /* (d, d) row-major orthogonal R (rotation.py:17-36) */
+  const float* centroids_hi;   /* (2^bits_hi,) */
+  const float* boundaries_hi;  /* (2^bits_hi - 1,) */
+  const float* centroids_lo;   /* (2^bits_lo,)  (== _hi for integer widths) */
+  const float* boundaries_lo;  /* (2^bits_lo - 1,) */
+  const float* qjl_proj;       /* (qjl_m, d) Gaussian S (qjl.py:23-36) or NULL */
+  int32_t qjl_m;               /* number of projections (multiple of 32) or 0 */
+  int32_t reserved;
+} tq_codec;
+
+/* A compressed store: packed codes, norms and optional QJL sketch.
+ * codes_hi rows are split*bits_hi/8 bytes, codes_lo rows (d-split)*bits_lo/8
+ * (NULL for integer widths), signs rows qjl_m/8 bytes (LSB-first, bit i set
+ * when projection i of the residual is >= 0). Head strides are in bytes for
+ * codes/signs and in elements for norms/gamma. */
+typedef struct tq_store {
+  uint8_t* codes_hi;
+  int64_t hi_head_stride;
+  uint8_t* codes_lo;
+  int64_t lo_head_stride;
+  float* norms;
+  int64_t norm_head_stride;
+  uint8_t* signs;
+  int64_t sign_head_stride;
+  float* gamma;
+  int64_t gamma_head_stride;
+} tq_store;
+
+/* Vector set addressed by (row, token): `rows` rows of `heads` heads per batch
+ * element; per-batch token counts / offsets are optional device int32 arrays
+ * (NULL = uniform `n_tok`, offset 0). */
+typedef struct tq_span {
+  int32_t rows;                  /* batch * heads */
+  int32_t heads;                 /* heads per batch element */
+  int32_t n_tok;                 /* tokens per row (upper bound when n_tok_b != NULL) */
+  int32_t reserved;
+  const int32_t* n_tok_b;        /* (batch,) tokens per row, or NULL */
+  const int32_t* src_tok0_b;     /* (batch,) first source token, or NULL */
+  const int32_t* dst_tok0_b;     /* (batch,) first destination token, or NULL */
+} tq_span;
+
+/* Library / error handling. */
+int tq_abi_version(void);
+const char* tq_last_error(void);
+/* Returns 1 when the library holds a code object for the current device. */
+int tq_device_supported(void);
+
+/* Compress fp16 vectors: norm -> normalise -> rotate -> quantize -> pack, and
+ * (when codec->qjl_proj != NULL and dst->signs != NULL) the QJL sign sketch and
+ * residual norm of x - dequantize(codes).
+ * Replaces TurboQuantKVCache._quantize_kv / _quantize_kv_fractional
+ * (mlx_turboquant/cache.py:232-274), TurboQuantMSE.quantize
+ * (quantizer.py:54-86) and metal_quantize_4bit (kernels.py:363-409); the QJL
+ * part replaces qjl_quantize on the residual (qjl.py:47-67, cache.py:396-427).
+ * x: x_dtype (TQ_F16 / TQ_BF16 / TQ_F32), element (r, t, i) at
+ * x[r*x_head_stride + t*d + i]; the value is cast to float32 exactly. */
+int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x_head_stride,
+                const tq_span* span, const tq_store* dst, void* stream);
+
+/* Dequantize: out = n * (c[idx] @ R) (+ QJL correction when apply_qjl and
+ * the store holds a sketch), float32, element (r, t, i) at
+ * out[r*out_head_stride + t*d + i].
+ * Replaces metal_dequantize (kernels.py:313-360), _dequantize_kv /
+ * _dequantize_kv_fractional (cache.py:276-343), TurboQuantMSE.dequantize
+ * (quantizer.py:88-109) and qjl_dequantize (qjl.py:70-94). */
+int tq_dequantize(const tq_codec* codec, const tq_store* src, const tq_span* span,
+                  float* out, int64_t out_head_stride, int32_t apply_qjl, void* stream);
+
+/* LSB-first bit packing of uint8 codes, rows of d codes.
+ * Replaces pack_indices / unpack_indices (packing.py:211-236). */
+int tq_pack_codes(const uint8_t* idx, int64_t n_rows, int32_t d, int32_t bits,
+                  uint8_t* packed, void* stream);
+int tq_unpack_codes(const uint8_t* packed, int64_t n_rows, int32_t d, int32_t bits,
+                    uint8_t* idx, void* stream);
+
+/* idx = #{k : y > boundaries[k]} for float32 y (codebook.py:203-225). */
+int tq_quantize_scalar(const float* y, int64_t n, const float* boundaries,
+                       int32_t n_boundaries, uint8_t* idx, void* stream);
+
+/* Decode attention over a TurboQuant cache (one query token per head).
+ * out[b, h] = softmax(scale * q[b,h] . K_b^T) V_b with K_b / V_b the tokens
+ * [sink | compressed | residual] of sequence b and kv head h / (hq / hkv),
+ * compressed tokens read from packed codes (no dequantized cache), with the
+ * QJL correction of the stored sketch when `qjl` is set.
+ * Replaces the decode step update_and_fetch -> concat -> SDPA
+ * (cache.py:620-706, docs/attention_source_dump.txt:22-31) and the research
+ * fused_qk_scores_* kernels (kernels.py:558-629); interface follows the
+ * proposed fused_attention_from_packed (docs/FUSED_SDPA_RESULTS.md:116-127). */
+typedef struct tq_attn_desc {
+  int32_t batch, hq, hkv, qjl;
+  float scale;
+  int32_t max_comp, max_sink, max_res;  /* host upper bounds (size the grid) */
+  int32_t q_dtype, kv_dtype;            /* TQ_F16 / TQ_BF16 / TQ_F32 of q and of sink/residual */
+  const void* q;                        /* (batch, hq, d) */
+  float* out;                           /* (batch, hq, d) float32 */
+  tq_store kstore, vstore;              /* rows = batch * hkv */
+  const int32_t* comp_len;              /* (batch,) or NULL = max_comp */
+  const void* sink_k;                   /* kv_dtype (batch*hkv, sink_cap, d) or NULL */
+  const void* sink_v;
+  int64_t sink_head_stride;             /* elements */
+  const int32_t* sink_len;              /* (batch,) or NULL = max_sink */
+  const void* res_k;                    /* kv_dtype ring (batch*hkv, res_cap, d) or NULL */
+  const void* res_v;
+  int64_t res_head_stride;              /* elements */
+  int32_t res_cap, res_start0;          /* ring capacity; ring start when res_start == NULL */
+  const int32_t* res_start;             /* (batch,) ring start, or NULL = res_start0 */
+  const int32_t* res_len;               /* (batch,) or NULL = max_res */
+} tq_attn_desc;
+
+size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* desc);
+int tq_decode_attention(const tq_codec* kcodec, const tq_codec* vcodec,
+                        const tq_attn_desc* desc, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQ_ABI_H */

@@ -1,0 +1,487 @@
+// Decode attention over a TurboQuant cache on gfx950 (split-T flash decoding).
+//
+// For sequence b, kv head g and its G = hq/hkv query heads the cache holds
+// [sink fp16 | compressed | residual fp16] tokens. Compressed tokens are scored
+// without dequantising (docs/FUSED_ATTENTION_DESIGN.md:62-67):
+//     q . k_hat = n_k * (q @ R^T) . c[idx_k]
+// and values are accumulated in rotated space with one inverse rotation at the
+// end (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40):
+//     sum_t p_t v_hat_t = (sum_t p_t n_t c[idx_t]) @ R.
+// With the QJL sketch (qjl.py:70-94) the corrections are
+//     q . dk = sqrt(pi/2)/D * gamma * (S q) . z,
+//     sum_t p_t dv_t = sqrt(pi/2)/D * (sum_t p_t gamma_t z_t) @ S.
+//
+// Launches: (1) rotate / scale the queries, (2) one workgroup per (token
+// chunk, kv head, sequence) writes a partial (max, sum, acc) per query head,
+// (3) one workgroup per (query head, sequence) merges the partials, applies
+// R once, adds the fp16-segment and QJL terms and normalises.
+
+#include <math.h>
+
+#include "tq_common.h"
+
+namespace tq {
+
+constexpr int CHUNK = 256;   // tokens per partial
+constexpr int NT = 256;      // threads per workgroup
+constexpr float SQRT_HALF_PI = 1.2533141373155003f;
+
+struct AttnArgs {
+  tq_attn_desc d;
+  int D;
+  const float* rot;
+  const float* kc_hi;
+  const float* kc_lo;
+  const float* vc_hi;
+  const float* vc_lo;
+  const float* proj;
+  int m;  // qjl projections (0 = off)
+  int kb_hi, kb_lo, ks, vb_hi, vb_lo, vs;
+  int k_row_hi, k_row_lo, v_row_hi, v_row_lo, row_sign;
+  float* qr;    // (B, Hq, D)  scale * q @ R^T
+  float* qs;    // (B, Hq, D)  scale * q
+  float* sq;    // (B, Hq, m)  S @ (scale * q)
+  float* part;  // (B, Hq, nch, PS)
+  int nc, ns, nr, nch, ps;
+};
+
+__host__ __device__ inline int part_stride(int D, int m) { return ((2 + D + m) + 3) & ~3; }
+
+__global__ void prologue_kernel(AttnArgs a) {
+  extern __shared__ float sm[];
+  const int h = blockIdx.x, b = blockIdx.y, D = a.D;
+  const int64_t qo = ((int64_t)b * a.d.hq + h) * D;
+  float* qsm = sm;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    const float v = a.d.scale * load_elem(a.d.q, qo + i, a.d.q_dtype);
+    qsm[i] = v;
+    a.qs[qo + i] = v;
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < D; j += blockDim.x) {
+    const float* rj = a.rot + (int64_t)j * D;
+    float acc = 0.f;
+    for (int i = 0; i < D; ++i) acc = fmaf(qsm[i], rj[i], acc);
+    a.qr[qo + j] = acc;
+  }
+  if (a.m > 0) {
+    const int64_t so = ((int64_t)b * a.d.hq + h) * a.m;
+    for (int i = threadIdx.x; i < a.m; i += blockDim.x) {
+      const float* si = a.proj + (int64_t)i * D;
+      float acc = 0.f;
+      for (int k = 0; k < D; ++k) acc = fmaf(qsm[k], si[k], acc);
+      a.sq[so + i] = acc;
+    }
+  }
+}
+
+// Code of dimension j in a packed row (LSB-first bitstream).
+__device__ inline uint32_t code_at(const uint8_t* row, int j, int bits) {
+  const int bit = bits * j;
+  uint32_t v = row[bit >> 3] >> (bit & 7);
+  if ((bit & 7) + bits > 8) v |= (uint32_t)row[(bit >> 3) + 1] << (8 - (bit & 7));
+  return v & ((1u << bits) - 1u);
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
+  constexpr int HP = NT / D > 0 ? NT / D : 1;  // threads per dim in the PV phase
+  constexpr int MAXM = 256;
+  __shared__ float qv[G][D];          // rotated (compressed) or plain (fp16) scaled query
+  __shared__ float w[G][CHUNK];       // p * n_v (or p) per token
+  __shared__ float pg[G][CHUNK];      // p * gamma_v (QJL)
+  __shared__ float red[G][NT / 64];
+  __shared__ float mx[G], lsum[G];
+  __shared__ float klut[2][16], vlut[2][16];
+  __shared__ float sqv[G][MAXM];
+  __shared__ uint8_t vtile[CHUNK * 128];
+
+  const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int hq = a.d.hq, tid = threadIdx.x;
+  const int row = b * a.d.hkv + g;
+
+  // segment of this chunk
+  int seg, base;
+  if (c < a.nc) { seg = 0; base = c * CHUNK; }
+  else if (c < a.nc + a.ns) { seg = 1; base = (c - a.nc) * CHUNK; }
+  else { seg = 2; base = (c - a.nc - a.ns) * CHUNK; }
+  int len;
+  if (seg == 0) len = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
+  else if (seg == 1) len = a.d.sink_len ? a.d.sink_len[b] : a.d.max_sink;
+  else len = a.d.res_len ? a.d.res_len[b] : a.d.max_res;
+  const int nvalid = max(0, min(CHUNK, len - base));
+
+  const bool packed = seg == 0;
+  const bool qjl = packed && a.m > 0;
+  for (int e = tid; e < G * D; e += NT) {
+    const int h = e / D, j = e % D;
+    const int64_t qo = ((int64_t)b * hq + g * G + h) * D + j;
+    qv[h][j] = packed ? a.qr[qo] : a.qs[qo];
+  }
+  if (qjl) {
+    for (int e = tid; e < G * a.m; e += NT) {
+      const int h = e / a.m, i = e % a.m;
+      sqv[h][i] = a.sq[((int64_t)b * hq + g * G + h) * a.m + i];
+    }
+  }
+  if (tid < 16) {
+    klut[0][tid] = tid < (1 << a.kb_hi) ? a.kc_hi[tid] : 0.f;
+    klut[1][tid] = tid < (1 << a.kb_lo) ? a.kc_lo[tid] : 0.f;
+    vlut[0][tid] = tid < (1 << a.vb_hi) ? a.vc_hi[tid] : 0.f;
+    vlut[1][tid] = tid < (1 << a.vb_lo) ? a.vc_lo[tid] : 0.f;
+  }
+  // stage packed V rows (hi then lo bytes per token) for the PV phase
+  const int vrb = a.v_row_hi + a.v_row_lo;
+  if (packed) {
+    const uint8_t* vh = a.d.vstore.codes_hi + (int64_t)row * a.d.vstore.hi_head_stride + (int64_t)base * a.v_row_hi;
+    for (int e = tid; e < nvalid * a.v_row_hi; e += NT)
+      vtile[(e / a.v_row_hi) * vrb + e % a.v_row_hi] = vh[e];
+    if (a.v_row_lo) {
+      const uint8_t* vl = a.d.vstore.codes_lo + (int64_t)row * a.d.vstore.lo_head_stride + (int64_t)base * a.v_row_lo;
+      for (int e = tid; e < nvalid * a.v_row_lo; e += NT)
+        vtile[(e / a.v_row_lo) * vrb + a.v_row_hi + e % a.v_row_lo] = vl[e];
+    }
+  }
+  __syncthreads();
+
+  // ---- scores: thread t owns token base + t
+  float s[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) s[h] = -INFINITY;
+  const int t = tid;
+  if (t < nvalid) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) s[h] = 0.f;
+    if (packed) {
+      const uint8_t* kh = a.d.kstore.codes_hi + (int64_t)row * a.d.kstore.hi_head_stride + (int64_t)(base + t) * a.k_row_hi;
+      const uint8_t* kl = a.k_row_lo ? a.d.kstore.codes_lo + (int64_t)row * a.d.kstore.lo_head_stride +
+                                           (int64_t)(base + t) * a.k_row_lo
+                                     : nullptr;
+      for (int j = 0; j < D; ++j) {
+        const bool hi = j < a.ks;
+        const float cv = hi ? klut[0][code_at(kh, j, a.kb_hi)] : klut[1][code_at(kl, j - a.ks, a.kb_lo)];
+#pragma unroll
+        for (int h = 0; h < G; ++h) s[h] = fmaf(qv[h][j], cv, s[h]);
+      }
+      const float nk = a.d.kstore.norms[(int64_t)row * a.d.kstore.norm_head_stride + base + t];
+#pragma unroll
+      for (int h = 0; h < G; ++h) s[h] *= nk;
+      if (qjl) {
+        const uint8_t* sg = a.d.kstore.signs + (int64_t)row * a.d.kstore.sign_head_stride + (int64_t)(base + t) * a.row_sign;
+        const float gk = a.d.kstore.gamma[(int64_t)row * a.d.kstore.gamma_head_stride + base + t];
+        float zs[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) zs[h] = 0.f;
+        for (int i = 0; i < a.m; ++i) {
+          const float z = ((sg[i >> 3] >> (i & 7)) & 1u) ? 1.f : -1.f;
+#pragma unroll
+          for (int h = 0; h < G; ++h) zs[h] = fmaf(sqv[h][i], z, zs[h]);
+        }
+        const float coef = SQRT_HALF_PI / (float)D * gk;
+#pragma unroll
+        for (int h = 0; h < G; ++h) s[h] = fmaf(coef, zs[h], s[h]);
+      }
+    } else {
+      const void* kp;
+      int64_t ko;
+      if (seg == 1) {
+        kp = a.d.sink_k;
+        ko = (int64_t)row * a.d.sink_head_stride + (int64_t)(base + t) * D;
+      } else {
+        const int st = a.d.res_start ? a.d.res_start[b] : a.d.res_start0;
+        const int pos = (st + base + t) % a.d.res_cap;
+        kp = a.d.res_k;
+        ko = (int64_t)row * a.d.res_head_stride + (int64_t)pos * D;
+      }
+      for (int j = 0; j < D; ++j) {
+        const float kv = load_elem(kp, ko + j, a.d.kv_dtype);
+#pragma unroll
+        for (int h = 0; h < G; ++h) s[h] = fmaf(qv[h][j], kv, s[h]);
+      }
+    }
+  }
+
+  // ---- chunk max per head
+  const int lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float v = s[h];
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    if (lane == 0) red[h][wv] = v;
+  }
+  __syncthreads();
+  if (tid < G) {
+    float v = red[tid][0];
+    for (int k = 1; k < NT / 64; ++k) v = fmaxf(v, red[tid][k]);
+    mx[tid] = v;
+  }
+  __syncthreads();
+  float p[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) p[h] = (t < nvalid && mx[h] > -INFINITY) ? expf(s[h] - mx[h]) : 0.f;
+  // weights for the PV phase
+  {
+    float nv = 1.f, gv = 0.f;
+    if (packed && t < nvalid) {
+      nv = a.d.vstore.norms[(int64_t)row * a.d.vstore.norm_head_stride + base + t];
+      if (qjl) gv = a.d.vstore.gamma[(int64_t)row * a.d.vstore.gamma_head_stride + base + t];
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      w[h][t] = p[h] * nv;
+      pg[h][t] = p[h] * gv;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float v = p[h];
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if (lane == 0) red[h][wv] = v;
+  }
+  __syncthreads();
+  if (tid < G) {
+    float v = 0.f;
+    for (int k = 0; k < NT / 64; ++k) v += red[tid][k];
+    lsum[tid] = v;
+  }
+  __syncthreads();
+
+  // ---- PV: thread (j, hp) accumulates dim j for heads hp, hp+HP, ...
+  float* outp = a.part;
+  for (int jj = tid; jj < D * HP; jj += NT) {
+    const int j = jj % D, hp = jj / D;
+    float acc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[h] = 0.f;
+    if (packed) {
+      const bool hi = j < a.vs;
+      const int bits = hi ? a.vb_hi : a.vb_lo;
+      const int jl = hi ? j : j - a.vs;
+      const int off = hi ? 0 : a.v_row_hi;
+      const float* lut = vlut[hi ? 0 : 1];
+      for (int tt = 0; tt < nvalid; ++tt) {
+        const float cv = lut[code_at(vtile + tt * vrb + off, jl, bits)];
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+          if (h % HP == hp) acc[h] = fmaf(w[h][tt], cv, acc[h]);
+      }
+    } else {
+      for (int tt = 0; tt < nvalid; ++tt) {
+        int64_t vo;
+        const void* vp;
+        if (seg == 1) {
+          vp = a.d.sink_v;
+          vo = (int64_t)row * a.d.sink_head_stride + (int64_t)(base + tt) * D;
+        } else {
+          const int st = a.d.res_start ? a.d.res_start[b] : a.d.res_start0;
+          const int pos = (st + base + tt) % a.d.res_cap;
+          vp = a.d.res_v;
+          vo = (int64_t)row * a.d.res_head_stride + (int64_t)pos * D;
+        }
+        const float vv = load_elem(vp, vo + j, a.d.kv_dtype);
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+          if (h % HP == hp) acc[h] = fmaf(w[h][tt], vv, acc[h]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      if (h % HP != hp) continue;
+      float* pp = outp + (((int64_t)b * hq + g * G + h) * a.nch + c) * a.ps;
+      pp[2 + j] = acc[h];
+    }
+  }
+  // QJL value term: az[h][i] = sum_t p_t gamma_t z_t,i
+  if (qjl) {
+    const uint8_t* sgb = a.d.vstore.signs + (int64_t)row * a.d.vstore.sign_head_stride + (int64_t)base * a.row_sign;
+    for (int e = tid; e < G * a.m; e += NT) {
+      const int h = e / a.m, i = e % a.m;
+      float acc = 0.f;
+      for (int tt = 0; tt < nvalid; ++tt) {
+        const float z = ((sgb[tt * a.row_sign + (i >> 3)] >> (i & 7)) & 1u) ? 1.f : -1.f;
+        acc = fmaf(pg[h][tt], z, acc);
+      }
+      float* pp = outp + (((int64_t)b * hq + g * G + h) * a.nch + c) * a.ps;
+      pp[2 + D + i] = acc;
+    }
+  }
+  if (tid < G) {
+    float* pp = outp + (((int64_t)b * hq + g * G + tid) * a.nch + c) * a.ps;
+    pp[0] = mx[tid];
+    pp[1] = lsum[tid];
+  }
+}
+
+__global__ void combine_kernel(AttnArgs a) {
+  extern __shared__ float sm[];
+  const int h = blockIdx.x, b = blockIdx.y, D = a.D;
+  const int hq = a.d.hq;
+  const float* pp = a.part + ((int64_t)b * hq + h) * a.nch * a.ps;
+  float M = -INFINITY;
+  for (int c = 0; c < a.nch; ++c) M = fmaxf(M, pp[(int64_t)c * a.ps]);
+  float* accr = sm;        // D rotated
+  float* azs = sm + D;     // m
+  float L = 0.f;
+  for (int c = 0; c < a.nch; ++c) {
+    const float mc = pp[(int64_t)c * a.ps];
+    if (mc > -INFINITY) L += expf(mc - M) * pp[(int64_t)c * a.ps + 1];
+  }
+  for (int j = threadIdx.x; j < D; j += blockDim.x) {
+    float r = 0.f;
+    for (int c = 0; c < a.nc; ++c) {
+      const float mc = pp[(int64_t)c * a.ps];
+      if (mc > -INFINITY) r = fmaf(expf(mc - M), pp[(int64_t)c * a.ps + 2 + j], r);
+    }
+    accr[j] = r;
+  }
+  for (int i = threadIdx.x; i < a.m; i += blockDim.x) {
+    float r = 0.f;
+    for (int c = 0; c < a.nc; ++c) {
+      const float mc = pp[(int64_t)c * a.ps];
+      if (mc > -INFINITY) r = fmaf(expf(mc - M), pp[(int64_t)c * a.ps + 2 + D + i], r);
+    }
+    azs[i] = r;
+  }
+  __syncthreads();
+  float* out = a.d.out + ((int64_t)b * hq + h) * D;
+  for (int j = threadIdx.x; j < D; j += blockDim.x) {
+    float o = 0.f;
+    for (int i = 0; i < D; ++i) o = fmaf(accr[i], a.rot[(int64_t)i * D + j], o);
+    float f = 0.f;
+    for (int c = a.nc; c < a.nch; ++c) {
+      const float mc = pp[(int64_t)c * a.ps];
+      if (mc > -INFINITY) f = fmaf(expf(mc - M), pp[(int64_t)c * a.ps + 2 + j], f);
+    }
+    o += f;
+    if (a.m > 0) {
+      float z = 0.f;
+      for (int i = 0; i < a.m; ++i) z = fmaf(azs[i], a.proj[(int64_t)i * D + j], z);
+      o = fmaf(SQRT_HALF_PI / (float)D, z, o);
+    }
+    out[j] = (L > 0.f) ? o / L : 0.f;
+  }
+}
+
+static void chunk_counts(const tq_attn_desc* d, int& nc, int& ns, int& nr) {
+  nc = (d->max_comp + CHUNK - 1) / CHUNK;
+  ns = (d->max_sink + CHUNK - 1) / CHUNK;
+  nr = (d->max_res + CHUNK - 1) / CHUNK;
+}
+
+template <int D>
+static void launch_chunks(const AttnArgs& a, int G, dim3 grid, hipStream_t s) {
+  switch (G) {
+    case 1: hipLaunchKernelGGL((chunk_kernel<D, 1>), grid, dim3(NT), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((chunk_kernel<D, 2>), grid, dim3(NT), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((chunk_kernel<D, 4>), grid, dim3(NT), 0, s, a); break;
+    default: hipLaunchKernelGGL((chunk_kernel<D, 8>), grid, dim3(NT), 0, s, a); break;
+  }
+}
+
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" {
+
+size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) {
+  if (!kcodec || !d) return 0;
+  int nc, ns, nr;
+  chunk_counts(d, nc, ns, nr);
+  const int D = kcodec->d;
+  const int m = d->qjl ? kcodec->qjl_m : 0;
+  const size_t nch = (size_t)(nc + ns + nr);
+  const size_t heads = (size_t)d->batch * d->hq;
+  size_t bytes = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
+  return (bytes + 255) & ~(size_t)255;
+}
+
+int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  int rc = check_codec(kc);
+  if (rc) return rc;
+  if ((rc = check_codec(vc))) return rc;
+  if (!d) return set_error(TQ_ERR_INVALID, "attention descriptor is NULL");
+  if (kc->d != vc->d) return set_error(TQ_ERR_INVALID, "key/value head_dim differ");
+  if (d->batch <= 0 || d->hkv <= 0 || d->hq <= 0 || d->hq % d->hkv)
+    return set_error(TQ_ERR_INVALID, "bad head counts hq=%d hkv=%d batch=%d", d->hq, d->hkv, d->batch);
+  const int G = d->hq / d->hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return set_error(TQ_ERR_UNSUPPORTED, "query heads per kv head %d not in {1,2,4,8}", G);
+  if (d->batch > 65535 || d->hkv > 65535) return set_error(TQ_ERR_UNSUPPORTED, "grid too large");
+  if (d->max_comp < 0 || d->max_sink < 0 || d->max_res < 0)
+    return set_error(TQ_ERR_INVALID, "negative segment length");
+  if (!d->q || !d->out) return set_error(TQ_ERR_INVALID, "q/out is NULL");
+  if (d->q_dtype < TQ_F16 || d->q_dtype > TQ_F32 || d->kv_dtype < TQ_F16 || d->kv_dtype > TQ_F32)
+    return set_error(TQ_ERR_UNSUPPORTED, "unknown q/kv dtype");
+  if (d->max_comp > 0 && (!d->kstore.codes_hi || !d->kstore.norms || !d->vstore.codes_hi || !d->vstore.norms))
+    return set_error(TQ_ERR_INVALID, "compressed store pointers are NULL");
+  if (d->max_sink > 0 && (!d->sink_k || !d->sink_v)) return set_error(TQ_ERR_INVALID, "sink pointers are NULL");
+  if (d->max_res > 0 && (!d->res_k || !d->res_v || d->res_cap <= 0))
+    return set_error(TQ_ERR_INVALID, "residual pointers are NULL");
+  const int row_v = row_bytes(vc->split, vc->bits_hi) + row_bytes(vc->d - vc->split, vc->bits_lo);
+  if (row_v > 128) return set_error(TQ_ERR_UNSUPPORTED, "value row of %d bytes > 128", row_v);
+  const bool qjl = d->qjl != 0;
+  if (qjl) {
+    if (!kc->qjl_proj || kc->qjl_m <= 0 || kc->qjl_m != vc->qjl_m || kc->qjl_proj != vc->qjl_proj)
+      return set_error(TQ_ERR_INVALID, "QJL attention needs one projection shared by keys and values");
+    if (kc->qjl_m > 256) return set_error(TQ_ERR_UNSUPPORTED, "qjl_m > 256");
+    if (d->max_comp > 0 && (!d->kstore.signs || !d->kstore.gamma || !d->vstore.signs || !d->vstore.gamma))
+      return set_error(TQ_ERR_INVALID, "QJL attention needs stored signs and gamma");
+  }
+  const size_t need = tq_decode_workspace_bytes(kc, d);
+  if (!workspace || workspace_bytes < need)
+    return set_error(TQ_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, need);
+
+  AttnArgs a;
+  a.d = *d;
+  a.D = kc->d;
+  a.rot = kc->rotation;
+  a.kc_hi = kc->centroids_hi;
+  a.kc_lo = kc->split < kc->d ? kc->centroids_lo : kc->centroids_hi;
+  a.vc_hi = vc->centroids_hi;
+  a.vc_lo = vc->split < vc->d ? vc->centroids_lo : vc->centroids_hi;
+  a.proj = qjl ? kc->qjl_proj : nullptr;
+  a.m = qjl ? kc->qjl_m : 0;
+  a.kb_hi = kc->bits_hi;
+  a.kb_lo = kc->split < kc->d ? kc->bits_lo : kc->bits_hi;
+  a.ks = kc->split;
+  a.vb_hi = vc->bits_hi;
+  a.vb_lo = vc->split < vc->d ? vc->bits_lo : vc->bits_hi;
+  a.vs = vc->split;
+  a.k_row_hi = row_bytes(kc->split, kc->bits_hi);
+  a.k_row_lo = row_bytes(kc->d - kc->split, a.kb_lo);
+  a.v_row_hi = row_bytes(vc->split, vc->bits_hi);
+  a.v_row_lo = row_bytes(vc->d - vc->split, a.vb_lo);
+  a.row_sign = a.m / 8;
+  chunk_counts(d, a.nc, a.ns, a.nr);
+  a.nch = a.nc + a.ns + a.nr;
+  a.ps = part_stride(a.D, a.m);
+  const size_t heads = (size_t)d->batch * d->hq;
+  float* ws = static_cast<float*>(workspace);
+  a.qr = ws;
+  a.qs = a.qr + heads * a.D;
+  a.sq = a.qs + heads * a.D;
+  a.part = a.sq + heads * a.m;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t pro_smem = (size_t)a.D * 4;
+  hipLaunchKernelGGL(prologue_kernel, dim3(d->hq, d->batch), dim3(128), pro_smem, s, a);
+  TQ_LAUNCH_CHECK("tq_decode_attention prologue");
+  if (a.nch > 0) {
+    dim3 grid(a.nch, d->hkv, d->batch);
+    switch (a.D) {
+      case 64: launch_chunks<64>(a, G, grid, s); break;
+      case 128: launch_chunks<128>(a, G, grid, s); break;
+      default: launch_chunks<256>(a, G, grid, s); break;
+    }
+    TQ_LAUNCH_CHECK("tq_decode_attention chunks");
+  }
+  const size_t cmb_smem = (size_t)(a.D + a.m) * 4;
+  hipLaunchKernelGGL(combine_kernel, dim3(d->hq, d->batch), dim3(128), cmb_smem, s, a);
+  TQ_LAUNCH_CHECK("tq_decode_attention combine");
+  return TQ_OK;
+}
+
+}  // extern "C"

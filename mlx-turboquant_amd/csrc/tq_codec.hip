@@ -1,0 +1,642 @@
+// TurboQuant codec kernels for gfx950: compress (norm -> normalise -> rotate
+// -> quantize -> pack [-> QJL sketch]), dequantize, bit packing utilities.
+//
+// Numeric contract (matches the CPU restatement used by the tests):
+//   n   = f32(sqrt(sum_j x_j^2)) with the sum taken in float64 in index order
+//         (mlx_turboquant/cache.py:235-236 computes mx.linalg.norm of the f32 cast);
+//   x_n = f32(x) / max(n, 1e-10f), IEEE float32 division (cache.py:237-238);
+//   y_j = sum_i x_n[i] * R[j][i] accumulated in float32 (rotation.py:65);
+//   idx = #{k : y > b_k} (codebook.py:220-223);
+//   codes packed as an LSB-first bitstream per row (packing.py:9-173).
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "tq_common.h"
+
+namespace tq {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_codec(const tq_codec* c) {
+  if (!c) return set_error(TQ_ERR_INVALID, "codec is NULL");
+  if (c->d != 64 && c->d != 128 && c->d != 256)
+    return set_error(TQ_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, 256)", c->d);
+  if (c->bits_hi < 1 || c->bits_hi > 4 || c->bits_lo < 1 || c->bits_lo > 4)
+    return set_error(TQ_ERR_UNSUPPORTED, "Unsupported bit-width: %d/%d. Use 1, 2, 3, or 4.",
+                     c->bits_hi, c->bits_lo);
+  if (c->split <= 0 || c->split > c->d || (c->split % 32) != 0)
+    return set_error(TQ_ERR_UNSUPPORTED, "split %d must be a positive multiple of 32 <= d", c->split);
+  if (!c->rotation || !c->centroids_hi || !c->boundaries_hi)
+    return set_error(TQ_ERR_INVALID, "codec rotation / codebook pointer is NULL");
+  if (c->split < c->d && (!c->centroids_lo || !c->boundaries_lo))
+    return set_error(TQ_ERR_INVALID, "fractional codec needs the low-width codebook");
+  if (c->qjl_proj && (c->qjl_m <= 0 || (c->qjl_m % 32) != 0 || c->qjl_m > 256))
+    return set_error(TQ_ERR_UNSUPPORTED, "qjl_m %d must be a multiple of 32 in [32, 256]", c->qjl_m);
+  return TQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Tiled float32 row-vector x matrix products for VPW vectors of dimension D.
+// Thread (v, q) owns output columns [32q, 32q+32) of vector v. The matrix tile
+// is staged in LDS with each 32-column segment padded to 36 floats so that the
+// NSEG segments of a wave read distinct LDS banks.
+// ---------------------------------------------------------------------------
+template <int D>
+struct Geo {
+  static constexpr int NSEG = D / 32;          // 32-column segments
+  static constexpr int VPW = 256 / NSEG;       // vectors per workgroup
+  static constexpr int XS = D + 1;             // padded row of the vector tile
+  static constexpr int SEGP = 36;              // padded segment
+  static constexpr int MROW = NSEG * SEGP;     // padded matrix row
+  static constexpr int TI = 32;                // matrix rows per LDS tile
+};
+
+struct CompressArgs {
+  const void* x;
+  int x_dtype;
+  int64_t x_hs;
+  tq_span span;
+  tq_store dst;
+  const float* rot;
+  const float* bnd_hi;
+  const float* bnd_lo;
+  const float* cen_hi;
+  const float* cen_lo;
+  const float* proj;
+  int bits_hi, bits_lo, split, qjl_m;
+  int row_hi, row_lo, row_sign;
+};
+
+template <int BITS>
+__device__ inline void store_codes(uint8_t* dst, const uint32_t (&code)[32]) {
+  uint32_t w[BITS];
+  pack32<BITS>(code, w);
+  uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+#pragma unroll
+  for (int i = 0; i < BITS; ++i) d32[i] = w[i];
+}
+
+__device__ inline void store_codes_dyn(int bits, uint8_t* dst, const uint32_t (&code)[32]) {
+  switch (bits) {
+    case 1: store_codes<1>(dst, code); break;
+    case 2: store_codes<2>(dst, code); break;
+    case 3: store_codes<3>(dst, code); break;
+    default: store_codes<4>(dst, code); break;
+  }
+}
+
+template <int BITS>
+__device__ inline void load_codes(const uint8_t* src, uint32_t (&code)[32]) {
+  uint32_t w[BITS];
+  const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
+#pragma unroll
+  for (int i = 0; i < BITS; ++i) w[i] = s32[i];
+  unpack32<BITS>(w, code);
+}
+
+__device__ inline void load_codes_dyn(int bits, const uint8_t* src, uint32_t (&code)[32]) {
+  switch (bits) {
+    case 1: load_codes<1>(src, code); break;
+    case 2: load_codes<2>(src, code); break;
+    case 3: load_codes<3>(src, code); break;
+    default: load_codes<4>(src, code); break;
+  }
+}
+
+// count of boundaries strictly below y (ties go low, NaN -> 0)
+__device__ inline uint32_t quantize_one(float y, const float* b, int nb) {
+  uint32_t idx = 0;
+  for (int k = 0; k < nb; ++k) idx += (y > b[k]) ? 1u : 0u;
+  return idx;
+}
+
+// acc[c] += sum_{i in tile} xs[v][i] * M[i][32q + c] for the LDS tile M.
+template <int D>
+__device__ inline void tile_madd(const float* __restrict__ xs_row, const float* __restrict__ mt,
+                                 int i0, int q, float (&acc)[32]) {
+  using G = Geo<D>;
+#pragma unroll 4
+  for (int ii = 0; ii < G::TI; ++ii) {
+    const float xv = xs_row[i0 + ii];
+    const float4* m4 = reinterpret_cast<const float4*>(mt + ii * G::MROW + q * G::SEGP);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 r = m4[k];
+      acc[4 * k + 0] = fmaf(xv, r.x, acc[4 * k + 0]);
+      acc[4 * k + 1] = fmaf(xv, r.y, acc[4 * k + 1]);
+      acc[4 * k + 2] = fmaf(xv, r.z, acc[4 * k + 2]);
+      acc[4 * k + 3] = fmaf(xv, r.w, acc[4 * k + 3]);
+    }
+  }
+}
+
+// Stage rows [i0, i0+TI) of M (row-major D x D, or its transpose when
+// TRANSPOSE) into the padded LDS tile mt[ii][seg][SEGP].
+template <int D, bool TRANSPOSE>
+__device__ inline void stage_tile(const float* __restrict__ m, int i0, float* mt) {
+  using G = Geo<D>;
+  for (int e = threadIdx.x; e < G::TI * D; e += blockDim.x) {
+    const int ii = e / D, j = e % D;
+    const float val = TRANSPOSE ? m[(int64_t)j * D + (i0 + ii)] : m[(int64_t)(i0 + ii) * D + j];
+    mt[ii * G::MROW + (j >> 5) * G::SEGP + (j & 31)] = val;
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
+  using G = Geo<D>;
+  __shared__ float xs[G::VPW * G::XS];
+  __shared__ float mt[G::TI * G::MROW];
+  __shared__ float nrm[G::VPW];
+  __shared__ float bnd[2][16];
+  __shared__ float cen[2][16];
+
+  const int r = blockIdx.y;
+  const int b = r / a.span.heads;
+  const int n_tok = a.span.n_tok_b ? a.span.n_tok_b[b] : a.span.n_tok;
+  const int t0 = blockIdx.x * G::VPW;
+  if (t0 >= n_tok) return;
+  const int nv = min(G::VPW, n_tok - t0);
+  const int src0 = (a.span.src_tok0_b ? a.span.src_tok0_b[b] : 0) + t0;
+  const int dst0 = (a.span.dst_tok0_b ? a.span.dst_tok0_b[b] : 0) + t0;
+  const int tid = threadIdx.x;
+
+  if (tid < 16) {
+    const int nbh = (1 << a.bits_hi) - 1, nbl = (1 << a.bits_lo) - 1;
+    bnd[0][tid] = tid < nbh ? a.bnd_hi[tid] : 0.f;
+    bnd[1][tid] = tid < nbl ? a.bnd_lo[tid] : 0.f;
+    cen[0][tid] = tid <= nbh ? a.cen_hi[tid] : 0.f;
+    cen[1][tid] = tid <= nbl ? a.cen_lo[tid] : 0.f;
+  }
+
+  // Load the fp16 tile as float32 (exact).
+  const int64_t xrow = (int64_t)r * a.x_hs + (int64_t)src0 * D;
+  for (int e = tid; e < G::VPW * D; e += blockDim.x) {
+    const int v = e / D, i = e % D;
+    xs[v * G::XS + i] = v < nv ? load_elem(a.x, xrow + (int64_t)v * D + i, a.x_dtype) : 0.f;
+  }
+  __syncthreads();
+
+  // Norm: float64 sum of squares in index order, rounded square root.
+  if (tid < G::VPW) {
+    double s = 0.0;
+    const float* row = xs + tid * G::XS;
+    for (int i = 0; i < D; ++i) {
+      const double xi = (double)row[i];
+      s = fma(xi, xi, s);
+    }
+    const float n = (float)sqrt(s);
+    nrm[tid] = n;
+    if (tid < nv) a.dst.norms[(int64_t)r * a.dst.norm_head_stride + dst0 + tid] = n;
+  }
+  __syncthreads();
+
+  // Normalise in place.
+  for (int e = tid; e < G::VPW * D; e += blockDim.x) {
+    const int v = e / D, i = e % D;
+    xs[v * G::XS + i] = xs[v * G::XS + i] / fmaxf(nrm[v], 1e-10f);
+  }
+
+  // Rotate: y = x_n @ R^T.
+  const int v = tid / G::NSEG, q = tid % G::NSEG;
+  float acc[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) acc[c] = 0.f;
+  for (int i0 = 0; i0 < D; i0 += G::TI) {
+    __syncthreads();
+    stage_tile<D, true>(a.rot, i0, mt);
+    __syncthreads();
+    tile_madd<D>(xs + v * G::XS, mt, i0, q, acc);
+  }
+
+  // Quantize + pack this thread's 32 coordinates.
+  const bool hi = 32 * q < a.split;
+  const int bits = hi ? a.bits_hi : a.bits_lo;
+  const float* bk = bnd[hi ? 0 : 1];
+  const int nb = (1 << bits) - 1;
+  uint32_t code[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) code[c] = quantize_one(acc[c], bk, nb);
+  if (v < nv) {
+    uint8_t* dst;
+    if (hi) {
+      dst = a.dst.codes_hi + (int64_t)r * a.dst.hi_head_stride + (int64_t)(dst0 + v) * a.row_hi +
+            (32 * q) * bits / 8;
+    } else {
+      dst = a.dst.codes_lo + (int64_t)r * a.dst.lo_head_stride + (int64_t)(dst0 + v) * a.row_lo +
+            (32 * q - a.split) * bits / 8;
+    }
+    store_codes_dyn(bits, dst, code);
+  }
+
+  if (!a.proj) return;
+
+  // QJL sketch of the residual r = x - n * (c[idx] @ R) (cache.py:396-427).
+  // Reconstruct in rotated space first: xs[v][j] <- c[idx_j] (overwrites x_n).
+  __syncthreads();
+  {
+    const float* ck = cen[hi ? 0 : 1];
+#pragma unroll
+    for (int c = 0; c < 32; ++c) xs[v * G::XS + 32 * q + c] = ck[code[c]];
+  }
+#pragma unroll
+  for (int c = 0; c < 32; ++c) acc[c] = 0.f;
+  for (int i0 = 0; i0 < D; i0 += G::TI) {
+    __syncthreads();
+    stage_tile<D, false>(a.rot, i0, mt);
+    __syncthreads();
+    tile_madd<D>(xs + v * G::XS, mt, i0, q, acc);
+  }
+  __syncthreads();
+  // residual in xs (float32: x - n * acc)
+  {
+    const float n = nrm[v];
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      const int i = 32 * q + c;
+      const float x = v < nv ? load_elem(a.x, xrow + (int64_t)v * D + i, a.x_dtype) : 0.f;
+      xs[v * G::XS + i] = x - n * acc[c];
+    }
+  }
+  __syncthreads();
+  if (tid < G::VPW) {
+    double s = 0.0;
+    const float* row = xs + tid * G::XS;
+    for (int i = 0; i < D; ++i) {
+      const double ri = (double)row[i];
+      s = fma(ri, ri, s);
+    }
+    if (tid < nv) a.dst.gamma[(int64_t)r * a.dst.gamma_head_stride + dst0 + tid] = (float)sqrt(s);
+  }
+  // proj = r @ S^T, m outputs in segments of 32 (S rows are projections).
+  const int nseg_m = a.qjl_m / 32;
+  for (int s0 = 0; s0 < nseg_m; s0 += G::NSEG) {
+    // Stage S^T columns [32*s0, 32*s0 + D) in tiles: reuse mt with rows i of S^T.
+    const int qs = s0 + q;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) acc[c] = 0.f;
+    for (int i0 = 0; i0 < D; i0 += G::TI) {
+      __syncthreads();
+      for (int e = tid; e < G::TI * D; e += blockDim.x) {
+        const int ii = e / D, j = e % D;  // j indexes projection 32*s0 + j
+        const int mrow = 32 * s0 + j;
+        mt[ii * G::MROW + (j >> 5) * G::SEGP + (j & 31)] =
+            mrow < a.qjl_m ? a.proj[(int64_t)mrow * D + i0 + ii] : 0.f;
+      }
+      __syncthreads();
+      tile_madd<D>(xs + v * G::XS, mt, i0, q, acc);
+    }
+    if (v < nv && qs < nseg_m) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) word |= (acc[c] >= 0.f ? 1u : 0u) << c;
+      uint32_t* sd = reinterpret_cast<uint32_t*>(a.dst.signs + (int64_t)r * a.dst.sign_head_stride +
+                                                 (int64_t)(dst0 + v) * a.row_sign);
+      sd[qs] = word;
+    }
+  }
+}
+
+struct DequantArgs {
+  tq_store src;
+  tq_span span;
+  float* out;
+  int64_t out_hs;
+  const float* rot;
+  const float* cen_hi;
+  const float* cen_lo;
+  const float* proj;
+  int bits_hi, bits_lo, split, qjl_m, apply_qjl;
+  int row_hi, row_lo, row_sign;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
+  using G = Geo<D>;
+  __shared__ float ys[G::VPW * G::XS];
+  __shared__ float mt[G::TI * G::MROW];
+  __shared__ float cen[2][16];
+  const int r = blockIdx.y;
+  const int b = r / a.span.heads;
+  const int n_tok = a.span.n_tok_b ? a.span.n_tok_b[b] : a.span.n_tok;
+  const int t0 = blockIdx.x * G::VPW;
+  if (t0 >= n_tok) return;
+  const int nv = min(G::VPW, n_tok - t0);
+  const int src0 = (a.span.src_tok0_b ? a.span.src_tok0_b[b] : 0) + t0;
+  const int dst0 = (a.span.dst_tok0_b ? a.span.dst_tok0_b[b] : 0) + t0;
+  const int tid = threadIdx.x;
+  if (tid < 16) {
+    cen[0][tid] = tid < (1 << a.bits_hi) ? a.cen_hi[tid] : 0.f;
+    cen[1][tid] = tid < (1 << a.bits_lo) ? a.cen_lo[tid] : 0.f;
+  }
+  __syncthreads();
+  const int v = tid / G::NSEG, q = tid % G::NSEG;
+  const bool hi = 32 * q < a.split;
+  const int bits = hi ? a.bits_hi : a.bits_lo;
+  uint32_t code[32];
+  if (v < nv) {
+    const uint8_t* src = hi ? a.src.codes_hi + (int64_t)r * a.src.hi_head_stride +
+                                  (int64_t)(src0 + v) * a.row_hi + (32 * q) * bits / 8
+                            : a.src.codes_lo + (int64_t)r * a.src.lo_head_stride +
+                                  (int64_t)(src0 + v) * a.row_lo + (32 * q - a.split) * bits / 8;
+    load_codes_dyn(bits, src, code);
+  } else {
+#pragma unroll
+    for (int c = 0; c < 32; ++c) code[c] = 0;
+  }
+  const float* ck = cen[hi ? 0 : 1];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) ys[v * G::XS + 32 * q + c] = ck[code[c]];
+  float acc[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) acc[c] = 0.f;
+  for (int i0 = 0; i0 < D; i0 += G::TI) {
+    __syncthreads();
+    stage_tile<D, false>(a.rot, i0, mt);
+    __syncthreads();
+    tile_madd<D>(ys + v * G::XS, mt, i0, q, acc);
+  }
+  const float n = v < nv ? a.src.norms[(int64_t)r * a.src.norm_head_stride + src0 + v] : 0.f;
+#pragma unroll
+  for (int c = 0; c < 32; ++c) acc[c] *= n;
+
+  if (a.apply_qjl) {
+    // + sqrt(pi/2)/D * gamma * (z @ S), z = +-1 from the stored signs.
+    __syncthreads();
+    const int nseg_m = a.qjl_m / 32;
+    // z rows into ys (m <= 256 fits the padded tile width only when m <= D;
+    // process the projections in chunks of D).
+    float corr[32];
+#pragma unroll
+    for (int c = 0; c < 32; ++c) corr[c] = 0.f;
+    for (int m0 = 0; m0 < a.qjl_m; m0 += D) {
+      __syncthreads();
+      if (v < nv) {
+        const uint32_t* sg = reinterpret_cast<const uint32_t*>(
+            a.src.signs + (int64_t)r * a.src.sign_head_stride + (int64_t)(src0 + v) * a.row_sign);
+        const int seg = m0 / 32 + q;
+        const uint32_t w = seg < nseg_m ? sg[seg] : 0u;
+#pragma unroll
+        for (int c = 0; c < 32; ++c)
+          ys[v * G::XS + 32 * q + c] = seg < nseg_m ? (((w >> c) & 1u) ? 1.f : -1.f) : 0.f;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 32; ++c) ys[v * G::XS + 32 * q + c] = 0.f;
+      }
+      const int mi = min(D, a.qjl_m - m0);
+      for (int i0 = 0; i0 < mi; i0 += G::TI) {
+        __syncthreads();
+        stage_tile<D, false>(a.proj + (int64_t)m0 * D, i0, mt);
+        __syncthreads();
+        tile_madd<D>(ys + v * G::XS, mt, i0, q, corr);
+      }
+    }
+    if (v < nv) {
+      const float g = a.src.gamma[(int64_t)r * a.src.gamma_head_stride + src0 + v];
+      const float sc = 1.2533141373155003f / (float)D * g;  // sqrt(pi/2)/D * gamma
+#pragma unroll
+      for (int c = 0; c < 32; ++c) acc[c] = fmaf(sc, corr[c], acc[c]);
+    }
+  }
+  if (v < nv) {
+    float4* o = reinterpret_cast<float4*>(a.out + (int64_t)r * a.out_hs + (int64_t)(dst0 + v) * D + 32 * q);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = make_float4(acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]);
+  }
+}
+
+__global__ void pack_kernel(const uint8_t* __restrict__ idx, int64_t n_rows, int d, int bits,
+                            uint8_t* __restrict__ out) {
+  const int rb = d * bits / 8;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n_rows * rb) return;
+  const int64_t row = e / rb;
+  const int k = (int)(e % rb);
+  const uint8_t* in = idx + row * d;
+  uint32_t byte = 0;
+  const int jlo = (8 * k) / bits, jhi = (8 * k + 7) / bits;
+  for (int j = jlo; j <= jhi && j < d; ++j) {
+    const int p = bits * j - 8 * k;  // bit offset of code j relative to this byte
+    const uint32_t c = in[j] & ((1u << bits) - 1u);
+    byte |= p >= 0 ? (c << p) : (c >> (-p));
+  }
+  out[e] = (uint8_t)(byte & 0xFFu);
+}
+
+__global__ void unpack_kernel(const uint8_t* __restrict__ in, int64_t n_rows, int d, int bits,
+                              uint8_t* __restrict__ idx) {
+  const int rb = d * bits / 8;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n_rows * d) return;
+  const int64_t row = e / d;
+  const int j = (int)(e % d);
+  const uint8_t* p = in + row * rb;
+  const int bit = bits * j;
+  uint32_t v = p[bit >> 3] >> (bit & 7);
+  if ((bit & 7) + bits > 8) v |= (uint32_t)p[(bit >> 3) + 1] << (8 - (bit & 7));
+  idx[e] = (uint8_t)(v & ((1u << bits) - 1u));
+}
+
+__global__ void quantize_scalar_kernel(const float* __restrict__ y, int64_t n,
+                                       const float* __restrict__ b, int nb, uint8_t* __restrict__ idx) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  idx[e] = (uint8_t)quantize_one(y[e], b, nb);
+}
+
+static int check_span(const tq_span* s) {
+  if (!s) return set_error(TQ_ERR_INVALID, "span is NULL");
+  if (s->rows < 0 || s->n_tok < 0 || s->heads <= 0 || (s->rows % s->heads) != 0)
+    return set_error(TQ_ERR_INVALID, "bad span rows=%d heads=%d n_tok=%d", s->rows, s->heads, s->n_tok);
+  if (s->rows > 65535) return set_error(TQ_ERR_UNSUPPORTED, "rows %d > 65535", s->rows);
+  return TQ_OK;
+}
+
+static bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" {
+
+int tq_abi_version(void) { return TQ_ABI_VERSION; }
+
+const char* tq_last_error(void) { return tq::g_err; }
+
+int tq_device_supported(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  hipDeviceProp_t p;
+  if (hipGetDeviceProperties(&p, dev) != hipSuccess) return 0;
+  return strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x_head_stride,
+                const tq_span* span, const tq_store* dst, void* stream) {
+  int rc = check_codec(codec);
+  if (rc) return rc;
+  if ((rc = check_span(span))) return rc;
+  if (x_dtype != TQ_F16 && x_dtype != TQ_BF16 && x_dtype != TQ_F32)
+    return set_error(TQ_ERR_UNSUPPORTED, "compress: unknown input dtype %d", x_dtype);
+  if (!x || !dst || !dst->codes_hi || !dst->norms)
+    return set_error(TQ_ERR_INVALID, "compress: NULL input/output pointer");
+  if (codec->split < codec->d && !dst->codes_lo)
+    return set_error(TQ_ERR_INVALID, "compress: fractional codec needs codes_lo");
+  const bool qjl = codec->qjl_proj && dst->signs;
+  if (qjl && !dst->gamma) return set_error(TQ_ERR_INVALID, "compress: QJL needs gamma output");
+  if (!aligned4(dst->codes_hi) || (dst->hi_head_stride & 3) ||
+      (dst->codes_lo && (!aligned4(dst->codes_lo) || (dst->lo_head_stride & 3))) ||
+      (qjl && (!aligned4(dst->signs) || (dst->sign_head_stride & 3))))
+    return set_error(TQ_ERR_INVALID, "compress: packed outputs must be 4-byte aligned");
+  if (span->rows == 0 || span->n_tok == 0) return TQ_OK;
+  CompressArgs a;
+  a.x = x;
+  a.x_dtype = x_dtype;
+  a.x_hs = x_head_stride;
+  a.span = *span;
+  a.dst = *dst;
+  a.rot = codec->rotation;
+  a.bnd_hi = codec->boundaries_hi;
+  a.bnd_lo = codec->split < codec->d ? codec->boundaries_lo : codec->boundaries_hi;
+  a.cen_hi = codec->centroids_hi;
+  a.cen_lo = codec->split < codec->d ? codec->centroids_lo : codec->centroids_hi;
+  a.proj = qjl ? codec->qjl_proj : nullptr;
+  a.qjl_m = qjl ? codec->qjl_m : 0;
+  a.bits_hi = codec->bits_hi;
+  a.bits_lo = codec->split < codec->d ? codec->bits_lo : codec->bits_hi;
+  a.split = codec->split;
+  a.row_hi = row_bytes(codec->split, codec->bits_hi);
+  a.row_lo = row_bytes(codec->d - codec->split, a.bits_lo);
+  a.row_sign = a.qjl_m / 8;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (codec->d) {
+    case 64: {
+      dim3 g((span->n_tok + Geo<64>::VPW - 1) / Geo<64>::VPW, span->rows);
+      hipLaunchKernelGGL(compress_kernel<64>, g, dim3(256), 0, s, a);
+      break;
+    }
+    case 128: {
+      dim3 g((span->n_tok + Geo<128>::VPW - 1) / Geo<128>::VPW, span->rows);
+      hipLaunchKernelGGL(compress_kernel<128>, g, dim3(256), 0, s, a);
+      break;
+    }
+    default: {
+      dim3 g((span->n_tok + Geo<256>::VPW - 1) / Geo<256>::VPW, span->rows);
+      hipLaunchKernelGGL(compress_kernel<256>, g, dim3(256), 0, s, a);
+      break;
+    }
+  }
+  TQ_LAUNCH_CHECK("tq_compress");
+  return TQ_OK;
+}
+
+int tq_dequantize(const tq_codec* codec, const tq_store* src, const tq_span* span, float* out,
+                  int64_t out_head_stride, int32_t apply_qjl, void* stream) {
+  int rc = check_codec(codec);
+  if (rc) return rc;
+  if ((rc = check_span(span))) return rc;
+  if (!src || !src->codes_hi || !src->norms || !out)
+    return set_error(TQ_ERR_INVALID, "dequantize: NULL input/output pointer");
+  if (codec->split < codec->d && !src->codes_lo)
+    return set_error(TQ_ERR_INVALID, "dequantize: fractional codec needs codes_lo");
+  const bool qjl = apply_qjl && codec->qjl_proj && src->signs && src->gamma;
+  if (apply_qjl && !qjl) return set_error(TQ_ERR_INVALID, "dequantize: QJL needs projection, signs, gamma");
+  if ((reinterpret_cast<uintptr_t>(out) & 15) || (out_head_stride & 3))
+    return set_error(TQ_ERR_INVALID, "dequantize: output must be 16-byte aligned");
+  if (span->rows == 0 || span->n_tok == 0) return TQ_OK;
+  DequantArgs a;
+  a.src = *src;
+  a.span = *span;
+  a.out = out;
+  a.out_hs = out_head_stride;
+  a.rot = codec->rotation;
+  a.cen_hi = codec->centroids_hi;
+  a.cen_lo = codec->split < codec->d ? codec->centroids_lo : codec->centroids_hi;
+  a.proj = qjl ? codec->qjl_proj : nullptr;
+  a.qjl_m = qjl ? codec->qjl_m : 0;
+  a.apply_qjl = qjl ? 1 : 0;
+  a.bits_hi = codec->bits_hi;
+  a.bits_lo = codec->split < codec->d ? codec->bits_lo : codec->bits_hi;
+  a.split = codec->split;
+  a.row_hi = row_bytes(codec->split, codec->bits_hi);
+  a.row_lo = row_bytes(codec->d - codec->split, a.bits_lo);
+  a.row_sign = a.qjl_m / 8;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (codec->d) {
+    case 64: {
+      dim3 g((span->n_tok + Geo<64>::VPW - 1) / Geo<64>::VPW, span->rows);
+      hipLaunchKernelGGL(dequant_kernel<64>, g, dim3(256), 0, s, a);
+      break;
+    }
+    case 128: {
+      dim3 g((span->n_tok + Geo<128>::VPW - 1) / Geo<128>::VPW, span->rows);
+      hipLaunchKernelGGL(dequant_kernel<128>, g, dim3(256), 0, s, a);
+      break;
+    }
+    default: {
+      dim3 g((span->n_tok + Geo<256>::VPW - 1) / Geo<256>::VPW, span->rows);
+      hipLaunchKernelGGL(dequant_kernel<256>, g, dim3(256), 0, s, a);
+      break;
+    }
+  }
+  TQ_LAUNCH_CHECK("tq_dequantize");
+  return TQ_OK;
+}
+
+int tq_pack_codes(const uint8_t* idx, int64_t n_rows, int32_t d, int32_t bits, uint8_t* packed,
+                  void* stream) {
+  if (bits < 1 || bits > 4)
+    return set_error(TQ_ERR_UNSUPPORTED, "Unsupported bit-width: %d. Use 1, 2, 3, or 4.", bits);
+  if (d <= 0 || (d * bits) % 8 != 0)
+    return set_error(TQ_ERR_INVALID, "Last dimension %d cannot be packed at %d bits", d, bits);
+  if (n_rows < 0) return set_error(TQ_ERR_INVALID, "n_rows < 0");
+  const int64_t n = n_rows * (int64_t)(d * bits / 8);
+  if (n == 0) return TQ_OK;
+  if (!idx || !packed) return set_error(TQ_ERR_INVALID, "pack: NULL pointer");
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), idx, n_rows, d, bits, packed);
+  TQ_LAUNCH_CHECK("tq_pack_codes");
+  return TQ_OK;
+}
+
+int tq_unpack_codes(const uint8_t* packed, int64_t n_rows, int32_t d, int32_t bits, uint8_t* idx,
+                    void* stream) {
+  if (bits < 1 || bits > 4)
+    return set_error(TQ_ERR_UNSUPPORTED, "Unsupported bit-width: %d. Use 1, 2, 3, or 4.", bits);
+  if (d <= 0 || (d * bits) % 8 != 0)
+    return set_error(TQ_ERR_INVALID, "Last dimension %d cannot be unpacked at %d bits", d, bits);
+  if (n_rows < 0) return set_error(TQ_ERR_INVALID, "n_rows < 0");
+  const int64_t n = n_rows * (int64_t)d;
+  if (n == 0) return TQ_OK;
+  if (!idx || !packed) return set_error(TQ_ERR_INVALID, "unpack: NULL pointer");
+  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), packed, n_rows, d, bits, idx);
+  TQ_LAUNCH_CHECK("tq_unpack_codes");
+  return TQ_OK;
+}
+
+int tq_quantize_scalar(const float* y, int64_t n, const float* boundaries, int32_t n_boundaries,
+                       uint8_t* idx, void* stream) {
+  if (n < 0 || n_boundaries < 0 || n_boundaries > 255)
+    return set_error(TQ_ERR_INVALID, "quantize_scalar: bad sizes");
+  if (n == 0) return TQ_OK;
+  if (!y || !idx || (n_boundaries && !boundaries))
+    return set_error(TQ_ERR_INVALID, "quantize_scalar: NULL pointer");
+  hipLaunchKernelGGL(quantize_scalar_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), y, n, boundaries, n_boundaries, idx);
+  TQ_LAUNCH_CHECK("tq_quantize_scalar");
+  return TQ_OK;
+}
+
+}  // extern "C"

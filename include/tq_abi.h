@@ -59,6 +59,8 @@ typedef struct tq_codec {
   const float* qjl_proj;       /* (qjl_m, d) Gaussian S (qjl.py:23-36) or NULL */
   int32_t qjl_m;               /* number of projections (multiple of 32) or 0 */
   int32_t reserved;
+  const float* rotation_t;     /* (d, d) row-major R^T, or NULL (the single-launch
+                                  decode kernel needs it; others ignore it) */
 } tq_codec;
 
 /* A compressed store: packed codes, norms and optional QJL sketch.
@@ -158,8 +160,17 @@ typedef struct tq_attn_desc {
   int32_t res_cap, res_start0;          /* ring capacity; ring start when res_start == NULL */
   const int32_t* res_start;             /* (batch,) ring start, or NULL = res_start0 */
   const int32_t* res_len;               /* (batch,) or NULL = max_res */
+  int32_t flags;                        /* TQ_ATTN_* bits */
+  int32_t reserved2;
 } tq_attn_desc;
 
+/* tq_attn_desc.flags: force the general kernel (every width / QJL) even where
+ * the single-launch K4/V2 kernel applies. */
+#define TQ_ATTN_GENERAL 1
+
+/* Workspace: the first 256-byte-rounded (batch * hkv * 4) bytes hold ticket
+ * counters that must be zero before the first call on a workspace; every
+ * call leaves them zero. Calls sharing a workspace must not overlap. */
 size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* desc);
 int tq_decode_attention(const tq_codec* kcodec, const tq_codec* vcodec,
                         const tq_attn_desc* desc, void* workspace,

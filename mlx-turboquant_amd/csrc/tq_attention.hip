@@ -19,6 +19,7 @@
 #include <math.h>
 
 #include "tq_common.h"
+#include "tq_decode_fast.h"
 
 namespace tq {
 
@@ -379,6 +380,43 @@ static void launch_chunks(const AttnArgs& a, int G, dim3 grid, hipStream_t s) {
   }
 }
 
+// Tickets of the single-launch kernel live at the front of the workspace.
+static size_t counter_bytes(const tq_attn_desc* d) {
+  return (((size_t)d->batch * d->hkv * 4) + 255) & ~(size_t)255;
+}
+
+static int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    hipDeviceProp_t p;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess)
+      cus = p.multiProcessorCount;
+    if (cus <= 0) cus = 256;
+  }
+  return cus;
+}
+
+// Workgroups per (sequence, kv head) and 32-token blocks per workgroup: one
+// workgroup per CU in total, blocks split evenly over its 8 waves.
+static void fast_geometry(const tq_attn_desc* d, int& nwg, int& bpw) {
+  const int nbt = (d->max_comp + 31) / 32 + (d->max_sink + 31) / 32 + (d->max_res + 31) / 32;
+  const int groups = d->batch * d->hkv > 0 ? d->batch * d->hkv : 1;
+  int target = (device_cus() + groups - 1) / groups;
+  const int maxwg = nbt > 0 ? (nbt + 7) / 8 : 1;
+  nwg = target < 1 ? 1 : (target > maxwg ? maxwg : target);
+  if (nwg > fast_max_wg()) nwg = fast_max_wg();
+  bpw = nbt > 0 ? (nbt + nwg - 1) / nwg : 0;
+  bpw = (bpw + 7) / 8 * 8;
+  if (bpw == 0) bpw = 8;
+}
+
+static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
+  const int G = d->hq / d->hkv;
+  return kc->rotation_t != nullptr && kc->d == 128 && kc->bits_hi == 4 && kc->split == 128 && vc->bits_hi == 2 && vc->split == 128 &&
+         !d->qjl && d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8);
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -393,7 +431,11 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
   const int m = d->qjl ? kcodec->qjl_m : 0;
   const size_t nch = (size_t)(nc + ns + nr);
   const size_t heads = (size_t)d->batch * d->hq;
-  size_t bytes = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
+  size_t general = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
+  int nwg, bpw;
+  fast_geometry(d, nwg, bpw);
+  const size_t fast = (size_t)d->batch * d->hkv * nwg * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
+  const size_t bytes = counter_bytes(d) + (general > fast ? general : fast);
   return (bytes + 255) & ~(size_t)255;
 }
 
@@ -434,6 +476,31 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   if (!workspace || workspace_bytes < need)
     return set_error(TQ_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, need);
 
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fast_eligible(kc, vc, d) && !(d->flags & TQ_ATTN_GENERAL)) {
+    if (fast_set_attributes() != 0)
+      return set_error(TQ_ERR_LAUNCH, "cannot raise the LDS limit of the decode kernel");
+    FastArgs f;
+    f.kc = d->kstore.codes_hi; f.k_hs = d->kstore.hi_head_stride;
+    f.kn = d->kstore.norms; f.kn_hs = d->kstore.norm_head_stride;
+    f.vc = d->vstore.codes_hi; f.v_hs = d->vstore.hi_head_stride;
+    f.vn = d->vstore.norms; f.vn_hs = d->vstore.norm_head_stride;
+    f.sink_k = d->sink_k; f.sink_v = d->sink_v; f.sink_hs = d->sink_head_stride;
+    f.res_k = d->res_k; f.res_v = d->res_v; f.res_hs = d->res_head_stride;
+    f.res_cap = d->res_cap; f.res_start0 = d->res_start0;
+    f.comp_len_b = d->comp_len; f.sink_len_b = d->sink_len; f.res_len_b = d->res_len; f.res_start_b = d->res_start;
+    f.max_comp = d->max_comp; f.max_sink = d->max_sink; f.max_res = d->max_res;
+    f.q = d->q; f.q_dtype = d->q_dtype; f.out = d->out;
+    f.hq = d->hq; f.hkv = d->hkv;
+    f.qscale = d->scale * 1.4426950408889634f;
+    f.rot = kc->rotation; f.rot_t = kc->rotation_t; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
+    f.counter = static_cast<int*>(workspace);
+    f.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes(d));
+    fast_geometry(d, f.nwg, f.bpw);
+    if (launch_fast_decode(f, G, d->batch, s) != 0) TQ_LAUNCH_CHECK("tq_decode_attention (fast)");
+    return TQ_OK;
+  }
+
   AttnArgs a;
   a.d = *d;
   a.D = kc->d;
@@ -459,13 +526,12 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   a.nch = a.nc + a.ns + a.nr;
   a.ps = part_stride(a.D, a.m);
   const size_t heads = (size_t)d->batch * d->hq;
-  float* ws = static_cast<float*>(workspace);
+  float* ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes(d));
   a.qr = ws;
   a.qs = a.qr + heads * a.D;
   a.sq = a.qs + heads * a.D;
   a.part = a.sq + heads * a.m;
 
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t pro_smem = (size_t)a.D * 4;
   hipLaunchKernelGGL(prologue_kernel, dim3(d->hq, d->batch), dim3(128), pro_smem, s, a);
   TQ_LAUNCH_CHECK("tq_decode_attention prologue");

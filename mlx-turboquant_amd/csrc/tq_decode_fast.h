@@ -1,0 +1,43 @@
+// Arguments of the single-launch K4/V2 decode-attention kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tq {
+
+struct FastArgs {
+  const uint8_t* kc;  int64_t k_hs;    // 4-bit key codes, 64-byte rows
+  const float* kn;    int64_t kn_hs;   // key norms
+  const uint8_t* vc;  int64_t v_hs;    // 2-bit value codes, 32-byte rows
+  const float* vn;    int64_t vn_hs;   // value norms
+  const void* sink_k; const void* sink_v; int64_t sink_hs;   // fp16, elements
+  const void* res_k;  const void* res_v;  int64_t res_hs;    // fp16 ring
+  int res_cap, res_start0;
+  const int32_t* comp_len_b;
+  const int32_t* sink_len_b;
+  const int32_t* res_len_b;
+  const int32_t* res_start_b;
+  int max_comp, max_sink, max_res;
+  const void* q; int q_dtype;
+  float* out;
+  int hq, hkv;
+  float qscale;          // scale * log2(e)
+  const float* rot;      // R (128 x 128)
+  const float* rot_t;    // R^T (128 x 128)
+  const float* kcen;     // 16 key centroids
+  const float* vcen;     // 4 value centroids
+  float* part;           // partials
+  int* counter;          // (batch * hkv) tickets, zero between calls
+  int nwg;               // workgroups per (sequence, kv head)
+  int bpw;               // 32-token blocks per workgroup
+};
+
+size_t fast_smem_bytes();
+int fast_set_attributes();
+int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s);
+int fast_max_wg();
+
+constexpr int FAST_PART_FLOATS = 132;  // per query head per workgroup
+
+}  // namespace tq

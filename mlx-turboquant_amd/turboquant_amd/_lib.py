@@ -35,7 +35,7 @@ class Codec(ctypes.Structure):
     _fields_ = [("d", _i32), ("bits_hi", _i32), ("bits_lo", _i32), ("split", _i32),
                 ("rotation", _p), ("centroids_hi", _p), ("boundaries_hi", _p),
                 ("centroids_lo", _p), ("boundaries_lo", _p), ("qjl_proj", _p),
-                ("qjl_m", _i32), ("reserved", _i32)]
+                ("qjl_m", _i32), ("reserved", _i32), ("rotation_t", _p)]
 
 
 class Store(ctypes.Structure):
@@ -62,7 +62,9 @@ class AttnDesc(ctypes.Structure):
                 ("sink_k", _p), ("sink_v", _p), ("sink_head_stride", _i64), ("sink_len", _p),
                 ("res_k", _p), ("res_v", _p), ("res_head_stride", _i64),
                 ("res_cap", _i32), ("res_start0", _i32),
-                ("res_start", _p), ("res_len", _p)]
+                ("res_start", _p), ("res_len", _p), ("flags", _i32), ("reserved2", _i32)]
+
+TQ_ATTN_GENERAL = 1
 
 
 _PC = ctypes.POINTER(Codec)

@@ -30,10 +30,12 @@ _workspaces: dict[tuple[str, int], torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per (device, stream) attention workspace. Zero-filled on allocation: its
+    leading ticket counters must start at zero and every call leaves them zero."""
     key = (str(device), _lib.stream_ptr(device))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 
@@ -298,7 +300,8 @@ class TurboQuantKVCache:
         return k, v
 
     # ------------------------------------------------------- fused attention
-    def attention_descriptor(self, q: torch.Tensor, out: torch.Tensor, scale: float) -> _lib.AttnDesc:
+    def attention_descriptor(self, q: torch.Tensor, out: torch.Tensor, scale: float,
+                             general: bool = False) -> _lib.AttnDesc:
         B, H = self._B, self._H
         hq = q.shape[1]
         empty = _lib.Store()
@@ -313,17 +316,20 @@ class TurboQuantKVCache:
             sink_head_stride=self.fp16_sink_size * self.head_dim, sink_len=None,
             res_k=_lib.ptr(self._res_k), res_v=_lib.ptr(self._res_v),
             res_head_stride=self._res_cap * self.head_dim, res_cap=self._res_cap,
-            res_start0=self._res_start, res_start=None, res_len=None)
+            res_start0=self._res_start, res_start=None, res_len=None,
+            flags=_lib.TQ_ATTN_GENERAL if general else 0)
 
     def attend(self, queries: torch.Tensor, scale: float | None = None,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, general_kernel: bool = False) -> torch.Tensor:
         """Decode attention of one query token per head over the whole cache,
         scoring compressed tokens directly from packed codes.
 
         ``queries``: (B, Hq, 1, D) or (B, Hq, D); Hq a multiple (1, 2, 4, 8) of
         the kv heads, query head h reads kv head h // (Hq / Hkv). Returns
         float32 (B, Hq, 1, D): softmax(scale * q K^T) V over the same tokens
-        update_and_fetch would return (default scale D**-0.5)."""
+        update_and_fetch would return (default scale D**-0.5).
+        ``general_kernel`` forces the general kernel where the single-launch
+        K4/V2 kernel would run (used to cross-check the two)."""
         if self._B is None or self.offset == 0:
             raise ValueError("attend() on an empty cache")
         q = queries
@@ -339,7 +345,7 @@ class TurboQuantKVCache:
             scale = D ** -0.5
         if out is None:
             out = torch.empty(B, hq, 1, D, dtype=torch.float32, device=q.device)
-        desc = self.attention_descriptor(q, out, scale)
+        desc = self.attention_descriptor(q, out, scale, general_kernel)
         lib = _lib.load()
         need = lib.tq_decode_workspace_bytes(self._kc.ref(), ctypes.byref(desc))
         ws = _workspace(q.device, need)

@@ -43,7 +43,7 @@ __all__ = [
     "vector_norms", "normalize", "rotate_f64", "split_bits", "compress",
     "CompressResult", "dequantize", "boundary_margin", "near_boundary_mask",
     "qjl_sketch", "qjl_correction", "attention", "detect_outlier_layers",
-    "CacheOracle",
+    "CacheOracle", "compress_f32", "reference_decode_step_f32",
 ]
 
 
@@ -453,3 +453,38 @@ class CacheOracle:
     def attend(self, q: np.ndarray, scale: float | None = None) -> np.ndarray:
         k, v = self.dense()
         return attention(q, k, v, scale)
+
+
+# --------------------------------------------------------------------------
+# float32 restatements of the reference's per-step CPU work, used only as the
+# timed CPU baseline of bench.py (not as a parity checker)
+# --------------------------------------------------------------------------
+def compress_f32(x: np.ndarray, rotation: np.ndarray, bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """The reference's compress arithmetic in float32 numpy/OpenBLAS:
+    norm, normalise, ``x_n @ R.T``, boundary count, pack (cache.py:232-251)."""
+    d = x.shape[-1]
+    xf = np.asarray(x, np.float32).reshape(-1, d)
+    n = np.sqrt(np.einsum("ij,ij->i", xf, xf)).astype(np.float32)
+    y = (xf / np.maximum(n, NORM_EPS)[:, None]) @ np.asarray(rotation, np.float32).T
+    _, b = codebook(d, bits)
+    idx = np.searchsorted(b, y, side="left").astype(np.uint8)  # == #{k: y > b_k}
+    return pack_bits(idx, bits), n
+
+
+def reference_decode_step_f32(sink_k, sink_v, deq_k, deq_v, res_k, res_v, q, scale=None):
+    """One decode step of the reference for one layer: concatenate
+    [sink | decompressed | residual] (cache.py:682-706) and run grouped
+    scaled-dot-product attention over the float32 result (mlx-lm SDPA)."""
+    k = np.concatenate([sink_k.astype(np.float32), deq_k, res_k.astype(np.float32)], axis=2)
+    v = np.concatenate([sink_v.astype(np.float32), deq_v, res_v.astype(np.float32)], axis=2)
+    B, Hq, _, D = q.shape
+    Hkv = k.shape[1]
+    g = Hq // Hkv
+    if scale is None:
+        scale = D ** -0.5
+    qq = (q.astype(np.float32) * np.float32(scale)).reshape(B, Hkv, g, D)
+    s = np.matmul(qq, k.transpose(0, 1, 3, 2))          # (B, Hkv, g, T)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.matmul(p, v).reshape(B, Hq, 1, D)

@@ -227,3 +227,42 @@ def test_ring_state_stages():
     ref_own = O.attention(q, kd.cpu().numpy(), vd.cpu().numpy())
     print("attn vs own dense", rel_err(out, ref_own), "vs oracle", rel_err(out, o.attend(q)))
     assert rel_err(out, ref_own) < REL_TOL, "attention over own cache"
+
+
+@pytest.mark.parametrize("G,T,sink,window,chunk", [
+    (4, 32768 // 8, 128, 128, 0),   # config-2 shape at 1/8 length
+    (1, 300, 0, 0, 0),               # compressed only, ragged tail
+    (2, 1000, 17, 50, 0),            # odd sink / window lengths
+    (8, 777, 5, 16, 4),              # chunked drains, ring wrap
+    (4, 20, 0, 64, 0),               # residual only
+    (4, 40, 64, 64, 0),              # sink only
+])
+def test_fast_kernel_matches_general_and_oracle(G, T, sink, window, chunk):
+    """The single-launch K4/V2 kernel against the general kernel and float64."""
+    k, v = _kv(1, 2, T, 128, seed=T + G)
+    rng = np.random.RandomState(G)
+    steps = [(rng.randn(1, 2, 1, 128).astype(np.float16), rng.randn(1, 2, 1, 128).astype(np.float16))
+             for _ in range(9)] if chunk else ()
+    c, o = build(dict(head_dim=128, num_kv_heads=2, key_bits=4, value_bits=2, residual_window=window,
+                      fp16_sink_size=sink, chunk_size=chunk), k, v, steps)
+    q = rng.randn(1, 2 * G, 1, 128).astype(np.float16)
+    qd = to_dev(q)
+    fast = c.attend(qd).cpu().numpy()
+    gen = c.attend(qd, general_kernel=True).cpu().numpy()
+    kk, vv = dense_from_gpu_codes(c, o)
+    ref = O.attention(q, kk, vv)
+    e_f, e_g = rel_err(fast, ref), rel_err(gen, ref)
+    print(f"G={G} T={T}: fast rel {e_f:.3e} general rel {e_g:.3e} fast-vs-general {rel_err(fast, gen):.3e}")
+    assert e_f < REL_TOL and min_cos(fast, ref) >= COS_TOL
+    assert e_g < REL_TOL
+
+
+def test_fast_kernel_repeat_calls_reset_tickets():
+    """Back-to-back calls on one workspace give identical outputs (the ticket
+    counters are left at zero)."""
+    k, v = _kv(1, 8, 5000, 128, seed=77)
+    c, _ = build(dict(head_dim=128, num_kv_heads=8, residual_window=128, fp16_sink_size=128), k, v)
+    q = to_dev(np.random.RandomState(78).randn(1, 32, 1, 128).astype(np.float16))
+    outs = [c.attend(q).clone() for _ in range(5)]
+    for x in outs[1:]:
+        assert torch.equal(x, outs[0])

@@ -411,10 +411,24 @@ static void fast_geometry(const tq_attn_desc* d, int& nwg, int& bpw) {
   if (bpw == 0) bpw = 8;
 }
 
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// The single-launch kernel reads keys / values / norms / queries in 16-byte
+// pieces: every base and head stride must keep them 16-byte aligned.
 static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
   const int G = d->hq / d->hkv;
-  return kc->rotation_t != nullptr && kc->d == 128 && kc->bits_hi == 4 && kc->split == 128 && vc->bits_hi == 2 && vc->split == 128 &&
-         !d->qjl && d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8);
+  if (!(kc->rotation_t != nullptr && kc->d == 128 && kc->bits_hi == 4 && kc->split == 128 && vc->bits_hi == 2 &&
+        vc->split == 128 && !d->qjl && d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8)))
+    return false;
+  if (!aligned16(d->q)) return false;
+  if (d->max_comp > 0 &&
+      !(aligned16(d->kstore.codes_hi) && d->kstore.hi_head_stride % 16 == 0 && aligned16(d->kstore.norms) &&
+        d->kstore.norm_head_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(d->vstore.codes_hi) & 1) == 0 &&
+        d->vstore.hi_head_stride % 2 == 0 && aligned16(d->vstore.norms) && d->vstore.norm_head_stride % 4 == 0))
+    return false;
+  if (d->max_sink > 0 && !(aligned16(d->sink_k) && aligned16(d->sink_v) && d->sink_head_stride % 8 == 0)) return false;
+  if (d->max_res > 0 && !(aligned16(d->res_k) && aligned16(d->res_v) && d->res_head_stride % 8 == 0)) return false;
+  return true;
 }
 
 }  // namespace tq

@@ -38,6 +38,6 @@ int fast_set_attributes();
 int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s);
 int fast_max_wg();
 
-constexpr int FAST_PART_FLOATS = 132;  // per query head per workgroup
+constexpr int FAST_PART_FLOATS = 260;  // per query head per workgroup: M, L, rot[128], orig[128], pad
 
 }  // namespace tq

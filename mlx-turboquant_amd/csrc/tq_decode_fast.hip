@@ -1,35 +1,42 @@
 // Single-launch fused decode attention for K4/V2 TurboQuant caches on gfx950.
 //
-// One workgroup (8 waves) per (token range, kv head g, sequence b). The
-// token range is a run of 32-token blocks of the sequence's
-// [compressed | sink | residual] block list; wave w takes every 8th block.
-// A wave issues the loads of its first four compressed blocks before any
-// set-up work and keeps three blocks in flight while it computes.
+// One workgroup (8 waves) per (token range, kv head g, sequence b). The token
+// range is a run of 32-token blocks of the sequence's [compressed | sink |
+// residual] block list; wave w takes every 8th block and keeps the loads of
+// the next two compressed blocks in flight while it computes one.
 //
-// Compressed block (rotated space, docs/FUSED_ATTENTION_DESIGN.md:62-67):
-//   S^T[h][t] = n_k[t] * sum_j q_rot[h][j] c4[idx[t][j]]       (MFMA 16x16x32 f16)
-//     A = q_rot split into fp16 hi/lo (rows = query heads of g),
-//     B = keys decoded through an LDS table byte -> (c_hi pair, c_lo pair),
-//     three products q_hi*c_hi + q_hi*c_lo + q_lo*c_hi, float32 accumulate.
-//   acc_rot[h][j] += sum_t p[h][t] n_v[t] c2[idx[t][j]]        (MFMA 16x16x32 f16)
-//     A = p * n_v split hi/lo (rows [hi heads | lo heads]),
-//     B = values decoded through an LDS table indexed by two tokens' code
-//     nibbles after an in-wave LDS transpose of the 32x32-byte code tile.
-// fp16 block (sink / residual, original space): same MFMAs with exact fp16
-// keys/values as B and q (hi/lo) as A, accumulated into acc_orig.
-// Online softmax in base 2 (scale * log2 e folded into q).
+// Scores are computed transposed, S^T = K q^T (MFMA 16x16x32 f16):
+//   A = 16 tokens x 32 k-slots of keys, B = 32 k-slots x 16 columns of queries.
+// Column r of B holds query head (r % G) of kv group g, either its fp16 high
+// part (even r / G) or the fp16 remainder (odd r / G), so a DPP row rotation
+// by G adds the two halves and every column ends up with the full score of
+// its head. In rotated space (compressed tokens, docs/FUSED_ATTENTION_DESIGN.md
+// :62-67) each key code byte (two 4-bit codes) is looked up in an LDS table
+// whose 8-byte entry is (c_hi[a], c_hi[b], c_lo[a], c_lo[b]); two lookups fill
+// one A operand, and the matching B k-slots repeat the two query values, so
+//   sum_k A B = sum_d (c_hi + c_lo)[idx_d] q_d   with c_lo = c - fp16(c).
+// Scaled by the key norm and run through an online softmax in base 2.
+// Output, transposed too: O^T += V^T P^T with A = 16 dims x 32 tokens of
+// values decoded from an LDS table indexed by one 2-bit-code byte (4 dims of
+// one token) and paired across tokens with v_perm, and B = p * n_v split into
+// fp16 high part / remainder along the same columns as the scores.
+// fp16 blocks (sink / residual ring, original space) use the same MFMAs with
+// exact fp16 keys / values, accumulated separately.
 //
-// q_rot = q @ R^T and the per-workgroup inverse rotation acc_rot @ R are
-// MFMAs too (R and R^T split into fp16 hi/lo; wave w owns output dims
-// [16w, 16w+16)). Each workgroup writes (max, sum, out_partial) per query
-// head in original space with device-coherent stores; the last workgroup of
-// each (b, g) (ticket counter in the workspace, reset by that workgroup)
-// merges them (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40).
+// Lane (column r, group q4) of a score tile holds tokens 4*q4 + i of the
+// tile, which is exactly the k-slot order (8*q4 + i) the P^T operand needs,
+// so softmax weights never leave their lane. The accumulator of lane
+// (column r, q4), MFMA nb, register i is rotated dim 32*q4 + 8*i + nb.
 //
-// Rotated dims are permuted inside the MFMAs: QK lane (col t, group q4) step
-// kb holds dims 32*q4 + 8*kb + i; PV N-block nb column n holds dim 8*n + nb.
+// The 8 waves of a workgroup are combined through LDS; each workgroup then
+// writes (max, sum, rotated partial, original-space partial) per query head
+// with device-coherent stores, and the last workgroup of each (b, g) (ticket
+// counter in the workspace, reset by that workgroup) merges them and applies
+// the inverse rotation (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40).
 
 #include <math.h>
+
+#include <type_traits>
 
 #include "tq_common.h"
 #include "tq_decode_fast.h"
@@ -39,14 +46,31 @@ namespace tq {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef __fp16 hx2 __attribute__((ext_vector_type(2)));
 
 constexpr int FD = 128;
-constexpr int FW = 8;            // waves per workgroup (FW * 16 == FD)
-constexpr int FT = FW * 64;      // threads
-constexpr int NCOPY = 16;        // LDS table replicas (lane % NCOPY)
-constexpr int VTS = 40;          // halfwords per row of the transposed V tile
-constexpr int PS = FAST_PART_FLOATS;  // floats per (head) partial: m, l, out[128], pad
-constexpr int MAXWG = 128;       // workgroups per (sequence, kv head)
+constexpr int FW = 8;                 // waves per workgroup (FW * 16 == FD)
+constexpr int FT = FW * 64;           // threads
+constexpr int PS = FAST_PART_FLOATS;  // floats per (workgroup, head) partial
+constexpr int P_ROT = 2;              // partial: [M, L, rot[128], orig[128], pad]
+constexpr int P_ORIG = 2 + FD;
+constexpr int MAXWG = 128;            // workgroups per (sequence, kv head)
+constexpr float M_INIT = -1e30f;      // running max before the first block
+constexpr int CROW = FD + 4;          // padded LDS row of the combine buffers
+constexpr int NCP_PAIRS = 16;         // table replicas per entry / 2 (one 16-byte store each)
+
+struct Layout {
+  static constexpr uint32_t lut_k = 0;        // 256 entries x 32 copies x 8 B
+  static constexpr uint32_t lut_v = 65536;    // 256 entries x 32 copies x 8 B
+  static constexpr uint32_t qrs = 131072;     // [8][128] f32 rotated q * qscale
+  static constexpr uint32_t qsh = qrs + 4096; // [8][128] f32 q * qscale
+  static constexpr uint32_t fin = qsh + 4096; // [2][8][128] f32 merged rot / orig
+  static constexpr uint32_t misc = fin + 8192;
+  static constexpr uint32_t total = misc + 1024;
+};
+// the combine buffers reuse the tables and the q staging, all dead by then
+static_assert(FW * 2 * 16 * CROW * 4 <= (int)Layout::fin, "combine buffers overlap the merge buffer");
 
 __device__ inline half8 as_h8(u4 v) { return __builtin_bit_cast(half8, v); }
 
@@ -54,20 +78,31 @@ __device__ inline f4 mfma(half8 a, half8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ inline float max16(float v) {
-  v = fmaxf(v, __shfl_xor(v, 1));
-  v = fmaxf(v, __shfl_xor(v, 2));
-  v = fmaxf(v, __shfl_xor(v, 4));
-  v = fmaxf(v, __shfl_xor(v, 8));
-  return v;
+__device__ inline float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// value of lane (i - n) mod 16 of the same 16-lane row
+template <int N>
+__device__ inline float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + N, 0xF, 0xF, true));
 }
 
-__device__ inline float sum16(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
-  return v;
+// max / sum over the four 16-lane rows (lanes l, l^16, l^32, l^48)
+__device__ inline float rows_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ inline float rows_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ inline uint32_t pk_rtz(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
 
 __device__ inline uint32_t pack_h2(float lo, float hi) {
@@ -75,7 +110,7 @@ __device__ inline uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-// 8 floats -> fp16 hi part and fp16 remainder
+// 8 floats -> fp16 high part and fp16 remainder
 __device__ inline void split8(const float4& x0, const float4& x1, half8& hi, half8& lo) {
   const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
@@ -94,39 +129,34 @@ __device__ inline float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-struct Layout {
-  static constexpr size_t lut_k = 0;
-  static constexpr size_t lut_v = lut_k + 256 * NCOPY * 8;
-  static constexpr size_t qrs = lut_v + 256 * NCOPY * 8;        // [8][128] f32 rotated q
-  static constexpr size_t qsh = qrs + 8 * FD * 4;                // [8][128] f32 scaled q
-  static constexpr size_t fin = qsh + 8 * FD * 4;                // [2][8][128] f32 rot / orig
-  static constexpr size_t vt = fin + 2 * 8 * FD * 4;             // FW x 16 x VTS u16
-  static constexpr size_t pb = vt + FW * 16 * VTS * 2;           // FW x 8 x 32 f32
-  static constexpr size_t misc = pb + FW * 8 * 32 * 4;           // scalars, merge tables
-  static constexpr size_t total = misc + 4 * 2 * MAXWG * 8 + 1024;
-  static constexpr size_t accb_bytes = lut_v + 256 * NCOPY * 8;  // reusable after the loop
-};
+__device__ inline u2 lds_u2(const uint8_t* smem, uint32_t addr) {
+  return *reinterpret_cast<const u2*>(smem + addr);
+}
 
-struct PackedLoad {
-  u4 k0, k1, v;
-  float nk0, nk1, nv0, nv1;
+// loads of one compressed 32-token block (lane r, q4)
+struct Blk {
+  u4 k0, k1;            // key codes of tokens t0 + r and t0 + 16 + r, bytes 16*q4 ..
+  uint32_t v[8];        // value code halfword r of tokens A0..A3, B0..B3 (zero-extended)
+  float4 nkA, nkB;      // key norms of tokens t0 + 4q4 + i, t0 + 16 + 4q4 + i
+  float4 nvA, nvB;      // value norms of the same tokens
 };
 
 template <int G>
 __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
-  extern __shared__ __align__(16) uint8_t smem[];
-  uint2* lut_k = reinterpret_cast<uint2*>(smem + Layout::lut_k);
-  uint2* lut_v = reinterpret_cast<uint2*>(smem + Layout::lut_v);
+  __shared__ __align__(16) uint8_t smem[Layout::total];
   float* qrs = reinterpret_cast<float*>(smem + Layout::qrs);
   float* qsh = reinterpret_cast<float*>(smem + Layout::qsh);
   float* fin = reinterpret_cast<float*>(smem + Layout::fin);
   float* misc = reinterpret_cast<float*>(smem + Layout::misc);
 
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int r = lane & 15, q4 = lane >> 4, cp = lane % NCOPY;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, q4 = lane >> 4;
   const int row = b * a.hkv + g;
   const int j0 = 16 * w;  // output-dim tile of this wave for the rotations
+  const int hd = r % G;   // query head of column r
+  const float partf = ((r / G) & 1) ? 1.f : 0.f;  // column holds the fp16 remainder
 
   const int comp = a.comp_len_b ? a.comp_len_b[b] : a.max_comp;
   const int sink = a.sink_len_b ? a.sink_len_b[b] : a.max_sink;
@@ -145,27 +175,11 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   const uint8_t* vcodes = a.vc + (int64_t)row * a.v_hs;
   const float* vnorm = a.vn + (int64_t)row * a.vn_hs;
 
-  auto load_packed = [&](int k) {
-    PackedLoad L;
-    const int t0 = (blk0 + w + k * FW) << 5;
-    const int tA = min(t0 + r, comp - 1), tB = min(t0 + 16 + r, comp - 1);
-    L.k0 = *reinterpret_cast<const u4*>(kcodes + (int64_t)tA * 64 + 16 * q4);
-    L.k1 = *reinterpret_cast<const u4*>(kcodes + (int64_t)tB * 64 + 16 * q4);
-    const int tv = min(t0 + (lane >> 1), comp - 1);
-    L.v = *reinterpret_cast<const u4*>(vcodes + (int64_t)tv * 32 + 16 * (lane & 1));
-    L.nk0 = knorm[tA];
-    L.nk1 = knorm[tB];
-    L.nv0 = vnorm[tA];
-    L.nv1 = vnorm[tB];
-    return L;
-  };
-
-  // ---- first loads: four compressed blocks, R rows for q_rot, q rows
-  PackedLoad r0, r1, r2, r3;
-  if (npk > 0) r0 = load_packed(0);
-  if (npk > 1) r1 = load_packed(1);
-  if (npk > 2) r2 = load_packed(2);
-  if (npk > 3) r3 = load_packed(3);
+  // ---- first loads: centroids, R rows and q (needed first), then two blocks
+  // table centroids: waves 0-3 build the key table (two 4-bit codes per
+  // entry), waves 4-7 the value table (four 2-bit codes per entry); each lane
+  // loads one centroid, the entries gather theirs with lane shuffles
+  const float cen_lane = (w < 4 ? a.kcen : a.vcen)[lane & (w < 4 ? 15 : 3)];
   float4 rq[8];
   {
     const float* rr = a.rot + (int64_t)(j0 + r) * FD + 8 * q4;
@@ -175,37 +189,120 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       rq[2 * kb + 1] = *reinterpret_cast<const float4*>(rr + 32 * kb + 4);
     }
   }
-  // q rows (original space) as MFMA A operands: row r = query head
-  half8 qo_hi[4], qo_lo[4];
+  // q rows (original space): raw 16-byte pieces now, converted after the block
+  // loads; for 2-byte types the second piece repeats the first (stays in bounds)
+  u4 qraw[8];
   {
     const int64_t qb = ((int64_t)b * a.hq + g * G + min(r, G - 1)) * FD + 8 * q4;
+    const int esz = a.q_dtype == TQ_F32 ? 4 : 2;
+    const uint8_t* p = static_cast<const uint8_t*>(a.q) + qb * esz;
+    const int second = a.q_dtype == TQ_F32 ? 16 : 0;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float v = r < G ? load_elem(a.q, qb + 32 * kb + i, a.q_dtype) : 0.f;
-        const _Float16 h = (_Float16)v;
-        qo_hi[kb][i] = h;
-        qo_lo[kb][i] = (_Float16)(v - (float)h);  // zero for fp16 queries
-      }
+      qraw[2 * kb] = *reinterpret_cast<const u4*>(p + 32 * kb * esz);
+      qraw[2 * kb + 1] = *reinterpret_cast<const u4*>(p + 32 * kb * esz + second);
     }
   }
-
-  // ---- tables: one entry per thread per table, replicated NCOPY times
-  {
-    float* cen = misc;  // 16 key + 4 value centroids
-    if (tid < 20) cen[tid] = tid < 16 ? a.kcen[tid] : a.vcen[tid - 16];
-    __syncthreads();
-    const int ent = tid & 255;
-    const float c0 = cen[ent & 15], c1 = cen[ent >> 4];
-    const float h0 = (float)(_Float16)c0, h1 = (float)(_Float16)c1;
-    const uint2 ek = make_uint2(pack_h2(c0, c1), pack_h2(c0 - h0, c1 - h1));
-    const uint2 ev = make_uint2(pack_h2(cen[16 + (ent & 3)], cen[16 + ((ent >> 4) & 3)]),
-                                pack_h2(cen[16 + ((ent >> 2) & 3)], cen[16 + ((ent >> 6) & 3)]));
+  // lane offsets (32-bit) from the uniform per-block bases
+  const uint32_t koff = (uint32_t)(r * 64 + 16 * q4);        // key row t0 + r, bytes 16*q4 ..
+  const uint32_t voff = (uint32_t)(4 * q4 * 32 + 2 * r);     // value row t0 + 4*q4, halfword r
+  const uint32_t noff = (uint32_t)(4 * q4);                  // norm of token t0 + 4*q4
+  // full compressed blocks of this wave come first; at most one partial block follows
+  const int nfull = comp >> 5;
+  const int npf = min(npk, nfull > blk0 + w ? (nfull - (blk0 + w) + FW - 1) / FW : 0);
+  // Full block k of this wave. Loads are issued unconditionally so the wait
+  // counts stay exact: k >= npf reads one line (zero lane offsets) of block 0,
+  // or of the rotation matrix when the wave has no full block.
+  const uint8_t* kbase = npf > 0 ? kcodes : reinterpret_cast<const uint8_t*>(a.rot);
+  const uint8_t* vbase = npf > 0 ? vcodes : reinterpret_cast<const uint8_t*>(a.rot);
+  const float* knbase = npf > 0 ? knorm : a.rot;
+  const float* vnbase = npf > 0 ? vnorm : a.rot;
+  auto load_blk = [&](int k) {
+    Blk L;
+    const bool valid = k < npf;
+    const int t0 = valid ? (blk0 + w + k * FW) << 5 : (npf > 0 ? (blk0 + w) << 5 : 0);
+    const uint32_t msk = valid ? 0xFFFFFFFFu : 0u;
+    const uint8_t* kb = kbase + (int64_t)t0 * 64;
+    const uint8_t* vb = vbase + (int64_t)t0 * 32;
+    const float* nkb = knbase + t0;
+    const float* nvb = vnbase + t0;
+    const uint32_t ko = koff & msk, vo = voff & msk, no = noff & msk;
+    L.k0 = *reinterpret_cast<const u4*>(kb + ko);
+    L.k1 = *reinterpret_cast<const u4*>(kb + ko + 16 * 64);
 #pragma unroll
-    for (int k = tid >> 8; k < NCOPY; k += FT / 256) {
-      lut_k[ent * NCOPY + k] = ek;
-      lut_v[ent * NCOPY + k] = ev;
+    for (int i = 0; i < 8; ++i)
+      L.v[i] = *reinterpret_cast<const uint16_t*>(vb + vo + (uint32_t)(((i >> 2) * 16 + (i & 3)) * 32));
+    L.nkA = *reinterpret_cast<const float4*>(nkb + no);
+    L.nkB = *reinterpret_cast<const float4*>(nkb + no + 16);
+    L.nvA = *reinterpret_cast<const float4*>(nvb + no);
+    L.nvB = *reinterpret_cast<const float4*>(nvb + no + 16);
+    return L;
+  };
+  // the sequence's last, partial block: every token clamped to the sequence
+  auto load_tail = [&](int k) {
+    Blk L;
+    const int t0 = (blk0 + w + k * FW) << 5;
+    const int lim = comp - 1;
+    const int ta = t0 + 4 * q4, tb = t0 + 16 + 4 * q4;
+    const uint8_t* vb = vcodes + 2 * r;
+    L.k0 = *reinterpret_cast<const u4*>(kcodes + (int64_t)min(t0 + r, lim) * 64 + 16 * q4);
+    L.k1 = *reinterpret_cast<const u4*>(kcodes + (int64_t)min(t0 + 16 + r, lim) * 64 + 16 * q4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      L.v[i] = *reinterpret_cast<const uint16_t*>(vb + (int64_t)min((i < 4 ? ta : tb) + (i & 3), lim) * 32);
+    float na[4], nb[4], va[4], vb4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      na[i] = knorm[min(ta + i, lim)];
+      nb[i] = knorm[min(tb + i, lim)];
+      va[i] = vnorm[min(ta + i, lim)];
+      vb4[i] = vnorm[min(tb + i, lim)];
+    }
+    L.nkA = make_float4(na[0], na[1], na[2], na[3]);
+    L.nkB = make_float4(nb[0], nb[1], nb[2], nb[3]);
+    L.nvA = make_float4(va[0], va[1], va[2], va[3]);
+    L.nvB = make_float4(vb4[0], vb4[1], vb4[2], vb4[3]);
+    return L;
+  };
+  Blk b0 = load_blk(0), b1 = load_blk(1), b2 = load_blk(2);
+
+  // ---- tables, 32 replicas (lane % 32) per entry, entry stride 256 bytes:
+  // key byte e -> (c_hi[e&15], c_hi[e>>4], c_lo[e&15], c_lo[e>>4]) fp16
+  // value byte e -> (c[e&3], c[(e>>2)&3], c[(e>>4)&3], c[(e>>6)&3]) fp16
+  {
+    const int e = tid & 255;
+    float cen[4];
+    const int sh = w < 4 ? 4 : 2, mk = w < 4 ? 15 : 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cen[i] = __shfl(cen_lane, (e >> (sh * i)) & mk);
+    const float h0 = (float)(_Float16)cen[0], h1 = (float)(_Float16)cen[1];
+    u4 ent;
+    ent[0] = pack_h2(cen[0], cen[1]);
+    ent[1] = w < 4 ? pack_h2(cen[0] - h0, cen[1] - h1) : pack_h2(cen[2], cen[3]);
+    ent[2] = ent[0];
+    ent[3] = ent[1];
+    uint8_t* base = smem + (w < 4 ? Layout::lut_k : Layout::lut_v) + e * 256;
+#pragma unroll
+    for (int k = 0; k < NCP_PAIRS; ++k)  // copies (2k', 2k'+1), rotated per entry against bank conflicts
+      *reinterpret_cast<u4*>(base + 16 * ((k + e) & (NCP_PAIRS - 1))) = ent;
+  }
+  // q rows as MFMA A operands (row r = query head): fp16 high part and remainder
+  half8 qo_hi[4], qo_lo[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float x;
+      if (a.q_dtype == TQ_F32) {
+        x = __uint_as_float(qraw[2 * kb + (i >> 2)][i & 3]);
+      } else {
+        const uint32_t h = (qraw[2 * kb][i >> 1] >> (16 * (i & 1))) & 0xFFFF;
+        x = a.q_dtype == TQ_F16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)h) : __uint_as_float(h << 16);
+      }
+      x = r < G ? x : 0.f;
+      const _Float16 hx = (_Float16)x;
+      qo_hi[kb][i] = hx;
+      qo_lo[kb][i] = (_Float16)(x - (float)hx);  // zero for fp16 queries
     }
   }
   // ---- q_rot tile: D[h][n] = sum_i q[h][i] R[j0+n][i]   (B[k=i][n] = R[j0+n][i])
@@ -225,7 +322,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       if (h < G) qrs[h * FD + j0 + r] = dq[i] * a.qscale;
     }
   }
-  // fp16 blocks use q * qscale in original space (kept in LDS)
+  // fp16 blocks use q * qscale in original space
   if (r < G) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
@@ -235,199 +332,264 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   }
   __syncthreads();
 
-  // A operands of the rotated-space QK: row r = query head, k slot (q4, i)
-  half8 qa_hi[4], qa_lo[4];
+  // B operands of the rotated-space scores, step s: k-slots (q4, i) hold
+  // q[d], q[d+1], q[d], q[d+1], q[d+2], q[d+3], q[d+2], q[d+3], d = 32*q4 + 4*s,
+  // matching the key table entry layout (hi pair, lo pair) of two code bytes.
+  half8 qop[8];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
+  for (int s = 0; s < 8; ++s) {
+    const float4 x = *reinterpret_cast<const float4*>(qrs + hd * FD + 32 * q4 + 4 * s);
+    const float v[4] = {x.x, x.y, x.z, x.w};
+    _Float16 h[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float v = r < G ? qrs[r * FD + 32 * q4 + 8 * kb + i] : 0.f;
-      const _Float16 hv = (_Float16)v;
-      qa_hi[kb][i] = hv;
-      qa_lo[kb][i] = (_Float16)(v - (float)hv);
+    for (int i = 0; i < 4; ++i) {
+      const _Float16 hi = (_Float16)v[i];
+      h[i] = partf != 0.f ? (_Float16)(v[i] - (float)hi) : hi;
     }
+    qop[s] = half8{h[0], h[1], h[0], h[1], h[2], h[3], h[2], h[3]};
   }
 
-  // ---- per-wave online softmax state (rows 4*q4 + i of the S tile)
-  float m_i[4], l_i[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) { m_i[i] = -INFINITY; l_i[i] = 0.f; }
+  // ---- per-lane online softmax state of column r (head hd)
+  float m_run = M_INIT, l_run = 0.f;
   f4 acc_r[8];
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) acc_r[nb] = f4{0.f, 0.f, 0.f, 0.f};
 
-  uint16_t* vt = reinterpret_cast<uint16_t*>(smem + Layout::vt) + w * 16 * VTS;
-  float* pb = reinterpret_cast<float*>(smem + Layout::pb) + w * 8 * 32;
-
-  // Online softmax of one 32-token block (scores s0: tokens 0..15, s1: 16..31
-  // of the block, rows = query heads): updates (m, l), returns the PV A operand
-  // (p * n_v split hi/lo) and the per-row correction of the accumulators.
-  auto softmax_block = [&](const f4& s0, const f4& s1, float nv0, float nv1, half8& pa, float (&cr)[4]) {
-    float corr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float mb = max16(fmaxf(s0[i], s1[i]));
-      const float mn = fmaxf(m_i[i], mb);
-      corr[i] = (m_i[i] == -INFINITY) ? 0.f : exp2f(m_i[i] - mn);
-      const float p0 = (s0[i] == -INFINITY) ? 0.f : exp2f(s0[i] - mn);
-      const float p1 = (s1[i] == -INFINITY) ? 0.f : exp2f(s1[i] - mn);
-      l_i[i] = l_i[i] * corr[i] + p0 + p1;
-      m_i[i] = mn;
-      const int rho = 4 * q4 + i;
-      if (rho < G) {
-        pb[rho * 32 + r] = p0 * nv0;
-        pb[rho * 32 + 16 + r] = p1 * nv1;
-      }
-    }
-    // Row rho = 4*q4 + i of an accumulator belongs to head rho % G; its
-    // softmax state lives in lane 16*(head/4), register head % 4, and that
-    // register index depends on i only.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int reg = (G >= 4) ? i : (i % G);
-      const int rho = 4 * q4 + i;
-      const int src = 16 * ((rho % G) >> 2);
-      const float v = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(corr[reg])));
-      cr[i] = rho < 2 * G ? v : 0.f;
-    }
-    __builtin_amdgcn_wave_barrier();
-    // row r = [p*n_v hi (heads 0..G-1) | lo (heads 0..G-1)], k slot = token 8*q4 + i
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int t = 8 * q4 + i;
-      float v = 0.f;
-      if (r < G) v = pb[r * 32 + t];
-      else if (r < 2 * G) v = pb[(r - G) * 32 + t];
-      const _Float16 hv = (_Float16)v;
-      pa[i] = (r < G) ? hv : (_Float16)(v - (float)hv);
-    }
+  const uint32_t cpv = (uint32_t)(lane & 31) * 8;  // replica offset within an entry
+  const uint32_t cpv_v = cpv | Layout::lut_v;      // byte 2 = 0x01: value table
+  auto kaddr = [&](uint32_t word, int byte) {      // (byte of word) << 8 | cpv
+    return __builtin_amdgcn_perm(word, cpv, 0x0C0C0000u | ((4u + byte) << 8));
+  };
+  auto vaddr = [&](uint32_t word, int byte) {      // 0x10000 | (byte of word) << 8 | cpv
+    return __builtin_amdgcn_perm(word, cpv_v, 0x0C020000u | ((4u + byte) << 8));
   };
 
-  // ---- compressed blocks (rotated space); blocks k+1..k+3 stay in flight
-  for (int k = 0; k < npk; ++k) {
-    const PackedLoad& cur = r0;
-    const int t0 = (blk0 + w + k * FW) << 5;
-    // stage the value codes transposed: vt[n][t] = halfword n of token t
+  // Online softmax of the 8 scores of this lane (tokens A0..A3, B0..B3 of
+  // the block, column r), returns the P^T operand (p * nv, high part or
+  // remainder by column) and rescales `acc` when the running max grows.
+  auto softmax_pv = [&](float (&s)[8], const float (&nv)[8], f4 (&acc)[8], f4 (&acc2)[8], bool two) {
+    float bm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    bm = rows_max(bm);
+    if (__builtin_amdgcn_ballot_w64(bm > m_run) != 0) {
+      const float mnew = fmaxf(m_run, bm);
+      const float corr = fexp2(m_run - mnew);
+      l_run *= corr;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      vt[(8 * (lane & 1) + j) * VTS + (lane >> 1)] = (uint16_t)(cur.v[j >> 1] >> (16 * (j & 1)));
-    f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      for (int nb = 0; nb < 8; ++nb) acc[nb] *= corr;
+      if (two) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const uint32_t w0 = cur.k0[kb], w1 = cur.k1[kb];
-      u4 bh0, bl0, bh1, bl1;
-#pragma unroll
-      for (int byte = 0; byte < 4; ++byte) {
-        const uint2 e0 = lut_k[((w0 >> (8 * byte)) & 0xFF) * NCOPY + cp];
-        const uint2 e1 = lut_k[((w1 >> (8 * byte)) & 0xFF) * NCOPY + cp];
-        bh0[byte] = e0.x; bl0[byte] = e0.y;
-        bh1[byte] = e1.x; bl1[byte] = e1.y;
+        for (int nb = 0; nb < 8; ++nb) acc2[nb] *= corr;
       }
-      s0 = mfma(qa_hi[kb], as_h8(bh0), s0);
-      s0 = mfma(qa_hi[kb], as_h8(bl0), s0);
-      s0 = mfma(qa_lo[kb], as_h8(bh0), s0);
-      s1 = mfma(qa_hi[kb], as_h8(bh1), s1);
-      s1 = mfma(qa_hi[kb], as_h8(bl1), s1);
-      s1 = mfma(qa_lo[kb], as_h8(bh1), s1);
+      m_run = mnew;
     }
-    const bool ok0 = t0 + r < comp, ok1 = t0 + 16 + r < comp;
+    float pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float p = fexp2(s[i] - m_run);
+      l_run += p;
+      pv[i] = p * nv[i];
+    }
+    u4 pb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const hx2 h = __builtin_amdgcn_cvt_pkrtz(pv[2 * j], pv[2 * j + 1]);
+      const float t0 = fmaf(-partf, (float)h[0], pv[2 * j]);
+      const float t1 = fmaf(-partf, (float)h[1], pv[2 * j + 1]);
+      pb[j] = pk_rtz(t0, t1);
+    }
+    return as_h8(pb);
+  };
+
+  // ---- one compressed block (rotated space); `tail` masks tokens past the sequence
+  auto packed_block = [&](const Blk& L, int k, auto tail) {
+    const int t0 = (blk0 + w + k * FW) << 5;
+    f4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const uint32_t wa = L.k0[s >> 1], wb = L.k1[s >> 1];
+      const int by = 2 * (s & 1);
+      const u2 ea0 = lds_u2(smem, kaddr(wa, by)), ea1 = lds_u2(smem, kaddr(wa, by + 1));
+      const u2 eb0 = lds_u2(smem, kaddr(wb, by)), eb1 = lds_u2(smem, kaddr(wb, by + 1));
+      sA = mfma(as_h8(u4{ea0[0], ea0[1], ea1[0], ea1[1]}), qop[s], sA);
+      sB = mfma(as_h8(u4{eb0[0], eb0[1], eb1[0], eb1[1]}), qop[s], sB);
+    }
+    float sc[8];
+    const float nk[8] = {L.nkA.x, L.nkA.y, L.nkA.z, L.nkA.w, L.nkB.x, L.nkB.y, L.nkB.z, L.nkB.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      s0[i] = ok0 ? s0[i] * cur.nk0 : -INFINITY;
-      s1[i] = ok1 ? s1[i] * cur.nk1 : -INFINITY;
+      sc[i] = (sA[i] + row_ror<G>(sA[i])) * nk[i];
+      sc[4 + i] = (sB[i] + row_ror<G>(sB[i])) * nk[4 + i];
     }
-    half8 pa;
-    float cr[4];
-    softmax_block(s0, s1, cur.nv0, cur.nv1, pa, cr);
+    if constexpr (decltype(tail)::value) {
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc_r[nb][i] *= cr[i];
-    const u4 vw = *reinterpret_cast<const u4*>(vt + r * VTS + 8 * q4);
-    u4 bv[8];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const uint32_t idx = ((vw[kk] >> (4 * p)) & 0xF) | (((vw[kk] >> (16 + 4 * p)) & 0xF) << 4);
-        const uint2 e = lut_v[idx * NCOPY + cp];
-        bv[2 * p][kk] = e.x;
-        bv[2 * p + 1][kk] = e.y;
+      for (int i = 0; i < 4; ++i) {
+        if (t0 + 4 * q4 + i >= comp) sc[i] = -INFINITY;
+        if (t0 + 16 + 4 * q4 + i >= comp) sc[4 + i] = -INFINITY;
       }
     }
+    const float nv[8] = {L.nvA.x, L.nvA.y, L.nvA.z, L.nvA.w, L.nvB.x, L.nvB.y, L.nvB.z, L.nvB.w};
+    const half8 pb = softmax_pv(sc, nv, acc_r, acc_r, false);
+    // V^T operands: row = dim 8r + nb, k-slot pairs = token pairs of the lane
+    u4 va[8];
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc_r[nb] = mfma(pa, as_h8(bv[nb]), acc_r[nb]);
-    __builtin_amdgcn_wave_barrier();
-    r0 = r1;
-    r1 = r2;
-    r2 = r3;
-    if (k + 4 < npk) r3 = load_packed(k + 4);
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t px = L.v[2 * j], py = L.v[2 * j + 1];  // token pair j
+      const u2 x0 = lds_u2(smem, vaddr(px, 0)), x1 = lds_u2(smem, vaddr(px, 1));
+      const u2 y0 = lds_u2(smem, vaddr(py, 0)), y1 = lds_u2(smem, vaddr(py, 1));
+      va[0][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x05040100u);
+      va[1][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x07060302u);
+      va[2][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x05040100u);
+      va[3][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x07060302u);
+      va[4][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x05040100u);
+      va[5][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x07060302u);
+      va[6][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x05040100u);
+      va[7][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x07060302u);
+    }
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc_r[nb] = mfma(as_h8(va[nb]), pb, acc_r[nb]);
+  };
+
+  // ---- compressed blocks: three load slots, two blocks in flight
+  {
+    constexpr std::false_type full{};
+    // loads stay unconditional (the wait counts need one issue order);
+    // only the compute is skipped past the wave's last full block
+    for (int k = 0; k < npf; k += 3) {
+      packed_block(b0, k, full);
+      b0 = load_blk(k + 3);
+      if (k + 1 < npf) packed_block(b1, k + 1, full);
+      b1 = load_blk(k + 4);
+      if (k + 2 < npf) packed_block(b2, k + 2, full);
+      b2 = load_blk(k + 5);
+    }
+    if (npf < npk) packed_block(load_tail(npf), npf, std::true_type{});
   }
 
   // ---- fp16 blocks of the sink and the residual ring (original space)
   f4 acc_o[8];
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) acc_o[nb] = f4{0.f, 0.f, 0.f, 0.f};
-  for (int blk = blk0 + w + npk * FW; blk < blk1; blk += FW) {
-    const bool is_sink = blk < nbc + nbs;
-    const int ft0 = (is_sink ? blk - nbc : blk - nbc - nbs) << 5;
-    const int flen = is_sink ? sink : res;
-    const int64_t hs = is_sink ? a.sink_hs : a.res_hs;
-    const uint16_t* fk = static_cast<const uint16_t*>(is_sink ? a.sink_k : a.res_k) + (int64_t)row * hs;
-    const uint16_t* fv = static_cast<const uint16_t*>(is_sink ? a.sink_v : a.res_v) + (int64_t)row * hs;
-    auto slot = [&](int t) {
-      t = min(t, flen - 1);
-      return is_sink ? t : (rstart + t) % a.res_cap;
-    };
-    const u4* kA = reinterpret_cast<const u4*>(fk + (int64_t)slot(ft0 + r) * FD + 32 * q4);
-    const u4* kB = reinterpret_cast<const u4*>(fk + (int64_t)slot(ft0 + 16 + r) * FD + 32 * q4);
-    f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  const int fblk = blk0 + w + npk * FW;
+  if (fblk < blk1) {
+    // B operands in original space, step kb: k-slot (q4, i) = dim 32*q4 + 8*kb + i
+    half8 qf[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      half8 qh, ql;
+      const float4 x0 = *reinterpret_cast<const float4*>(qsh + hd * FD + 32 * q4 + 8 * kb);
+      const float4 x1 = *reinterpret_cast<const float4*>(qsh + hd * FD + 32 * q4 + 8 * kb + 4);
+      half8 hi, lo;
+      split8(x0, x1, hi, lo);
+      qf[kb] = partf != 0.f ? lo : hi;
+    }
+    for (int blk = fblk; blk < blk1; blk += FW) {
+      const bool is_sink = blk < nbc + nbs;
+      const int ft0 = (is_sink ? blk - nbc : blk - nbc - nbs) << 5;
+      const int flen = is_sink ? sink : res;
+      const int64_t hs = is_sink ? a.sink_hs : a.res_hs;
+      const uint16_t* fk = static_cast<const uint16_t*>(is_sink ? a.sink_k : a.res_k) + (int64_t)row * hs;
+      const uint16_t* fv = static_cast<const uint16_t*>(is_sink ? a.sink_v : a.res_v) + (int64_t)row * hs;
+      auto slot = [&](int t) {
+        t = min(t, flen - 1);
+        return is_sink ? t : (rstart + t) % a.res_cap;
+      };
+      const u4* kA = reinterpret_cast<const u4*>(fk + (int64_t)slot(ft0 + r) * FD + 32 * q4);
+      const u4* kB = reinterpret_cast<const u4*>(fk + (int64_t)slot(ft0 + 16 + r) * FD + 32 * q4);
+      u4 vr[8];  // dims 8r .. 8r+7 of tokens A0..A3, B0..B3
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float v = r < G ? qsh[r * FD + 32 * q4 + 8 * kb + i] : 0.f;
-        const _Float16 hv = (_Float16)v;
-        qh[i] = hv;
-        ql[i] = (_Float16)(v - (float)hv);
+        const int t = ft0 + (i < 4 ? 4 * q4 + i : 16 + 4 * q4 + i - 4);
+        vr[i] = *reinterpret_cast<const u4*>(fv + (int64_t)slot(t) * FD + 8 * r);
       }
-      const half8 ba = as_h8(kA[kb]), bb = as_h8(kB[kb]);
-      s0 = mfma(qh, ba, s0);
-      s0 = mfma(ql, ba, s0);
-      s1 = mfma(qh, bb, s1);
-      s1 = mfma(ql, bb, s1);
+      f4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        sA = mfma(as_h8(kA[kb]), qf[kb], sA);
+        sB = mfma(as_h8(kB[kb]), qf[kb], sB);
+      }
+      float sc[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = sA[i] + row_ror<G>(sA[i]);
+        sc[4 + i] = sB[i] + row_ror<G>(sB[i]);
+        if (ft0 + 4 * q4 + i >= flen) sc[i] = -INFINITY;
+        if (ft0 + 16 + 4 * q4 + i >= flen) sc[4 + i] = -INFINITY;
+      }
+      const float ones[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+      const half8 pb = softmax_pv(sc, ones, acc_o, acc_r, true);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
+        u4 bv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bv[j] = __builtin_amdgcn_perm(vr[2 * j + 1][nb >> 1], vr[2 * j][nb >> 1], sel);
+        acc_o[nb] = mfma(as_h8(bv), pb, acc_o[nb]);
+      }
     }
-    const bool ok0 = ft0 + r < flen, ok1 = ft0 + 16 + r < flen;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (!ok0) s0[i] = -INFINITY;
-      if (!ok1) s1[i] = -INFINITY;
-    }
-    half8 pa;
-    float cr[4];
-    softmax_block(s0, s1, 1.f, 1.f, pa, cr);
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) { acc_r[nb][i] *= cr[i]; acc_o[nb][i] *= cr[i]; }
-    // B = V rows: lane (n = r, q4) needs dims 8n..8n+7 of tokens 8*q4 + i
-    u4 vr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) vr[i] = *reinterpret_cast<const u4*>(fv + (int64_t)slot(ft0 + 8 * q4 + i) * FD + 8 * r);
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
-      u4 bvv;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        bvv[kk] = __builtin_amdgcn_perm(vr[2 * kk + 1][nb >> 1], vr[2 * kk][nb >> 1], sel);
-      acc_o[nb] = mfma(pa, as_h8(bvv), acc_o[nb]);
-    }
-    __builtin_amdgcn_wave_barrier();
   }
 
-  // ---- R^T rows of this wave for the inverse rotation (latency overlaps the combine)
+  // ---- combine the 8 waves of this workgroup
+  l_run = rows_sum(l_run);
+  float* wm = misc;           // [FW][8]
+  float* wl = misc + FW * 8;  // [FW][8]
+  int* flag = reinterpret_cast<int*>(misc + 2 * FW * 8);
+  constexpr int SIDE = 2 * G * CROW;  // floats per wave per side
+  float* cbuf = reinterpret_cast<float*>(smem);
+  __syncthreads();  // every wave is done with the tables
+  if (r < 2 * G) {
+    float* dr = cbuf + (w * 2) * SIDE + r * CROW + 32 * q4;
+    float* dor = cbuf + (w * 2 + 1) * SIDE + r * CROW + 32 * q4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<float4*>(dr + 8 * i) = make_float4(acc_r[0][i], acc_r[1][i], acc_r[2][i], acc_r[3][i]);
+      *reinterpret_cast<float4*>(dr + 8 * i + 4) = make_float4(acc_r[4][i], acc_r[5][i], acc_r[6][i], acc_r[7][i]);
+      if (wg_has_fp16) {
+        *reinterpret_cast<float4*>(dor + 8 * i) = make_float4(acc_o[0][i], acc_o[1][i], acc_o[2][i], acc_o[3][i]);
+        *reinterpret_cast<float4*>(dor + 8 * i + 4) = make_float4(acc_o[4][i], acc_o[5][i], acc_o[6][i], acc_o[7][i]);
+      }
+    }
+  }
+  if (lane < G) {
+    wm[w * 8 + lane] = m_run;
+    wl[w * 8 + lane] = l_run;
+  }
+  __syncthreads();
+  float* part = a.part + ((int64_t)row * a.nwg + c) * G * PS;
+  for (int e = tid; e < G * FD; e += FT) {
+    const int h = e / FD, j = e % FD;
+    float M = M_INIT;
+#pragma unroll
+    for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, wm[ww * 8 + h]);
+    float sr = 0.f, so = 0.f, L = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < FW; ++ww) {
+      const float sc = fexp2(wm[ww * 8 + h] - M);
+      const float* src = cbuf + (ww * 2) * SIDE;
+      sr = fmaf(sc, src[h * CROW + j] + src[(G + h) * CROW + j], sr);
+      if (wg_has_fp16) so = fmaf(sc, src[SIDE + h * CROW + j] + src[SIDE + (G + h) * CROW + j], so);
+      L = fmaf(sc, wl[ww * 8 + h], L);
+    }
+    store_coherent(part + h * PS + P_ROT + j, sr);
+    if (wg_has_fp16) store_coherent(part + h * PS + P_ORIG + j, so);
+    if (j == 0) {
+      store_coherent(part + h * PS + 0, M);
+      store_coherent(part + h * PS + 1, L);
+    }
+  }
+
+  // ---- last workgroup of (b, g) merges all partials
+  // Every thread waits until its device-coherent stores have completed
+  // (s_waitcnt vmcnt(0): gfx9 counts stores in vmcnt) before the ticket; the
+  // partials were written write-through (sc1), so no L2 writeback is needed.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+  if (tid == 0) {
+    const int old = __hip_atomic_fetch_add(a.counter + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = (old == a.nwg - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (*flag == 0) return;
+
+  // R^T rows of this wave for the inverse rotation (latency overlaps the merge)
   float4 rt[8];
   {
     const float* tr = a.rot_t + (int64_t)(j0 + r) * FD + 8 * q4;
@@ -437,62 +599,46 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       rt[2 * kb + 1] = *reinterpret_cast<const float4*>(tr + 32 * kb + 4);
     }
   }
-
-  // ---- combine the 8 waves of this workgroup
+  // workgroups whose block range reaches the sink / residual blocks
+  const int cf = (nbs + nbr > 0) ? nbc / a.bpw : a.nwg;
+  const float* pall = a.part + (int64_t)row * a.nwg * G * PS;
+  for (int e = tid; e < G * FD; e += FT) {
+    const int h = e / FD, j = e % FD;
+    float M = M_INIT, L = 0.f, sr = 0.f, so = 0.f;
+    for (int c0 = 0; c0 < a.nwg; c0 += 16) {
+      float mv[16], lv[16], rv[16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) l_i[i] = sum16(l_i[i]);
-  float* wm = misc;            // [FW][8]
-  float* wl = misc + FW * 8;   // [FW][8]
-  float* hM = misc + 2 * FW * 8;
-  float* hL = hM + 8;
-  int* flag = reinterpret_cast<int*>(hL + 8);
-  float* pm = misc + 2 * FW * 8 + 32;  // [MAXWG * 8] merge tables
-  float* pl = pm + MAXWG * 8;
-  // accumulators of every wave (unscaled) into LDS, reusing the table space
-  constexpr int SIDE = FW * 2 * G * FD;                         // floats per side
-  constexpr bool ONE_PASS = 2 * SIDE * 4 <= (int)Layout::accb_bytes;
-  float* accb = reinterpret_cast<float*>(smem);
-  __syncthreads();  // every wave is done with the tables
-  if (r == 0) {
+      for (int k = 0; k < 16; ++k) {
+        const int cc = min(c0 + k, a.nwg - 1);
+        const float* p = pall + (cc * G + h) * PS;
+        mv[k] = c0 + k < a.nwg ? load_coherent(p) : M_INIT;
+        lv[k] = load_coherent(p + 1);
+        rv[k] = load_coherent(p + P_ROT + j);
+      }
+      float Mb = M;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rho = 4 * q4 + i;
-      if (rho < G) { wm[w * 8 + rho] = m_i[i]; wl[w * 8 + rho] = l_i[i]; }
-    }
-  }
-  const int nside = wg_has_fp16 ? 2 : 1;
-  for (int side = 0; side < nside; ++side) {
-    float* dst = accb + (ONE_PASS ? side * SIDE : 0);
+      for (int k = 0; k < 16; ++k) Mb = fmaxf(Mb, mv[k]);
+      const float sc = fexp2(M - Mb);
+      L *= sc;
+      sr *= sc;
+      so *= sc;
+      M = Mb;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rho = 4 * q4 + i;
-      if (rho < 2 * G) {
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb)
-          dst[(w * 2 * G + rho) * FD + 8 * r + nb] = side == 0 ? acc_r[nb][i] : acc_o[nb][i];
+      for (int k = 0; k < 16; ++k) {
+        if (c0 + k < a.nwg) {
+          const float wgt = fexp2(mv[k] - M);
+          L = fmaf(wgt, lv[k], L);
+          sr = fmaf(wgt, rv[k], sr);
+          if (c0 + k >= cf && (c0 + k) * a.bpw < nbt) so = fmaf(wgt, load_coherent(pall + ((c0 + k) * G + h) * PS + P_ORIG + j), so);
+        }
       }
     }
-    __syncthreads();
-    for (int e = tid; e < G * FD; e += FT) {
-      const int h = e / FD, j = e % FD;
-      float M = -INFINITY;
-#pragma unroll
-      for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, wm[ww * 8 + h]);
-      float s = 0.f, L = 0.f;
-#pragma unroll
-      for (int ww = 0; ww < FW; ++ww) {
-        const float mw = wm[ww * 8 + h];
-        const float sc = mw > -INFINITY ? exp2f(mw - M) : 0.f;
-        s = fmaf(sc, dst[(ww * 2 * G + h) * FD + j] + dst[(ww * 2 * G + G + h) * FD + j], s);
-        L = fmaf(sc, wl[ww * 8 + h], L);
-      }
-      fin[side * 8 * FD + e] = s;
-      if (side == 0 && j == 0) { hM[h] = M; hL[h] = L; }
-    }
-    __syncthreads();
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    fin[h * FD + j] = sr * inv;
+    fin[8 * FD + h * FD + j] = so * inv;
   }
-  // ---- partial in original space: out = rot @ R + orig  (B[k=i][n] = R[i][j0+n] = R^T[j0+n][i])
-  float* part = a.part + ((int64_t)row * a.nwg + c) * G * PS;
+  __syncthreads();
+  // out = fin_rot @ R + fin_orig   (B[k=i][n] = R[i][j0+n] = R^T[j0+n][i])
   {
     f4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -520,64 +666,8 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
         lo = (i + G < 4) ? d[(i + G) & 3] : 0.f;
       }
       const int h = 4 * q4 + i;
-      if (h < G) {
-        const float o = wg_has_fp16 ? fin[8 * FD + h * FD + j0 + r] : 0.f;
-        store_coherent(part + h * PS + 2 + j0 + r, d[i] + lo + o);
-      }
+      if (h < G) a.out[((int64_t)b * a.hq + g * G + h) * FD + j0 + r] = d[i] + lo + fin[8 * FD + h * FD + j0 + r];
     }
-    if (tid < G) {
-      store_coherent(part + tid * PS + 0, hM[tid]);
-      store_coherent(part + tid * PS + 1, hL[tid]);
-    }
-  }
-
-  // ---- last workgroup of (b, g) merges all partials
-  // Every thread waits until its device-coherent stores have completed
-  // (s_waitcnt vmcnt(0): gfx9 counts stores in vmcnt) before the ticket; the
-  // partials were written write-through (sc1), so no L2 writeback is needed.
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  __syncthreads();
-  if (tid == 0) {
-    const int old = __hip_atomic_fetch_add(a.counter + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *flag = (old == a.nwg - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (*flag == 0) return;
-  const float* pall = a.part + (int64_t)row * a.nwg * G * PS;
-  for (int e = tid; e < a.nwg * G; e += FT) {
-    pm[e] = load_coherent(pall + e * PS);
-    pl[e] = load_coherent(pall + e * PS + 1);
-  }
-  __syncthreads();
-  if (tid < G) {
-    float M = -INFINITY;
-    for (int cc = 0; cc < a.nwg; ++cc) M = fmaxf(M, pm[cc * G + tid]);
-    float L = 0.f;
-    for (int cc = 0; cc < a.nwg; ++cc)
-      if (pm[cc * G + tid] > -INFINITY) L += exp2f(pm[cc * G + tid] - M) * pl[cc * G + tid];
-    hM[tid] = M;
-    hL[tid] = L;
-  }
-  __syncthreads();
-  for (int e = tid; e < a.nwg * G; e += FT) {
-    const int h = e % G;
-    pm[e] = pm[e] > -INFINITY ? exp2f(pm[e] - hM[h]) : 0.f;
-  }
-  __syncthreads();
-  for (int e = tid; e < G * FD; e += FT) {
-    const int h = e / FD, j = e % FD;
-    float o = 0.f;
-    int cc = 0;
-    for (; cc + 16 <= a.nwg; cc += 16) {
-      float v[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = load_coherent(pall + ((cc + k) * G + h) * PS + 2 + j);
-#pragma unroll
-      for (int k = 0; k < 16; ++k) o = fmaf(pm[(cc + k) * G + h], v[k], o);
-    }
-    for (; cc < a.nwg; ++cc) o = fmaf(pm[cc * G + h], load_coherent(pall + (cc * G + h) * PS + 2 + j), o);
-    const float L = hL[h];
-    a.out[((int64_t)b * a.hq + g * G + h) * FD + j] = L > 0.f ? o / L : 0.f;
   }
   if (tid == 0) __hip_atomic_store(a.counter + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -588,28 +678,16 @@ int fast_max_wg() { return MAXWG; }
 
 int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s) {
   dim3 grid(a.nwg, a.hkv, batch);
-  const size_t smem = Layout::total;
   switch (G) {
-    case 1: hipLaunchKernelGGL((fast_decode_kernel<1>), grid, dim3(FT), smem, s, a); break;
-    case 2: hipLaunchKernelGGL((fast_decode_kernel<2>), grid, dim3(FT), smem, s, a); break;
-    case 4: hipLaunchKernelGGL((fast_decode_kernel<4>), grid, dim3(FT), smem, s, a); break;
-    default: hipLaunchKernelGGL((fast_decode_kernel<8>), grid, dim3(FT), smem, s, a); break;
+    case 1: hipLaunchKernelGGL((fast_decode_kernel<1>), grid, dim3(FT), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((fast_decode_kernel<2>), grid, dim3(FT), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((fast_decode_kernel<4>), grid, dim3(FT), 0, s, a); break;
+    default: hipLaunchKernelGGL((fast_decode_kernel<8>), grid, dim3(FT), 0, s, a); break;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int fast_set_attributes() {
-  static int done = 0;
-  if (done) return 0;
-  const int bytes = (int)Layout::total;
-  hipError_t e = hipSuccess;
-  e = hipFuncSetAttribute((const void*)fast_decode_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e == hipSuccess) e = hipFuncSetAttribute((const void*)fast_decode_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e == hipSuccess) e = hipFuncSetAttribute((const void*)fast_decode_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e == hipSuccess) e = hipFuncSetAttribute((const void*)fast_decode_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e != hipSuccess) return -1;
-  done = 1;
-  return 0;
-}
+// The kernel's LDS is static (Layout::total bytes); nothing to raise.
+int fast_set_attributes() { return 0; }
 
 }  // namespace tq

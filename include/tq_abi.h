@@ -59,8 +59,9 @@ typedef struct tq_codec {
   const float* qjl_proj;       /* (qjl_m, d) Gaussian S (qjl.py:23-36) or NULL */
   int32_t qjl_m;               /* number of projections (multiple of 32) or 0 */
   int32_t reserved;
-  const float* rotation_t;     /* (d, d) row-major R^T, or NULL (the single-launch
-                                  decode kernel needs it; others ignore it) */
+  const uint16_t* rotation_f16; /* (2, d, d) binary16: [0] = fp16(R), [1] = fp16(R - [0]),
+                                   row-major, or NULL (the single-launch decode kernel
+                                   needs it; others ignore it) */
 } tq_codec;
 
 /* A compressed store: packed codes, norms and optional QJL sketch.

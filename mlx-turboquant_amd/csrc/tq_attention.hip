@@ -417,7 +417,7 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // pieces: every base and head stride must keep them 16-byte aligned.
 static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
   const int G = d->hq / d->hkv;
-  if (!(kc->rotation_t != nullptr && kc->d == 128 && kc->bits_hi == 4 && kc->split == 128 && vc->bits_hi == 2 &&
+  if (!(kc->rotation_f16 != nullptr && kc->d == 128 && kc->bits_hi == 4 && kc->split == 128 && vc->bits_hi == 2 &&
         vc->split == 128 && !d->qjl && d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8)))
     return false;
   if (!aligned16(d->q)) return false;
@@ -448,7 +448,7 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
   size_t general = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
   int nwg, bpw;
   fast_geometry(d, nwg, bpw);
-  const size_t fast = (size_t)d->batch * d->hkv * nwg * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
+  const size_t fast = (size_t)d->batch * d->hkv * nwg * FAST_WAVES * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
   const size_t bytes = counter_bytes(d) + (general > fast ? general : fast);
   return (bytes + 255) & ~(size_t)255;
 }
@@ -507,7 +507,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     f.q = d->q; f.q_dtype = d->q_dtype; f.out = d->out;
     f.hq = d->hq; f.hkv = d->hkv;
     f.qscale = d->scale * 1.4426950408889634f;
-    f.rot = kc->rotation; f.rot_t = kc->rotation_t; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
+    f.rot = kc->rotation; f.rot16 = kc->rotation_f16; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
     f.counter = static_cast<int*>(workspace);
     f.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes(d));
     fast_geometry(d, f.nwg, f.bpw);

@@ -24,7 +24,7 @@ struct FastArgs {
   int hq, hkv;
   float qscale;          // scale * log2(e)
   const float* rot;      // R (128 x 128)
-  const float* rot_t;    // R^T (128 x 128)
+  const uint16_t* rot16; // (2, 128, 128) fp16 high part / remainder of R
   const float* kcen;     // 16 key centroids
   const float* vcen;     // 4 value centroids
   float* part;           // partials
@@ -38,6 +38,7 @@ int fast_set_attributes();
 int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s);
 int fast_max_wg();
 
-constexpr int FAST_PART_FLOATS = 260;  // per query head per workgroup: M, L, rot[128], orig[128], pad
+constexpr int FAST_WAVES = 8;          // waves per workgroup of the decode kernel
+constexpr int FAST_PART_FLOATS = 260;  // per query head per wave: M, L, has_orig, pad, rot[128], orig[128]
 
 }  // namespace tq

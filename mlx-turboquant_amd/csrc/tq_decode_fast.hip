@@ -3,7 +3,7 @@
 // One workgroup (8 waves) per (token range, kv head g, sequence b). The token
 // range is a run of 32-token blocks of the sequence's [compressed | sink |
 // residual] block list; wave w takes every 8th block and keeps the loads of
-// the next two compressed blocks in flight while it computes one.
+// the next compressed block in flight while it computes one.
 //
 // Scores are computed transposed, S^T = K q^T (MFMA 16x16x32 f16):
 //   A = 16 tokens x 32 k-slots of keys, B = 32 k-slots x 16 columns of queries.
@@ -29,10 +29,10 @@
 // (column r, q4), MFMA nb, register i is rotated dim 32*q4 + 8*i + nb.
 //
 // The 8 waves of a workgroup are combined through LDS; each workgroup then
-// writes (max, sum, rotated partial, original-space partial) per query head
-// with device-coherent stores, and the last workgroup of each (b, g) (ticket
-// counter in the workspace, reset by that workgroup) merges them and applies
-// the inverse rotation (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40).
+// writes (max, sum, rotated partial, original-space partial) per query head,
+// and a second, small kernel on the same stream merges the partials of each
+// (b, g) and applies the inverse rotation (docs/FULL_FUSED_ATTENTION_RESULTS.md
+// :34-40). The kernel boundary orders the two; no device-scope handshake.
 
 #include <math.h>
 
@@ -50,27 +50,22 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef __fp16 hx2 __attribute__((ext_vector_type(2)));
 
 constexpr int FD = 128;
-constexpr int FW = 8;                 // waves per workgroup (FW * 16 == FD)
+constexpr int FW = FAST_WAVES;        // waves per workgroup (FW * 16 == FD)
 constexpr int FT = FW * 64;           // threads
 constexpr int PS = FAST_PART_FLOATS;  // floats per (workgroup, head) partial
-constexpr int P_ROT = 2;              // partial: [M, L, rot[128], orig[128], pad]
-constexpr int P_ORIG = 2 + FD;
+constexpr int P_ROT = 4;              // partial: [M, L, has_orig, pad, rot[128], orig[128]]
+constexpr int P_ORIG = 4 + FD;
 constexpr int MAXWG = 128;            // workgroups per (sequence, kv head)
 constexpr float M_INIT = -1e30f;      // running max before the first block
-constexpr int CROW = FD + 4;          // padded LDS row of the combine buffers
 constexpr int NCP_PAIRS = 16;         // table replicas per entry / 2 (one 16-byte store each)
 
 struct Layout {
   static constexpr uint32_t lut_k = 0;        // 256 entries x 32 copies x 8 B
   static constexpr uint32_t lut_v = 65536;    // 256 entries x 32 copies x 8 B
-  static constexpr uint32_t qrs = 131072;     // [8][128] f32 rotated q * qscale
-  static constexpr uint32_t qsh = qrs + 4096; // [8][128] f32 q * qscale
-  static constexpr uint32_t fin = qsh + 4096; // [2][8][128] f32 merged rot / orig
-  static constexpr uint32_t misc = fin + 8192;
-  static constexpr uint32_t total = misc + 1024;
+  static constexpr uint32_t qop = 131072;     // [8 heads][2 parts][4][8][8] fp16 score B operands
+  static constexpr uint32_t qsh = qop + 8192; // [8][128] f32 q * qscale
+  static constexpr uint32_t total = qsh + 4096;
 };
-// the combine buffers reuse the tables and the q staging, all dead by then
-static_assert(FW * 2 * 16 * CROW * 4 <= (int)Layout::fin, "combine buffers overlap the merge buffer");
 
 __device__ inline half8 as_h8(u4 v) { return __builtin_bit_cast(half8, v); }
 
@@ -121,14 +116,6 @@ __device__ inline void split8(const float4& x0, const float4& x1, half8& hi, hal
   }
 }
 
-__device__ inline void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ inline float load_coherent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 __device__ inline u2 lds_u2(const uint8_t* smem, uint32_t addr) {
   return *reinterpret_cast<const u2*>(smem + addr);
 }
@@ -144,10 +131,7 @@ struct Blk {
 template <int G>
 __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   __shared__ __align__(16) uint8_t smem[Layout::total];
-  float* qrs = reinterpret_cast<float*>(smem + Layout::qrs);
   float* qsh = reinterpret_cast<float*>(smem + Layout::qsh);
-  float* fin = reinterpret_cast<float*>(smem + Layout::fin);
-  float* misc = reinterpret_cast<float*>(smem + Layout::misc);
 
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -168,7 +152,6 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   const int blkc = min(blk1, nbc);
   // compressed blocks of this wave: blk0 + w + k*FW, k < npk
   const int npk = blkc > blk0 + w ? (blkc - (blk0 + w) + FW - 1) / FW : 0;
-  const bool wg_has_fp16 = blk1 > nbc;
 
   const uint8_t* kcodes = a.kc + (int64_t)row * a.k_hs;
   const float* knorm = a.kn + (int64_t)row * a.kn_hs;
@@ -180,13 +163,15 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   // entry), waves 4-7 the value table (four 2-bit codes per entry); each lane
   // loads one centroid, the entries gather theirs with lane shuffles
   const float cen_lane = (w < 4 ? a.kcen : a.vcen)[lane & (w < 4 ? 15 : 3)];
-  float4 rq[8];
+  // R rows j0 + n as MFMA B operands (k-slot (q4, i) of step kb = dim 32*kb + 8*q4 + i),
+  // fp16 high part and remainder precomputed by the codec
+  u4 rqh[4], rql[4];
   {
-    const float* rr = a.rot + (int64_t)(j0 + r) * FD + 8 * q4;
+    const uint16_t* rh = a.rot16 + (j0 + r) * FD + 8 * q4;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      rq[2 * kb] = *reinterpret_cast<const float4*>(rr + 32 * kb);
-      rq[2 * kb + 1] = *reinterpret_cast<const float4*>(rr + 32 * kb + 4);
+      rqh[kb] = *reinterpret_cast<const u4*>(rh + 32 * kb);
+      rql[kb] = *reinterpret_cast<const u4*>(rh + FD * FD + 32 * kb);
     }
   }
   // q rows (original space): raw 16-byte pieces now, converted after the block
@@ -264,7 +249,10 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     L.nvB = make_float4(vb4[0], vb4[1], vb4[2], vb4[3]);
     return L;
   };
-  Blk b0 = load_blk(0), b1 = load_blk(1), b2 = load_blk(2);
+  // One block per wave goes out before the set-up work; one block in flight
+  // per wave already covers HBM latency at full bandwidth, and deeper queues
+  // stall the issuing wave.
+  Blk b0 = load_blk(0);
 
   // ---- tables, 32 replicas (lane % 32) per entry, entry stride 256 bytes:
   // key byte e -> (c_hi[e&15], c_hi[e>>4], c_lo[e&15], c_lo[e>>4]) fp16
@@ -288,42 +276,55 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   }
   // q rows as MFMA A operands (row r = query head): fp16 high part and remainder
   half8 qo_hi[4], qo_lo[4];
+  if (a.q_dtype == TQ_F16) {
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < 4; ++kb) {
+      qo_hi[kb] = as_h8(qraw[2 * kb]);
+      qo_lo[kb] = half8{};
+    }
+  } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float x;
-      if (a.q_dtype == TQ_F32) {
-        x = __uint_as_float(qraw[2 * kb + (i >> 2)][i & 3]);
-      } else {
-        const uint32_t h = (qraw[2 * kb][i >> 1] >> (16 * (i & 1))) & 0xFFFF;
-        x = a.q_dtype == TQ_F16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)h) : __uint_as_float(h << 16);
+    for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t hw = (qraw[2 * kb][i >> 1] >> (16 * (i & 1))) & 0xFFFF;
+        const float x = a.q_dtype == TQ_F32 ? __uint_as_float(qraw[2 * kb + (i >> 2)][i & 3]) : __uint_as_float(hw << 16);
+        const _Float16 hx = (_Float16)x;
+        qo_hi[kb][i] = hx;
+        qo_lo[kb][i] = (_Float16)(x - (float)hx);
       }
-      x = r < G ? x : 0.f;
-      const _Float16 hx = (_Float16)x;
-      qo_hi[kb][i] = hx;
-      qo_lo[kb][i] = (_Float16)(x - (float)hx);  // zero for fp16 queries
     }
   }
-  // ---- q_rot tile: D[h][n] = sum_i q[h][i] R[j0+n][i]   (B[k=i][n] = R[j0+n][i])
+  // ---- q_rot tile: D[h][n] = sum_i q[h][i] R[j0+n][i]   (B[k=i][n] = R[j0+n][i]),
+  // written (times qscale) as fp16 high part / remainder straight into the
+  // score B-operand layout [head][part][q4][s][8 halves]: dim j = 32*q4 + 4*s + e
+  // sits at halves (e & 1) + 4*(e >> 1) and + 2 (see the operand layout below)
   {
     f4 dq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      half8 bh, bl;
-      split8(rq[2 * kb], rq[2 * kb + 1], bh, bl);
-      dq = mfma(qo_hi[kb], bh, dq);
-      dq = mfma(qo_hi[kb], bl, dq);
-      dq = mfma(qo_lo[kb], bh, dq);
+      dq = mfma(qo_hi[kb], as_h8(rqh[kb]), dq);
+      dq = mfma(qo_hi[kb], as_h8(rql[kb]), dq);
+      dq = mfma(qo_lo[kb], as_h8(rqh[kb]), dq);
     }
+    const int j = j0 + r, e = j & 3;
+    const uint32_t off = ((uint32_t)(j >> 5) * 8 + ((j >> 2) & 7)) * 16 + 2 * ((e & 1) + 4 * (e >> 1));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * q4 + i;
-      if (h < G) qrs[h * FD + j0 + r] = dq[i] * a.qscale;
+      if (h < G) {
+        const float v = dq[i] * a.qscale;
+        const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
+        uint8_t* dh = smem + Layout::qop + (uint32_t)(h * 2) * 512 + off;
+        *reinterpret_cast<_Float16*>(dh) = hi;
+        *reinterpret_cast<_Float16*>(dh + 4) = hi;
+        *reinterpret_cast<_Float16*>(dh + 512) = lo;
+        *reinterpret_cast<_Float16*>(dh + 516) = lo;
+      }
     }
   }
-  // fp16 blocks use q * qscale in original space
-  if (r < G) {
+  // fp16 blocks use q * qscale in original space (written by wave 0 only)
+  if (w == 0 && r < G && blk1 > nbc) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -334,19 +335,13 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
 
   // B operands of the rotated-space scores, step s: k-slots (q4, i) hold
   // q[d], q[d+1], q[d], q[d+1], q[d+2], q[d+3], q[d+2], q[d+3], d = 32*q4 + 4*s,
-  // matching the key table entry layout (hi pair, lo pair) of two code bytes.
+  // matching the key table entry layout (hi pair, lo pair) of two code bytes;
+  // column r reads the high part (even r / G) or the remainder of head r % G.
   half8 qop[8];
+  {
+    const uint8_t* src = smem + Layout::qop + (uint32_t)(hd * 2 + (partf != 0.f ? 1 : 0)) * 512 + (uint32_t)q4 * 128;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const float4 x = *reinterpret_cast<const float4*>(qrs + hd * FD + 32 * q4 + 4 * s);
-    const float v[4] = {x.x, x.y, x.z, x.w};
-    _Float16 h[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const _Float16 hi = (_Float16)v[i];
-      h[i] = partf != 0.f ? (_Float16)(v[i] - (float)hi) : hi;
-    }
-    qop[s] = half8{h[0], h[1], h[0], h[1], h[2], h[3], h[2], h[3]};
+    for (int s = 0; s < 8; ++s) qop[s] = *reinterpret_cast<const half8*>(src + 16 * s);
   }
 
   // ---- per-lane online softmax state of column r (head hd)
@@ -454,13 +449,12 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     constexpr std::false_type full{};
     // loads stay unconditional (the wait counts need one issue order);
     // only the compute is skipped past the wave's last full block
-    for (int k = 0; k < npf; k += 3) {
+    Blk b1 = load_blk(1);
+    for (int k = 0; k < npf; k += 2) {
       packed_block(b0, k, full);
-      b0 = load_blk(k + 3);
+      b0 = load_blk(k + 2);
       if (k + 1 < npf) packed_block(b1, k + 1, full);
-      b1 = load_blk(k + 4);
-      if (k + 2 < npf) packed_block(b2, k + 2, full);
-      b2 = load_blk(k + 5);
+      b1 = load_blk(k + 3);
     }
     if (npf < npk) packed_block(load_tail(npf), npf, std::true_type{});
   }
@@ -527,149 +521,172 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     }
   }
 
-  // ---- combine the 8 waves of this workgroup
+  // ---- per-wave partial: (max, sum, rotated acc, original-space acc) per head.
+  // Columns r and r + G hold the fp16 high part / remainder products of head r:
+  // one DPP row rotation by G adds them; lanes r < G then hold head r.
   l_run = rows_sum(l_run);
-  float* wm = misc;           // [FW][8]
-  float* wl = misc + FW * 8;  // [FW][8]
-  int* flag = reinterpret_cast<int*>(misc + 2 * FW * 8);
-  constexpr int SIDE = 2 * G * CROW;  // floats per wave per side
-  float* cbuf = reinterpret_cast<float*>(smem);
-  __syncthreads();  // every wave is done with the tables
-  if (r < 2 * G) {
-    float* dr = cbuf + (w * 2) * SIDE + r * CROW + 32 * q4;
-    float* dor = cbuf + (w * 2 + 1) * SIDE + r * CROW + 32 * q4;
+  const bool wave_has_fp16 = fblk < blk1;
+  float* pwv = a.part + (((int64_t)row * a.nwg + c) * FW + w) * G * PS;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<float4*>(dr + 8 * i) = make_float4(acc_r[0][i], acc_r[1][i], acc_r[2][i], acc_r[3][i]);
-      *reinterpret_cast<float4*>(dr + 8 * i + 4) = make_float4(acc_r[4][i], acc_r[5][i], acc_r[6][i], acc_r[7][i]);
-      if (wg_has_fp16) {
-        *reinterpret_cast<float4*>(dor + 8 * i) = make_float4(acc_o[0][i], acc_o[1][i], acc_o[2][i], acc_o[3][i]);
-        *reinterpret_cast<float4*>(dor + 8 * i + 4) = make_float4(acc_o[4][i], acc_o[5][i], acc_o[6][i], acc_o[7][i]);
+  for (int i = 0; i < 4; ++i) {
+    float vr[8], vo[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      vr[nb] = acc_r[nb][i] + row_ror<G>(acc_r[nb][i]);
+      vo[nb] = acc_o[nb][i] + row_ror<G>(acc_o[nb][i]);
+    }
+    if (r < G) {
+      float* d = pwv + r * PS + P_ROT + 32 * q4 + 8 * i;
+      *reinterpret_cast<float4*>(d) = make_float4(vr[0], vr[1], vr[2], vr[3]);
+      *reinterpret_cast<float4*>(d + 4) = make_float4(vr[4], vr[5], vr[6], vr[7]);
+      if (wave_has_fp16) {
+        float* o = pwv + r * PS + P_ORIG + 32 * q4 + 8 * i;
+        *reinterpret_cast<float4*>(o) = make_float4(vo[0], vo[1], vo[2], vo[3]);
+        *reinterpret_cast<float4*>(o + 4) = make_float4(vo[4], vo[5], vo[6], vo[7]);
       }
     }
   }
-  if (lane < G) {
-    wm[w * 8 + lane] = m_run;
-    wl[w * 8 + lane] = l_run;
-  }
-  __syncthreads();
-  float* part = a.part + ((int64_t)row * a.nwg + c) * G * PS;
-  for (int e = tid; e < G * FD; e += FT) {
-    const int h = e / FD, j = e % FD;
-    float M = M_INIT;
-#pragma unroll
-    for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, wm[ww * 8 + h]);
-    float sr = 0.f, so = 0.f, L = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < FW; ++ww) {
-      const float sc = fexp2(wm[ww * 8 + h] - M);
-      const float* src = cbuf + (ww * 2) * SIDE;
-      sr = fmaf(sc, src[h * CROW + j] + src[(G + h) * CROW + j], sr);
-      if (wg_has_fp16) so = fmaf(sc, src[SIDE + h * CROW + j] + src[SIDE + (G + h) * CROW + j], so);
-      L = fmaf(sc, wl[ww * 8 + h], L);
-    }
-    store_coherent(part + h * PS + P_ROT + j, sr);
-    if (wg_has_fp16) store_coherent(part + h * PS + P_ORIG + j, so);
-    if (j == 0) {
-      store_coherent(part + h * PS + 0, M);
-      store_coherent(part + h * PS + 1, L);
-    }
-  }
+  if (lane < G) *reinterpret_cast<float4*>(pwv + lane * PS) = make_float4(m_run, l_run, wave_has_fp16 ? 1.f : 0.f, 0.f);
+}
 
-  // ---- last workgroup of (b, g) merges all partials
-  // Every thread waits until its device-coherent stores have completed
-  // (s_waitcnt vmcnt(0): gfx9 counts stores in vmcnt) before the ticket; the
-  // partials were written write-through (sc1), so no L2 writeback is needed.
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  __syncthreads();
-  if (tid == 0) {
-    const int old = __hip_atomic_fetch_add(a.counter + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *flag = (old == a.nwg - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (*flag == 0) return;
+// Merge of the per-wave partials of one query head of (kv head g, sequence b)
+// and the inverse rotation, a second launch on the same stream (the kernel
+// boundary makes the partials visible):
+//   out = (sum_p w_p rot_p) R + sum_p w_p orig_p,  w_p = 2^(M_p - M) / L
+// (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40). One workgroup (4 waves) per
+// query head; reductions across lanes use permlane / DPP, not LDS loops.
+constexpr int MT = 256;  // merge threads
 
-  // R^T rows of this wave for the inverse rotation (latency overlaps the merge)
-  float4 rt[8];
-  {
-    const float* tr = a.rot_t + (int64_t)(j0 + r) * FD + 8 * q4;
+__device__ inline float wave_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));  // quad_perm 1,0,3,2
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));  // quad_perm 2,3,0,1
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true))); // row_half_mirror
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true))); // row_mirror
+  return rows_max(v);
+}
+
+__device__ inline float wave_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true));
+  return rows_sum(v);
+}
+
+template <int G>
+__global__ __launch_bounds__(MT) void fast_merge_kernel(FastArgs a) {
+  __shared__ float wt[MAXWG * FW];            // per-partial weight w_p
+  __shared__ float flg[MAXWG * FW];           // partial holds an original-space part
+  __shared__ __align__(16) float red[2][8][FD];  // per-group sums (rot, orig)
+  __shared__ float fin[FD], fino[FD], rsum[2][FD];
+  __shared__ float wred[2][MT / 64];
+  const int h = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int row = b * a.hkv + g;
+  const int np = a.nwg * FW;
+  const float* pb = a.part + (int64_t)row * np * G * PS + h * PS;  // partial p at pb + p * G * PS
+
+  // rotation rows for the final product, issued first: thread t owns output dim
+  // t % 128 and input dims [64 * (t / 128), +64)
+  const int jo = tid & (FD - 1), ih = tid >> 7;
+  float rr[64];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      rt[2 * kb] = *reinterpret_cast<const float4*>(tr + 32 * kb);
-      rt[2 * kb + 1] = *reinterpret_cast<const float4*>(tr + 32 * kb + 4);
+  for (int i = 0; i < 64; ++i) rr[i] = a.rot[(64 * ih + i) * FD + jo];
+
+  // phase 1: M = max_p M_p, L = sum_p 2^(M_p - M) L_p, weights into LDS
+  float mv[MAXWG * FW / MT], lv[MAXWG * FW / MT];
+  float m = M_INIT;
+#pragma unroll
+  for (int k = 0; k < MAXWG * FW / MT; ++k) {
+    const int p = tid + k * MT;
+    mv[k] = M_INIT;
+    lv[k] = 0.f;
+    if (p < np) {
+      const float4 x = *reinterpret_cast<const float4*>(pb + (int64_t)p * G * PS);
+      mv[k] = x.x;
+      lv[k] = x.y;
+      flg[p] = x.z;
     }
+    m = fmaxf(m, mv[k]);
   }
-  // workgroups whose block range reaches the sink / residual blocks
-  const int cf = (nbs + nbr > 0) ? nbc / a.bpw : a.nwg;
-  const float* pall = a.part + (int64_t)row * a.nwg * G * PS;
-  for (int e = tid; e < G * FD; e += FT) {
-    const int h = e / FD, j = e % FD;
-    float M = M_INIT, L = 0.f, sr = 0.f, so = 0.f;
-    for (int c0 = 0; c0 < a.nwg; c0 += 16) {
-      float mv[16], lv[16], rv[16];
+  m = wave_max(m);
+  if (lane == 0) wred[0][w] = m;
+  __syncthreads();
+  float M = wred[0][0];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int cc = min(c0 + k, a.nwg - 1);
-        const float* p = pall + (cc * G + h) * PS;
-        mv[k] = c0 + k < a.nwg ? load_coherent(p) : M_INIT;
-        lv[k] = load_coherent(p + 1);
-        rv[k] = load_coherent(p + P_ROT + j);
-      }
-      float Mb = M;
+  for (int k = 1; k < MT / 64; ++k) M = fmaxf(M, wred[0][k]);
+  float l = 0.f;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) Mb = fmaxf(Mb, mv[k]);
-      const float sc = fexp2(M - Mb);
-      L *= sc;
-      sr *= sc;
-      so *= sc;
-      M = Mb;
+  for (int k = 0; k < MAXWG * FW / MT; ++k) {
+    mv[k] = fexp2(mv[k] - M);
+    l = fmaf(mv[k], lv[k], l);
+  }
+  l = wave_sum(l);
+  if (lane == 0) wred[1][w] = l;
+  __syncthreads();
+  float L = 0.f;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        if (c0 + k < a.nwg) {
-          const float wgt = fexp2(mv[k] - M);
-          L = fmaf(wgt, lv[k], L);
-          sr = fmaf(wgt, rv[k], sr);
-          if (c0 + k >= cf && (c0 + k) * a.bpw < nbt) so = fmaf(wgt, load_coherent(pall + ((c0 + k) * G + h) * PS + P_ORIG + j), so);
-        }
-      }
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    fin[h * FD + j] = sr * inv;
-    fin[8 * FD + h * FD + j] = so * inv;
+  for (int k = 0; k < MT / 64; ++k) L += wred[1][k];
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXWG * FW / MT; ++k) {
+    const int p = tid + k * MT;
+    if (p < np) wt[p] = mv[k] * inv;
   }
   __syncthreads();
-  // out = fin_rot @ R + fin_orig   (B[k=i][n] = R[i][j0+n] = R^T[j0+n][i])
-  {
-    f4 d = {0.f, 0.f, 0.f, 0.f};
+
+  // phase 2: thread (group grp, dims 4 * jq ..) sums partials p = grp, grp + 8, ...
+  const int jq = tid & 31, grp = tid >> 5;
+  float4 sr = make_float4(0.f, 0.f, 0.f, 0.f), so = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int p0 = grp; p0 < np; p0 += 8 * 16) {
+    float4 v[16];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      half8 ar;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int hh = r < G ? r : r - G;
-        const float v = r < 2 * G ? fin[hh * FD + 32 * kb + 8 * q4 + i] : 0.f;
-        const _Float16 hv = (_Float16)v;
-        ar[i] = r < G ? hv : (_Float16)(v - (float)hv);
-      }
-      half8 bh, bl;
-      split8(rt[2 * kb], rt[2 * kb + 1], bh, bl);
-      d = mfma(ar, bh, d);
-      d = mfma(ar, bl, d);
+    for (int k = 0; k < 16; ++k) {
+      const int p = min(p0 + 8 * k, np - 1);
+      v[k] = *reinterpret_cast<const float4*>(pb + (int64_t)p * G * PS + P_ROT + 4 * jq);
     }
-    // row h (hi part) + row G + h (lo part): same lane for G < 4, lane + 16*(G/4) otherwise
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float lo;
-      if (G >= 4) {
-        lo = __shfl_down(d[i], 16 * (G / 4));
-      } else {
-        lo = (i + G < 4) ? d[(i + G) & 3] : 0.f;
-      }
-      const int h = 4 * q4 + i;
-      if (h < G) a.out[((int64_t)b * a.hq + g * G + h) * FD + j0 + r] = d[i] + lo + fin[8 * FD + h * FD + j0 + r];
+    for (int k = 0; k < 16; ++k) {
+      const int p = p0 + 8 * k;
+      const float wp = p < np ? wt[p] : 0.f;
+      sr.x = fmaf(wp, v[k].x, sr.x);
+      sr.y = fmaf(wp, v[k].y, sr.y);
+      sr.z = fmaf(wp, v[k].z, sr.z);
+      sr.w = fmaf(wp, v[k].w, sr.w);
     }
   }
-  if (tid == 0) __hip_atomic_store(a.counter + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // original-space parts: only the few waves that reached the sink / residual blocks
+  for (int p = grp; p < np; p += 8) {
+    if (flg[p] != 0.f) {
+      const float4 o = *reinterpret_cast<const float4*>(pb + (int64_t)p * G * PS + P_ORIG + 4 * jq);
+      const float wp = wt[p];
+      so.x = fmaf(wp, o.x, so.x);
+      so.y = fmaf(wp, o.y, so.y);
+      so.z = fmaf(wp, o.z, so.z);
+      so.w = fmaf(wp, o.w, so.w);
+    }
+  }
+  *reinterpret_cast<float4*>(&red[0][grp][4 * jq]) = sr;
+  *reinterpret_cast<float4*>(&red[1][grp][4 * jq]) = so;
+  __syncthreads();
+  if (tid < FD) {
+    float x = 0.f, y = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      x += red[0][k][tid];
+      y += red[1][k][tid];
+    }
+    fin[tid] = x;
+    fino[tid] = y;
+  }
+  __syncthreads();
+  // phase 3: out = fin @ R + fino in fp32 (rows i of R, output dim jo)
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) acc = fmaf(fin[64 * ih + i], rr[i], acc);
+  rsum[ih][jo] = acc;
+  __syncthreads();
+  if (tid < FD) a.out[((int64_t)b * a.hq + g * G + h) * FD + tid] = rsum[0][tid] + rsum[1][tid] + fino[tid];
 }
 
 size_t fast_smem_bytes() { return Layout::total; }
@@ -677,12 +694,24 @@ size_t fast_smem_bytes() { return Layout::total; }
 int fast_max_wg() { return MAXWG; }
 
 int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s) {
-  dim3 grid(a.nwg, a.hkv, batch);
+  const dim3 grid(a.nwg, a.hkv, batch), mgrid(G, a.hkv, batch);
   switch (G) {
-    case 1: hipLaunchKernelGGL((fast_decode_kernel<1>), grid, dim3(FT), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((fast_decode_kernel<2>), grid, dim3(FT), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((fast_decode_kernel<4>), grid, dim3(FT), 0, s, a); break;
-    default: hipLaunchKernelGGL((fast_decode_kernel<8>), grid, dim3(FT), 0, s, a); break;
+    case 1:
+      hipLaunchKernelGGL((fast_decode_kernel<1>), grid, dim3(FT), 0, s, a);
+      hipLaunchKernelGGL((fast_merge_kernel<1>), mgrid, dim3(MT), 0, s, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((fast_decode_kernel<2>), grid, dim3(FT), 0, s, a);
+      hipLaunchKernelGGL((fast_merge_kernel<2>), mgrid, dim3(MT), 0, s, a);
+      break;
+    case 4:
+      hipLaunchKernelGGL((fast_decode_kernel<4>), grid, dim3(FT), 0, s, a);
+      hipLaunchKernelGGL((fast_merge_kernel<4>), mgrid, dim3(MT), 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((fast_decode_kernel<8>), grid, dim3(FT), 0, s, a);
+      hipLaunchKernelGGL((fast_merge_kernel<8>), mgrid, dim3(MT), 0, s, a);
+      break;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

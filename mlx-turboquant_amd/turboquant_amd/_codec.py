@@ -37,7 +37,9 @@ class DeviceCodec:
             raise ValueError(f"Unsupported bit-width: {bits}. Use 1, 2, 3, or 4.")
         self.device = device
         self.rotation = get_rotation_matrix(d, seed, device)
-        self.rotation_t = self.rotation.t().contiguous()
+        # fp16 high part and remainder of R, the MFMA operands of the query rotation
+        hi = self.rotation.half()
+        self.rotation_f16 = torch.stack([hi, (self.rotation - hi.float()).half()]).contiguous()
         self.c_hi, self.b_hi = get_codebook(d, self.bits_hi, device)
         self.c_lo, self.b_lo = get_codebook(d, self.bits_lo, device)
         self.qjl_m = qjl_m
@@ -51,7 +53,7 @@ class DeviceCodec:
             boundaries_hi=self.b_hi.data_ptr(), centroids_lo=self.c_lo.data_ptr(),
             boundaries_lo=self.b_lo.data_ptr(),
             qjl_proj=self.proj.data_ptr() if self.proj is not None else None,
-            qjl_m=qjl_m, reserved=0, rotation_t=self.rotation_t.data_ptr())
+            qjl_m=qjl_m, reserved=0, rotation_f16=self.rotation_f16.data_ptr())
 
     @property
     def fractional(self) -> bool:

@@ -35,7 +35,7 @@ class Codec(ctypes.Structure):
     _fields_ = [("d", _i32), ("bits_hi", _i32), ("bits_lo", _i32), ("split", _i32),
                 ("rotation", _p), ("centroids_hi", _p), ("boundaries_hi", _p),
                 ("centroids_lo", _p), ("boundaries_lo", _p), ("qjl_proj", _p),
-                ("qjl_m", _i32), ("reserved", _i32), ("rotation_t", _p)]
+                ("qjl_m", _i32), ("reserved", _i32), ("rotation_f16", _p)]
 
 
 class Store(ctypes.Structure):

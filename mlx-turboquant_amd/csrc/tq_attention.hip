@@ -448,7 +448,7 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
   size_t general = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
   int nwg, bpw;
   fast_geometry(d, nwg, bpw);
-  const size_t fast = (size_t)d->batch * d->hkv * nwg * FAST_WAVES * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
+  const size_t fast = (size_t)d->batch * d->hkv * nwg * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
   const size_t bytes = counter_bytes(d) + (general > fast ? general : fast);
   return (bytes + 255) & ~(size_t)255;
 }

@@ -39,6 +39,6 @@ int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s);
 int fast_max_wg();
 
 constexpr int FAST_WAVES = 8;          // waves per workgroup of the decode kernel
-constexpr int FAST_PART_FLOATS = 260;  // per query head per wave: M, L, has_orig, pad, rot[128], orig[128]
+constexpr int FAST_PART_FLOATS = 260;  // per query head per workgroup: M, L, has_orig, pad, rot[128], orig[128]
 
 }  // namespace tq

@@ -57,12 +57,15 @@ constexpr int P_ROT = 4;              // partial: [M, L, has_orig, pad, rot[128]
 constexpr int P_ORIG = 4 + FD;
 constexpr int MAXWG = 128;            // workgroups per (sequence, kv head)
 constexpr float M_INIT = -1e30f;      // running max before the first block
-constexpr int NCP_PAIRS = 16;         // table replicas per entry / 2 (one 16-byte store each)
+constexpr int NCP = 16;               // table replicas per entry (lane % 16)
 
 struct Layout {
-  static constexpr uint32_t lut_k = 0;        // 256 entries x 32 copies x 8 B
-  static constexpr uint32_t lut_v = 65536;    // 256 entries x 32 copies x 8 B
-  static constexpr uint32_t qop = 131072;     // [8 heads][2 parts][4][8][8] fp16 score B operands
+  // tables: entry e of both tables in one 256-byte row, key copies in bytes
+  // [0, 128), value copies in [128, 256), copy c at 8*c
+  static constexpr uint32_t lut = 0;          // 256 rows x 256 B
+  static constexpr uint32_t cmb = 65536;      // [8 waves][8 heads][2][128] f32 wave partials
+  static constexpr uint32_t cml = cmb + 65536;  // [8 waves][8 heads][2] f32 wave max / sum
+  static constexpr uint32_t qop = cml + 512;  // [8 heads][2 parts][4][8][8] fp16 score B operands
   static constexpr uint32_t qsh = qop + 8192; // [8][128] f32 q * qscale
   static constexpr uint32_t total = qsh + 4096;
 };
@@ -254,7 +257,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   // stall the issuing wave.
   Blk b0 = load_blk(0);
 
-  // ---- tables, 32 replicas (lane % 32) per entry, entry stride 256 bytes:
+  // ---- tables, 16 replicas (lane % 16) per entry, entry stride 256 bytes:
   // key byte e -> (c_hi[e&15], c_hi[e>>4], c_lo[e&15], c_lo[e>>4]) fp16
   // value byte e -> (c[e&3], c[(e>>2)&3], c[(e>>4)&3], c[(e>>6)&3]) fp16
   {
@@ -269,10 +272,10 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     ent[1] = w < 4 ? pack_h2(cen[0] - h0, cen[1] - h1) : pack_h2(cen[2], cen[3]);
     ent[2] = ent[0];
     ent[3] = ent[1];
-    uint8_t* base = smem + (w < 4 ? Layout::lut_k : Layout::lut_v) + e * 256;
+    uint8_t* base = smem + Layout::lut + e * 256 + (w < 4 ? 0 : 128);
 #pragma unroll
-    for (int k = 0; k < NCP_PAIRS; ++k)  // copies (2k', 2k'+1), rotated per entry against bank conflicts
-      *reinterpret_cast<u4*>(base + 16 * ((k + e) & (NCP_PAIRS - 1))) = ent;
+    for (int k = 0; k < NCP / 2; ++k)  // copies (2k', 2k'+1), rotated per entry against bank conflicts
+      *reinterpret_cast<u4*>(base + 16 * ((k + e) & (NCP / 2 - 1))) = ent;
   }
   // q rows as MFMA A operands (row r = query head): fp16 high part and remainder
   half8 qo_hi[4], qo_lo[4];
@@ -350,13 +353,13 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) acc_r[nb] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const uint32_t cpv = (uint32_t)(lane & 31) * 8;  // replica offset within an entry
-  const uint32_t cpv_v = cpv | Layout::lut_v;      // byte 2 = 0x01: value table
+  const uint32_t cpv = (uint32_t)(lane & (NCP - 1)) * 8;  // key replica offset within a row
+  const uint32_t cpv_v = cpv + 128;                       // value replica offset
   auto kaddr = [&](uint32_t word, int byte) {      // (byte of word) << 8 | cpv
     return __builtin_amdgcn_perm(word, cpv, 0x0C0C0000u | ((4u + byte) << 8));
   };
-  auto vaddr = [&](uint32_t word, int byte) {      // 0x10000 | (byte of word) << 8 | cpv
-    return __builtin_amdgcn_perm(word, cpv_v, 0x0C020000u | ((4u + byte) << 8));
+  auto vaddr = [&](uint32_t word, int byte) {      // (byte of word) << 8 | cpv_v
+    return __builtin_amdgcn_perm(word, cpv_v, 0x0C0C0000u | ((4u + byte) << 8));
   };
 
   // Online softmax of the 8 scores of this lane (tokens A0..A3, B0..B3 of
@@ -521,35 +524,62 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     }
   }
 
-  // ---- per-wave partial: (max, sum, rotated acc, original-space acc) per head.
+  // ---- combine the 8 waves of this workgroup through LDS (own region, one barrier).
   // Columns r and r + G hold the fp16 high part / remainder products of head r:
   // one DPP row rotation by G adds them; lanes r < G then hold head r.
   l_run = rows_sum(l_run);
   const bool wave_has_fp16 = fblk < blk1;
-  float* pwv = a.part + (((int64_t)row * a.nwg + c) * FW + w) * G * PS;
+  const bool wg_has_fp16 = blk1 > nbc;
+  float* cm = reinterpret_cast<float*>(smem + Layout::cmb) + (w * 8) * 2 * FD;  // [head][side][128]
+  float* cl = reinterpret_cast<float*>(smem + Layout::cml) + w * 16;             // [head][max, sum]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float vr[8], vo[8];
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
       vr[nb] = acc_r[nb][i] + row_ror<G>(acc_r[nb][i]);
-      vo[nb] = acc_o[nb][i] + row_ror<G>(acc_o[nb][i]);
+      vo[nb] = wave_has_fp16 ? acc_o[nb][i] + row_ror<G>(acc_o[nb][i]) : 0.f;
     }
     if (r < G) {
-      float* d = pwv + r * PS + P_ROT + 32 * q4 + 8 * i;
+      float* d = cm + r * 2 * FD + 32 * q4 + 8 * i;
       *reinterpret_cast<float4*>(d) = make_float4(vr[0], vr[1], vr[2], vr[3]);
       *reinterpret_cast<float4*>(d + 4) = make_float4(vr[4], vr[5], vr[6], vr[7]);
-      if (wave_has_fp16) {
-        float* o = pwv + r * PS + P_ORIG + 32 * q4 + 8 * i;
-        *reinterpret_cast<float4*>(o) = make_float4(vo[0], vo[1], vo[2], vo[3]);
-        *reinterpret_cast<float4*>(o + 4) = make_float4(vo[4], vo[5], vo[6], vo[7]);
+      if (wg_has_fp16) {
+        *reinterpret_cast<float4*>(d + FD) = make_float4(vo[0], vo[1], vo[2], vo[3]);
+        *reinterpret_cast<float4*>(d + FD + 4) = make_float4(vo[4], vo[5], vo[6], vo[7]);
       }
     }
   }
-  if (lane < G) *reinterpret_cast<float4*>(pwv + lane * PS) = make_float4(m_run, l_run, wave_has_fp16 ? 1.f : 0.f, 0.f);
+  if (lane < G) {
+    cl[2 * lane] = m_run;
+    cl[2 * lane + 1] = l_run;
+  }
+  __syncthreads();
+  // thread (head, dim): merge the 8 waves, write the workgroup partial
+  float* part = a.part + ((int64_t)row * a.nwg + c) * G * PS;
+  const float* cms = reinterpret_cast<const float*>(smem + Layout::cmb);
+  const float* cls = reinterpret_cast<const float*>(smem + Layout::cml);
+  for (int e = tid; e < G * FD; e += FT) {
+    const int h = e / FD, j = e % FD;
+    float M = M_INIT;
+#pragma unroll
+    for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, cls[ww * 16 + 2 * h]);
+    float sr = 0.f, so = 0.f, L = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < FW; ++ww) {
+      const float sc = fexp2(cls[ww * 16 + 2 * h] - M);
+      const float* src = cms + ((ww * 8 + h) * 2) * FD + j;
+      sr = fmaf(sc, src[0], sr);
+      if (wg_has_fp16) so = fmaf(sc, src[FD], so);
+      L = fmaf(sc, cls[ww * 16 + 2 * h + 1], L);
+    }
+    part[h * PS + P_ROT + j] = sr;
+    if (wg_has_fp16) part[h * PS + P_ORIG + j] = so;
+    if (j == 0) *reinterpret_cast<float4*>(part + h * PS) = make_float4(M, L, wg_has_fp16 ? 1.f : 0.f, 0.f);
+  }
 }
 
-// Merge of the per-wave partials of one query head of (kv head g, sequence b)
+// Merge of the per-workgroup partials of one query head of (kv head g, sequence b)
 // and the inverse rotation, a second launch on the same stream (the kernel
 // boundary makes the partials visible):
 //   out = (sum_p w_p rot_p) R + sum_p w_p orig_p,  w_p = 2^(M_p - M) / L
@@ -575,118 +605,97 @@ __device__ inline float wave_sum(float v) {
 
 template <int G>
 __global__ __launch_bounds__(MT) void fast_merge_kernel(FastArgs a) {
-  __shared__ float wt[MAXWG * FW];            // per-partial weight w_p
-  __shared__ float flg[MAXWG * FW];           // partial holds an original-space part
-  __shared__ __align__(16) float red[2][8][FD];  // per-group sums (rot, orig)
-  __shared__ float fin[FD], fino[FD], rsum[2][FD];
-  __shared__ float wred[2][MT / 64];
+  constexpr int PPT = 4;                             // partials per thread per pass
+  __shared__ __align__(16) float red[8][FD + 4];     // per-group sums of rot (then of the rotation)
+  __shared__ __align__(16) float redo[8][FD + 4];    // per-group sums of orig
+  __shared__ __align__(16) float fin[FD];
   const int h = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int row = b * a.hkv + g;
-  const int np = a.nwg * FW;
+  const int np = a.nwg;
   const float* pb = a.part + (int64_t)row * np * G * PS + h * PS;  // partial p at pb + p * G * PS
+  const int jq = tid & 31, grp = tid >> 5;  // dims 4*jq .. 4*jq+3, partials grp, grp + 8, ...
 
-  // rotation rows for the final product, issued first: thread t owns output dim
-  // t % 128 and input dims [64 * (t / 128), +64)
-  const int jo = tid & (FD - 1), ih = tid >> 7;
-  float rr[64];
+  // rotation rows for the final product: thread (grp, jq) holds R[16*grp + i][4*jq .. +3]
+  float4 rr[16];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) rr[i] = a.rot[(64 * ih + i) * FD + jo];
+  for (int i = 0; i < 16; ++i) rr[i] = *reinterpret_cast<const float4*>(a.rot + (16 * grp + i) * FD + 4 * jq);
 
-  // phase 1: M = max_p M_p, L = sum_p 2^(M_p - M) L_p, weights into LDS
-  float mv[MAXWG * FW / MT], lv[MAXWG * FW / MT];
-  float m = M_INIT;
+  // global max / sum: every wave reduces all partial headers itself (no barrier)
+  float M = M_INIT;
+  float mh[MAXWG / 64], lh[MAXWG / 64];
 #pragma unroll
-  for (int k = 0; k < MAXWG * FW / MT; ++k) {
-    const int p = tid + k * MT;
-    mv[k] = M_INIT;
-    lv[k] = 0.f;
-    if (p < np) {
-      const float4 x = *reinterpret_cast<const float4*>(pb + (int64_t)p * G * PS);
-      mv[k] = x.x;
-      lv[k] = x.y;
-      flg[p] = x.z;
-    }
-    m = fmaxf(m, mv[k]);
+  for (int k = 0; k < MAXWG / 64; ++k) {
+    const int p = lane + 64 * k;  // loads stay unconditional (exact wait counts), values masked
+    const float4 x = *reinterpret_cast<const float4*>(pb + (int64_t)min(p, np - 1) * G * PS);
+    mh[k] = p < np ? x.x : M_INIT;
+    lh[k] = p < np ? x.y : 0.f;
+    M = fmaxf(M, mh[k]);
   }
-  m = wave_max(m);
-  if (lane == 0) wred[0][w] = m;
-  __syncthreads();
-  float M = wred[0][0];
-#pragma unroll
-  for (int k = 1; k < MT / 64; ++k) M = fmaxf(M, wred[0][k]);
-  float l = 0.f;
-#pragma unroll
-  for (int k = 0; k < MAXWG * FW / MT; ++k) {
-    mv[k] = fexp2(mv[k] - M);
-    l = fmaf(mv[k], lv[k], l);
-  }
-  l = wave_sum(l);
-  if (lane == 0) wred[1][w] = l;
-  __syncthreads();
+  M = wave_max(M);
   float L = 0.f;
 #pragma unroll
-  for (int k = 0; k < MT / 64; ++k) L += wred[1][k];
+  for (int k = 0; k < MAXWG / 64; ++k) L = fmaf(fexp2(mh[k] - M), lh[k], L);
+  L = wave_sum(L);
   const float inv = L > 0.f ? 1.f / L : 0.f;
+
+  // weighted sums of this thread's partials
+  float4 sr = make_float4(0.f, 0.f, 0.f, 0.f), so = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int p0 = grp; p0 < np; p0 += 8 * PPT) {
+    float4 hv[PPT], rv[PPT];
 #pragma unroll
-  for (int k = 0; k < MAXWG * FW / MT; ++k) {
-    const int p = tid + k * MT;
-    if (p < np) wt[p] = mv[k] * inv;
+    for (int k = 0; k < PPT; ++k) {
+      const int p = min(p0 + 8 * k, np - 1);
+      hv[k] = *reinterpret_cast<const float4*>(pb + (int64_t)p * G * PS);
+      rv[k] = *reinterpret_cast<const float4*>(pb + (int64_t)p * G * PS + P_ROT + 4 * jq);
+    }
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const float wp = p0 + 8 * k < np ? fexp2(hv[k].x - M) * inv : 0.f;
+      sr.x = fmaf(wp, rv[k].x, sr.x);
+      sr.y = fmaf(wp, rv[k].y, sr.y);
+      sr.z = fmaf(wp, rv[k].z, sr.z);
+      sr.w = fmaf(wp, rv[k].w, sr.w);
+      if (p0 + 8 * k < np && hv[k].z != 0.f) {  // original-space part (sink / residual blocks)
+        const float4 o = *reinterpret_cast<const float4*>(pb + (int64_t)(p0 + 8 * k) * G * PS + P_ORIG + 4 * jq);
+        so.x = fmaf(wp, o.x, so.x);
+        so.y = fmaf(wp, o.y, so.y);
+        so.z = fmaf(wp, o.z, so.z);
+        so.w = fmaf(wp, o.w, so.w);
+      }
+    }
+  }
+  *reinterpret_cast<float4*>(&red[grp][4 * jq]) = sr;
+  *reinterpret_cast<float4*>(&redo[grp][4 * jq]) = so;
+  __syncthreads();
+  if (tid < FD) {
+    float x = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x += red[k][tid];
+    fin[tid] = x;
   }
   __syncthreads();
-
-  // phase 2: thread (group grp, dims 4 * jq ..) sums partials p = grp, grp + 8, ...
-  const int jq = tid & 31, grp = tid >> 5;
-  float4 sr = make_float4(0.f, 0.f, 0.f, 0.f), so = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int p0 = grp; p0 < np; p0 += 8 * 16) {
-    float4 v[16];
+  // out[j] = sum_i fin[i] R[i][j] + orig[j]: group grp covers rows i = 16*grp .. +15
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int p = min(p0 + 8 * k, np - 1);
-      v[k] = *reinterpret_cast<const float4*>(pb + (int64_t)p * G * PS + P_ROT + 4 * jq);
-    }
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int p = p0 + 8 * k;
-      const float wp = p < np ? wt[p] : 0.f;
-      sr.x = fmaf(wp, v[k].x, sr.x);
-      sr.y = fmaf(wp, v[k].y, sr.y);
-      sr.z = fmaf(wp, v[k].z, sr.z);
-      sr.w = fmaf(wp, v[k].w, sr.w);
-    }
+  for (int i = 0; i < 16; ++i) {
+    const float f = fin[16 * grp + i];
+    acc.x = fmaf(f, rr[i].x, acc.x);
+    acc.y = fmaf(f, rr[i].y, acc.y);
+    acc.z = fmaf(f, rr[i].z, acc.z);
+    acc.w = fmaf(f, rr[i].w, acc.w);
   }
-  // original-space parts: only the few waves that reached the sink / residual blocks
-  for (int p = grp; p < np; p += 8) {
-    if (flg[p] != 0.f) {
-      const float4 o = *reinterpret_cast<const float4*>(pb + (int64_t)p * G * PS + P_ORIG + 4 * jq);
-      const float wp = wt[p];
-      so.x = fmaf(wp, o.x, so.x);
-      so.y = fmaf(wp, o.y, so.y);
-      so.z = fmaf(wp, o.z, so.z);
-      so.w = fmaf(wp, o.w, so.w);
-    }
-  }
-  *reinterpret_cast<float4*>(&red[0][grp][4 * jq]) = sr;
-  *reinterpret_cast<float4*>(&red[1][grp][4 * jq]) = so;
+  *reinterpret_cast<float4*>(&red[grp][4 * jq]) = acc;
   __syncthreads();
   if (tid < FD) {
     float x = 0.f, y = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      x += red[0][k][tid];
-      y += red[1][k][tid];
+      x += red[k][tid];
+      y += redo[k][tid];
     }
-    fin[tid] = x;
-    fino[tid] = y;
+    a.out[((int64_t)b * a.hq + g * G + h) * FD + tid] = x + y;
   }
-  __syncthreads();
-  // phase 3: out = fin @ R + fino in fp32 (rows i of R, output dim jo)
-  float acc = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; ++i) acc = fmaf(fin[64 * ih + i], rr[i], acc);
-  rsum[ih][jo] = acc;
-  __syncthreads();
-  if (tid < FD) a.out[((int64_t)b * a.hq + g * G + h) * FD + tid] = rsum[0][tid] + rsum[1][tid] + fino[tid];
 }
 
 size_t fast_smem_bytes() { return Layout::total; }

@@ -64,10 +64,10 @@ struct Layout {
   // [0, 128), value copies in [128, 256), copy c at 8*c
   static constexpr uint32_t lut = 0;          // 256 rows x 256 B
   static constexpr uint32_t cmb = 65536;      // [8 waves][8 heads][2][128] f32 wave partials
-  static constexpr uint32_t cml = cmb + 65536;  // [8 waves][8 heads][2] f32 wave max / sum
-  static constexpr uint32_t qop = cml + 512;  // [8 heads][2 parts][4][8][8] fp16 score B operands
-  static constexpr uint32_t qsh = qop + 8192; // [8][128] f32 q * qscale
-  static constexpr uint32_t total = qsh + 4096;
+  static constexpr uint32_t cml = cmb + 65536;  // [8 waves][8 heads][4] f32 max, sum, max of the orig part
+  static constexpr uint32_t qop = cml + 1024; // [8 heads][2 parts][4][8][8] fp16 rotated-q B operands
+  static constexpr uint32_t qfo = qop + 8192; // [8 heads][2 parts][4][4][8] fp16 original-space q B operands
+  static constexpr uint32_t total = qfo + 4096;
 };
 
 __device__ inline half8 as_h8(u4 v) { return __builtin_bit_cast(half8, v); }
@@ -134,7 +134,6 @@ struct Blk {
 template <int G>
 __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   __shared__ __align__(16) uint8_t smem[Layout::total];
-  float* qsh = reinterpret_cast<float*>(smem + Layout::qsh);
 
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -145,6 +144,21 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   const int hd = r % G;   // query head of column r
   const float partf = ((r / G) & 1) ? 1.f : 0.f;  // column holds the fp16 remainder
 
+  // All kernel arguments the set-up needs are loaded in one batch of scalar
+  // loads and waited for once (a branch on an argument would otherwise split
+  // them into dependent round trips).
+  {
+    const void* p0 = a.comp_len_b; const void* p1 = a.sink_len_b;
+    const void* p2 = a.res_len_b; const void* p3 = a.res_start_b;
+    const void* p4 = a.kc; const void* p5 = a.kn; const void* p6 = a.vc; const void* p7 = a.vn;
+    const void* p8 = a.q; const void* p9 = a.rot16; const void* p10 = a.kcen; const void* p11 = a.vcen;
+    const int64_t s0 = a.k_hs, s1 = a.kn_hs, s2 = a.v_hs, s3 = a.vn_hs;
+    const int i0 = a.max_comp, i1 = a.max_sink, i2 = a.max_res, i3 = a.res_start0, i4 = a.bpw, i5 = a.hkv,
+              i6 = a.hq, i7 = a.q_dtype;
+    asm volatile("" ::"s"(p0), "s"(p1), "s"(p2), "s"(p3), "s"(p4), "s"(p5), "s"(p6), "s"(p7), "s"(p8), "s"(p9),
+                 "s"(p10), "s"(p11), "s"(s0), "s"(s1), "s"(s2), "s"(s3), "s"(i0), "s"(i1), "s"(i2), "s"(i3), "s"(i4),
+                 "s"(i5), "s"(i6), "s"(i7));
+  }
   const int comp = a.comp_len_b ? a.comp_len_b[b] : a.max_comp;
   const int sink = a.sink_len_b ? a.sink_len_b[b] : a.max_sink;
   const int res = a.res_len_b ? a.res_len_b[b] : a.max_res;
@@ -257,6 +271,45 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   // stall the issuing wave.
   Blk b0 = load_blk(0);
 
+  // fp16 (sink / residual ring, original space) blocks of this wave follow its
+  // compressed ones in the block list but are processed first; the loads of
+  // the first one go out now. Loads stay unconditional: a wave without fp16
+  // blocks reads one line of the rotation operands instead.
+  const int fblk = blk0 + w + npk * FW;
+  const bool wave_has_fp16 = fblk < blk1;
+  struct F16Blk {
+    u4 kA[4], kB[4];  // keys: tokens ft0 + r / ft0 + 16 + r, dims 32*q4 + 8*kb ..
+    u4 v[8];          // values: dims 8r .. 8r+7 of tokens A0..A3, B0..B3
+  };
+  auto load_f16 = [&](int blk, bool valid) {
+    F16Blk L;
+    const bool is_sink = blk < nbc + nbs;
+    const int ft0 = (is_sink ? blk - nbc : blk - nbc - nbs) << 5;
+    const int flen = max(is_sink ? sink : res, 1);
+    const int64_t hs = is_sink ? a.sink_hs : a.res_hs;
+    const uint16_t* fk = valid ? static_cast<const uint16_t*>(is_sink ? a.sink_k : a.res_k) + (int64_t)row * hs : a.rot16;
+    const uint16_t* fv = valid ? static_cast<const uint16_t*>(is_sink ? a.sink_v : a.res_v) + (int64_t)row * hs : a.rot16;
+    auto slot = [&](int t) {  // ring position of token t (rstart + t < 2 * res_cap)
+      t = min(t, flen - 1);
+      const int sl = rstart + t;
+      return is_sink ? t : (sl >= a.res_cap ? sl - a.res_cap : sl);
+    };
+    const uint32_t msk = valid ? 0xFFFFFFFFu : 0u;
+    const uint32_t oA = ((uint32_t)slot(ft0 + r) * FD + 32 * q4) & msk;
+    const uint32_t oB = ((uint32_t)slot(ft0 + 16 + r) * FD + 32 * q4) & msk;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      L.kA[kb] = *reinterpret_cast<const u4*>(fk + oA + 8 * (kb & (int)msk));
+      L.kB[kb] = *reinterpret_cast<const u4*>(fk + oB + 8 * (kb & (int)msk));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = ft0 + (i < 4 ? 4 * q4 + i : 16 + 4 * q4 + i - 4);
+      L.v[i] = *reinterpret_cast<const u4*>(fv + (((uint32_t)slot(t) * FD + 8 * r) & msk));
+    }
+    return L;
+  };
+
   // ---- tables, 16 replicas (lane % 16) per entry, entry stride 256 bytes:
   // key byte e -> (c_hi[e&15], c_hi[e>>4], c_lo[e&15], c_lo[e>>4]) fp16
   // value byte e -> (c[e&3], c[(e>>2)&3], c[(e>>4)&3], c[(e>>6)&3]) fp16
@@ -326,32 +379,30 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       }
     }
   }
-  // fp16 blocks use q * qscale in original space (written by wave 0 only)
+  // fp16 blocks use the (unscaled) q in original space as score B operands,
+  // step kb k-slot (q4, i) = dim 32*q4 + 8*kb + i: fp16 high part / remainder
+  // in [head][part][q4][kb][8 halves]; the lane holding dims 32*kb + 8*q4 ..
+  // of head r copies its operand halves there (wave 0, workgroups with fp16 blocks)
   if (w == 0 && r < G && blk1 > nbc) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        qsh[r * FD + 32 * kb + 8 * q4 + i] = ((float)qo_hi[kb][i] + (float)qo_lo[kb][i]) * a.qscale;
+    for (int kb = 0; kb < 4; ++kb) {
+      uint8_t* d = smem + Layout::qfo + ((uint32_t)(r * 2 * 4 + kb) * 4 + q4) * 16;
+      *reinterpret_cast<half8*>(d) = qo_hi[kb];
+      *reinterpret_cast<half8*>(d + 4 * 4 * 16) = qo_lo[kb];
+    }
   }
+  // the first fp16 block's loads go out before the barrier (the rest of the
+  // set-up has waited for its own loads already)
+  F16Blk f0 = load_f16(fblk, wave_has_fp16);
   __syncthreads();
-
-  // B operands of the rotated-space scores, step s: k-slots (q4, i) hold
-  // q[d], q[d+1], q[d], q[d+1], q[d+2], q[d+3], q[d+2], q[d+3], d = 32*q4 + 4*s,
-  // matching the key table entry layout (hi pair, lo pair) of two code bytes;
-  // column r reads the high part (even r / G) or the remainder of head r % G.
-  half8 qop[8];
-  {
-    const uint8_t* src = smem + Layout::qop + (uint32_t)(hd * 2 + (partf != 0.f ? 1 : 0)) * 512 + (uint32_t)q4 * 128;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qop[s] = *reinterpret_cast<const half8*>(src + 16 * s);
-  }
 
   // ---- per-lane online softmax state of column r (head hd)
   float m_run = M_INIT, l_run = 0.f;
-  f4 acc_r[8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) acc_r[nb] = f4{0.f, 0.f, 0.f, 0.f};
+  float m_orig = M_INIT;  // running max the stored original-space partial refers to
+  half8 qop[8];           // rotated-space score B operands (set after the fp16 blocks)
+  f4 acc_r[8];            // rotated-space output accumulators
+  float* cm = reinterpret_cast<float*>(smem + Layout::cmb) + (w * 8) * 2 * FD;  // [head][side][128]
+  float* cl = reinterpret_cast<float*>(smem + Layout::cml) + w * 32;             // [head][4]
 
   const uint32_t cpv = (uint32_t)(lane & (NCP - 1)) * 8;  // key replica offset within a row
   const uint32_t cpv_v = cpv + 128;                       // value replica offset
@@ -365,7 +416,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   // Online softmax of the 8 scores of this lane (tokens A0..A3, B0..B3 of
   // the block, column r), returns the P^T operand (p * nv, high part or
   // remainder by column) and rescales `acc` when the running max grows.
-  auto softmax_pv = [&](float (&s)[8], const float (&nv)[8], f4 (&acc)[8], f4 (&acc2)[8], bool two) {
+  auto softmax_pv = [&](float (&s)[8], const float (&nv)[8], f4 (&acc)[8]) {
     float bm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
     bm = rows_max(bm);
     if (__builtin_amdgcn_ballot_w64(bm > m_run) != 0) {
@@ -374,10 +425,6 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       l_run *= corr;
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) acc[nb] *= corr;
-      if (two) {
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) acc2[nb] *= corr;
-      }
       m_run = mnew;
     }
     float pv[8];
@@ -426,7 +473,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       }
     }
     const float nv[8] = {L.nvA.x, L.nvA.y, L.nvA.z, L.nvA.w, L.nvB.x, L.nvB.y, L.nvB.z, L.nvB.w};
-    const half8 pb = softmax_pv(sc, nv, acc_r, acc_r, false);
+    const half8 pb = softmax_pv(sc, nv, acc_r);
     // V^T operands: row = dim 8r + nb, k-slot pairs = token pairs of the lane
     u4 va[8];
 #pragma unroll
@@ -447,7 +494,77 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     for (int nb = 0; nb < 8; ++nb) acc_r[nb] = mfma(as_h8(va[nb]), pb, acc_r[nb]);
   };
 
-  // ---- compressed blocks: three load slots, two blocks in flight
+  // ---- fp16 blocks of the sink and the residual ring (original space), first
+  if (wave_has_fp16) {
+    half8 qf[4];
+    {
+      const uint8_t* src = smem + Layout::qfo + ((uint32_t)(hd * 2 + (partf != 0.f ? 1 : 0)) * 4 + q4) * 4 * 16;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) qf[kb] = *reinterpret_cast<const half8*>(src + 16 * kb);
+    }
+    f4 acc_o[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc_o[nb] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int blk = fblk; blk < blk1; blk += FW) {
+      const F16Blk L = blk == fblk ? f0 : load_f16(blk, true);
+      const bool is_sink = blk < nbc + nbs;
+      const int ft0 = (is_sink ? blk - nbc : blk - nbc - nbs) << 5;
+      const int flen = is_sink ? sink : res;
+      f4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        sA = mfma(as_h8(L.kA[kb]), qf[kb], sA);
+        sB = mfma(as_h8(L.kB[kb]), qf[kb], sB);
+      }
+      float sc[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = (sA[i] + row_ror<G>(sA[i])) * a.qscale;
+        sc[4 + i] = (sB[i] + row_ror<G>(sB[i])) * a.qscale;
+        if (ft0 + 4 * q4 + i >= flen) sc[i] = -INFINITY;
+        if (ft0 + 16 + 4 * q4 + i >= flen) sc[4 + i] = -INFINITY;
+      }
+      const float ones[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+      const half8 pb = softmax_pv(sc, ones, acc_o);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
+        u4 bv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bv[j] = __builtin_amdgcn_perm(L.v[2 * j + 1][nb >> 1], L.v[2 * j][nb >> 1], sel);
+        acc_o[nb] = mfma(as_h8(bv), pb, acc_o[nb]);
+      }
+    }
+    // park the original-space partial (hi + lo columns summed) in LDS with the
+    // running max it refers to; later blocks only rescale it at the combine
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float vo[8];
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) vo[nb] = acc_o[nb][i] + row_ror<G>(acc_o[nb][i]);
+      if (r < G) {
+        float* d = cm + r * 2 * FD + FD + 32 * q4 + 8 * i;
+        *reinterpret_cast<float4*>(d) = make_float4(vo[0], vo[1], vo[2], vo[3]);
+        *reinterpret_cast<float4*>(d + 4) = make_float4(vo[4], vo[5], vo[6], vo[7]);
+      }
+    }
+    m_orig = m_run;
+  }
+
+  // B operands of the rotated-space scores, step s: k-slots (q4, i) hold
+  // q[d], q[d+1], q[d], q[d+1], q[d+2], q[d+3], q[d+2], q[d+3], d = 32*q4 + 4*s,
+  // matching the key table entry layout (hi pair, lo pair) of two code bytes;
+  // column r reads the high part (even r / G) or the remainder of head r % G.
+  {
+    const uint8_t* src = smem + Layout::qop + (uint32_t)(hd * 2 + (partf != 0.f ? 1 : 0)) * 512 + (uint32_t)q4 * 128;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qop[s] = *reinterpret_cast<const half8*>(src + 16 * s);
+  }
+
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) acc_r[nb] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // ---- compressed blocks: two load slots, one block in flight
   {
     constexpr std::false_type full{};
     // loads stay unconditional (the wait counts need one issue order);
@@ -462,98 +579,23 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     if (npf < npk) packed_block(load_tail(npf), npf, std::true_type{});
   }
 
-  // ---- fp16 blocks of the sink and the residual ring (original space)
-  f4 acc_o[8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) acc_o[nb] = f4{0.f, 0.f, 0.f, 0.f};
-  const int fblk = blk0 + w + npk * FW;
-  if (fblk < blk1) {
-    // B operands in original space, step kb: k-slot (q4, i) = dim 32*q4 + 8*kb + i
-    half8 qf[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const float4 x0 = *reinterpret_cast<const float4*>(qsh + hd * FD + 32 * q4 + 8 * kb);
-      const float4 x1 = *reinterpret_cast<const float4*>(qsh + hd * FD + 32 * q4 + 8 * kb + 4);
-      half8 hi, lo;
-      split8(x0, x1, hi, lo);
-      qf[kb] = partf != 0.f ? lo : hi;
-    }
-    for (int blk = fblk; blk < blk1; blk += FW) {
-      const bool is_sink = blk < nbc + nbs;
-      const int ft0 = (is_sink ? blk - nbc : blk - nbc - nbs) << 5;
-      const int flen = is_sink ? sink : res;
-      const int64_t hs = is_sink ? a.sink_hs : a.res_hs;
-      const uint16_t* fk = static_cast<const uint16_t*>(is_sink ? a.sink_k : a.res_k) + (int64_t)row * hs;
-      const uint16_t* fv = static_cast<const uint16_t*>(is_sink ? a.sink_v : a.res_v) + (int64_t)row * hs;
-      auto slot = [&](int t) {
-        t = min(t, flen - 1);
-        return is_sink ? t : (rstart + t) % a.res_cap;
-      };
-      const u4* kA = reinterpret_cast<const u4*>(fk + (int64_t)slot(ft0 + r) * FD + 32 * q4);
-      const u4* kB = reinterpret_cast<const u4*>(fk + (int64_t)slot(ft0 + 16 + r) * FD + 32 * q4);
-      u4 vr[8];  // dims 8r .. 8r+7 of tokens A0..A3, B0..B3
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int t = ft0 + (i < 4 ? 4 * q4 + i : 16 + 4 * q4 + i - 4);
-        vr[i] = *reinterpret_cast<const u4*>(fv + (int64_t)slot(t) * FD + 8 * r);
-      }
-      f4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        sA = mfma(as_h8(kA[kb]), qf[kb], sA);
-        sB = mfma(as_h8(kB[kb]), qf[kb], sB);
-      }
-      float sc[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[i] = sA[i] + row_ror<G>(sA[i]);
-        sc[4 + i] = sB[i] + row_ror<G>(sB[i]);
-        if (ft0 + 4 * q4 + i >= flen) sc[i] = -INFINITY;
-        if (ft0 + 16 + 4 * q4 + i >= flen) sc[4 + i] = -INFINITY;
-      }
-      const float ones[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-      const half8 pb = softmax_pv(sc, ones, acc_o, acc_r, true);
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) {
-        const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
-        u4 bv;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bv[j] = __builtin_amdgcn_perm(vr[2 * j + 1][nb >> 1], vr[2 * j][nb >> 1], sel);
-        acc_o[nb] = mfma(as_h8(bv), pb, acc_o[nb]);
-      }
-    }
-  }
-
   // ---- combine the 8 waves of this workgroup through LDS (own region, one barrier).
   // Columns r and r + G hold the fp16 high part / remainder products of head r:
   // one DPP row rotation by G adds them; lanes r < G then hold head r.
   l_run = rows_sum(l_run);
-  const bool wave_has_fp16 = fblk < blk1;
   const bool wg_has_fp16 = blk1 > nbc;
-  float* cm = reinterpret_cast<float*>(smem + Layout::cmb) + (w * 8) * 2 * FD;  // [head][side][128]
-  float* cl = reinterpret_cast<float*>(smem + Layout::cml) + w * 16;             // [head][max, sum]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    float vr[8], vo[8];
+    float vr[8];
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      vr[nb] = acc_r[nb][i] + row_ror<G>(acc_r[nb][i]);
-      vo[nb] = wave_has_fp16 ? acc_o[nb][i] + row_ror<G>(acc_o[nb][i]) : 0.f;
-    }
+    for (int nb = 0; nb < 8; ++nb) vr[nb] = acc_r[nb][i] + row_ror<G>(acc_r[nb][i]);
     if (r < G) {
       float* d = cm + r * 2 * FD + 32 * q4 + 8 * i;
       *reinterpret_cast<float4*>(d) = make_float4(vr[0], vr[1], vr[2], vr[3]);
       *reinterpret_cast<float4*>(d + 4) = make_float4(vr[4], vr[5], vr[6], vr[7]);
-      if (wg_has_fp16) {
-        *reinterpret_cast<float4*>(d + FD) = make_float4(vo[0], vo[1], vo[2], vo[3]);
-        *reinterpret_cast<float4*>(d + FD + 4) = make_float4(vo[4], vo[5], vo[6], vo[7]);
-      }
     }
   }
-  if (lane < G) {
-    cl[2 * lane] = m_run;
-    cl[2 * lane + 1] = l_run;
-  }
+  if (lane < G) *reinterpret_cast<float4*>(cl + 4 * lane) = make_float4(m_run, l_run, m_orig, 0.f);
   __syncthreads();
   // thread (head, dim): merge the 8 waves, write the workgroup partial
   float* part = a.part + ((int64_t)row * a.nwg + c) * G * PS;
@@ -563,15 +605,17 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     const int h = e / FD, j = e % FD;
     float M = M_INIT;
 #pragma unroll
-    for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, cls[ww * 16 + 2 * h]);
+    for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, cls[ww * 32 + 4 * h]);
     float sr = 0.f, so = 0.f, L = 0.f;
 #pragma unroll
     for (int ww = 0; ww < FW; ++ww) {
-      const float sc = fexp2(cls[ww * 16 + 2 * h] - M);
+      const float4 st = *reinterpret_cast<const float4*>(cls + ww * 32 + 4 * h);
+      const float sc = fexp2(st.x - M);
       const float* src = cms + ((ww * 8 + h) * 2) * FD + j;
       sr = fmaf(sc, src[0], sr);
-      if (wg_has_fp16) so = fmaf(sc, src[FD], so);
-      L = fmaf(sc, cls[ww * 16 + 2 * h + 1], L);
+      // original-space part, parked at max st.z (absent: M_INIT, the LDS row is unwritten)
+      if (wg_has_fp16 && st.z > M_INIT) so = fmaf(fexp2(st.z - M), src[FD], so);
+      L = fmaf(sc, st.y, L);
     }
     part[h * PS + P_ROT + j] = sr;
     if (wg_has_fp16) part[h * PS + P_ORIG + j] = so;
@@ -611,6 +655,11 @@ __global__ __launch_bounds__(MT) void fast_merge_kernel(FastArgs a) {
   __shared__ __align__(16) float fin[FD];
   const int h = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
+  {  // one batch of scalar loads for the arguments (see the decode kernel)
+    const void* p0 = a.part; const void* p1 = a.rot; const void* p2 = a.out;
+    const int i0 = a.nwg, i1 = a.hkv, i2 = a.hq;
+    asm volatile("" ::"s"(p0), "s"(p1), "s"(p2), "s"(i0), "s"(i1), "s"(i2));
+  }
   const int row = b * a.hkv + g;
   const int np = a.nwg;
   const float* pb = a.part + (int64_t)row * np * G * PS + h * PS;  // partial p at pb + p * G * PS

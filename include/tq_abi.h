@@ -169,9 +169,9 @@ typedef struct tq_attn_desc {
  * the single-launch K4/V2 kernel applies. */
 #define TQ_ATTN_GENERAL 1
 
-/* Workspace: the first 256-byte-rounded (batch * hkv * 4) bytes hold ticket
- * counters that must be zero before the first call on a workspace; every
- * call leaves them zero. Calls sharing a workspace must not overlap. */
+/* Workspace: scratch for the per-workgroup partials of one call (no state is
+ * kept between calls, no initial contents are needed). Calls sharing a
+ * workspace must be ordered on one stream or must not overlap. */
 size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* desc);
 int tq_decode_attention(const tq_codec* kcodec, const tq_codec* vcodec,
                         const tq_attn_desc* desc, void* workspace,

@@ -380,11 +380,6 @@ static void launch_chunks(const AttnArgs& a, int G, dim3 grid, hipStream_t s) {
   }
 }
 
-// Tickets of the single-launch kernel live at the front of the workspace.
-static size_t counter_bytes(const tq_attn_desc* d) {
-  return (((size_t)d->batch * d->hkv * 4) + 255) & ~(size_t)255;
-}
-
 static int device_cus() {
   static int cus = 0;
   if (cus == 0) {
@@ -449,7 +444,7 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
   int nwg, bpw;
   fast_geometry(d, nwg, bpw);
   const size_t fast = (size_t)d->batch * d->hkv * nwg * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
-  const size_t bytes = counter_bytes(d) + (general > fast ? general : fast);
+  const size_t bytes = general > fast ? general : fast;
   return (bytes + 255) & ~(size_t)255;
 }
 
@@ -508,8 +503,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     f.hq = d->hq; f.hkv = d->hkv;
     f.qscale = d->scale * 1.4426950408889634f;
     f.rot = kc->rotation; f.rot16 = kc->rotation_f16; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
-    f.counter = static_cast<int*>(workspace);
-    f.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes(d));
+    f.part = static_cast<float*>(workspace);
     fast_geometry(d, f.nwg, f.bpw);
     if (launch_fast_decode(f, G, d->batch, s) != 0) TQ_LAUNCH_CHECK("tq_decode_attention (fast)");
     return TQ_OK;
@@ -540,7 +534,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   a.nch = a.nc + a.ns + a.nr;
   a.ps = part_stride(a.D, a.m);
   const size_t heads = (size_t)d->batch * d->hq;
-  float* ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes(d));
+  float* ws = static_cast<float*>(workspace);
   a.qr = ws;
   a.qs = a.qr + heads * a.D;
   a.sq = a.qs + heads * a.D;

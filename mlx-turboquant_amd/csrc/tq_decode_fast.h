@@ -27,8 +27,7 @@ struct FastArgs {
   const uint16_t* rot16; // (2, 128, 128) fp16 high part / remainder of R
   const float* kcen;     // 16 key centroids
   const float* vcen;     // 4 value centroids
-  float* part;           // partials
-  int* counter;          // (batch * hkv) tickets, zero between calls
+  float* part;           // per-workgroup partials (workspace)
   int nwg;               // workgroups per (sequence, kv head)
   int bpw;               // 32-token blocks per workgroup
 };

@@ -30,12 +30,12 @@ _workspaces: dict[tuple[str, int], torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per (device, stream) attention workspace. Zero-filled on allocation: its
-    leading ticket counters must start at zero and every call leaves them zero."""
+    """Per (device, stream) attention workspace: scratch for the partials of
+    one call, reused by every later call ordered on the same stream."""
     key = (str(device), _lib.stream_ptr(device))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 

@@ -12,6 +12,14 @@ replayed; inputs are resident in HBM.
 value = algorithmic bytes read per step / time per step (GB/s): packed codes +
 norms of every compressed token, the fp16 sink/residual tokens, q and out.
 
+roofline: the dominant kernel is the partials kernel of the single-launch
+K4/V2 path (fast_decode_kernel); its average duration is timed with events on
+the launch stream around graph replays of one partials-only call
+(TQ_ATTN_PARTIALS_ONLY) per layer, so its bytes stream from HBM as in the
+step (one layer's 28 MB would otherwise stay in the 256 MB last-level cache). traffic = HBM bytes per launch from rocprofv3
+FETCH_SIZE / WRITE_SIZE runs of `bench.py --pmc-workload`, scaled by the
+same counters on a copy of known size; read from the committed summary.
+
 Also reported: compress throughput on configs[2] (131072-token prefill drained
 in 4096-token chunks, K3/V2 and K3.5/V3.5), the roofline of the decode
 attention call, and a CPU baseline (float32 numpy restatement of the
@@ -32,6 +40,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "mlx-turboquant_amd")]
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fast_decode_kernel_k4v2_32k_traffic.md")
 METRIC = "fused decode-attn GB/s over packed KV (% HBM peak) + compress vectors/s"
 
 
@@ -126,7 +135,7 @@ def bench_compress(dev, kb, vb, total=131072, chunk=4096, reps=3):
             "vectors_per_s": n_vec / (ms * 1e-3), "GBps": n_vec * per_vec / (ms * 1e-3) / 1e9}
 
 
-def cpu_baseline(caches, qs, budget_s: float = 8.0):
+def cpu_baseline(caches, qs, budget_s: float = 12.0):
     """Reference per-step CPU work for one layer (concat + SDPA, float32
     numpy/OpenBLAS), repeated within a time budget, scaled to a 32-layer step."""
     import numpy as np
@@ -165,6 +174,72 @@ def cpu_baseline(caches, qs, budget_s: float = 8.0):
     return per_layer, threads, len(times), 65536 / t_c
 
 
+def call_partials_only(c, q, out):
+    """One attention call that launches only the partials kernel."""
+    import ctypes
+    import torch
+    from turboquant_amd import _lib
+    from turboquant_amd.cache import _workspace
+    lib = _lib.load()
+    qq = q[:, :, 0].contiguous()
+    desc = c.attention_descriptor(qq, out, q.shape[-1] ** -0.5)
+    desc.flags = _lib.TQ_ATTN_PARTIALS_ONLY
+    need = lib.tq_decode_workspace_bytes(c._kc.ref(), ctypes.byref(desc))
+    ws = _workspace(q.device, need)
+    _lib.check(lib.tq_decode_attention(c._kc.ref(), c._vc.ref(), ctypes.byref(desc), ws.data_ptr(), ws.numel(),
+                                       _lib.stream_ptr(q.device)), "tq_decode_attention")
+
+
+def time_partials_kernel(caches, qs, outs, reps: int, warmup: int):
+    """Average duration (ms) of one launch of the partials kernel under the
+    step's streaming conditions: a graph of one partials-only call per layer
+    (each layer's cache, so the step's bytes come from HBM as in the step),
+    replayed `reps` times between two events on the launch stream (torch's
+    current stream, which the library is handed)."""
+    import torch
+
+    def fn():
+        for c, q, o in zip(caches, qs, outs):
+            call_partials_only(c, q, o)
+
+    ms, _, _ = time_graph(fn, reps, warmup)
+    return ms / len(caches)
+
+
+def read_traffic():
+    """HBM bytes per launch of the partials kernel from the committed counter
+    summary (line 'traffic_bytes_per_launch: N'), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def pmc_workload(ctx: int):
+    """Short program for the counter runs: a copy of known size (the scale of
+    FETCH_SIZE / WRITE_SIZE), then 20 partials-kernel launches of layer 0."""
+    import torch
+    from turboquant_amd import _lib
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    caches, qs = build_decode(1, ctx, dev)
+    out = torch.empty(1, 32, 1, 128, dtype=torch.float32, device=dev)
+    for _ in range(20):
+        call_partials_only(caches[0], qs[0], out)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "partials_launches": 20,
+                      "algorithmic_bytes_per_launch": decode_bytes_per_layer(caches[0], 32)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -174,11 +249,16 @@ def main():
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compress", action="store_true")
+    ap.add_argument("--pmc-workload", action="store_true", help="short program for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.pmc_workload:
+        pmc_workload(args.ctx)
+        return
 
     import torch
     from turboquant_amd import _lib
@@ -198,10 +278,11 @@ def main():
 
     log("timing decode step")
     ms_step, wall_step, _ = time_graph(step, args.steps, args.warmup)
-    # one layer's call on its own (roofline of the attention call)
-    ms_layer, _, _ = time_graph(lambda: caches[0].attend(qs[0], out=outs[0]), max(200, args.steps * 10), 20)
+    # the partials kernel alone, one launch per layer per replay
+    ms_kernel = time_partials_kernel(caches, qs, outs, args.steps, args.warmup)
     gbps = bytes_step / (ms_step * 1e-3) / 1e9
-    ach = bytes_layer[0] / (ms_layer * 1e-3) / 1e9
+    ach = bytes_layer[0] / (ms_kernel * 1e-3) / 1e9
+    traffic = read_traffic()
 
     result = {
         "metric": METRIC,
@@ -214,7 +295,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16 MFMA (fp16 high part + remainder operands), f32 accumulate",
         "data": "synthetic (seeded N(0,1) keys x LogNormal(0,0.5) channel scale, N(0,1) values/queries)",
         "config": {"workload": "configs[1]: Llama-3.1-8B decode attention, T=32768 = 128 sink + 32512 K4/V2 "
                                "+ 128 residual, 32 layers, Hq=32 Hkv=8 D=128, per-layer fused attend in a HIP graph",
@@ -223,10 +304,13 @@ def main():
         "decode_steps_per_s": round(1e3 / ms_step, 2),
         "wall_ms_per_step": round(wall_step, 5),
         "bytes_per_step": bytes_step,
-        "roofline": {"kernel": "tq_decode_attention (one layer: q-rotate + chunk partials + combine)",
+        "roofline": {"kernel": "fast_decode_kernel<4> (partials of one layer: q rotation, packed K4/V2 + fp16 "
+                               "blocks, workgroup combine)",
                      "bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": bytes_layer[0], "avg_launch_us": round(ms_layer * 1e3, 3)},
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if traffic else None,
+                     "bytes_per_launch": bytes_layer[0], "avg_launch_us": round(ms_kernel * 1e3, 3),
+                     "whole_call_us": round(ms_step * 1e3 / len(caches), 3)},
     }
     if not args.no_compress:
         log("timing compress")

@@ -168,6 +168,10 @@ typedef struct tq_attn_desc {
 /* tq_attn_desc.flags: force the general kernel (every width / QJL) even where
  * the single-launch K4/V2 kernel applies. */
 #define TQ_ATTN_GENERAL 1
+/* Measurement only: on the single-launch K4/V2 path, launch the partials
+ * kernel and skip the merge (out is not written). Lets a caller time the
+ * dominant kernel alone with events on its stream; no reference counterpart. */
+#define TQ_ATTN_PARTIALS_ONLY 2
 
 /* Workspace: scratch for the per-workgroup partials of one call (no state is
  * kept between calls, no initial contents are needed). Calls sharing a

@@ -505,7 +505,8 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     f.rot = kc->rotation; f.rot16 = kc->rotation_f16; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
     f.part = static_cast<float*>(workspace);
     fast_geometry(d, f.nwg, f.bpw);
-    if (launch_fast_decode(f, G, d->batch, s) != 0) TQ_LAUNCH_CHECK("tq_decode_attention (fast)");
+    if (launch_fast_decode(f, G, d->batch, !(d->flags & TQ_ATTN_PARTIALS_ONLY), s) != 0)
+      TQ_LAUNCH_CHECK("tq_decode_attention (fast)");
     return TQ_OK;
   }
 

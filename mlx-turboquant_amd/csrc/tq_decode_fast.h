@@ -34,7 +34,7 @@ struct FastArgs {
 
 size_t fast_smem_bytes();
 int fast_set_attributes();
-int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s);
+int launch_fast_decode(const FastArgs& a, int G, int batch, bool merge, hipStream_t s);
 int fast_max_wg();
 
 constexpr int FAST_WAVES = 8;          // waves per workgroup of the decode kernel

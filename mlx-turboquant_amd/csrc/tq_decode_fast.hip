@@ -751,25 +751,18 @@ size_t fast_smem_bytes() { return Layout::total; }
 
 int fast_max_wg() { return MAXWG; }
 
-int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s) {
-  const dim3 grid(a.nwg, a.hkv, batch), mgrid(G, a.hkv, batch);
+template <int G>
+static void launch_pair(const FastArgs& a, int batch, bool merge, hipStream_t s) {
+  hipLaunchKernelGGL((fast_decode_kernel<G>), dim3(a.nwg, a.hkv, batch), dim3(FT), 0, s, a);
+  if (merge) hipLaunchKernelGGL((fast_merge_kernel<G>), dim3(G, a.hkv, batch), dim3(MT), 0, s, a);
+}
+
+int launch_fast_decode(const FastArgs& a, int G, int batch, bool merge, hipStream_t s) {
   switch (G) {
-    case 1:
-      hipLaunchKernelGGL((fast_decode_kernel<1>), grid, dim3(FT), 0, s, a);
-      hipLaunchKernelGGL((fast_merge_kernel<1>), mgrid, dim3(MT), 0, s, a);
-      break;
-    case 2:
-      hipLaunchKernelGGL((fast_decode_kernel<2>), grid, dim3(FT), 0, s, a);
-      hipLaunchKernelGGL((fast_merge_kernel<2>), mgrid, dim3(MT), 0, s, a);
-      break;
-    case 4:
-      hipLaunchKernelGGL((fast_decode_kernel<4>), grid, dim3(FT), 0, s, a);
-      hipLaunchKernelGGL((fast_merge_kernel<4>), mgrid, dim3(MT), 0, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((fast_decode_kernel<8>), grid, dim3(FT), 0, s, a);
-      hipLaunchKernelGGL((fast_merge_kernel<8>), mgrid, dim3(MT), 0, s, a);
-      break;
+    case 1: launch_pair<1>(a, batch, merge, s); break;
+    case 2: launch_pair<2>(a, batch, merge, s); break;
+    case 4: launch_pair<4>(a, batch, merge, s); break;
+    default: launch_pair<8>(a, batch, merge, s); break;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -65,6 +65,7 @@ class AttnDesc(ctypes.Structure):
                 ("res_start", _p), ("res_len", _p), ("flags", _i32), ("reserved2", _i32)]
 
 TQ_ATTN_GENERAL = 1
+TQ_ATTN_PARTIALS_ONLY = 2
 
 
 _PC = ctypes.POINTER(Codec)

@@ -66,12 +66,27 @@ class DeviceCodec:
 _codecs: dict[tuple, DeviceCodec] = {}
 
 
+_supported: dict[str, bool] = {}
+
+
+def _require_gfx950(dev: torch.device) -> None:
+    """The library holds gfx950 code objects only; refuse other devices."""
+    if dev.type != "cuda":
+        raise RuntimeError("turboquant_amd runs on the GPU only; got device " + str(dev))
+    if str(dev) not in _supported:
+        with torch.cuda.device(dev):
+            _supported[str(dev)] = bool(_lib.load().tq_device_supported())
+    if not _supported[str(dev)]:
+        raise RuntimeError(f"turboquant_amd: {dev} is not a gfx950 (MI355X) device")
+
+
 def get_codec(d: int, bits: float, seed: int, qjl_m: int, device) -> DeviceCodec:
     dev = torch.device(device)
     if dev.type == "cuda" and dev.index is None:
         dev = torch.device("cuda", torch.cuda.current_device())
     key = (d, float(bits), seed, qjl_m, str(dev))
     if key not in _codecs:
+        _require_gfx950(dev)
         _codecs[key] = DeviceCodec(d, bits, seed, qjl_m, dev)
     return _codecs[key]
 

@@ -48,6 +48,7 @@ def cpu_cache(monkeypatch):
     monkeypatch.setattr(_codec, "compress_into", fake_compress)
     monkeypatch.setattr(_codec, "dequantize_into", fake_dequant)
     monkeypatch.setattr(_lib, "require_device", lambda t: None)
+    monkeypatch.setattr(_codec, "_require_gfx950", lambda dev: None)
     return cache_mod.TurboQuantKVCache
 
 

@@ -113,6 +113,12 @@ int tq_device_supported(void);
 int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x_head_stride,
                 const tq_span* span, const tq_store* dst, void* stream);
 
+/* Testing aid, no reference counterpart: route every tq_compress call of the
+ * process through the general (VALU) kernel (on != 0) instead of the MFMA
+ * kernel that fp16 / head_dim 128 / no-QJL calls use, so tests can compare the
+ * two. Not thread-safe; default 0. */
+void tq_compress_force_general(int32_t on);
+
 /* Dequantize: out = n * (c[idx] @ R) (+ QJL correction when apply_qjl and
  * the store holds a sketch), float32, element (r, t, i) at
  * out[r*out_head_stride + t*d + i].

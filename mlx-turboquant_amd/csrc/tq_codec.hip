@@ -2,8 +2,9 @@
 // -> quantize -> pack [-> QJL sketch]), dequantize, bit packing utilities.
 //
 // Numeric contract (matches the CPU restatement used by the tests):
-//   n   = f32(sqrt(sum_j x_j^2)) with the sum taken in float64 in index order
-//         (mlx_turboquant/cache.py:235-236 computes mx.linalg.norm of the f32 cast);
+//   n   = f32(sqrt(S)), S the float64 sum of squares in 32-dim blocks (each
+//         summed sequentially) combined pairwise (sumsq_blocks in tq_codec.h;
+//         mlx_turboquant/cache.py:235-236 computes mx.linalg.norm of the f32 cast);
 //   x_n = f32(x) / max(n, 1e-10f), IEEE float32 division (cache.py:237-238);
 //   y_j = sum_i x_n[i] * R[j][i] accumulated in float32 (rotation.py:65);
 //   idx = #{k : y > b_k} (codebook.py:220-223);
@@ -14,10 +15,12 @@
 #include <cstring>
 
 #include "tq_common.h"
+#include "tq_codec.h"
 
 namespace tq {
 
 static thread_local char g_err[512] = "";
+static bool g_force_general = false;  // tq_compress_force_general(1): tests cross-check the two kernels
 
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
@@ -60,31 +63,6 @@ struct Geo {
   static constexpr int MROW = NSEG * SEGP;     // padded matrix row
   static constexpr int TI = 32;                // matrix rows per LDS tile
 };
-
-struct CompressArgs {
-  const void* x;
-  int x_dtype;
-  int64_t x_hs;
-  tq_span span;
-  tq_store dst;
-  const float* rot;
-  const float* bnd_hi;
-  const float* bnd_lo;
-  const float* cen_hi;
-  const float* cen_lo;
-  const float* proj;
-  int bits_hi, bits_lo, split, qjl_m;
-  int row_hi, row_lo, row_sign;
-};
-
-template <int BITS>
-__device__ inline void store_codes(uint8_t* dst, const uint32_t (&code)[32]) {
-  uint32_t w[BITS];
-  pack32<BITS>(code, w);
-  uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
-#pragma unroll
-  for (int i = 0; i < BITS; ++i) d32[i] = w[i];
-}
 
 __device__ inline void store_codes_dyn(int bits, uint8_t* dst, const uint32_t (&code)[32]) {
   switch (bits) {
@@ -187,15 +165,9 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
   }
   __syncthreads();
 
-  // Norm: float64 sum of squares in index order, rounded square root.
+  // Norm: float64 sum of squares in the library's block order, rounded square root.
   if (tid < G::VPW) {
-    double s = 0.0;
-    const float* row = xs + tid * G::XS;
-    for (int i = 0; i < D; ++i) {
-      const double xi = (double)row[i];
-      s = fma(xi, xi, s);
-    }
-    const float n = (float)sqrt(s);
+    const float n = (float)sqrt(sumsq_blocks<D>(xs + tid * G::XS));
     nrm[tid] = n;
     if (tid < nv) a.dst.norms[(int64_t)r * a.dst.norm_head_stride + dst0 + tid] = n;
   }
@@ -472,6 +444,8 @@ extern "C" {
 
 int tq_abi_version(void) { return TQ_ABI_VERSION; }
 
+void tq_compress_force_general(int32_t on) { tq::g_force_general = on != 0; }
+
 const char* tq_last_error(void) { return tq::g_err; }
 
 int tq_device_supported(void) {
@@ -520,6 +494,11 @@ int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x
   a.row_lo = row_bytes(codec->d - codec->split, a.bits_lo);
   a.row_sign = a.qjl_m / 8;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // fp16, head_dim 128, no QJL sketch: the MFMA kernel (tq_compress_fast.hip)
+  if (codec->d == 128 && !g_force_general && launch_compress_fast(a, s)) {
+    TQ_LAUNCH_CHECK("tq_compress");
+    return TQ_OK;
+  }
   switch (codec->d) {
     case 64: {
       dim3 g((span->n_tok + Geo<64>::VPW - 1) / Geo<64>::VPW, span->rows);

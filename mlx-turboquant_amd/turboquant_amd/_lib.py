@@ -79,6 +79,7 @@ SIGNATURES = {
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_device_supported": (_i32, []),
     "tq_compress": (_i32, [_PC, _p, _i32, _i64, _PSp, _PS, _p]),
+    "tq_compress_force_general": (None, [_i32]),
     "tq_dequantize": (_i32, [_PC, _PS, _PSp, _p, _i64, _i32, _p]),
     "tq_pack_codes": (_i32, [_p, _i64, _i32, _i32, _p, _p]),
     "tq_unpack_codes": (_i32, [_p, _i64, _i32, _i32, _p, _p]),

@@ -5,9 +5,14 @@ imports this module.
 
 Numeric contract (what "bit-exact" is measured against):
 
-* norms: ``n = f32(sqrt(S))`` where ``S`` is the float64 sum of squares taken in
-  index order j = 0..d-1 (squares of fp16/fp32 inputs are exact in float64),
-  restating ``mx.linalg.norm`` of the float32 cast (cache.py:235-236).
+* norms: ``n = f32(sqrt(S))`` where ``S`` is the float64 sum of squares in a
+  fixed order: dims in blocks of 32, each block summed sequentially from 0.0,
+  block sums combined pairwise level by level in index order ((B0+B1)+(B2+B3)
+  for d = 128; an odd block at a level carries up unchanged). Squares of
+  fp16/fp32 inputs are exact in float64. This restates ``mx.linalg.norm`` of
+  the float32 cast (cache.py:235-236) with an order every kernel can follow;
+  any float64 order gives the correctly rounded float32 norm except within
+  ~2^-29 of a float32 rounding tie (``test_norms_correctly_rounded``).
 * normalised input: ``x_n = f32(x) / max(n, f32(1e-10))`` with IEEE float32
   division (cache.py:237-238).
 * rotated coordinate: ``y = x_n @ R.T`` (rotation.py:65) evaluated in float64
@@ -40,7 +45,7 @@ NORM_EPS = np.float32(1e-10)  # cache.py:237
 __all__ = [
     "CODEBOOK_DIR", "rotation_matrix", "projection_matrix", "codebook",
     "quantize_scalar", "dequantize_scalar", "pack_bits", "unpack_bits",
-    "vector_norms", "normalize", "rotate_f64", "split_bits", "compress",
+    "sumsq_f64", "vector_norms", "normalize", "rotate_f64", "split_bits", "compress",
     "CompressResult", "dequantize", "boundary_margin", "near_boundary_mask",
     "qjl_sketch", "qjl_correction", "attention", "detect_outlier_layers",
     "CacheOracle", "compress_f32", "reference_decode_step_f32",
@@ -134,20 +139,35 @@ def unpack_bits(packed: np.ndarray, bits: int, d: int) -> np.ndarray:
 # --------------------------------------------------------------------------
 # a8: norm / normalise / rotate
 # --------------------------------------------------------------------------
-def vector_norms(x: np.ndarray) -> np.ndarray:
-    """L2 norm over the last axis (cache.py:235-236), float32 result.
-
-    Sum of squares in float64 in index order, then a float64 square root
-    rounded to float32 (equal to the correctly rounded float32 square root of
-    the float64 sum, since 53 >= 2*24 + 2).
-    """
+def sumsq_f64(x: np.ndarray) -> np.ndarray:
+    """float64 sum of squares over the last axis in the norm order of the
+    module docstring: 32-dim blocks summed sequentially from 0.0, block sums
+    combined pairwise level by level (an odd block carries up)."""
     x = np.asarray(x)
     d = x.shape[-1]
     xf = x.reshape(-1, d).astype(np.float64)
-    acc = np.zeros(xf.shape[0], dtype=np.float64)
-    for j in range(d):
-        acc = acc + xf[:, j] * xf[:, j]
-    return np.sqrt(acc).astype(np.float32).reshape(x.shape[:-1])
+    blocks = []
+    for b0 in range(0, d, 32):
+        acc = np.zeros(xf.shape[0], dtype=np.float64)
+        for j in range(b0, min(b0 + 32, d)):
+            acc = acc + xf[:, j] * xf[:, j]
+        blocks.append(acc)
+    while len(blocks) > 1:
+        nxt = [blocks[i] + blocks[i + 1] for i in range(0, len(blocks) - 1, 2)]
+        if len(blocks) % 2:
+            nxt.append(blocks[-1])
+        blocks = nxt
+    return blocks[0].reshape(x.shape[:-1])
+
+
+def vector_norms(x: np.ndarray) -> np.ndarray:
+    """L2 norm over the last axis (cache.py:235-236), float32 result.
+
+    ``sqrt(sumsq_f64(x))`` in float64 rounded to float32 (equal to the
+    correctly rounded float32 square root of the float64 sum, since
+    53 >= 2*24 + 2).
+    """
+    return np.sqrt(sumsq_f64(x)).astype(np.float32)
 
 
 def normalize(x: np.ndarray, norms: np.ndarray) -> np.ndarray:

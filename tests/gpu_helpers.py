@@ -41,13 +41,15 @@ def unpack_codes(codes_hi, codes_lo, bits: float, d: int) -> np.ndarray:
     return idx
 
 
-def code_parity(x: np.ndarray, bits: float, gpu=None):
-    """Compare GPU codes/norms with the oracle.
+def code_parity(x: np.ndarray, bits: float, gpu=None, ref=None):
+    """Compare GPU codes/norms with the oracle (``ref``: a precomputed
+    ``O.compress`` result of the same input).
 
-    Returns (n_mismatch, n_outside_band, n_within_1ulp, total, norms_equal)."""
+    Returns (n_mismatch, n_outside_band, n_within_1ulp, total, norms_equal, ref)."""
     D = x.shape[-1]
     R = O.rotation_matrix(D)
-    ref = O.compress(x, R, bits)
+    if ref is None:
+        ref = O.compress(x, R, bits)
     ch, cl, nrm, _, _ = gpu if gpu is not None else gpu_compress(x, bits)
     idx = unpack_codes(ch, cl, bits, D)
     mism = idx != ref.idx

@@ -179,6 +179,27 @@ def test_norms_correctly_rounded():
         assert n[i] == np.float32(exact)
 
 
+def test_sumsq_order_blocks_then_pairs():
+    """The float64 sum follows 32-dim sequential blocks combined pairwise:
+    2^30 in block 0 absorbs each 2^-24 of block 1 added one by one (below
+    half an ulp), but not their block sum 2^-19; index order would give 2^30."""
+    x = np.zeros((1, 128), np.float16)
+    x[0, 0] = 2.0 ** 15
+    x[0, 32:64] = 2.0 ** -12
+    assert O.sumsq_f64(x)[0] == 2.0 ** 30 + 2.0 ** -19
+    # block 2 and 3 join block 0+1 only at the second level
+    y = np.zeros((1, 128), np.float16)
+    y[0, 64] = 2.0 ** 15
+    y[0, 0:32] = 2.0 ** -12
+    y[0, 96:128] = 2.0 ** -12
+    assert O.sumsq_f64(y)[0] == 2.0 ** 30 + 2.0 ** -18
+    # d = 96: the odd third block carries up: (B0 + B1) + B2
+    z = np.zeros((1, 96), np.float16)
+    z[0, 0] = 2.0 ** 15
+    z[0, 64:96] = 2.0 ** -12
+    assert O.sumsq_f64(z)[0] == 2.0 ** 30 + 2.0 ** -19
+
+
 def test_compress_roundtrip_quality_and_mse_bound():
     rng = np.random.RandomState(2)
     x = rng.randn(2000, 128).astype(np.float32)

@@ -1,4 +1,5 @@
-// MFMA compress for TurboQuant on gfx950: fp16 vectors of head_dim 128 ->
+// MFMA compress for TurboQuant on gfx950: fp16 vectors of head_dim 128 at 2-4
+// bits (integer, or fractional with split d/2) ->
 // norm, rotation, quantization and bit packing in one persistent kernel
 // (replaces TurboQuantKVCache._quantize_kv / _quantize_kv_fractional,
 // mlx_turboquant/cache.py:232-274, for fp16 inputs without a QJL sketch).
@@ -12,20 +13,27 @@
 // dot-product band within which the reference's own GEMM does not fix a code.
 //
 // Work split: a workgroup of 4 waves walks tiles of 64 vectors of one (batch,
-// head) row. Wave w owns rotated dims [32w, 32w+32) and keeps its rows of 256R
-// as MFMA A operands in registers for the whole launch. Per tile:
-//   1. the x tile (16 KB, loaded one tile ahead) is stored to LDS;
+// head) row, with the x tiles of the next two tiles in flight. Wave w owns
+// rotated dims [32w, 32w+32) and keeps its rows of 256R as MFMA A operands in
+// registers for the whole launch. Per tile:
+//   1. the x tile (16 KB) is stored to LDS;
 //   2. each thread sums the squares of 32 dims of one vector in float64 and
 //      lanes 4v..4v+3 combine them pairwise (the library's norm order);
-//   3. each wave multiplies its A operands by the tile (B = x^T read from LDS):
-//      D[m][n] = rotated dim 32w + 16*n2 + m of vector n; lane (n = l & 15,
-//      g = l >> 4) holds dims 32w + 16*n2 + 4g + e, e = 0..3;
-//   4. coordinates are scaled, quantized (count of boundaries below, ties low,
-//      NaN -> 0; codebook.py:220-223) and written as code bytes to LDS;
-//   5. each thread packs 32 codes of one vector into BITS dwords (LSB-first
-//      bitstream, packing.py) and stores them.
+//   3. each wave multiplies its A operands by the tile (B = x^T read from LDS).
+//      A row r of output block n2 is rotated dim 32w + 8(r >> 2) + 4*n2 + (r & 3),
+//      so lane (vector n = l & 15, g = l >> 4) ends up holding the 8
+//      consecutive dims 32w + 8g .. 32w + 8g + 7 of vector n;
+//   4. coordinates are scaled and quantized (count of boundaries below, ties
+//      low, NaN -> 0; codebook.py:220-223) through a 64-cell table (cell
+//      width 1/64; with at most one boundary per cell, code = base +
+//      (y > boundary); a codebook that puts two boundaries in one cell is
+//      counted instead);
+//   5. the lane's 8 codes form 8*BITS consecutive bits of the LSB-first row
+//      bitstream (packing.py); lanes assemble whole dwords and store them.
 
 #include <math.h>
+
+#include <type_traits>
 
 #include "tq_codec.h"
 
@@ -40,16 +48,27 @@ constexpr int CD = 128;        // head_dim
 constexpr int CT = 64;         // vectors per tile
 constexpr int CTHR = 256;      // threads per workgroup (4 waves)
 constexpr int XS = 272;        // LDS row stride of the x tile, bytes (256 + 16: conflict-free b128 reads)
-constexpr int CS = 144;        // LDS row stride of the code tile, bytes
 constexpr float RSC = 256.f;   // scale of R before the fp16 split
+constexpr int NCELL = 64;      // quantizer cells: c = round(64 y + 32) clamped to [0, 63]
+constexpr float MAGIC = 12582912.f;  // 1.5 * 2^23: fma(y, 64, 32 + MAGIC) holds round(64 y + 32) in its low bits
+constexpr uint32_t MAGIC_BITS = 0x4B400000u;
 
 constexpr uint32_t L_X0 = 0;
 constexpr uint32_t L_X1 = CT * XS;
-constexpr uint32_t L_CODES = 2 * CT * XS;
-constexpr uint32_t L_SCALE = L_CODES + CT * CS;
-constexpr uint32_t L_TOTAL = L_SCALE + CT * 4;
+constexpr uint32_t L_SCALE = 2 * CT * XS;
+constexpr uint32_t L_QT = L_SCALE + 2 * CT * 4;     // [2 codebooks][NCELL] {boundary, base}
+constexpr uint32_t L_BND = L_QT + 2 * NCELL * 8;    // [2 codebooks][16] boundaries
+constexpr uint32_t L_FLAG = L_BND + 2 * 16 * 4;
+constexpr uint32_t L_TOTAL = L_FLAG + 16;
 
 __device__ inline half8 as_h8(u4 v) { return __builtin_bit_cast(half8, v); }
+
+// p[i] through the constant address space: the per-batch span arrays are
+// read-only while the kernel runs, so uniform reads become scalar loads (and
+// never wait on the vector-memory counter that tracks the prefetched tiles)
+__device__ inline int ld_span(const int32_t* p, int i) {
+  return ((const __attribute__((address_space(4))) int32_t*)(p))[i];
+}
 
 struct Tile {
   int id;          // tile index; >= total: none left
@@ -58,12 +77,18 @@ struct Tile {
   int src0, dst0;  // first source / destination token of the tile
 };
 
-template <int NB>
-__device__ inline uint32_t quant(float y, const float (&b)[NB]) {
-  uint32_t idx = 0;
-#pragma unroll
-  for (int k = 0; k < NB; ++k) idx += y > b[k] ? 1u : 0u;
-  return idx;
+struct QCell {
+  float bnd;      // the one boundary that can fall inside the cell, or +inf
+  uint32_t base;  // boundaries below every value of the cell
+};
+
+// code of a finite y from the cell table `tbl` (LDS); non-finite y only occur
+// in vectors with a non-finite norm, whose codes are set to 0 by the caller
+__device__ inline uint32_t quant_table(float y, const uint8_t* tbl) {
+  const int r = (int)__float_as_uint(fmaf(y, 64.f, 32.f + MAGIC));
+  const int c = min(max(r, (int)MAGIC_BITS), (int)MAGIC_BITS + NCELL - 1) - (int)MAGIC_BITS;
+  const QCell q = *reinterpret_cast<const QCell*>(tbl + 8 * c);
+  return q.base + (y > q.bnd ? 1u : 0u);
 }
 
 template <int BH, int BL>
@@ -73,14 +98,46 @@ __global__ __launch_bounds__(CTHR) void compress_fast_kernel(CompressArgs a, int
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m = lane & 15, g = lane >> 4;
   const bool whi = 32 * w < a.split;  // this wave's dims use the high-width codebook
+  constexpr int NBH = (1 << BH) - 1, NBL = (1 << BL) - 1;
 
-  // A operands: rows 32w + 16*n2 + m of 256R, k-slots 32*kb + 8*g + e
+  // quantizer tables of both codebooks; the flag records a cell holding two
+  // boundaries (then every code is counted instead)
+  uint32_t* flag = reinterpret_cast<uint32_t*>(smem + L_FLAG);
+  if (tid == 0) *flag = 0u;
+  __syncthreads();
+  if (tid < 32) {  // boundaries for the counting fallback: [hi 16][lo 16]
+    const int cb = tid >> 4, k = tid & 15;
+    reinterpret_cast<float*>(smem + L_BND)[tid] = k < (cb ? NBL : NBH) ? (cb ? a.bnd_lo : a.bnd_hi)[k] : 0.f;
+  }
+  if (tid < 2 * NCELL) {
+    const int cb = tid / NCELL, c = tid % NCELL;
+    const float* bp = cb ? a.bnd_lo : a.bnd_hi;
+    const int nb = cb ? NBL : NBH;
+    const float eps = 0x1p-20f;  // > the rounding of the cell index near a cell edge, in y units
+    const float lo = c == 0 ? -INFINITY : ((float)c - 32.5f) * (1.f / 64.f) - eps;
+    const float hi = c == NCELL - 1 ? INFINITY : ((float)c - 31.5f) * (1.f / 64.f) + eps;
+    uint32_t base = 0, amb = 0;
+    float bnd = INFINITY;
+    for (int k = 0; k < nb; ++k) {
+      const float b = bp[k];
+      if (b < lo) ++base;
+      else if (b <= hi) { ++amb; bnd = b; }
+    }
+    QCell* q = reinterpret_cast<QCell*>(smem + L_QT) + cb * NCELL + c;
+    q->bnd = bnd;
+    q->base = base;
+    if (amb > 1) atomicOr(flag, 1u);
+  }
+
+  // A operands: output row r of block n2 = rotated dim 32w + 8(r >> 2) + 4*n2 + (r & 3)
+  // of 256R, k-slots 32*kb + 8*g + e
   half8 ah[2][4], al[2][4];
 #pragma unroll
   for (int n2 = 0; n2 < 2; ++n2)
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const float* src = a.rot + (32 * w + 16 * n2 + m) * CD + 32 * kb + 8 * g;
+      const int j = 32 * w + 8 * (m >> 2) + 4 * n2 + (m & 3);
+      const float* src = a.rot + j * CD + 32 * kb + 8 * g;
       const float4 f0 = *reinterpret_cast<const float4*>(src);
       const float4 f1 = *reinterpret_cast<const float4*>(src + 4);
       const float f[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
@@ -92,12 +149,9 @@ __global__ __launch_bounds__(CTHR) void compress_fast_kernel(CompressArgs a, int
         al[n2][kb][e] = (_Float16)(v - (float)h);
       }
     }
-  constexpr int NBH = (1 << BH) - 1, NBL = (1 << BL) - 1;
-  float bh[NBH], bl[NBL];
-#pragma unroll
-  for (int k = 0; k < NBH; ++k) bh[k] = a.bnd_hi[k];
-#pragma unroll
-  for (int k = 0; k < NBL; ++k) bl[k] = a.bnd_lo[k];
+  __syncthreads();
+  const bool table = *flag == 0u;
+  const uint8_t* qtab = smem + L_QT + (whi ? 0 : NCELL * 8);
 
   // next non-empty tile at or after `id` in this workgroup's sequence
   auto make_tile = [&](int id) {
@@ -105,14 +159,14 @@ __global__ __launch_bounds__(CTHR) void compress_fast_kernel(CompressArgs a, int
     t.id = id;
     t.row = t.nv = t.src0 = t.dst0 = 0;
     for (; t.id < total; t.id += gridDim.x) {
-      t.row = t.id / tiles_per_row;
+      t.row = __builtin_amdgcn_readfirstlane(t.id / tiles_per_row);  // uniform: scalar loads below
       const int t0 = (t.id - t.row * tiles_per_row) * CT;
-      const int b = t.row / a.span.heads;
-      const int n = a.span.n_tok_b ? a.span.n_tok_b[b] : a.span.n_tok;
+      const int b = __builtin_amdgcn_readfirstlane(t.row / a.span.heads);
+      const int n = a.span.n_tok_b ? ld_span(a.span.n_tok_b, b) : a.span.n_tok;
       t.nv = min(CT, n - t0);
       if (t.nv > 0) {
-        t.src0 = (a.span.src_tok0_b ? a.span.src_tok0_b[b] : 0) + t0;
-        t.dst0 = (a.span.dst_tok0_b ? a.span.dst_tok0_b[b] : 0) + t0;
+        t.src0 = (a.span.src_tok0_b ? ld_span(a.span.src_tok0_b, b) : 0) + t0;
+        t.dst0 = (a.span.dst_tok0_b ? ld_span(a.span.dst_tok0_b, b) : 0) + t0;
         break;
       }
     }
@@ -121,8 +175,7 @@ __global__ __launch_bounds__(CTHR) void compress_fast_kernel(CompressArgs a, int
 
   // x tile: 1024 chunks of 16 bytes, chunk c = vector c >> 4, bytes 16*(c & 15);
   // vectors past the tile's end re-read its last vector (results not stored)
-  u4 xr[4];
-  auto load_x = [&](const Tile& t) {
+  auto load_x = [&](u4 (&xr)[4], const Tile& t) {
     const uint8_t* base = static_cast<const uint8_t*>(a.x) + ((int64_t)t.row * a.x_hs + (int64_t)t.src0 * CD) * 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -132,54 +185,54 @@ __global__ __launch_bounds__(CTHR) void compress_fast_kernel(CompressArgs a, int
     }
   };
 
-  Tile cur = make_tile(blockIdx.x);
-  if (cur.id >= total) return;
-  load_x(cur);
-  uint32_t xoff = L_X0;
-  float* scl = reinterpret_cast<float*>(smem + L_SCALE);
-  while (true) {
-    uint8_t* xb = smem + xoff;
+  const int split_w = a.split / 32;  // waves whose dims use the high-width codebook
+
+  // x registers -> LDS tile at xoff
+  auto write_x = [&](const u4 (&xr)[4], uint32_t xoff) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + CTHR * i;
-      *reinterpret_cast<u4*>(xb + (c >> 4) * XS + (c & 15) * 16) = xr[i];
+      *reinterpret_cast<u4*>(smem + xoff + (c >> 4) * XS + (c & 15) * 16) = xr[i];
     }
-    const Tile nxt = make_tile(cur.id + gridDim.x);
-    if (nxt.id < total) load_x(nxt);
-    __syncthreads();
+  };
 
-    // norms: thread (v, quarter p) sums dims [32p, 32p+32) in order; lanes
-    // combine (Q0 + Q1) + (Q2 + Q3)
-    {
-      const int v = tid >> 2, p = tid & 3;
-      const uint8_t* rp = xb + v * XS + 64 * p;
-      double s = 0.0;
+  // Norms of the tile at xoff: thread (v, quarter p) sums dims [32p, 32p+32)
+  // in order; lanes combine (Q0 + Q1) + (Q2 + Q3). The four lanes of a vector
+  // hold the same value and all store it (lanes past the tile's end store the
+  // last vector's norm: their inputs are copies of it). The per-vector scale
+  // 1 / (256 max(n, 1e-10)) goes to LDS at scl; 0 marks a non-finite norm.
+  auto norms = [&](uint32_t xoff, const Tile& t, float* scl) {
+    const int v = tid >> 2, p = tid & 3;
+    const uint8_t* rp = smem + xoff + v * XS + 64 * p;
+    double s = 0.0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const half8 h = as_h8(*reinterpret_cast<const u4*>(rp + 16 * i));
+    for (int i = 0; i < 4; ++i) {
+      const half8 h = as_h8(*reinterpret_cast<const u4*>(rp + 16 * i));
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const double xv = (double)(float)h[e];
-          s = fma(xv, xv, s);
-        }
-      }
-      s += __shfl_xor(s, 1);
-      s += __shfl_xor(s, 2);
-      if (p == 0) {
-        const float n = (float)sqrt(s);
-        if (v < cur.nv) a.dst.norms[(int64_t)cur.row * a.dst.norm_head_stride + cur.dst0 + v] = n;
-        scl[v] = 1.f / (RSC * fmaxf(n, 1e-10f));
+      for (int e = 0; e < 8; ++e) {
+        const double xv = (double)(float)h[e];
+        s = fma(xv, xv, s);
       }
     }
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    const float n = (float)sqrt(s);
+    a.dst.norms[(int64_t)t.row * a.dst.norm_head_stride + t.dst0 + min(v, t.nv - 1)] = n;
+    scl[v] = __builtin_isfinite(n) ? 1.f / (RSC * fmaxf(n, 1e-10f)) : 0.f;
+  };
 
-    // rotation: z^T tiles of 16 dims x 16 vectors
-    f4 acc[4][2];
+  // rotation of the tile at xoff: z^T blocks of 16 dims x 16 vectors
+  struct Acc {
+    f4 v[4][2];
+  };
+  auto rotate = [&](uint32_t xoff) {
+    Acc r;
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
       half8 bx[4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
-        bx[kb] = as_h8(*reinterpret_cast<const u4*>(xb + (16 * s4 + m) * XS + 64 * kb + 16 * g));
+        bx[kb] = as_h8(*reinterpret_cast<const u4*>(smem + xoff + (16 * s4 + m) * XS + 64 * kb + 16 * g));
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) {
         f4 c = {0.f, 0.f, 0.f, 0.f};
@@ -188,59 +241,119 @@ __global__ __launch_bounds__(CTHR) void compress_fast_kernel(CompressArgs a, int
           c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[n2][kb], bx[kb], c, 0, 0, 0);
           c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[n2][kb], bx[kb], c, 0, 0, 0);
         }
-        acc[s4][n2] = c;
+        r.v[s4][n2] = c;
       }
     }
-    __syncthreads();  // scales of every vector are in LDS
+    return r;
+  };
 
-    // quantize: 4 codes (dims 32w + 16*n2 + 4g + e) per word, as bytes
+  // Quantize the lane's 8 consecutive dims of each sub-tile, pack, store.
+  // The wave's 32 codes of vector v are B dwords at byte 4*B*wl of its row;
+  // lane g holds bits [8Bg, 8Bg + 8B) of them. Lanes past the tile's end write
+  // the last vector's row (their inputs are copies of it).
+  const int B = whi ? BH : BL;  // wave-uniform
+  uint8_t* const codes = whi ? a.dst.codes_hi : a.dst.codes_lo;
+  const int64_t head_stride = whi ? a.dst.hi_head_stride : a.dst.lo_head_stride;
+  const int row_bytes = whi ? a.row_hi : a.row_lo;
+  const int wl = whi ? w : w - split_w;
+  const float* bnd_l = reinterpret_cast<const float*>(smem + L_BND) + (whi ? 0 : 16);
+  const int nbnd = (1 << B) - 1;
+  auto quant_store = [&](auto table_tag, const Acc& acc, const Tile& t, const float* scl) {
+    constexpr bool TABLE = decltype(table_tag)::value;
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-      const float sc = scl[16 * s4 + m];
+      const int v = 16 * s4 + m;
+      const float sc = scl[v];
+      uint32_t V = 0;  // codes of dims 32w + 8g + k at bits B*k
 #pragma unroll
-      for (int n2 = 0; n2 < 2; ++n2) {
-        uint32_t word = 0;
+      for (int n2 = 0; n2 < 2; ++n2)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float y = acc[s4][n2][e] * sc;
+          const float y = acc.v[s4][n2][e] * sc;
           uint32_t c;
-          if constexpr (BH == BL) c = quant(y, bh);
-          else c = whi ? quant(y, bh) : quant(y, bl);
-          word |= c << (8 * e);
+          if constexpr (TABLE) {
+            c = quant_table(y, qtab);
+          } else {
+            c = 0;
+            for (int k = 0; k < nbnd; ++k) c += y > bnd_l[k] ? 1u : 0u;
+          }
+          V |= c << (B * (4 * n2 + e));
         }
-        *reinterpret_cast<uint32_t*>(smem + L_CODES + (16 * s4 + m) * CS + 32 * w + 16 * n2 + 4 * g) = word;
+      if (sc == 0.f) V = 0u;  // non-finite norm: every coordinate is NaN -> code 0
+      uint32_t* rowp = reinterpret_cast<uint32_t*>(codes + (int64_t)t.row * head_stride +
+                                                   (int64_t)(t.dst0 + min(v, t.nv - 1)) * row_bytes + 4 * B * wl);
+      if constexpr (BH == BL && BH == 4) {
+        rowp[g] = V;
+      } else if constexpr (BH == BL && BH == 2) {
+        // lanes g = 2k, 2k + 1 both store dword k
+        const auto pr = __builtin_amdgcn_permlane16_swap(V, V, false, false);
+        rowp[g >> 1] = pr[0] | (pr[1] << 16);
+      } else {
+        // dword k = min(g, B - 1) holds bits of lanes la = 4k / B and la + 1
+        // (a lane past the last dword repeats it)
+        const int k = min(g, B - 1);
+        const int la = (4 * k) / B;
+        const int off = 32 * k - 8 * B * la;
+        const int sh2 = 8 * B - off;
+        const uint32_t Va = __shfl(V, m + 16 * la);
+        const uint32_t Vb = __shfl(V, m + 16 * min(la + 1, 3));
+        rowp[k] = (Va >> off) | (sh2 < 32 ? Vb << sh2 : 0u);
       }
     }
-    __syncthreads();
+  };
 
-    // pack 32 codes (dims [32p, 32p+32) of vector v) and store them
+  // Software pipeline over the tiles t, t + grid, ... of this workgroup: an
+  // iteration stores tile k+1 to LDS, computes its norms and rotation, and
+  // quantizes tile k from the previous iteration's accumulators, so the MFMAs
+  // of one tile overlap the quantization of the other; one barrier per tile.
+  // x of tile k+2 is loaded while tile k+1 is processed. Every global load and
+  // store is issued unconditionally and in the same order on every path into
+  // the loop ([4 loads][5 stores] pending at its top), so the compiler's
+  // memory-counter waits keep the next tile's loads in flight.
+  auto run_tiles = [&](auto table_tag) {
+    const Tile t0 = make_tile(blockIdx.x);
+    if (t0.id >= total) return;
+    Tile nxt = make_tile(t0.id + gridDim.x);
+    u4 xr[4];
+    load_x(xr, nxt.id < total ? nxt : t0);  // tile 1 first: its loads stay pending below
+    __builtin_amdgcn_sched_barrier(0);       // keep that order through scheduling
     {
-      const int v = tid >> 2, p = tid & 3;
-      if (v < cur.nv) {
-        const uint8_t* cp = smem + L_CODES + v * CS + 32 * p;
-        const u4 c0 = *reinterpret_cast<const u4*>(cp);
-        const u4 c1 = *reinterpret_cast<const u4*>(cp + 16);
-        uint32_t code[32];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          code[i] = (c0[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-          code[16 + i] = (c1[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-        }
-        if (32 * p < a.split) {
-          uint8_t* dst = a.dst.codes_hi + (int64_t)cur.row * a.dst.hi_head_stride +
-                         (int64_t)(cur.dst0 + v) * a.row_hi + 4 * BH * p;
-          store_codes<BH>(dst, code);
-        } else {
-          uint8_t* dst = a.dst.codes_lo + (int64_t)cur.row * a.dst.lo_head_stride +
-                         (int64_t)(cur.dst0 + v) * a.row_lo + 4 * BL * (p - a.split / 32);
-          store_codes<BL>(dst, code);
-        }
-      }
+      u4 x0[4];
+      load_x(x0, t0);
+      write_x(x0, L_X0);
     }
-    if (nxt.id >= total) break;
-    cur = nxt;
-    xoff ^= (L_X0 ^ L_X1);
-  }
+    float* scl0 = reinterpret_cast<float*>(smem + L_SCALE);
+    float* scl1 = scl0 + CT;
+    __syncthreads();
+    norms(L_X0, t0, scl0);
+    Acc acc = rotate(L_X0);
+    Tile cur = t0;
+    uint32_t xo = L_X1;
+    float* scl_cur = scl0;
+    float* scl_nxt = scl1;
+    while (nxt.id < total) {
+      const Tile far = make_tile(nxt.id + gridDim.x);
+      write_x(xr, xo);
+      load_x(xr, far.id < total ? far : nxt);
+      __syncthreads();
+      norms(xo, nxt, scl_nxt);
+      const Acc acc_n = rotate(xo);
+      quant_store(table_tag, acc, cur, scl_cur);
+      acc = acc_n;
+      cur = nxt;
+      nxt = far;
+      xo ^= (L_X0 ^ L_X1);
+      float* tmp = scl_cur;
+      scl_cur = scl_nxt;
+      scl_nxt = tmp;
+    }
+    __syncthreads();  // scales of the last tile
+    quant_store(table_tag, acc, cur, scl_cur);
+  };
+  if (table)
+    run_tiles(std::true_type{});
+  else
+    run_tiles(std::false_type{});
 }
 
 template <int BH, int BL>
@@ -255,7 +368,7 @@ int launch_bh(const CompressArgs& a, hipStream_t s) {
     cus = 256;
   const int tpr = (a.span.n_tok + CT - 1) / CT;
   const int64_t total = (int64_t)tpr * a.span.rows;
-  if (total <= 0 || total > (int64_t)0x7FFFFFFF) return 0;
+  if (total <= 0 || total >= ((int64_t)1 << 30)) return 0;  // tile ids + 2 grids stay within int
   const int grid = (int)std::min<int64_t>(total, (int64_t)cus * std::max(occ, 1));
   hipLaunchKernelGGL((compress_fast_kernel<BH, BL>), dim3(grid), dim3(CTHR), 0, s, a, tpr, (int)total);
   return 1;
@@ -266,23 +379,20 @@ int launch_bh(const CompressArgs& a, hipStream_t s) {
 int launch_compress_fast(const CompressArgs& a, hipStream_t s) {
   if (a.x_dtype != TQ_F16 || a.proj) return 0;
   if ((reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_hs & 7)) return 0;
-  if (a.split != CD && a.split != CD / 2) return 0;
   const int bh = a.bits_hi, bl = a.bits_lo;
-  if (bh == bl) {
+  if (bh == bl && a.split == CD) {
     switch (bh) {
-      case 1: return launch_bh<1, 1>(a, s);
       case 2: return launch_bh<2, 2>(a, s);
       case 3: return launch_bh<3, 3>(a, s);
       case 4: return launch_bh<4, 4>(a, s);
     }
-  } else if (bh == bl + 1) {
+  } else if (bh == bl + 1 && a.split == CD / 2) {
     switch (bh) {
-      case 2: return launch_bh<2, 1>(a, s);
       case 3: return launch_bh<3, 2>(a, s);
       case 4: return launch_bh<4, 3>(a, s);
     }
   }
-  return 0;
+  return 0;  // 1-bit widths and other splits: the general kernel
 }
 
 }  // namespace tq

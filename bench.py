@@ -12,7 +12,7 @@ replayed; inputs are resident in HBM.
 value = algorithmic bytes read per step / time per step (GB/s): packed codes +
 norms of every compressed token, the fp16 sink/residual tokens, q and out.
 
-roofline: the dominant kernel is the partials kernel of the single-launch
+roofline: the dominant kernel is the partials kernel of the two-kernel
 K4/V2 path (fast_decode_kernel); its average duration is timed with events on
 the launch stream around graph replays of one partials-only call
 (TQ_ATTN_PARTIALS_ONLY) per layer, so its bytes stream from HBM as in the

@@ -60,7 +60,7 @@ typedef struct tq_codec {
   int32_t qjl_m;               /* number of projections (multiple of 32) or 0 */
   int32_t reserved;
   const uint16_t* rotation_f16; /* (2, d, d) binary16: [0] = fp16(R), [1] = fp16(R - [0]),
-                                   row-major, or NULL (the single-launch decode kernel
+                                   row-major, or NULL (the K4/V2 decode kernel
                                    needs it; others ignore it) */
 } tq_codec;
 
@@ -172,11 +172,11 @@ typedef struct tq_attn_desc {
 } tq_attn_desc;
 
 /* tq_attn_desc.flags: force the general kernel (every width / QJL) even where
- * the single-launch K4/V2 kernel applies. */
+ * the K4/V2 partials + merge kernels apply. */
 #define TQ_ATTN_GENERAL 1
-/* Measurement only: on the single-launch K4/V2 path, launch the partials
- * kernel and skip the merge (out is not written). Lets a caller time the
- * dominant kernel alone with events on its stream; no reference counterpart. */
+/* Measurement only: on the K4/V2 path, launch the partials kernel and skip
+ * the merge kernel (out is not written). Lets a caller time the dominant
+ * kernel alone with events on its stream; no reference counterpart. */
 #define TQ_ATTN_PARTIALS_ONLY 2
 
 /* Workspace: scratch for the per-workgroup partials of one call (no state is

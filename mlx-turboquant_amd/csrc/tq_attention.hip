@@ -392,23 +392,32 @@ static int device_cus() {
   return cus;
 }
 
-// Workgroups per (sequence, kv head) and 32-token blocks per workgroup: one
-// workgroup per CU in total, blocks split evenly over its 8 waves.
-static void fast_geometry(const tq_attn_desc* d, int& nwg, int& bpw) {
-  const int nbt = (d->max_comp + 31) / 32 + (d->max_sink + 31) / 32 + (d->max_res + 31) / 32;
+// Workgroups per (sequence, kv head) for the K4/V2 partials kernel, its
+// compressed blocks and fp16 tokens per workgroup: about one workgroup per CU
+// in total, at most 4 compressed blocks per wave and 32 fp16 tokens per
+// workgroup. Returns false when the context needs more than FAST_MAX_WG
+// workgroups (the general kernel takes it).
+static bool fast_geometry(const tq_attn_desc* d, int& nwg, int& bpw, int& fpw) {
+  const int nbc = (d->max_comp + 31) / 32;
+  const int n16 = d->max_sink + d->max_res;
   const int groups = d->batch * d->hkv > 0 ? d->batch * d->hkv : 1;
-  int target = (device_cus() + groups - 1) / groups;
-  const int maxwg = nbt > 0 ? (nbt + 7) / 8 : 1;
-  nwg = target < 1 ? 1 : (target > maxwg ? maxwg : target);
-  if (nwg > fast_max_wg()) nwg = fast_max_wg();
-  bpw = nbt > 0 ? (nbt + nwg - 1) / nwg : 0;
-  bpw = (bpw + 7) / 8 * 8;
-  if (bpw == 0) bpw = 8;
+  const int target = (device_cus() + groups - 1) / groups;
+  const int per_wg = FAST_WAVES * FAST_BLOCKS_PER_WAVE;
+  int lo = (nbc + per_wg - 1) / per_wg;
+  const int lo16 = (n16 + FAST_FP16_PER_WG - 1) / FAST_FP16_PER_WG;
+  if (lo16 > lo) lo = lo16;
+  if (lo < 1) lo = 1;
+  int hi = (nbc + FAST_WAVES - 1) / FAST_WAVES;  // at least one block per wave
+  if (hi < lo) hi = lo;
+  nwg = target < lo ? lo : (target > hi ? hi : target);
+  bpw = (nbc + nwg - 1) / nwg;
+  fpw = (n16 + nwg - 1) / nwg;
+  return nwg <= FAST_MAX_WG;
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// The single-launch kernel reads keys / values / norms / queries in 16-byte
+// The K4/V2 partials kernel reads keys / values / norms / queries in 16-byte
 // pieces: every base and head stride must keep them 16-byte aligned.
 static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
   const int G = d->hq / d->hkv;
@@ -423,7 +432,8 @@ static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_
     return false;
   if (d->max_sink > 0 && !(aligned16(d->sink_k) && aligned16(d->sink_v) && d->sink_head_stride % 8 == 0)) return false;
   if (d->max_res > 0 && !(aligned16(d->res_k) && aligned16(d->res_v) && d->res_head_stride % 8 == 0)) return false;
-  return true;
+  int nwg, bpw, fpw;
+  return fast_geometry(d, nwg, bpw, fpw);
 }
 
 }  // namespace tq
@@ -441,9 +451,10 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
   const size_t nch = (size_t)(nc + ns + nr);
   const size_t heads = (size_t)d->batch * d->hq;
   size_t general = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
-  int nwg, bpw;
-  fast_geometry(d, nwg, bpw);
-  const size_t fast = (size_t)d->batch * d->hkv * nwg * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
+  int nwg, bpw, fpw;
+  size_t fast = 0;
+  if (fast_geometry(d, nwg, bpw, fpw))
+    fast = (size_t)d->batch * d->hkv * nwg * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
   const size_t bytes = general > fast ? general : fast;
   return (bytes + 255) & ~(size_t)255;
 }
@@ -504,8 +515,9 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     f.qscale = d->scale * 1.4426950408889634f;
     f.rot = kc->rotation; f.rot16 = kc->rotation_f16; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
     f.part = static_cast<float*>(workspace);
-    fast_geometry(d, f.nwg, f.bpw);
-    if (launch_fast_decode(f, G, d->batch, !(d->flags & TQ_ATTN_PARTIALS_ONLY), s) != 0)
+    fast_geometry(d, f.nwg, f.bpw, f.fpw);
+    f.merge = (d->flags & TQ_ATTN_PARTIALS_ONLY) ? 0 : 1;
+    if (launch_fast_decode(f, G, d->batch, s) != 0)
       TQ_LAUNCH_CHECK("tq_decode_attention (fast)");
     return TQ_OK;
   }

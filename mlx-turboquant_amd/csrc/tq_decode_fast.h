@@ -1,4 +1,4 @@
-// Arguments of the single-launch K4/V2 decode-attention kernel.
+// Arguments of the K4/V2 decode-attention kernels (per-workgroup partials, then a merge).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -29,15 +29,19 @@ struct FastArgs {
   const float* vcen;     // 4 value centroids
   float* part;           // per-workgroup partials (workspace)
   int nwg;               // workgroups per (sequence, kv head)
-  int bpw;               // 32-token blocks per workgroup
+  int bpw;               // compressed 32-token blocks per workgroup (<= FAST_WAVES * FAST_BLOCKS_PER_WAVE)
+  int fpw;               // fp16 (sink / residual) tokens per workgroup (<= FAST_FP16_PER_WG)
+  int merge;             // 1: launch the merge kernel too; 0: partials only (measurement)
 };
 
 size_t fast_smem_bytes();
 int fast_set_attributes();
-int launch_fast_decode(const FastArgs& a, int G, int batch, bool merge, hipStream_t s);
-int fast_max_wg();
+int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s);
 
-constexpr int FAST_WAVES = 8;          // waves per workgroup of the decode kernel
-constexpr int FAST_PART_FLOATS = 260;  // per query head per workgroup: M, L, has_orig, pad, rot[128], orig[128]
+constexpr int FAST_WAVES = 8;            // waves per workgroup of the decode kernel
+constexpr int FAST_BLOCKS_PER_WAVE = 4;  // compressed blocks per wave (two in flight at a time)
+constexpr int FAST_FP16_PER_WG = 32;     // fp16 tokens per workgroup, staged in LDS
+constexpr int FAST_MAX_WG = 256;         // workgroups per (sequence, kv head)
+constexpr int FAST_PART_FLOATS = 260;    // per query head per workgroup: M, L, has_orig, pad, rot[128], orig[128]
 
 }  // namespace tq

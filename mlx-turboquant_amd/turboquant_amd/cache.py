@@ -328,8 +328,8 @@ class TurboQuantKVCache:
         the kv heads, query head h reads kv head h // (Hq / Hkv). Returns
         float32 (B, Hq, 1, D): softmax(scale * q K^T) V over the same tokens
         update_and_fetch would return (default scale D**-0.5).
-        ``general_kernel`` forces the general kernel where the single-launch
-        K4/V2 kernel would run (used to cross-check the two)."""
+        ``general_kernel`` forces the general kernel where the K4/V2 fast
+        kernels would run (used to cross-check the two)."""
         if self._B is None or self.offset == 0:
             raise ValueError("attend() on an empty cache")
         q = queries

@@ -236,9 +236,12 @@ def test_ring_state_stages():
     (8, 777, 5, 16, 4),              # chunked drains, ring wrap
     (4, 20, 0, 64, 0),               # residual only
     (4, 40, 64, 64, 0),              # sink only
+    (4, 65536, 128, 128, 0),         # 128 workgroups per kv head
+    (8, 200, 4, 8, 0),               # one workgroup per kv head
+    (2, 5000, 300, 300, 0),          # more fp16 tokens than one workgroup stages
 ])
 def test_fast_kernel_matches_general_and_oracle(G, T, sink, window, chunk):
-    """The single-launch K4/V2 kernel against the general kernel and float64."""
+    """The K4/V2 partials + merge kernels against the general kernel and float64."""
     k, v = _kv(1, 2, T, 128, seed=T + G)
     rng = np.random.RandomState(G)
     steps = [(rng.randn(1, 2, 1, 128).astype(np.float16), rng.randn(1, 2, 1, 128).astype(np.float16))
@@ -266,3 +269,4 @@ def test_fast_kernel_repeat_calls_identical():
     outs = [c.attend(q).clone() for _ in range(5)]
     for x in outs[1:]:
         assert torch.equal(x, outs[0])
+

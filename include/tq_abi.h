@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TQ_ABI_VERSION 1
+#define TQ_ABI_VERSION 2
 
 /* Element types of floating-point inputs. */
 enum { TQ_F16 = 0, TQ_BF16 = 1, TQ_F32 = 2 };
@@ -59,9 +59,13 @@ typedef struct tq_codec {
   const float* qjl_proj;       /* (qjl_m, d) Gaussian S (qjl.py:23-36) or NULL */
   int32_t qjl_m;               /* number of projections (multiple of 32) or 0 */
   int32_t reserved;
-  const uint16_t* rotation_f16; /* (2, d, d) binary16: [0] = fp16(R), [1] = fp16(R - [0]),
-                                   row-major, or NULL (the K4/V2 decode kernel
-                                   needs it; others ignore it) */
+  const uint16_t* rotation_parts; /* (4, d, d) 16-bit words, row-major, or NULL:
+                                     [0] = fp16(R), [1] = fp16(R - [0]),
+                                     [2] = bf16(R^T), [3] = bf16(R^T - [2]).
+                                     The K4/V2 decode kernels need it (query
+                                     rotation from the key codec's [0..1],
+                                     inverse rotation of the output from the
+                                     value codec's [2..3]); others ignore it. */
 } tq_codec;
 
 /* A compressed store: packed codes, norms and optional QJL sketch.

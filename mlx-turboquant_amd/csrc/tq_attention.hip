@@ -30,7 +30,8 @@ constexpr float SQRT_HALF_PI = 1.2533141373155003f;
 struct AttnArgs {
   tq_attn_desc d;
   int D;
-  const float* rot;
+  const float* rot;   // key codec R: query rotation
+  const float* vrot;  // value codec R: inverse rotation of the output
   const float* kc_hi;
   const float* kc_lo;
   const float* vc_hi;
@@ -348,7 +349,7 @@ __global__ void combine_kernel(AttnArgs a) {
   float* out = a.d.out + ((int64_t)b * hq + h) * D;
   for (int j = threadIdx.x; j < D; j += blockDim.x) {
     float o = 0.f;
-    for (int i = 0; i < D; ++i) o = fmaf(accr[i], a.rot[(int64_t)i * D + j], o);
+    for (int i = 0; i < D; ++i) o = fmaf(accr[i], a.vrot[(int64_t)i * D + j], o);
     float f = 0.f;
     for (int c = a.nc; c < a.nch; ++c) {
       const float mc = pp[(int64_t)c * a.ps];
@@ -421,7 +422,7 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // pieces: every base and head stride must keep them 16-byte aligned.
 static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
   const int G = d->hq / d->hkv;
-  if (!(kc->rotation_f16 != nullptr && kc->d == 128 && kc->bits_hi == 4 && kc->split == 128 && vc->bits_hi == 2 &&
+  if (!(kc->rotation_parts != nullptr && vc->rotation_parts != nullptr && vc->d == 128 && kc->d == 128 && kc->bits_hi == 4 && kc->split == 128 && vc->bits_hi == 2 &&
         vc->split == 128 && !d->qjl && d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8)))
     return false;
   if (!aligned16(d->q)) return false;
@@ -513,7 +514,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     f.q = d->q; f.q_dtype = d->q_dtype; f.out = d->out;
     f.hq = d->hq; f.hkv = d->hkv;
     f.qscale = d->scale * 1.4426950408889634f;
-    f.rot = kc->rotation; f.rot16 = kc->rotation_f16; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
+    f.rot16 = kc->rotation_parts; f.rotT = vc->rotation_parts + 2 * 128 * 128; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
     f.part = static_cast<float*>(workspace);
     fast_geometry(d, f.nwg, f.bpw, f.fpw);
     f.merge = (d->flags & TQ_ATTN_PARTIALS_ONLY) ? 0 : 1;
@@ -526,6 +527,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   a.d = *d;
   a.D = kc->d;
   a.rot = kc->rotation;
+  a.vrot = vc->rotation;
   a.kc_hi = kc->centroids_hi;
   a.kc_lo = kc->split < kc->d ? kc->centroids_lo : kc->centroids_hi;
   a.vc_hi = vc->centroids_hi;

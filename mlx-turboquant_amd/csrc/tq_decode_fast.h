@@ -23,8 +23,8 @@ struct FastArgs {
   float* out;
   int hq, hkv;
   float qscale;          // scale * log2(e)
-  const float* rot;      // R (128 x 128)
-  const uint16_t* rot16; // (2, 128, 128) fp16 high part / remainder of R
+  const uint16_t* rot16; // (2, 128, 128) fp16 high part / remainder of R (key codec)
+  const uint16_t* rotT;  // (2, 128, 128) bf16 high part / remainder of R^T (value codec)
   const float* kcen;     // 16 key centroids
   const float* vcen;     // 4 value centroids
   float* part;           // per-workgroup partials (workspace)
@@ -40,8 +40,8 @@ int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s);
 
 constexpr int FAST_WAVES = 8;            // waves per workgroup of the decode kernel
 constexpr int FAST_BLOCKS_PER_WAVE = 4;  // compressed blocks per wave (two in flight at a time)
-constexpr int FAST_FP16_PER_WG = 32;     // fp16 tokens per workgroup, staged in LDS
+constexpr int FAST_FP16_PER_WG = 16;     // fp16 tokens per workgroup, staged in LDS
 constexpr int FAST_MAX_WG = 256;         // workgroups per (sequence, kv head)
-constexpr int FAST_PART_FLOATS = 260;    // per query head per workgroup: M, L, has_orig, pad, rot[128], orig[128]
+constexpr int FAST_PART_FLOATS = 132;    // per query head per workgroup: M, L, pad, pad, out[128] (original space, / L)
 
 }  // namespace tq

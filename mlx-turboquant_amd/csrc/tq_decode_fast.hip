@@ -1,10 +1,11 @@
-// Single-launch fused decode attention for K4/V2 TurboQuant caches on gfx950.
+// Fused decode attention for K4/V2 TurboQuant caches on gfx950: a partials
+// kernel over the compressed / fp16 tokens and a small merge kernel.
 //
 // Grid (nwg, hkv, batch): workgroup c of (sequence b, kv head g) owns
 //  - the compressed 32-token blocks [c*bpw, (c+1)*bpw) of the sequence (bpw <=
 //    32): wave w takes blocks c*bpw + w + 8k, k < 4, with two blocks' loads in
 //    flight while it computes;
-//  - the fp16 tokens [c*fpw, (c+1)*fpw) (fpw <= 32) of the sequence's [sink |
+//  - the fp16 tokens [c*fpw, (c+1)*fpw) (fpw <= 16) of the sequence's [sink |
 //    residual ring] list, staged in LDS during set-up and scored by the last
 //    wave before its compressed blocks.
 //
@@ -31,10 +32,11 @@
 // so softmax weights never leave their lane. The accumulator of lane
 // (column r, q4), MFMA nb, register i is rotated dim 32*q4 + 8*i + nb.
 //
-// The 8 waves of a workgroup are combined through LDS; each workgroup writes
-// (max, sum, rotated partial, original-space partial) per query head, and a
-// second small kernel merges the partials of each (b, g) and applies the
-// inverse rotation.
+// The 8 waves of a workgroup are combined through LDS; the workgroup applies
+// the inverse rotation to its rotated sum (MFMA 16x16x32 bf16, high part /
+// remainder of both operands), adds the original-space sum, and writes
+// (max, sum, output / sum) per query head. The merge kernel combines the
+// partials of each (b, g) with their softmax weights.
 
 #include <math.h>
 
@@ -46,6 +48,7 @@
 namespace tq {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
@@ -55,38 +58,47 @@ constexpr int FD = 128;
 constexpr int FW = FAST_WAVES;            // waves per workgroup (FW * 16 == FD)
 constexpr int FT = FW * 64;               // threads
 constexpr int PS = FAST_PART_FLOATS;      // floats per (workgroup, head) partial
-constexpr int P_ROT = 4;                  // partial: [M, L, has_orig, pad, rot[128], orig[128]]
-constexpr int P_ORIG = 4 + FD;
+constexpr int P_OUT = 4;                  // partial: [M, L, pad, pad, out[128]]
 constexpr int NPW = FAST_BLOCKS_PER_WAVE; // compressed blocks per wave
 constexpr int MAXWG = FAST_MAX_WG;        // workgroups per (sequence, kv head)
 constexpr int FROW = 272;                 // LDS row of a staged fp16 token (256 + 16 against bank conflicts)
 constexpr float M_INIT = -1e30f;          // running max before the first block
-constexpr int NCPK = 32;                  // key table replicas per entry (lane % 32: one per lane of an LDS pass)
-constexpr int NCPV = 16;                  // value table replicas per entry (lane % 16)
+constexpr int NCP = 32;                   // table replicas per entry (lane % 32: one per lane of an LDS pass)
 
 struct Layout {
-  // Lookup tables: value entry e (four 2-bit codes) in a 128-byte row of 16
-  // replicas, key entry e (two 4-bit codes) in a 256-byte row of 32 replicas;
-  // replica c at 8*c. Once every wave is past its blocks the table region
-  // holds the wave partials (cmb).
-  static constexpr uint32_t vlut = 0;            // 256 rows x 128 B
-  static constexpr uint32_t klut = 32768;        // 256 rows x 256 B
+  // Lookup tables: value entry e (four 2-bit codes) and key entry e (two
+  // 4-bit codes) each in a 256-byte row of 32 replicas, replica c at 8*c, so
+  // the LDS address of an entry is one byte permute of the code word. Once
+  // every wave is past its blocks the table region holds the combine buffers.
+  static constexpr uint32_t vlut = 0;            // 256 rows x 256 B
+  static constexpr uint32_t klut = 65536;        // 256 rows x 256 B
   static constexpr uint32_t cmb = 0;             // [8 waves][8 heads][128] f32
-  static constexpr uint32_t cml = 98304;         // [8 waves][8 heads][4] f32 max, sum, max of the orig part
+  static constexpr uint32_t aop = 32768;         // [8 heads][2 parts][128] bf16 normalised rotated sum (after cmb)
+  static constexpr uint32_t onr = aop + 4096;    // [8 heads][128] f32 normalised original-space sum
+  static constexpr uint32_t cml = 131072;        // [8 waves][8 heads][4] f32 max, sum, max of the orig part
   static constexpr uint32_t qop = cml + 1024;    // [8 heads][2 parts][4][8][8] fp16 rotated-q B operands
   static constexpr uint32_t qfo = qop + 8192;    // [8 heads][2 parts][4][4][8] fp16 original-space q B operands
   static constexpr uint32_t opk = qfo + 4096;    // [8 heads][128] f32 parked original-space partial
   static constexpr uint32_t nst = opk + 4096;    // [8 waves][64] f32 norm staging
   static constexpr uint32_t qst = nst + 2048;    // [8 heads][128] q as given (up to 4 bytes per element)
-  static constexpr uint32_t f16s = qst + 4096;   // [32 tokens][keys, values][FROW] staged fp16 tokens
-  static constexpr uint32_t total = f16s + 32 * 2 * FROW;
+  static constexpr uint32_t f16s = qst + 4096;   // [16 tokens][keys, values][FROW] staged fp16 tokens
+  static constexpr uint32_t total = f16s + FAST_FP16_PER_WG * 2 * FROW;
 };
-static_assert(FW * 8 * FD * 4 <= 65536, "wave partials fit the table region");
+static_assert(FW * 8 * FD * 4 <= Layout::aop && Layout::onr + 8 * FD * 4 <= Layout::cml,
+              "combine buffers fit the table region");
+static_assert(Layout::total <= 160 * 1024, "LDS of one workgroup");
+static_assert(FAST_FP16_PER_WG == 16, "fp16 tokens: one 16-token score tile, one staging pass");
 
 __device__ inline half8 as_h8(u4 v) { return __builtin_bit_cast(half8, v); }
 
 __device__ inline f4 mfma(half8 a, half8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ inline bf8 as_b8(u4 v) { return __builtin_bit_cast(bf8, v); }
+
+__device__ inline f4 mfma_bf(bf8 a, bf8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 __device__ inline float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -127,107 +139,91 @@ __device__ inline u2 lds_u2(const uint8_t* smem, uint32_t addr) {
 
 
 // Merge of the partials of (sequence b, kv head g), a second launch on the
-// same stream (the kernel boundary makes the partials visible), and the
-// inverse rotation, in float32 (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40):
-//   out_h = (sum_p w_p rot_p) R + sum_p w_p orig_p,  w_p = 2^(M_p - M) / L,
+// same stream (the kernel boundary makes the partials visible), in float32
+// (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40). Each partial p holds its max
+// M_p, its sum L_p and its output x_p in original space, normalised by L_p:
+//   out = sum_p w_p x_p,  w_p = 2^(M_p - M) L_p / L,
 //   M = max_p M_p,  L = sum_p 2^(M_p - M) L_p.
-// Workgroup (h, jq) of (g, b) writes dims [32 jq, 32 jq + 32) of query head
-// h: it needs the full weighted rotated sum of its head and the matching 32
-// columns of R. Every load is issued in one batch before the weights are
-// formed.
-constexpr int MT = 256;  // merge threads
-constexpr int MB = 16;   // partials per thread and batch of loads
+// One wave per (query head, half of the dims): lane p + 64k holds the
+// header of partial p + 64k, lane j sums dim 64 * half + j.
+constexpr int MB = 32;  // partials per batch of loads
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
 
 template <int G>
-__global__ __launch_bounds__(MT) void fast_merge_kernel(FastArgs a) {
-  __shared__ __align__(16) float4 hdr[MAXWG];  // (M, L, has_orig), then the weight in .x
-  __shared__ float red[2][FD];                 // rotated sums over the two halves of the partials
-  __shared__ float rotv[FD];
-  __shared__ float fold[8][32];                // rotation over row groups + original-space sums
-  __shared__ float hml[2];
-  const int h = blockIdx.x >> 2, jq = blockIdx.x & 3, g = blockIdx.y, b = blockIdx.z;
-  const int row = b * a.hkv + g;
-  const int tid = threadIdx.x;
+__global__ __launch_bounds__(64) void fast_merge_kernel(FastArgs a) {
+  const int half = blockIdx.x, hqi = blockIdx.y, b = blockIdx.z;
+  const int g = hqi / G, h = hqi % G;
+  const int lane = threadIdx.x;
   const int np = a.nwg;
   const int64_t pstride = (int64_t)G * PS;
-  const float* pall = a.part + (int64_t)row * np * pstride + h * PS;  // partial p at pall + p*pstride
+  const float* pall = a.part + (int64_t)(b * a.hkv + g) * np * pstride + h * PS;  // partial p at pall + p*pstride
+  const int dim = 64 * half + lane;
 
-  // rotated sums: thread (half, i) takes dim i of partials [pb, pe)
-  const int i = tid & 127, half = tid >> 7;
-  const int pb = half ? (np + 1) / 2 : 0, pe = half ? np : (np + 1) / 2;
-  // original-space sums and rotation: thread (iq, jl) takes column 32 jq + jl,
-  // partials iq, iq + 8, ... and rows [16 iq, 16 iq + 16) of R
-  const int jl = tid & 31, iq = tid >> 5;
-  const int jc = 32 * jq + jl;
-
-  // ---- one batch of loads: headers, the first MB partials of each sum, R
-  float4 h4 = make_float4(M_INIT, 0.f, 0.f, 0.f);
-  if (tid < np) h4 = *reinterpret_cast<const float4*>(pall + tid * pstride);
-  float xr[MB], xo[MB];
+  // headers (partials past np re-read the last one and are masked), then the
+  // first batch of outputs
+  static_assert(MAXWG == 256 && MB == 32, "merge register layout");
+  float2 hd[MAXWG / 64];
 #pragma unroll
-  for (int k = 0; k < MB; ++k) {
-    xr[k] = pall[min(pb + k, np - 1) * pstride + P_ROT + i];
-    xo[k] = pall[min(iq + 8 * k, np - 1) * pstride + P_ORIG + jc];
-  }
-  float rr[16];
+  for (int k = 0; k < MAXWG / 64; ++k)
+    hd[k] = *reinterpret_cast<const float2*>(pall + min(lane + 64 * k, np - 1) * pstride);
+  float x[MB];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) rr[k] = a.rot[(16 * iq + k) * FD + jc];
+  for (int i = 0; i < MB; ++i) x[i] = pall[min(i, np - 1) * pstride + P_OUT + dim];
 
-  // ---- weights
-  if (tid < MAXWG) hdr[tid] = h4;
-  __syncthreads();
-  if (tid == 0) {
-    float M = M_INIT;
-    for (int p = 0; p < np; ++p) M = fmaxf(M, hdr[p].x);
-    float L = 0.f;
-    for (int p = 0; p < np; ++p) L = fmaf(fexp2(hdr[p].x - M), hdr[p].y, L);
-    hml[0] = M;
-    hml[1] = L > 0.f ? 1.f / L : 0.f;
+  float m = M_INIT;
+#pragma unroll
+  for (int k = 0; k < MAXWG / 64; ++k)
+    if (lane + 64 * k < np) m = fmaxf(m, hd[k].x);
+  m = wave_max(m);
+  float w[MAXWG / 64];
+  float l = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXWG / 64; ++k) {
+    w[k] = lane + 64 * k < np ? fexp2(hd[k].x - m) * hd[k].y : 0.f;
+    l += w[k];
   }
-  __syncthreads();
-  if (tid < np) hdr[tid].x = fexp2(hdr[tid].x - hml[0]) * hml[1];
-  __syncthreads();
+  l = wave_sum(l);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
 
-  // ---- weighted sums (partials past the first batch are loaded in further batches)
-  float sr = 0.f, so = 0.f;
+  float acc = 0.f;
   for (int p0 = 0;; p0 += MB) {
+    // partials p0 .. p0 + MB - 1 (uniform) all sit in register p0 >> 6 of w
+    const int kb = p0 >> 6;
+    const float wk = kb == 0 ? w[0] : kb == 1 ? w[1] : kb == 2 ? w[2] : w[3];
 #pragma unroll
-    for (int k = 0; k < MB; ++k) {
-      if (pb + p0 + k < pe) sr = fmaf(hdr[pb + p0 + k].x, xr[k], sr);
-      const int p = iq + 8 * (p0 + k);
-      if (p < np && hdr[p].z != 0.f) so = fmaf(hdr[p].x, xo[k], so);
+    for (int i = 0; i < MB; ++i) {
+      const float wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), (p0 & 63) + i));
+      acc = fmaf(p0 + i < np ? wp : 0.f, x[i], acc);
     }
-    if (pb + p0 + MB >= pe && iq + 8 * (p0 + MB) >= np) break;
+    if (p0 + MB >= np) break;
 #pragma unroll
-    for (int k = 0; k < MB; ++k) {
-      xr[k] = pall[min(pb + p0 + MB + k, np - 1) * pstride + P_ROT + i];
-      xo[k] = pall[min(iq + 8 * (p0 + MB + k), np - 1) * pstride + P_ORIG + jc];
-    }
+    for (int i = 0; i < MB; ++i) x[i] = pall[min(p0 + MB + i, np - 1) * pstride + P_OUT + dim];
   }
-  red[half][i] = sr;
-  __syncthreads();
-  if (tid < FD) rotv[tid] = red[0][tid] + red[1][tid];
-  __syncthreads();
-  // ---- out[j] = sum_i rotv[i] R[i][j] + orig[j]
-  float acc = so;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) acc = fmaf(rotv[16 * iq + k], rr[k], acc);
-  fold[iq][jl] = acc;
-  __syncthreads();
-  if (tid < 32) {
-    float x = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) x += fold[k][tid];
-    a.out[((int64_t)b * a.hq + g * G + h) * FD + 32 * jq + tid] = x;
-  }
+  a.out[((int64_t)b * a.hq + hqi) * FD + dim] = acc * inv;
 }
 
 // The compressed blocks of one wave: loads issued at kernel start (lane r, q4)
 struct Blk {
   u4 k0, k1;      // key codes of tokens t0 + r and t0 + 16 + r, bytes 16*q4 ..
   uint32_t v[8];  // value code halfword r of tokens A0..A3 (t0 + 4q4 + i), B0..B3 (t0 + 16 + 4q4 + i)
-  float nrm;      // lane l < 32: key norm of token t0 + l; l >= 32: value norm of token t0 + l - 32
+  float nk, nv;   // key / value norm of token t0 + (lane & 31)
 };
+
+// Raw buffer over `bytes` bytes at p (stride 0): loads past the end read zero.
+__device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
 
 template <int G>
 __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
@@ -267,11 +263,11 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   const int blk0 = c * a.bpw, blk1 = min(blk0 + a.bpw, nbc);
   const int f0 = c * a.fpw, nf = max(0, min(a.fpw, sink + res - f0));  // fp16 tokens [f0, f0 + nf)
 
-  // ---- set-up loads: centroids, R rows, q and the staged fp16 tokens. The
-  // compressed blocks are requested after the first barrier, so this small
-  // set-up data is not queued behind a GPU-wide flood of block loads. All
-  // loads are issued unconditionally (past the data, from valid addresses) so
-  // the compiler's memory-counter waits stay exact.
+  // ---- set-up loads: centroids, R rows, q and the staged fp16 tokens, issued
+  // before any compressed block so this small set-up data is not queued
+  // behind a GPU-wide flood of block loads. All loads are issued
+  // unconditionally (past the data, from valid addresses) so the compiler's
+  // memory-counter waits stay exact.
   // table centroids: each lane loads one key and one value centroid; table
   // entries gather theirs with lane shuffles
   const float kcen_lane = a.kcen[lane & 15];
@@ -297,13 +293,13 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     const int e = tid < qchunks ? tid : 0;
     qld = *reinterpret_cast<const u4*>(qp + 16 * e);
   }
-  // fp16 tokens of this workgroup: 1024 chunks of 16 bytes, chunk e = token slot
-  // e >> 5, keys ((e >> 4) & 1 == 0) or values, bytes 16*(e & 15) of the row
-  u4 fst[2];
+  // fp16 tokens of this workgroup: 512 chunks of 16 bytes, chunk e = tid =
+  // token slot e >> 5, keys ((e >> 4) & 1 == 0) or values, bytes 16*(e & 15)
+  // of the row
+  u4 fst;
   {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = tid + FT * i;
+    {
+      const int e = tid;
       const int u = f0 + min(e >> 5, max(nf - 1, 0));  // token of the [sink | residual] list
       const bool is_v = (e >> 4) & 1;
       const uint16_t* src;
@@ -316,14 +312,52 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
         sl = sl >= a.res_cap ? sl - a.res_cap : sl;
         src = static_cast<const uint16_t*>(is_v ? a.res_v : a.res_k) + (int64_t)row * a.res_hs + (int64_t)sl * FD;
       }
-      fst[i] = *reinterpret_cast<const u4*>(src + 8 * (e & 15));
+      fst = *reinterpret_cast<const u4*>(src + 8 * (e & 15));
     }
   }
+  // ---- loads of the compressed blocks of this wave: blocks blk0 + w + 8k.
+  // Buffer loads over the tokens [t0, comp) of the row: bytes past the
+  // sequence read as zero (those tokens are masked), slots past the wave's
+  // blocks re-read block 0 and are masked.
+  const bool has_comp = comp > 0;
+  const uint8_t* kcodes = has_comp ? a.kc + (int64_t)row * a.k_hs : nullptr;
+  const uint8_t* vcodes = has_comp ? a.vc + (int64_t)row * a.v_hs : nullptr;
+  const float* knorm = has_comp ? a.kn + (int64_t)row * a.kn_hs : nullptr;
+  const float* vnorm = has_comp ? a.vn + (int64_t)row * a.vn_hs : nullptr;
+  auto slot_t0 = [&](int k) {
+    const int blk = blk0 + w + FW * k;
+    return blk < blk1 ? blk << 5 : 0;
+  };
+  // lane byte offsets within a block: key bytes 16*q4 .. of token r (token
+  // 16 + r at +1024); value halfword r of token 4*q4 (token 4*q4 + i at
+  // +32 i, token 16 + 4*q4 + i at +512 + 32 i); norm of token lane & 31
+  const int ko = r * 64 + 16 * q4;
+  const int vo = q4 * 128 + 2 * r;
+  const int no = (lane & 31) * 4;
+  Blk B[NPW];
+  auto load_slot = [&](int k) {
+    const int t0 = slot_t0(k);
+    const int n = has_comp ? comp - t0 : 0;  // tokens readable from t0 on
+    const __amdgpu_buffer_rsrc_t rk = rsrc(kcodes + (int64_t)t0 * 64, n * 64);
+    const __amdgpu_buffer_rsrc_t rv = rsrc(vcodes + (int64_t)t0 * 32, n * 32);
+    const __amdgpu_buffer_rsrc_t rkn = rsrc(knorm + t0, n * 4);
+    const __amdgpu_buffer_rsrc_t rvn = rsrc(vnorm + t0, n * 4);
+    B[k].k0 = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0);
+    B[k].k1 = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 1024, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      B[k].v[i] = __builtin_amdgcn_raw_buffer_load_b16(rv, vo + (i < 4 ? 32 * i : 512 + 32 * (i - 4)), 0, 0);
+    B[k].nk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rkn, no, 0, 0));
+    B[k].nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvn, no, 0, 0));
+  };
+  // block 0 is requested right behind the set-up loads: waiting for those
+  // does not wait for it
+  load_slot(0);
   // ---- tables:
-  // key byte e -> (c_hi[e&15], c_hi[e>>4], c_lo[e&15], c_lo[e>>4]) fp16, 32 replicas
-  // value byte e -> (c[e&3], c[(e>>2)&3], c[(e>>4)&3], c[(e>>6)&3]) fp16, 16 replicas
-  // thread t fills replicas [16h, 16h + 16) of key entry t & 255 and
-  // [8h, 8h + 8) of value entry t & 255, h = t >> 8
+  // key byte e -> (c_hi[e&15], c_hi[e>>4], c_lo[e&15], c_lo[e>>4]) fp16
+  // value byte e -> (c[e&3], c[(e>>2)&3], c[(e>>4)&3], c[(e>>6)&3]) fp16
+  // thread t fills replicas [16h, 16h + 16) of key and value entry t & 255,
+  // h = t >> 8
   {
     const int e = tid & 255, hh = tid >> 8;
     const float c0 = __shfl(kcen_lane, e & 15), c1 = __shfl(kcen_lane, e >> 4);
@@ -345,52 +379,18 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     ve[1] = pack_h2(cv[2], cv[3]);
     ve[2] = ve[0];
     ve[3] = ve[1];
-    uint8_t* vbp = smem + Layout::vlut + e * 128 + 64 * hh;
+    uint8_t* vbp = smem + Layout::vlut + e * 256 + 128 * hh;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) *reinterpret_cast<u4*>(vbp + 16 * ((k + e) & 3)) = ve;
+    for (int k = 0; k < 8; ++k) *reinterpret_cast<u4*>(vbp + 16 * ((k + e) & 7)) = ve;
   }
   if (tid < qchunks) *reinterpret_cast<u4*>(smem + Layout::qst + 16 * tid) = qld;
   // staged fp16 tokens: [slot][keys | values][272-byte row]
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int e = tid + FT * i;
-    *reinterpret_cast<u4*>(smem + Layout::f16s + (e >> 5) * (2 * FROW) + ((e >> 4) & 1) * FROW + 16 * (e & 15)) = fst[i];
-  }
+  *reinterpret_cast<u4*>(smem + Layout::f16s + (tid >> 5) * (2 * FROW) + ((tid >> 4) & 1) * FROW + 16 * (tid & 15)) = fst;
   __syncthreads();
 
-  // ---- loads of the compressed blocks of this wave: blocks blk0 + w + 8k,
-  // tokens clamped to the sequence (slots past the wave's blocks re-read
-  // block 0 and are masked)
-  const uint8_t* kcodes = a.kc + (int64_t)row * a.k_hs;
-  const float* knorm = a.kn + (int64_t)row * a.kn_hs;
-  const uint8_t* vcodes = a.vc + (int64_t)row * a.v_hs;
-  const float* vnorm = a.vn + (int64_t)row * a.vn_hs;
-  const bool has_comp = comp > 0;
-  const uint8_t* kbase = has_comp ? kcodes : reinterpret_cast<const uint8_t*>(a.rot16);
-  const uint8_t* vbase = has_comp ? vcodes : reinterpret_cast<const uint8_t*>(a.rot16);
-  const float* knb = has_comp ? knorm : reinterpret_cast<const float*>(a.rot16);
-  const float* vnb = has_comp ? vnorm : reinterpret_cast<const float*>(a.rot16);
-  const int lim = max(comp - 1, 0);
-  auto slot_t0 = [&](int k) {
-    const int blk = blk0 + w + FW * k;
-    return blk < blk1 ? blk << 5 : 0;
-  };
-  Blk B[NPW];
-  auto load_slot = [&](int k) {
-    const int t0 = slot_t0(k);
-    B[k].k0 = *reinterpret_cast<const u4*>(kbase + (int64_t)min(t0 + r, lim) * 64 + 16 * q4);
-    B[k].k1 = *reinterpret_cast<const u4*>(kbase + (int64_t)min(t0 + 16 + r, lim) * 64 + 16 * q4);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int t = t0 + (i < 4 ? 4 * q4 + i : 16 + 4 * q4 + i - 4);
-      B[k].v[i] = *reinterpret_cast<const uint16_t*>(vbase + (int64_t)min(t, lim) * 32 + 2 * r);
-    }
-    B[k].nrm = (lane < 32 ? knb : vnb)[min(t0 + (lane & 31), lim)];
-  };
-  // two blocks in flight per wave: blocks 0 and 1 now, block k + 2 once
-  // block k is done (a wave issuing more stalls in issue while the memory
-  // system is saturated, and cannot compute meanwhile)
-  load_slot(0);
+  // two blocks in flight per wave: block 1 once the tables are built, block
+  // k + 2 once block k is done (a wave issuing more stalls in issue while the
+  // memory system is saturated, and cannot compute meanwhile)
   load_slot(1);
 
 
@@ -467,13 +467,14 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   float m_orig = M_INIT;  // running max the parked original-space partial refers to
   f4 acc_r[8];            // rotated-space output accumulators
 
-  const uint32_t cpk = (uint32_t)(lane & (NCPK - 1)) * 8;  // key replica offset within a row
-  const uint32_t cpv = (uint32_t)(lane & (NCPV - 1)) * 8;  // value replica offset within a row
-  auto kaddr = [&](uint32_t word, int byte) {      // klut + (byte of word) * 256 + cpk
-    return Layout::klut + __builtin_amdgcn_perm(word, cpk, 0x0C0C0000u | ((4u + byte) << 8));
+  const uint32_t cp = (uint32_t)(lane & (NCP - 1)) * 8;  // replica offset within a table row
+  static_assert(Layout::klut == 0x10000 && Layout::vlut == 0, "table addresses are byte permutes");
+  const uint32_t cpk = cp | Layout::klut;
+  auto kaddr = [&](uint32_t word, int byte) {      // klut + (byte of word) * 256 + cp: bytes (cp, code byte, 1, 0)
+    return __builtin_amdgcn_perm(word, cpk, 0x0C020000u | ((4u + byte) << 8));
   };
-  auto vaddr = [&](uint32_t word, int byte) {      // vlut + (byte of word) * 128 + cpv
-    return Layout::vlut + ((((word >> (8 * byte)) & 0xFFu) << 7) | cpv);
+  auto vaddr = [&](uint32_t word, int byte) {      // vlut + (byte of word) * 256 + cp
+    return Layout::vlut + __builtin_amdgcn_perm(word, cp, 0x0C0C0000u | ((4u + byte) << 8));
   };
 
   // Online softmax of the 8 scores of this lane (tokens A0..A3, B0..B3 of
@@ -521,30 +522,27 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc_o[nb] = f4{0.f, 0.f, 0.f, 0.f};
     const uint8_t* fs = smem + Layout::f16s;
-    f4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
+    // one 16-token score tile (tokens r); the k-slots of tokens 16.. of the
+    // P^T operand stay empty
+    f4 sA = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const u4 kA = *reinterpret_cast<const u4*>(fs + r * (2 * FROW) + 64 * q4 + 16 * kb);
-      const u4 kB = *reinterpret_cast<const u4*>(fs + (16 + r) * (2 * FROW) + 64 * q4 + 16 * kb);
       sA = mfma(as_h8(kA), qf[kb], sA);
-      sB = mfma(as_h8(kB), qf[kb], sB);
     }
     float sc[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       sc[i] = (sA[i] + row_ror<G>(sA[i])) * a.qscale;
-      sc[4 + i] = (sB[i] + row_ror<G>(sB[i])) * a.qscale;
       if (4 * q4 + i >= nf) sc[i] = -INFINITY;
-      if (16 + 4 * q4 + i >= nf) sc[4 + i] = -INFINITY;
+      sc[4 + i] = -INFINITY;
     }
     const float ones[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
     const half8 pb = softmax_pv(sc, ones, acc_o);
-    u4 vv[8];  // values: dims 8r .. 8r+7 of tokens A0..A3, B0..B3
+    u4 vv[8];  // values: dims 8r .. 8r+7 of tokens A0..A3 (k-slots of B0..B3 zero)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int t = i < 4 ? 4 * q4 + i : 16 + 4 * q4 + i - 4;
-      vv[i] = *reinterpret_cast<const u4*>(fs + t * (2 * FROW) + FROW + 16 * r);
-    }
+    for (int i = 0; i < 8; ++i)
+      vv[i] = i < 4 ? *reinterpret_cast<const u4*>(fs + (4 * q4 + i) * (2 * FROW) + FROW + 16 * r) : u4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
       const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
@@ -582,6 +580,20 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) acc_r[nb] = f4{0.f, 0.f, 0.f, 0.f};
 
+  // R^T rows 16w + r as bf16 MFMA B operands of the inverse rotation (k-slot
+  // (q4, i) of step kb = rotated dim 32*kb + 8*q4 + i), high part and
+  // remainder; requested once the wave's last block is in flight
+  u4 rth[4], rtl[4];
+  auto load_rt = [&]() {
+    const uint16_t* rt = a.rotT + (16 * w + r) * FD + 8 * q4;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      rth[kb] = *reinterpret_cast<const u4*>(rt + 32 * kb);
+      rtl[kb] = *reinterpret_cast<const u4*>(rt + FD * FD + 32 * kb);
+    }
+  };
+  static_assert(NPW >= 2, "two blocks in flight");
+
   // ---- the compressed blocks of this wave (rotated space)
   uint8_t* nst = smem + Layout::nst + w * 256;  // this wave's norm staging: [key norms 32][value norms 32]
 #pragma unroll
@@ -592,7 +604,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     const Blk& L = B[k];
     const int t0 = slot_t0(k);
     const int tend = blk0 + w + FW * k < blk1 ? comp : 0;
-    *reinterpret_cast<float*>(nst + 4 * lane) = L.nrm;
+    *reinterpret_cast<float*>(nst + 4 * lane) = lane < 32 ? L.nk : L.nv;
     const float4 nkA = *reinterpret_cast<const float4*>(nst + 16 * q4);
     const float4 nkB = *reinterpret_cast<const float4*>(nst + 64 + 16 * q4);
     const float4 nvA = *reinterpret_cast<const float4*>(nst + 128 + 16 * q4);
@@ -613,8 +625,13 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     for (int i = 0; i < 4; ++i) {
       sc[i] = (sA[i] + row_ror<G>(sA[i])) * nk[i];
       sc[4 + i] = (sB[i] + row_ror<G>(sB[i])) * nk[4 + i];
-      if (t0 + 4 * q4 + i >= tend) sc[i] = -INFINITY;
-      if (t0 + 16 + 4 * q4 + i >= tend) sc[4 + i] = -INFINITY;
+    }
+    if (t0 + 32 > tend) {  // uniform: only the last block of a sequence and empty slots mask
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (t0 + 4 * q4 + i >= tend) sc[i] = -INFINITY;
+        if (t0 + 16 + 4 * q4 + i >= tend) sc[4 + i] = -INFINITY;
+      }
     }
     const float nv[8] = {nvA.x, nvA.y, nvA.z, nvA.w, nvB.x, nvB.y, nvB.z, nvB.w};
     const half8 pb = softmax_pv(sc, nv, acc_r);
@@ -637,6 +654,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc_r[nb] = mfma(as_h8(va[nb]), pb, acc_r[nb]);
     if (k + 2 < NPW) load_slot(k + 2);
+    if (k + 2 == NPW) load_rt();
   }
 
   // ---- combine the 8 waves of this workgroup through LDS (the table region,
@@ -660,7 +678,10 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   }
   if (lane < G) *reinterpret_cast<float4*>(cl + 4 * lane) = make_float4(m_run, l_run, m_orig, 0.f);
   __syncthreads();
-  // thread (head, dim): merge the 8 waves, write the workgroup partial
+  // thread (head, dim): merge the 8 waves into the workgroup's rotated sum
+  // and original-space sum at the workgroup max M, both divided by the
+  // workgroup sum L; the rotated one goes to LDS as bf16 high part /
+  // remainder (A operand of the inverse rotation), the other as float
   float* part = a.part + ((int64_t)row * a.nwg + c) * G * PS;
   const bool wg_has_fp16 = nf > 0;
   {
@@ -680,13 +701,43 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
         sr = fmaf(sc, cms[(ww * 8 + h) * FD + j], sr);
         L = fmaf(sc, st.y, L);
       }
-      part[h * PS + P_ROT + j] = sr;
+      float so = 0.f;
       if (wg_has_fp16) {
         // original-space part of the last wave, parked at its max then
         const float mo = cls[(FW - 1) * 32 + 4 * h + 2];
-        part[h * PS + P_ORIG + j] = mo > M_INIT ? fexp2(mo - M) * opk[h * FD + j] : 0.f;
+        so = mo > M_INIT ? fexp2(mo - M) * opk[h * FD + j] : 0.f;
       }
-      if (j == 0) *reinterpret_cast<float4*>(part + h * PS) = make_float4(M, L, wg_has_fp16 ? 1.f : 0.f, 0.f);
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      const float rn = sr * inv;
+      const __bf16 bh = (__bf16)rn;
+      const __bf16 bl = (__bf16)(rn - (float)bh);
+      uint16_t* ao = reinterpret_cast<uint16_t*>(smem + Layout::aop) + h * 2 * FD + j;
+      ao[0] = __builtin_bit_cast(uint16_t, bh);
+      ao[FD] = __builtin_bit_cast(uint16_t, bl);
+      reinterpret_cast<float*>(smem + Layout::onr)[h * FD + j] = so * inv;
+      if (j == 0) *reinterpret_cast<float4*>(part + h * PS) = make_float4(M, L, 0.f, 0.f);
+    }
+  }
+  __syncthreads();
+  // ---- inverse rotation, wave w: out[h][j] = sum_i rn[h][i] R[i][j] + on[h][j]
+  // for j in [16w, 16w + 16): A = rn (row = head min(r, G-1)), B = R^T rows
+  {
+    const uint8_t* src = smem + Layout::aop + (uint32_t)min(r, G - 1) * 2 * FD * 2 + (uint32_t)(8 * q4) * 2;
+    f4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const bf8 ah = *reinterpret_cast<const bf8*>(src + 64 * kb);
+      const bf8 al = *reinterpret_cast<const bf8*>(src + FD * 2 + 64 * kb);
+      d = mfma_bf(ah, as_b8(rth[kb]), d);
+      d = mfma_bf(ah, as_b8(rtl[kb]), d);
+      d = mfma_bf(al, as_b8(rth[kb]), d);
+    }
+    const int j = 16 * w + r;
+    const float* onr = reinterpret_cast<const float*>(smem + Layout::onr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * q4 + i;
+      if (h < G) part[h * PS + P_OUT + j] = d[i] + onr[h * FD + j];
     }
   }
 }
@@ -696,7 +747,7 @@ size_t fast_smem_bytes() { return Layout::total; }
 template <int G>
 static void launch_g(const FastArgs& a, int batch, hipStream_t s) {
   hipLaunchKernelGGL((fast_decode_kernel<G>), dim3(a.nwg, a.hkv, batch), dim3(FT), 0, s, a);
-  if (a.merge) hipLaunchKernelGGL((fast_merge_kernel<G>), dim3(4 * G, a.hkv, batch), dim3(MT), 0, s, a);
+  if (a.merge) hipLaunchKernelGGL((fast_merge_kernel<G>), dim3(2, a.hq, batch), dim3(64), 0, s, a);
 }
 
 int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s) {

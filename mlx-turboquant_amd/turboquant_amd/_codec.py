@@ -37,9 +37,15 @@ class DeviceCodec:
             raise ValueError(f"Unsupported bit-width: {bits}. Use 1, 2, 3, or 4.")
         self.device = device
         self.rotation = get_rotation_matrix(d, seed, device)
-        # fp16 high part and remainder of R, the MFMA operands of the query rotation
+        # MFMA operands of the decode kernels: fp16 high part and remainder of
+        # R (query rotation), bf16 high part and remainder of R^T (inverse
+        # rotation of the output), as 16-bit words
         hi = self.rotation.half()
-        self.rotation_f16 = torch.stack([hi, (self.rotation - hi.float()).half()]).contiguous()
+        rt = self.rotation.t().contiguous()
+        bhi = rt.bfloat16()
+        self.rotation_parts = torch.stack([
+            hi.view(torch.int16), (self.rotation - hi.float()).half().view(torch.int16),
+            bhi.view(torch.int16), (rt - bhi.float()).bfloat16().view(torch.int16)]).contiguous()
         self.c_hi, self.b_hi = get_codebook(d, self.bits_hi, device)
         self.c_lo, self.b_lo = get_codebook(d, self.bits_lo, device)
         self.qjl_m = qjl_m
@@ -53,7 +59,7 @@ class DeviceCodec:
             boundaries_hi=self.b_hi.data_ptr(), centroids_lo=self.c_lo.data_ptr(),
             boundaries_lo=self.b_lo.data_ptr(),
             qjl_proj=self.proj.data_ptr() if self.proj is not None else None,
-            qjl_m=qjl_m, reserved=0, rotation_f16=self.rotation_f16.data_ptr())
+            qjl_m=qjl_m, reserved=0, rotation_parts=self.rotation_parts.data_ptr())
 
     @property
     def fractional(self) -> bool:

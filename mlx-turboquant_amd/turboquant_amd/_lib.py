@@ -35,7 +35,7 @@ class Codec(ctypes.Structure):
     _fields_ = [("d", _i32), ("bits_hi", _i32), ("bits_lo", _i32), ("split", _i32),
                 ("rotation", _p), ("centroids_hi", _p), ("boundaries_hi", _p),
                 ("centroids_lo", _p), ("boundaries_lo", _p), ("qjl_proj", _p),
-                ("qjl_m", _i32), ("reserved", _i32), ("rotation_f16", _p)]
+                ("qjl_m", _i32), ("reserved", _i32), ("rotation_parts", _p)]
 
 
 class Store(ctypes.Structure):
@@ -109,7 +109,7 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.tq_abi_version() != 1:
+    if lib.tq_abi_version() != 2:
         raise TurboQuantLibraryError("turboquant_amd: ABI version mismatch")
     _lib = lib
     return lib

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} not bound in _lib.SIGNATURES"
-    assert lib.tq_abi_version() == 1
+    assert lib.tq_abi_version() == 2
 
 
 def test_struct_layouts_match_header():

@@ -72,20 +72,27 @@ struct Layout {
   // every wave is past its blocks the table region holds the combine buffers.
   static constexpr uint32_t vlut = 0;            // 256 rows x 256 B
   static constexpr uint32_t klut = 65536;        // 256 rows x 256 B
-  static constexpr uint32_t cmb = 0;             // [8 waves][8 heads][128] f32
-  static constexpr uint32_t aop = 32768;         // [8 heads][2 parts][128] bf16 normalised rotated sum (after cmb)
-  static constexpr uint32_t onr = aop + 4096;    // [8 heads][128] f32 normalised original-space sum
+  static constexpr uint32_t cmb = 0;             // [8 waves][8 heads][CMS] f32
+  static constexpr uint32_t aop = 34816;         // [8 heads][AOPS bytes: 2 parts x 128 bf16] normalised rotated sum
+  static constexpr uint32_t onr = aop + 8 * 576; // [8 heads][128] f32 normalised original-space sum
   static constexpr uint32_t cml = 131072;        // [8 waves][8 heads][4] f32 max, sum, max of the orig part
-  static constexpr uint32_t qop = cml + 1024;    // [8 heads][2 parts][4][8][8] fp16 rotated-q B operands
-  static constexpr uint32_t qfo = qop + 8192;    // [8 heads][2 parts][4][4][8] fp16 original-space q B operands
+  static constexpr uint32_t qop = cml + 1024;    // [8 heads][2 parts][QOPS bytes: 4][8][8] fp16 rotated-q B operands
+  static constexpr uint32_t qfo = qop + 16 * 528; // [8 heads][2 parts][4][4][8] fp16 original-space q B operands
   static constexpr uint32_t opk = qfo + 4096;    // [8 heads][128] f32 parked original-space partial
   static constexpr uint32_t nst = opk + 4096;    // [8 waves][64] f32 norm staging
   static constexpr uint32_t qst = nst + 2048;    // [8 heads][128] q as given (up to 4 bytes per element)
   static constexpr uint32_t f16s = qst + 4096;   // [16 tokens][keys, values][FROW] staged fp16 tokens
   static constexpr uint32_t total = f16s + FAST_FP16_PER_WG * 2 * FROW;
 };
-static_assert(FW * 8 * FD * 4 <= Layout::aop && Layout::onr + 8 * FD * 4 <= Layout::cml,
-              "combine buffers fit the table region");
+// Row strides padded so that rows read by different lanes of one LDS
+// instruction start in different banks: the rotated-q operand rows of the 8
+// (head, part) columns, the combine rows of the G heads, the inverse-rotation
+// operand rows of the G heads.
+constexpr uint32_t QOPS = 528;  // bytes per (head, part) of qop (512 + 16)
+constexpr int CMS = FD + 4;     // floats per (wave, head) of cmb
+constexpr uint32_t AOPS = 576;  // bytes per head of aop (2 x 256 + 64)
+static_assert(FW * 8 * CMS * 4 <= Layout::aop && Layout::onr == Layout::aop + 8 * AOPS &&
+              Layout::onr + 8 * FD * 4 <= Layout::cml, "combine buffers fit the table region");
 static_assert(Layout::total <= 160 * 1024, "LDS of one workgroup");
 static_assert(FAST_FP16_PER_WG == 16, "fp16 tokens: one 16-token score tile, one staging pass");
 
@@ -133,6 +140,12 @@ __device__ inline uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+// A float at a uniform address, read through the scalar cache (constant
+// address space: the value is not written during the kernel).
+__device__ inline float ld_uniform(const float* p, int i) {
+  return ((const __attribute__((address_space(4))) float*)(p))[i];
+}
+
 __device__ inline u2 lds_u2(const uint8_t* smem, uint32_t addr) {
   return *reinterpret_cast<const u2*>(smem + addr);
 }
@@ -148,20 +161,27 @@ __device__ inline u2 lds_u2(const uint8_t* smem, uint32_t addr) {
 // header of partial p + 64k, lane j sums dim 64 * half + j.
 constexpr int MB = 32;  // partials per batch of loads
 
+// max / sum over the wave: DPP rotations within each 16-lane row, then the
+// four rows
 __device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  v = fmaxf(v, row_ror<1>(v));
+  return rows_max(v);
 }
 
 __device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  return rows_sum(v);
 }
 
 template <int G>
 __global__ __launch_bounds__(64) void fast_merge_kernel(FastArgs a) {
+  __shared__ __align__(16) float wsh[MAXWG];  // w_p, written and read back by the one wave
   const int half = blockIdx.x, hqi = blockIdx.y, b = blockIdx.z;
   const int g = hqi / G, h = hqi % G;
   const int lane = threadIdx.x;
@@ -195,16 +215,18 @@ __global__ __launch_bounds__(64) void fast_merge_kernel(FastArgs a) {
   }
   l = wave_sum(l);
   const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXWG / 64; ++k) wsh[lane + 64 * k] = w[k];  // zero past np
 
   float acc = 0.f;
   for (int p0 = 0;; p0 += MB) {
-    // partials p0 .. p0 + MB - 1 (uniform) all sit in register p0 >> 6 of w
-    const int kb = p0 >> 6;
-    const float wk = kb == 0 ? w[0] : kb == 1 ? w[1] : kb == 2 ? w[2] : w[3];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      const float wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), (p0 & 63) + i));
-      acc = fmaf(p0 + i < np ? wp : 0.f, x[i], acc);
+    for (int i = 0; i < MB; i += 4) {
+      const float4 wp = *reinterpret_cast<const float4*>(wsh + p0 + i);  // one address: a broadcast
+      acc = fmaf(wp.x, x[i], acc);
+      acc = fmaf(wp.y, x[i + 1], acc);
+      acc = fmaf(wp.z, x[i + 2], acc);
+      acc = fmaf(wp.w, x[i + 3], acc);
     }
     if (p0 + MB >= np) break;
 #pragma unroll
@@ -268,10 +290,14 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   // behind a GPU-wide flood of block loads. All loads are issued
   // unconditionally (past the data, from valid addresses) so the compiler's
   // memory-counter waits stay exact.
-  // table centroids: each lane loads one key and one value centroid; table
-  // entries gather theirs with lane shuffles
-  const float kcen_lane = a.kcen[lane & 15];
-  const float vcen_lane = a.vcen[lane & 3];
+  // table centroids of this lane (lane group qg of the table build): key
+  // centroids 4m + qg, value centroid qg; the others the build needs are
+  // uniform
+  const int qg = lane >> 4;
+  float kcq[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) kcq[m] = a.kcen[4 * m + qg];
+  const float vcq = a.vcen[qg];
   // R rows j0 + n as MFMA B operands (k-slot (q4, i) of step kb = dim 32*kb + 8*q4 + i),
   // fp16 high part and remainder precomputed by the codec
   u4 rqh[4], rql[4];
@@ -356,41 +382,34 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   // ---- tables:
   // key byte e -> (c_hi[e&15], c_hi[e>>4], c_lo[e&15], c_lo[e>>4]) fp16
   // value byte e -> (c[e&3], c[(e>>2)&3], c[(e>>4)&3], c[(e>>6)&3]) fp16
-  // thread t fills replicas [16h, 16h + 16) of key and value entry t & 255,
-  // h = t >> 8
-  {
-    const int e = tid & 255, hh = tid >> 8;
-    const float c0 = __shfl(kcen_lane, e & 15), c1 = __shfl(kcen_lane, e >> 4);
-    const float h0 = (float)(_Float16)c0, h1 = (float)(_Float16)c1;
+  // Store k of wave w fills rows 4s .. 4s + 3 (s = 8w + k) of a table with one
+  // 16-byte store (two replicas) per lane, lane-linear and so conflict-free:
+  // lane l writes entry e = 4s + (l >> 4), replicas 2(l & 15) and 2(l & 15) + 1.
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int sx = 8 * w + k;             // uniform
+    const float ca = kcq[k & 3];           // c[e & 15], e & 15 = 4 (k & 3) + qg
+    const float cb = ld_uniform(a.kcen, sx >> 2);  // c[e >> 4]
+    const float ha = (float)(_Float16)ca, hb = (float)(_Float16)cb;
     u4 ke;
-    ke[0] = pack_h2(c0, c1);
-    ke[1] = pack_h2(c0 - h0, c1 - h1);
+    ke[0] = pack_h2(ca, cb);
+    ke[1] = pack_h2(ca - ha, cb - hb);
     ke[2] = ke[0];
     ke[3] = ke[1];
-    uint8_t* kbp = smem + Layout::klut + e * 256 + 128 * hh;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)  // replica pairs, rotated per entry against bank conflicts
-      *reinterpret_cast<u4*>(kbp + 16 * ((k + e) & 7)) = ke;
-    float cv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cv[i] = __shfl(vcen_lane, (e >> (2 * i)) & 3);
+    *reinterpret_cast<u4*>(smem + Layout::klut + sx * 1024 + lane * 16) = ke;
     u4 ve;
-    ve[0] = pack_h2(cv[0], cv[1]);
-    ve[1] = pack_h2(cv[2], cv[3]);
+    ve[0] = pack_h2(vcq, ld_uniform(a.vcen, k & 3));
+    ve[1] = pack_h2(ld_uniform(a.vcen, (sx >> 2) & 3), ld_uniform(a.vcen, sx >> 4));
     ve[2] = ve[0];
     ve[3] = ve[1];
-    uint8_t* vbp = smem + Layout::vlut + e * 256 + 128 * hh;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) *reinterpret_cast<u4*>(vbp + 16 * ((k + e) & 7)) = ve;
+    *reinterpret_cast<u4*>(smem + Layout::vlut + sx * 1024 + lane * 16) = ve;
   }
   if (tid < qchunks) *reinterpret_cast<u4*>(smem + Layout::qst + 16 * tid) = qld;
   // staged fp16 tokens: [slot][keys | values][272-byte row]
   *reinterpret_cast<u4*>(smem + Layout::f16s + (tid >> 5) * (2 * FROW) + ((tid >> 4) & 1) * FROW + 16 * (tid & 15)) = fst;
   __syncthreads();
 
-  // two blocks in flight per wave: block 1 once the tables are built, block
-  // k + 2 once block k is done (a wave issuing more stalls in issue while the
-  // memory system is saturated, and cannot compute meanwhile)
+  // block 1 once the tables are built; block k + 2 as slot k starts
   load_slot(1);
 
 
@@ -440,11 +459,11 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       if (h < G) {
         const float v = dq[i] * a.qscale;
         const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
-        uint8_t* dh = smem + Layout::qop + (uint32_t)(h * 2) * 512 + off;
+        uint8_t* dh = smem + Layout::qop + (uint32_t)(h * 2) * QOPS + off;
         *reinterpret_cast<_Float16*>(dh) = hi;
         *reinterpret_cast<_Float16*>(dh + 4) = hi;
-        *reinterpret_cast<_Float16*>(dh + 512) = lo;
-        *reinterpret_cast<_Float16*>(dh + 516) = lo;
+        *reinterpret_cast<_Float16*>(dh + QOPS) = lo;
+        *reinterpret_cast<_Float16*>(dh + QOPS + 4) = lo;
       }
     }
   }
@@ -573,7 +592,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   // column r reads the high part (even r / G) or the remainder of head r % G.
   half8 qop[8];
   {
-    const uint8_t* src = smem + Layout::qop + (uint32_t)(hd * 2 + (partf != 0.f ? 1 : 0)) * 512 + (uint32_t)q4 * 128;
+    const uint8_t* src = smem + Layout::qop + (uint32_t)(hd * 2 + (partf != 0.f ? 1 : 0)) * QOPS + (uint32_t)q4 * 128;
 #pragma unroll
     for (int s = 0; s < 8; ++s) qop[s] = *reinterpret_cast<const half8*>(src + 16 * s);
   }
@@ -582,7 +601,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
 
   // R^T rows 16w + r as bf16 MFMA B operands of the inverse rotation (k-slot
   // (q4, i) of step kb = rotated dim 32*kb + 8*q4 + i), high part and
-  // remainder; requested once the wave's last block is in flight
+  // remainder; requested as the wave's last-but-one slot starts
   u4 rth[4], rtl[4];
   auto load_rt = [&]() {
     const uint16_t* rt = a.rotT + (16 * w + r) * FD + 8 * q4;
@@ -600,7 +619,13 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   for (int k = 0; k < NPW; ++k) {
     // every slot is computed (no branch between them, so the scheduler can
     // overlap one block's lookups with the previous block's softmax); a slot
-    // past the wave's blocks masks all its tokens
+    // past the wave's blocks masks all its tokens. Block k + 2 (or, past the
+    // last block, R^T) is requested as slot k starts, so two blocks stay in
+    // flight while slot k computes; the scheduling barrier keeps those loads
+    // ahead of every wait of slot k.
+    if (k + 2 < NPW) load_slot(k + 2);
+    if (k + 2 == NPW) load_rt();
+    __builtin_amdgcn_sched_barrier(0);
     const Blk& L = B[k];
     const int t0 = slot_t0(k);
     const int tend = blk0 + w + FW * k < blk1 ? comp : 0;
@@ -653,8 +678,6 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     }
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc_r[nb] = mfma(as_h8(va[nb]), pb, acc_r[nb]);
-    if (k + 2 < NPW) load_slot(k + 2);
-    if (k + 2 == NPW) load_rt();
   }
 
   // ---- combine the 8 waves of this workgroup through LDS (the table region,
@@ -663,7 +686,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   // adds them; lanes r < G then hold head r.
   l_run = rows_sum(l_run);
   __syncthreads();
-  float* cm = reinterpret_cast<float*>(smem + Layout::cmb) + (w * 8) * FD;  // [wave][head][128]
+  float* cm = reinterpret_cast<float*>(smem + Layout::cmb) + (w * 8) * CMS;  // [wave][head][CMS]
   float* cl = reinterpret_cast<float*>(smem + Layout::cml) + w * 32;        // [wave][head][4]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -671,7 +694,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) vr[nb] = acc_r[nb][i] + row_ror<G>(acc_r[nb][i]);
     if (r < G) {
-      float* d = cm + r * FD + 32 * q4 + 8 * i;
+      float* d = cm + r * CMS + 32 * q4 + 8 * i;
       *reinterpret_cast<float4*>(d) = make_float4(vr[0], vr[1], vr[2], vr[3]);
       *reinterpret_cast<float4*>(d + 4) = make_float4(vr[4], vr[5], vr[6], vr[7]);
     }
@@ -698,7 +721,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       for (int ww = 0; ww < FW; ++ww) {
         const float4 st = *reinterpret_cast<const float4*>(cls + ww * 32 + 4 * h);
         const float sc = fexp2(st.x - M);
-        sr = fmaf(sc, cms[(ww * 8 + h) * FD + j], sr);
+        sr = fmaf(sc, cms[(ww * 8 + h) * CMS + j], sr);
         L = fmaf(sc, st.y, L);
       }
       float so = 0.f;
@@ -711,7 +734,7 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       const float rn = sr * inv;
       const __bf16 bh = (__bf16)rn;
       const __bf16 bl = (__bf16)(rn - (float)bh);
-      uint16_t* ao = reinterpret_cast<uint16_t*>(smem + Layout::aop) + h * 2 * FD + j;
+      uint16_t* ao = reinterpret_cast<uint16_t*>(smem + Layout::aop + h * AOPS) + j;
       ao[0] = __builtin_bit_cast(uint16_t, bh);
       ao[FD] = __builtin_bit_cast(uint16_t, bl);
       reinterpret_cast<float*>(smem + Layout::onr)[h * FD + j] = so * inv;
@@ -722,16 +745,17 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   // ---- inverse rotation, wave w: out[h][j] = sum_i rn[h][i] R[i][j] + on[h][j]
   // for j in [16w, 16w + 16): A = rn (row = head min(r, G-1)), B = R^T rows
   {
-    const uint8_t* src = smem + Layout::aop + (uint32_t)min(r, G - 1) * 2 * FD * 2 + (uint32_t)(8 * q4) * 2;
-    f4 d = {0.f, 0.f, 0.f, 0.f};
+    const uint8_t* src = smem + Layout::aop + (uint32_t)min(r, G - 1) * AOPS + (uint32_t)(8 * q4) * 2;
+    f4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0, d2 = d0;  // three independent MFMA chains
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const bf8 ah = *reinterpret_cast<const bf8*>(src + 64 * kb);
       const bf8 al = *reinterpret_cast<const bf8*>(src + FD * 2 + 64 * kb);
-      d = mfma_bf(ah, as_b8(rth[kb]), d);
-      d = mfma_bf(ah, as_b8(rtl[kb]), d);
-      d = mfma_bf(al, as_b8(rth[kb]), d);
+      d0 = mfma_bf(ah, as_b8(rth[kb]), d0);
+      d1 = mfma_bf(ah, as_b8(rtl[kb]), d1);
+      d2 = mfma_bf(al, as_b8(rth[kb]), d2);
     }
+    const f4 d = d0 + (d1 + d2);
     const int j = 16 * w + r;
     const float* onr = reinterpret_cast<const float*>(smem + Layout::onr);
 #pragma unroll

@@ -21,6 +21,7 @@ from __future__ import annotations
 import ctypes
 from typing import Any
 
+import numpy as np
 import torch
 
 from . import _codec, _lib
@@ -94,11 +95,11 @@ class TurboQuantKVCache:
         self._dense_v: torch.Tensor | None = None
         self._dense_comp = 0     # compressed tokens already dequantised into the view
         self._dense_sink = 0     # sink tokens already copied into the view
-        self._qjl_applied = qjl_correction  # False after a state reload (cache.py:352-356)
         self._B = self._H = None
         self._dtype = None
         self.offset = 0
         self.drains: list[int] = []
+        self._pending_meta: dict | None = None  # meta_state set before state
 
     # ------------------------------------------------------------------ setup
     def _setup(self, keys: torch.Tensor) -> None:
@@ -277,7 +278,7 @@ class TurboQuantKVCache:
             self._dense_sink = S
         if self._dense_comp < C:
             n = C - self._dense_comp
-            apply = self.qjl_correction and self._qjl_applied
+            apply = self.qjl_correction
             _codec.dequantize_into(self._kc, self._kstore, self._dense_comp, n, dk, S + self._dense_comp, apply)
             _codec.dequantize_into(self._vc, self._vstore, self._dense_comp, n, dv, S + self._dense_comp, apply)
             self._dense_comp = C
@@ -308,7 +309,7 @@ class TurboQuantKVCache:
         ks = self._kstore.struct(0) if self._compressed_len else empty
         vs = self._vstore.struct(0) if self._compressed_len else empty
         return _lib.AttnDesc(
-            batch=B, hq=hq, hkv=H, qjl=1 if (self.qjl_correction and self._qjl_applied) else 0,
+            batch=B, hq=hq, hkv=H, qjl=1 if self.qjl_correction else 0,
             scale=scale, max_comp=self._compressed_len, max_sink=self._sink_len, max_res=self._fp16_len,
             q_dtype=_lib.dtype_code(q.dtype), kv_dtype=_lib.dtype_code(self._dtype),
             q=q.data_ptr(), out=out.data_ptr(), kstore=ks, vstore=vs, comp_len=None,
@@ -361,6 +362,163 @@ class TurboQuantKVCache:
     @property
     def values(self):
         return self._residual_linear()[1] if self._res_k is not None else None
+
+    # ------------------------------------------------------- saved state
+    @property
+    def state(self) -> tuple:
+        """The reference's 10-tuple (cache.py:118-131): (keys, values,
+        compressed_keys, compressed_key_norms, compressed_values,
+        compressed_value_norms, sink_keys, sink_values, compressed_keys_lo,
+        compressed_values_lo), as torch tensors on the cache's device.
+
+        keys / values hold the residual window in order, (B, H, fp16_len, D),
+        so meta_state's fp16_capacity equals fp16_len. Packed codes are
+        (B, H, compressed_len, row bytes) uint8 and norms (B, H,
+        compressed_len) float32, the reference's layouts; the lo parts are
+        None for integer widths. With qjl_correction four more entries follow
+        (key signs, key gamma, value signs, value gamma), so a reload keeps
+        the correction; the reference stores no sketch."""
+        if self._B is None:
+            return (None,) * 10
+        keys, values = self._residual_linear() if self._res_k is not None and self._fp16_len else (None, None)
+        if keys is not None:
+            keys, values = keys.contiguous().clone(), values.contiguous().clone()
+        sk = self.sink_keys.clone() if self.sink_keys is not None else None
+        sv = self.sink_values.clone() if self.sink_values is not None else None
+        kh, kl, kn = self.packed("k")
+        vh, vl, vn = self.packed("v")
+        out = (keys, values, kh, kn, vh, vn, sk, sv, kl, vl)
+        if self.qjl_correction:
+            ks, vs = self.sketch("k"), self.sketch("v")
+            out += (ks[0] if ks else None, ks[1] if ks else None, vs[0] if vs else None, vs[1] if vs else None)
+        return out
+
+    @state.setter
+    def state(self, v) -> None:
+        """Load a saved tuple (cache.py:133-173): 6 entries (no sink, no lo
+        parts), 8 (with sink), 10 (with sink and lo parts) or 14 (this build's
+        tuple with the QJL sketch). Entries may be torch tensors on any device
+        or numpy arrays. Lengths come from a meta_state set before or after
+        (mlx-lm sets state first), else from the array shapes. Compressed
+        tokens loaded without a sketch get gamma = 0, so QJL corrects only the
+        tokens compressed after the reload, as in the reference."""
+        n = len(v)
+        if n not in (6, 8, 10, 14):
+            raise ValueError(f"state tuple of {n} entries; expected 6, 8, 10 or 14")
+        v = list(v) + [None] * (14 - n)
+        keys, values, kh, kn, vh, vn, sk, sv, kl, vl, ks, kg, vs, vg = v
+        dev = self._device
+        if dev is None:
+            if torch.cuda.is_available():
+                dev = torch.device("cuda", torch.cuda.current_device())
+            else:  # host-only use (tests): the tensors' own device
+                dev = next((t.device for t in v if isinstance(t, torch.Tensor)), torch.device("cpu"))
+
+        def dev_t(a):
+            if a is None:
+                return None
+            t = a if isinstance(a, torch.Tensor) else torch.as_tensor(np.asarray(a))
+            return t.to(dev)
+
+        keys, values, kh, kn, vh, vn, sk, sv, kl, vl, ks, kg, vs, vg = map(
+            dev_t, (keys, values, kh, kn, vh, vn, sk, sv, kl, vl, ks, kg, vs, vg))
+        shape_src = next((t for t in (keys, sk) if t is not None), None)
+        if shape_src is not None:
+            B, H, D, dtype = shape_src.shape[0], shape_src.shape[1], shape_src.shape[3], shape_src.dtype
+        elif kh is not None:
+            B, H, D, dtype = kh.shape[0], kh.shape[1], self.head_dim, torch.float16
+        else:
+            self.__init__(**self._ctor_args())
+            return
+        if D != self.head_dim:
+            raise ValueError(f"state head_dim {D} != cache head_dim {self.head_dim}")
+        meta = self._pending_meta
+        self.__init__(**self._ctor_args())
+        self._setup(torch.empty(B, H, 0, D, dtype=dtype, device=dev))
+        C = kh.shape[2] if kh is not None else 0
+        R = keys.shape[2] if keys is not None else 0
+        S = sk.shape[2] if sk is not None else 0
+        if meta is not None:
+            C = min(C, meta.get("compressed_len", C))
+            R = min(R, meta.get("fp16_len", R))
+            S = min(S, meta.get("sink_len", S))
+        if sk is not None:
+            cap_s = max(self.fp16_sink_size, sk.shape[2])
+            self.sink_keys = torch.zeros(B, H, cap_s, D, dtype=dtype, device=dev)
+            self.sink_values = torch.zeros_like(self.sink_keys)
+            self.sink_keys[:, :, :S] = sk[:, :, :S].to(dtype)
+            self.sink_values[:, :, :S] = sv[:, :, :S].to(dtype)
+            self._sink_len = S
+        if C:
+            for st, codes_hi, codes_lo, norms, signs, gamma, side in (
+                    (self._kstore, kh, kl, kn, ks, kg, "key"), (self._vstore, vh, vl, vn, vs, vg, "value")):
+                c = st.codec
+                if codes_hi.shape[-1] != c.row_hi or (c.fractional and (codes_lo is None or codes_lo.shape[-1] != c.row_lo)):
+                    raise ValueError(f"saved {side} codes do not match {side} bits of this cache")
+                st.reserve(C, 0)
+                st.codes_hi[:, :, :C] = codes_hi[:, :, :C].to(torch.uint8)
+                if c.fractional:
+                    st.codes_lo[:, :, :C] = codes_lo[:, :, :C].to(torch.uint8)
+                st.norms[:, :, :C] = norms.reshape(B, H, -1)[:, :, :C].float()
+                if st.signs is not None and signs is not None and gamma is not None:
+                    st.signs[:, :, :C] = signs[:, :, :C].to(torch.uint8)
+                    st.gamma[:, :, :C] = gamma.reshape(B, H, -1)[:, :, :C].float()
+            self._compressed_len = C
+        if R:
+            cap = max(self._ring_capacity(), R)
+            self._res_k = torch.zeros(B, H, cap, D, dtype=dtype, device=dev)
+            self._res_v = torch.zeros_like(self._res_k)
+            self._res_k[:, :, :R] = keys[:, :, :R].to(dtype)
+            self._res_v[:, :, :R] = values[:, :, :R].to(dtype)
+            self._res_start = 0
+            self._fp16_len = R
+        self.offset = meta["offset"] if meta is not None and "offset" in meta else S + C + R
+        self._pending_meta = None
+
+    @property
+    def meta_state(self) -> dict:
+        """The reference's string dict (cache.py:175-187)."""
+        return {
+            "offset": str(self.offset),
+            "compressed_len": str(self._compressed_len),
+            "head_dim": str(self.head_dim),
+            "key_bits": str(self.key_bits),
+            "value_bits": str(self.value_bits),
+            "fp16_sink_size": str(self.fp16_sink_size),
+            "sink_len": str(self._sink_len),
+            "fp16_len": str(self._fp16_len),
+            "fp16_capacity": str(self._fp16_len),
+        }
+
+    @meta_state.setter
+    def meta_state(self, v) -> None:
+        """Lengths of a saved cache (cache.py:189-200). Applied to a state
+        already loaded, or kept for the state setter when it comes first."""
+        meta = {"offset": int(v["offset"]), "compressed_len": int(v["compressed_len"])}
+        for key in ("sink_len", "fp16_len"):
+            if key in v:
+                meta[key] = int(v[key])
+        if "fp16_sink_size" in v:
+            self.fp16_sink_size = int(v["fp16_sink_size"])
+        if self._B is None:
+            self._pending_meta = meta
+            self.offset = meta["offset"]
+            return
+        for key, attr in (("compressed_len", "_compressed_len"), ("sink_len", "_sink_len"), ("fp16_len", "_fp16_len")):
+            if key in meta:
+                if meta[key] > getattr(self, attr):
+                    raise ValueError(f"meta_state {key} {meta[key]} exceeds the loaded state's {getattr(self, attr)}")
+                setattr(self, attr, meta[key])
+        self._dense_comp = min(self._dense_comp, self._compressed_len)
+        self._dense_sink = min(self._dense_sink, self._sink_len)
+        self.offset = meta["offset"]
+
+    def _ctor_args(self) -> dict:
+        return dict(head_dim=self.head_dim, num_kv_heads=self.num_kv_heads, key_bits=self.key_bits,
+                    value_bits=self.value_bits, residual_window=self.residual_window,
+                    rotation_seed=self.rotation_seed, fp16_sink_size=self.fp16_sink_size,
+                    chunk_size=self.chunk_size, qjl_correction=self.qjl_correction,
+                    qjl_n_proj=self.qjl_n_proj, device=self._device)
 
     def empty(self) -> bool:
         return self._fp16_len == 0 and self._compressed_len == 0 and self._sink_len == 0

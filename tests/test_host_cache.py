@@ -118,3 +118,61 @@ def test_drain_schedule():
     assert drain_schedule(129, 128, 1) == [1]
     assert drain_schedule(10, 0, 0) == [10]
     assert drain_schedule(0, 0, 0) == []
+
+
+@pytest.mark.parametrize("kw,chunks,more", [
+    (dict(residual_window=32, chunk_size=8, fp16_sink_size=8), [200] + [1] * 7, [1] * 40),
+    (dict(residual_window=16, key_bits=3.5, value_bits=2.5, fp16_sink_size=4), [90, 3], [1] * 50),
+    (dict(residual_window=4, chunk_size=1, qjl_correction=True, qjl_n_proj=32), [40], [1] * 12),
+])
+def test_state_round_trip_host(cpu_cache, kw, chunks, more):
+    """state / meta_state (cache.py:118-200): a reloaded cache holds the same
+    tokens as the oracle and keeps following it through later drains."""
+    kw = dict(head_dim=128, num_kv_heads=2, **kw)
+    c, o = _run(cpu_cache, kw, chunks)
+    st, meta = c.state, c.meta_state
+    assert len(st) == (14 if kw.get("qjl_correction") else 10)
+    assert meta == {k: str(x) for k, x in dict(
+        offset=o.offset, compressed_len=o.compressed_len, head_dim=128, key_bits=kw.get("key_bits", 4),
+        value_bits=kw.get("value_bits", 2), fp16_sink_size=kw.get("fp16_sink_size", 0), sink_len=o.sink_len,
+        fp16_len=o.fp16_len, fp16_capacity=o.fp16_len).items()}
+    r = cpu_cache(**kw)
+    r.state = st
+    r.meta_state = meta
+    _assert_state_equal(r, o)
+    rng = np.random.RandomState(1)
+    for T in more:
+        k = rng.randn(1, 2, T, 128).astype(np.float16)
+        v = rng.randn(1, 2, T, 128).astype(np.float16)
+        r.update(torch.from_numpy(k), torch.from_numpy(v))
+        o.update(k, v)
+    assert (r.offset, r._compressed_len, r._fp16_len, r._sink_len) == (o.offset, o.compressed_len, o.fp16_len, o.sink_len)
+    _assert_state_equal(r, o)
+
+
+def test_state_reference_layout_host(cpu_cache):
+    """The reference's layout: residual buffer at capacity with a valid
+    prefix, lengths in meta_state set after the arrays (mlx-lm's order)."""
+    kw = dict(head_dim=128, num_kv_heads=2, residual_window=32, fp16_sink_size=8)
+    c, o = _run(cpu_cache, kw, [150, 1, 1])
+    keys, values, *rest = c.state
+    cap = keys.shape[2] + 256
+    kbuf = torch.zeros(1, 2, cap, 128, dtype=keys.dtype)
+    vbuf = torch.zeros_like(kbuf)
+    kbuf[:, :, :keys.shape[2]] = keys
+    vbuf[:, :, :keys.shape[2]] = values
+    r = cpu_cache(**kw)
+    r.state = tuple(t.numpy() if t is not None else None for t in (kbuf, vbuf, *rest))
+    assert r._fp16_len == cap  # lengths from shapes until meta_state arrives
+    r.meta_state = dict(c.meta_state, fp16_capacity=str(cap))
+    _assert_state_equal(r, o)
+
+
+def test_state_shapes_and_errors():
+    from turboquant_amd import TurboQuantKVCache
+    c = TurboQuantKVCache(head_dim=128, num_kv_heads=2)
+    assert c.state == (None,) * 10
+    assert c.meta_state["offset"] == "0" and c.meta_state["fp16_capacity"] == "0"
+    for n in (5, 7, 9, 11):
+        with pytest.raises(ValueError):
+            c.state = (None,) * n

@@ -634,6 +634,24 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     const float4 nkB = *reinterpret_cast<const float4*>(nst + 64 + 16 * q4);
     const float4 nvA = *reinterpret_cast<const float4*>(nst + 128 + 16 * q4);
     const float4 nvB = *reinterpret_cast<const float4*>(nst + 192 + 16 * q4);
+    // V^T operands (row = dim 8r + nb, k-slot pairs = token pairs of the
+    // lane), looked up first: they depend only on the codes, and their LDS
+    // latency then overlaps the scores and the softmax
+    u4 va[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t px = L.v[2 * j], py = L.v[2 * j + 1];  // token pair j
+      const u2 x0 = lds_u2(smem, vaddr(px, 0)), x1 = lds_u2(smem, vaddr(px, 1));
+      const u2 y0 = lds_u2(smem, vaddr(py, 0)), y1 = lds_u2(smem, vaddr(py, 1));
+      va[0][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x05040100u);
+      va[1][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x07060302u);
+      va[2][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x05040100u);
+      va[3][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x07060302u);
+      va[4][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x05040100u);
+      va[5][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x07060302u);
+      va[6][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x05040100u);
+      va[7][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x07060302u);
+    }
     f4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -660,22 +678,6 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     }
     const float nv[8] = {nvA.x, nvA.y, nvA.z, nvA.w, nvB.x, nvB.y, nvB.z, nvB.w};
     const half8 pb = softmax_pv(sc, nv, acc_r);
-    // V^T operands: row = dim 8r + nb, k-slot pairs = token pairs of the lane
-    u4 va[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t px = L.v[2 * j], py = L.v[2 * j + 1];  // token pair j
-      const u2 x0 = lds_u2(smem, vaddr(px, 0)), x1 = lds_u2(smem, vaddr(px, 1));
-      const u2 y0 = lds_u2(smem, vaddr(py, 0)), y1 = lds_u2(smem, vaddr(py, 1));
-      va[0][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x05040100u);
-      va[1][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x07060302u);
-      va[2][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x05040100u);
-      va[3][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x07060302u);
-      va[4][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x05040100u);
-      va[5][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x07060302u);
-      va[6][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x05040100u);
-      va[7][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x07060302u);
-    }
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc_r[nb] = mfma(as_h8(va[nb]), pb, acc_r[nb]);
   }

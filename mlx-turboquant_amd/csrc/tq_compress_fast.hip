@@ -12,8 +12,8 @@
 // 2^-22 of sum_i |x_n,i R_ji| plus the float32 accumulation, inside the float32
 // dot-product band within which the reference's own GEMM does not fix a code.
 //
-// Work split: a workgroup of 4 waves walks tiles of 64 vectors of one (batch,
-// head) row, with the x tiles of the next two tiles in flight. Wave w owns
+// Work split: a workgroup of 4 waves (three workgroups per CU) walks tiles of
+// 64 vectors of one (batch, head) row, the next tile's x in flight. Wave w owns
 // rotated dims [32w, 32w+32) and keeps its rows of 256R as MFMA A operands in
 // registers for the whole launch. Per tile:
 //   1. the x tile (16 KB) is stored to LDS;
@@ -56,7 +56,7 @@ constexpr uint32_t MAGIC_BITS = 0x4B400000u;
 constexpr uint32_t L_X0 = 0;
 constexpr uint32_t L_X1 = CT * XS;
 constexpr uint32_t L_SCALE = 2 * CT * XS;
-constexpr uint32_t L_QT = L_SCALE + 2 * CT * 4;     // [2 codebooks][NCELL] {boundary, base}
+constexpr uint32_t L_QT = L_SCALE + CT * 4;         // [2 codebooks][NCELL] {boundary, base}
 constexpr uint32_t L_BND = L_QT + 2 * NCELL * 8;    // [2 codebooks][16] boundaries
 constexpr uint32_t L_FLAG = L_BND + 2 * 16 * 4;
 constexpr uint32_t L_TOTAL = L_FLAG + 16;
@@ -92,7 +92,7 @@ __device__ inline uint32_t quant_table(float y, const uint8_t* tbl) {
 }
 
 template <int BH, int BL>
-__global__ __launch_bounds__(CTHR) void compress_fast_kernel(CompressArgs a, int tiles_per_row, int total) {
+__global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, int tiles_per_row, int total) {
   __shared__ __align__(16) uint8_t smem[L_TOTAL];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -302,53 +302,44 @@ __global__ __launch_bounds__(CTHR) void compress_fast_kernel(CompressArgs a, int
     }
   };
 
-  // Software pipeline over the tiles t, t + grid, ... of this workgroup: an
-  // iteration stores tile k+1 to LDS, computes its norms and rotation, and
-  // quantizes tile k from the previous iteration's accumulators, so the MFMAs
-  // of one tile overlap the quantization of the other; one barrier per tile.
-  // x of tile k+2 is loaded while tile k+1 is processed. Every global load and
-  // store is issued unconditionally and in the same order on every path into
-  // the loop ([4 loads][5 stores] pending at its top), so the compiler's
-  // memory-counter waits keep the next tile's loads in flight.
+  // Tiles t, t + grid, ... of this workgroup. Per tile: the x tile already
+  // in LDS gets its norms and rotation, the next tile's x (loaded during the
+  // previous tile) goes to the other LDS buffer and the one after is loaded,
+  // then the tile is quantized and stored. One accumulator set per wave keeps
+  // the kernel at three workgroups per CU (12 waves); the MFMAs of one wave
+  // overlap the quantization of the others. Every global load and store is
+  // issued in the same order on every path through the loop, so the
+  // compiler's memory-counter waits keep the prefetched tile in flight.
   auto run_tiles = [&](auto table_tag) {
-    const Tile t0 = make_tile(blockIdx.x);
-    if (t0.id >= total) return;
-    Tile nxt = make_tile(t0.id + gridDim.x);
+    Tile cur = make_tile(blockIdx.x);
+    if (cur.id >= total) return;
+    Tile nxt = make_tile(cur.id + gridDim.x);
     u4 xr[4];
-    load_x(xr, nxt.id < total ? nxt : t0);  // tile 1 first: its loads stay pending below
-    __builtin_amdgcn_sched_barrier(0);       // keep that order through scheduling
     {
       u4 x0[4];
-      load_x(x0, t0);
+      load_x(x0, cur);
+      load_x(xr, nxt.id < total ? nxt : cur);
       write_x(x0, L_X0);
     }
-    float* scl0 = reinterpret_cast<float*>(smem + L_SCALE);
-    float* scl1 = scl0 + CT;
-    __syncthreads();
-    norms(L_X0, t0, scl0);
-    Acc acc = rotate(L_X0);
-    Tile cur = t0;
-    uint32_t xo = L_X1;
-    float* scl_cur = scl0;
-    float* scl_nxt = scl1;
-    while (nxt.id < total) {
-      const Tile far = make_tile(nxt.id + gridDim.x);
-      write_x(xr, xo);
-      load_x(xr, far.id < total ? far : nxt);
-      __syncthreads();
-      norms(xo, nxt, scl_nxt);
-      const Acc acc_n = rotate(xo);
-      quant_store(table_tag, acc, cur, scl_cur);
-      acc = acc_n;
+    float* scl = reinterpret_cast<float*>(smem + L_SCALE);
+    uint32_t xo = L_X0;
+    for (;;) {
+      __syncthreads();  // x of cur in LDS; every wave is done with the previous tile
+      norms(xo, cur, scl);
+      const Acc acc = rotate(xo);
+      const bool more = nxt.id < total;
+      const Tile far = more ? make_tile(nxt.id + gridDim.x) : nxt;
+      if (more) {
+        write_x(xr, xo ^ (L_X0 ^ L_X1));
+        load_x(xr, far.id < total ? far : nxt);
+      }
+      __syncthreads();  // scales of cur
+      quant_store(table_tag, acc, cur, scl);
+      if (!more) break;
       cur = nxt;
       nxt = far;
       xo ^= (L_X0 ^ L_X1);
-      float* tmp = scl_cur;
-      scl_cur = scl_nxt;
-      scl_nxt = tmp;
     }
-    __syncthreads();  // scales of the last tile
-    quant_store(table_tag, acc, cur, scl_cur);
   };
   if (table)
     run_tiles(std::true_type{});

@@ -70,6 +70,20 @@ __device__ inline int ld_span(const int32_t* p, int i) {
   return ((const __attribute__((address_space(4))) int32_t*)(p))[i];
 }
 
+// n / d for uniform 0 <= n < 2^30 and d >= 1, with m = (2^32 - 1) / d from
+// the host: umulhi(n, m) is floor(n / d) or one less, fixed by one remainder
+// test; the operations stay on the scalar unit
+__device__ inline int udiv_uniform(int n, int d, uint32_t m) {
+  int q = (int)__umulhi((uint32_t)n, m);
+  if (n - q * d >= d) ++q;
+  return q;
+}
+
+struct Div {
+  int d;       // divisor
+  uint32_t m;  // (2^32 - 1) / d
+};
+
 struct Tile {
   int id;          // tile index; >= total: none left
   int row;         // (batch, head) row
@@ -82,17 +96,21 @@ struct QCell {
   uint32_t base;  // boundaries below every value of the cell
 };
 
-// code of a finite y from the cell table `tbl` (LDS); non-finite y only occur
-// in vectors with a non-finite norm, whose codes are set to 0 by the caller
-__device__ inline uint32_t quant_table(float y, const uint8_t* tbl) {
+// code of a finite y from the cell table at LDS byte offset `tbl_adj` +
+// 8 * MAGIC_BITS (smem is the kernel's only LDS object, at offset 0; the
+// magic bias is folded into the base so the cell address is one shift-add);
+// non-finite y only occur in vectors with a non-finite norm, whose codes are
+// set to 0 by the caller
+__device__ inline uint32_t quant_table(float y, const uint8_t* smem, uint32_t tbl_adj) {
   const int r = (int)__float_as_uint(fmaf(y, 64.f, 32.f + MAGIC));
-  const int c = min(max(r, (int)MAGIC_BITS), (int)MAGIC_BITS + NCELL - 1) - (int)MAGIC_BITS;
-  const QCell q = *reinterpret_cast<const QCell*>(tbl + 8 * c);
+  const uint32_t rc = (uint32_t)min(max(r, (int)MAGIC_BITS), (int)MAGIC_BITS + NCELL - 1);
+  const QCell q = *reinterpret_cast<const QCell*>(smem + (tbl_adj + 8u * rc));
   return q.base + (y > q.bnd ? 1u : 0u);
 }
 
 template <int BH, int BL>
-__global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, int tiles_per_row, int total) {
+__global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, Div tiles_per_row, Div heads,
+                                                                int total) {
   __shared__ __align__(16) uint8_t smem[L_TOTAL];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -151,7 +169,7 @@ __global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, 
     }
   __syncthreads();
   const bool table = *flag == 0u;
-  const uint8_t* qtab = smem + L_QT + (whi ? 0 : NCELL * 8);
+  const uint32_t qtab_adj = L_QT + (whi ? 0u : NCELL * 8u) - 8u * MAGIC_BITS;  // wraps: see quant_table
 
   // next non-empty tile at or after `id` in this workgroup's sequence
   auto make_tile = [&](int id) {
@@ -159,9 +177,9 @@ __global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, 
     t.id = id;
     t.row = t.nv = t.src0 = t.dst0 = 0;
     for (; t.id < total; t.id += gridDim.x) {
-      t.row = __builtin_amdgcn_readfirstlane(t.id / tiles_per_row);  // uniform: scalar loads below
-      const int t0 = (t.id - t.row * tiles_per_row) * CT;
-      const int b = __builtin_amdgcn_readfirstlane(t.row / a.span.heads);
+      t.row = udiv_uniform(t.id, tiles_per_row.d, tiles_per_row.m);
+      const int t0 = (t.id - t.row * tiles_per_row.d) * CT;
+      const int b = udiv_uniform(t.row, heads.d, heads.m);
       const int n = a.span.n_tok_b ? ld_span(a.span.n_tok_b, b) : a.span.n_tok;
       t.nv = min(CT, n - t0);
       if (t.nv > 0) {
@@ -272,7 +290,7 @@ __global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, 
           const float y = acc.v[s4][n2][e] * sc;
           uint32_t c;
           if constexpr (TABLE) {
-            c = quant_table(y, qtab);
+            c = quant_table(y, smem, qtab_adj);
           } else {
             c = 0;
             for (int k = 0; k < nbnd; ++k) c += y > bnd_l[k] ? 1u : 0u;
@@ -361,7 +379,8 @@ int launch_bh(const CompressArgs& a, hipStream_t s) {
   const int64_t total = (int64_t)tpr * a.span.rows;
   if (total <= 0 || total >= ((int64_t)1 << 30)) return 0;  // tile ids + 2 grids stay within int
   const int grid = (int)std::min<int64_t>(total, (int64_t)cus * std::max(occ, 1));
-  hipLaunchKernelGGL((compress_fast_kernel<BH, BL>), dim3(grid), dim3(CTHR), 0, s, a, tpr, (int)total);
+  const Div dt{tpr, 0xFFFFFFFFu / (uint32_t)tpr}, dh{a.span.heads, 0xFFFFFFFFu / (uint32_t)a.span.heads};
+  hipLaunchKernelGGL((compress_fast_kernel<BH, BL>), dim3(grid), dim3(CTHR), 0, s, a, dt, dh, (int)total);
   return 1;
 }
 

@@ -11,10 +11,13 @@
 //
 // Scores are computed transposed, S^T = K q^T (MFMA 16x16x32 f16):
 //   A = 16 tokens x 32 k-slots of keys, B = 32 k-slots x 16 columns of queries.
-// Column r of B holds query head (r % G) of kv group g, either its fp16 high
-// part (even r / G) or the fp16 remainder (odd r / G), so a DPP row rotation
-// by G adds the two halves and every column ends up with the full score of
-// its head. In rotated space (compressed tokens, docs/FUSED_ATTENTION_DESIGN.md
+// A block of 32 tokens is two 16-token tiles. For G <= 4 the 16 columns are
+// two groups of 8, group t serving tile t: column c8 of a group holds the
+// fp16 high part of query head c8 % G (c8 < 4) or the remainder of head
+// (7 - c8) % G, so a DPP row half-mirror (c8 <-> 7 - c8) adds the two parts,
+// and each lane goes on with the 4 scores of its own tile only. For G = 8
+// column r holds part r >> 3 of head r & 7 (a rotation by 8 pairs them) and
+// every lane sees both tiles. In rotated space (compressed tokens, docs/FUSED_ATTENTION_DESIGN.md
 // :62-67) each key code byte (two 4-bit codes) is looked up in an LDS table
 // whose 8-byte entry is (c_hi[a], c_hi[b], c_lo[a], c_lo[b]); two lookups fill
 // one A operand, and the matching B k-slots repeat the two query values, so
@@ -23,13 +26,15 @@
 // Output, transposed too: O^T += V^T P^T with A = 16 dims x 32 tokens of
 // values decoded from an LDS table indexed by one 2-bit-code byte (4 dims of
 // one token) and paired across tokens with v_perm, and B = p * n_v split into
-// fp16 high part / remainder along the same columns as the scores.
+// fp16 high part / remainder along the same columns as the scores (zero in
+// the k-slots of the other tile).
 // fp16 tokens (original space) use the same MFMAs with exact fp16 keys /
 // values, accumulated separately.
 //
 // Lane (column r, group q4) of a score tile holds tokens 4*q4 + i of the
-// tile, which is exactly the k-slot order (8*q4 + i) the P^T operand needs,
-// so softmax weights never leave their lane. The accumulator of lane
+// tile, which is exactly the k-slot order (8*q4 + i, tile 1 at + 4) the P^T
+// operand needs, so softmax weights never leave their lane. The running max
+// is raised with a margin, so most blocks need no rescale. The accumulator of lane
 // (column r, q4), MFMA nb, register i is rotated dim 32*q4 + 8*i + nb.
 //
 // The 8 waves of a workgroup are combined through LDS; the workgroup applies
@@ -64,6 +69,10 @@ constexpr int MAXWG = FAST_MAX_WG;        // workgroups per (sequence, kv head)
 constexpr int FROW = 272;                 // LDS row of a staged fp16 token (256 + 16 against bank conflicts)
 constexpr float M_INIT = -1e30f;          // running max before the first block
 constexpr int NCP = 32;                   // table replicas per entry (lane % 32: one per lane of an LDS pass)
+// A block whose max exceeds the running max m raises m to that max + this
+// margin (base-2 units), so later blocks rarely trigger a rescale; weights
+// stay <= 1.
+constexpr float RESCALE_MARGIN = 3.f;
 
 struct Layout {
   // Lookup tables: value entry e (four 2-bit codes) and key entry e (two
@@ -129,6 +138,16 @@ __device__ inline float rows_sum(float v) {
   v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// the value of the column holding the other fp16 part of the same query head
+// (and tile): row half-mirror for G <= 4, rotation by 8 for G = 8
+template <int G>
+__device__ inline float partner(float v) {
+  if constexpr (G <= 4)
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true));
+  else
+    return row_ror<8>(v);
 }
 
 __device__ inline uint32_t pk_rtz(float a, float b) {
@@ -257,8 +276,14 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   const int r = lane & 15, q4 = lane >> 4;
   const int row = b * a.hkv + g;
   const int j0 = 16 * w;  // output-dim tile of this wave for the query rotation
-  const int hd = r % G;   // query head of column r
-  const float partf = ((r / G) & 1) ? 1.f : 0.f;  // column holds the fp16 remainder
+  constexpr int TS = G <= 4 ? 2 : 1;  // tiles sharing the columns
+  constexpr int NS = 8 / TS;           // scores per lane per block
+  const int tile = TS == 2 ? r >> 3 : 0;  // tile of column r (TS == 2)
+  const int c8 = r & 7;
+  const int hd = TS == 2 ? (c8 < 4 ? c8 : 7 - c8) % G : c8;  // query head of column r
+  const bool lo_part = TS == 2 ? c8 >= 4 : r >= 8;          // column holds the fp16 remainder
+  const float partf = lo_part ? 1.f : 0.f;
+  const bool writer = !lo_part && c8 < G;  // one column per (tile, head) writes the combine rows
 
   // All kernel arguments the set-up needs are loaded in one batch of scalar
   // loads and waited for once (a branch on an argument would otherwise split
@@ -496,34 +521,47 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     return Layout::vlut + __builtin_amdgcn_perm(word, cp, 0x0C0C0000u | ((4u + byte) << 8));
   };
 
-  // Online softmax of the 8 scores of this lane (tokens A0..A3, B0..B3 of
-  // the block, column r), returns the P^T operand (p * nv, high part or
-  // remainder by column) and rescales `acc` when the running max grows.
-  auto softmax_pv = [&](float (&s)[8], const float (&nv)[8], f4 (&acc)[8]) {
-    float bm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  // Online softmax of the NS scores of this lane (tokens A0..A3 and / or
+  // B0..B3 of the block, column r), returns the P^T operand (p * nv, high
+  // part or remainder by column, zero in the k-slots of the other tile) and
+  // rescales `acc` when a block's max exceeds the running max.
+  auto softmax_pv = [&](float (&s)[NS], const float (&nv)[NS], f4 (&acc)[8]) {
+    float bm = s[0];
+#pragma unroll
+    for (int i = 1; i < NS; ++i) bm = fmaxf(bm, s[i]);
     bm = rows_max(bm);
     if (__builtin_amdgcn_ballot_w64(bm > m_run) != 0) {
-      const float mnew = fmaxf(m_run, bm);
+      const float mnew = bm > m_run ? bm + RESCALE_MARGIN : m_run;
       const float corr = fexp2(m_run - mnew);
       l_run *= corr;
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) acc[nb] *= corr;
       m_run = mnew;
     }
-    float pv[8];
+    float pv[NS];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < NS; ++i) {
       const float p = fexp2(s[i] - m_run);
       l_run += p;
       pv[i] = p * nv[i];
     }
-    u4 pb;
+    uint32_t d[NS / 2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NS / 2; ++j) {
       const hx2 h = __builtin_amdgcn_cvt_pkrtz(pv[2 * j], pv[2 * j + 1]);
       const float t0 = fmaf(-partf, (float)h[0], pv[2 * j]);
       const float t1 = fmaf(-partf, (float)h[1], pv[2 * j + 1]);
-      pb[j] = pk_rtz(t0, t1);
+      d[j] = pk_rtz(t0, t1);
+    }
+    u4 pb;
+    if constexpr (TS == 2) {
+      pb[0] = tile ? 0u : d[0];
+      pb[1] = tile ? 0u : d[1];
+      pb[2] = tile ? d[0] : 0u;
+      pb[3] = tile ? d[1] : 0u;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pb[j] = d[j];
     }
     return as_h8(pb);
   };
@@ -549,14 +587,15 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       const u4 kA = *reinterpret_cast<const u4*>(fs + r * (2 * FROW) + 64 * q4 + 16 * kb);
       sA = mfma(as_h8(kA), qf[kb], sA);
     }
-    float sc[8];
+    float sc[NS], ones[NS];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sc[i] = (sA[i] + row_ror<G>(sA[i])) * a.qscale;
-      if (4 * q4 + i >= nf) sc[i] = -INFINITY;
-      sc[4 + i] = -INFINITY;
+      const float full = (sA[i] + partner<G>(sA[i])) * a.qscale;
+      sc[i] = tile == 0 && 4 * q4 + i < nf ? full : -INFINITY;  // the tile-1 columns see no fp16 token
+      if constexpr (NS == 8) sc[4 + i] = -INFINITY;
     }
-    const float ones[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int i = 0; i < NS; ++i) ones[i] = 1.f;
     const half8 pb = softmax_pv(sc, ones, acc_o);
     u4 vv[8];  // values: dims 8r .. 8r+7 of tokens A0..A3 (k-slots of B0..B3 zero)
 #pragma unroll
@@ -576,9 +615,9 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     for (int i = 0; i < 4; ++i) {
       float vo[8];
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) vo[nb] = acc_o[nb][i] + row_ror<G>(acc_o[nb][i]);
-      if (r < G) {
-        float* d = reinterpret_cast<float*>(smem + Layout::opk) + r * FD + 32 * q4 + 8 * i;
+      for (int nb = 0; nb < 8; ++nb) vo[nb] = acc_o[nb][i] + partner<G>(acc_o[nb][i]);
+      if (writer && tile == 0) {
+        float* d = reinterpret_cast<float*>(smem + Layout::opk) + hd * FD + 32 * q4 + 8 * i;
         *reinterpret_cast<float4*>(d) = make_float4(vo[0], vo[1], vo[2], vo[3]);
         *reinterpret_cast<float4*>(d + 4) = make_float4(vo[4], vo[5], vo[6], vo[7]);
       }
@@ -630,10 +669,15 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     const int t0 = slot_t0(k);
     const int tend = blk0 + w + FW * k < blk1 ? comp : 0;
     *reinterpret_cast<float*>(nst + 4 * lane) = lane < 32 ? L.nk : L.nv;
-    const float4 nkA = *reinterpret_cast<const float4*>(nst + 16 * q4);
-    const float4 nkB = *reinterpret_cast<const float4*>(nst + 64 + 16 * q4);
-    const float4 nvA = *reinterpret_cast<const float4*>(nst + 128 + 16 * q4);
-    const float4 nvB = *reinterpret_cast<const float4*>(nst + 192 + 16 * q4);
+    // key / value norms of the lane's tokens: tile `tile` (TS == 2) or both
+    float nk[NS], nv[NS];
+#pragma unroll
+    for (int t = 0; t < 2 / TS; ++t) {
+      const float4 k4 = *reinterpret_cast<const float4*>(nst + 64 * (t + tile) + 16 * q4);
+      const float4 v4 = *reinterpret_cast<const float4*>(nst + 128 + 64 * (t + tile) + 16 * q4);
+      nk[4 * t] = k4.x; nk[4 * t + 1] = k4.y; nk[4 * t + 2] = k4.z; nk[4 * t + 3] = k4.w;
+      nv[4 * t] = v4.x; nv[4 * t + 1] = v4.y; nv[4 * t + 2] = v4.z; nv[4 * t + 3] = v4.w;
+    }
     // V^T operands (row = dim 8r + nb, k-slot pairs = token pairs of the
     // lane), looked up first: they depend only on the codes, and their LDS
     // latency then overlaps the scores and the softmax
@@ -662,30 +706,31 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       sA = mfma(as_h8(u4{ea0[0], ea0[1], ea1[0], ea1[1]}), qop[s], sA);
       sB = mfma(as_h8(u4{eb0[0], eb0[1], eb1[0], eb1[1]}), qop[s], sB);
     }
-    float sc[8];
-    const float nk[8] = {nkA.x, nkA.y, nkA.z, nkA.w, nkB.x, nkB.y, nkB.z, nkB.w};
+    float sc[NS];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sc[i] = (sA[i] + row_ror<G>(sA[i])) * nk[i];
-      sc[4 + i] = (sB[i] + row_ror<G>(sB[i])) * nk[4 + i];
+      if constexpr (TS == 2) {
+        const float sv = tile ? sB[i] : sA[i];
+        sc[i] = (sv + partner<G>(sv)) * nk[i];
+      } else {
+        sc[i] = (sA[i] + partner<G>(sA[i])) * nk[i];
+        sc[4 + i] = (sB[i] + partner<G>(sB[i])) * nk[4 + i];
+      }
     }
     if (t0 + 32 > tend) {  // uniform: only the last block of a sequence and empty slots mask
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (t0 + 4 * q4 + i >= tend) sc[i] = -INFINITY;
-        if (t0 + 16 + 4 * q4 + i >= tend) sc[4 + i] = -INFINITY;
-      }
+      for (int i = 0; i < NS; ++i)
+        if (t0 + 16 * (tile + (i >> 2)) + 4 * q4 + (i & 3) >= tend) sc[i] = -INFINITY;
     }
-    const float nv[8] = {nvA.x, nvA.y, nvA.z, nvA.w, nvB.x, nvB.y, nvB.z, nvB.w};
     const half8 pb = softmax_pv(sc, nv, acc_r);
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc_r[nb] = mfma(as_h8(va[nb]), pb, acc_r[nb]);
   }
 
   // ---- combine the 8 waves of this workgroup through LDS (the table region,
-  // free once every wave is past its blocks). Columns r and r + G hold the
-  // fp16 high part / remainder products of head r: one DPP row rotation by G
-  // adds them; lanes r < G then hold head r.
+  // free once every wave is past its blocks). The two fp16 parts of a (tile,
+  // head) meet through `partner`; the high-part column of each (tile, head)
+  // then writes row t * G + head (a virtual head: tiles keep separate maxima).
   l_run = rows_sum(l_run);
   __syncthreads();
   float* cm = reinterpret_cast<float*>(smem + Layout::cmb) + (w * 8) * CMS;  // [wave][head][CMS]
@@ -694,14 +739,14 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   for (int i = 0; i < 4; ++i) {
     float vr[8];
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) vr[nb] = acc_r[nb][i] + row_ror<G>(acc_r[nb][i]);
-    if (r < G) {
-      float* d = cm + r * CMS + 32 * q4 + 8 * i;
+    for (int nb = 0; nb < 8; ++nb) vr[nb] = acc_r[nb][i] + partner<G>(acc_r[nb][i]);
+    if (writer) {
+      float* d = cm + (tile * G + hd) * CMS + 32 * q4 + 8 * i;
       *reinterpret_cast<float4*>(d) = make_float4(vr[0], vr[1], vr[2], vr[3]);
       *reinterpret_cast<float4*>(d + 4) = make_float4(vr[4], vr[5], vr[6], vr[7]);
     }
   }
-  if (lane < G) *reinterpret_cast<float4*>(cl + 4 * lane) = make_float4(m_run, l_run, m_orig, 0.f);
+  if (q4 == 0 && writer) *reinterpret_cast<float4*>(cl + 4 * (tile * G + hd)) = make_float4(m_run, l_run, m_orig, 0.f);
   __syncthreads();
   // thread (head, dim): merge the 8 waves into the workgroup's rotated sum
   // and original-space sum at the workgroup max M, both divided by the
@@ -717,15 +762,19 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       const int h = e / FD, j = e % FD;
       float M = M_INIT;
 #pragma unroll
-      for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, cls[ww * 32 + 4 * h]);
+      for (int ww = 0; ww < FW; ++ww)
+#pragma unroll
+        for (int t = 0; t < TS; ++t) M = fmaxf(M, cls[ww * 32 + 4 * (t * G + h)]);
       float sr = 0.f, L = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < FW; ++ww) {
-        const float4 st = *reinterpret_cast<const float4*>(cls + ww * 32 + 4 * h);
-        const float sc = fexp2(st.x - M);
-        sr = fmaf(sc, cms[(ww * 8 + h) * CMS + j], sr);
-        L = fmaf(sc, st.y, L);
-      }
+      for (int ww = 0; ww < FW; ++ww)
+#pragma unroll
+        for (int t = 0; t < TS; ++t) {
+          const float4 st = *reinterpret_cast<const float4*>(cls + ww * 32 + 4 * (t * G + h));
+          const float sc = fexp2(st.x - M);
+          sr = fmaf(sc, cms[(ww * 8 + t * G + h) * CMS + j], sr);
+          L = fmaf(sc, st.y, L);
+        }
       float so = 0.f;
       if (wg_has_fp16) {
         // original-space part of the last wave, parked at its max then

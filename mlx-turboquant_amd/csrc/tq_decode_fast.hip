@@ -6,8 +6,8 @@
 //    32): wave w takes blocks c*bpw + w + 8k, k < 4, with two blocks' loads in
 //    flight while it computes;
 //  - the fp16 tokens [c*fpw, (c+1)*fpw) (fpw <= 16) of the sequence's [sink |
-//    residual ring] list, staged in LDS during set-up and scored by the last
-//    wave before its compressed blocks.
+//    residual ring] list, staged in LDS during set-up and scored by wave 0
+//    (the first to be issued on its SIMD) before its compressed blocks.
 //
 // Scores are computed transposed, S^T = K q^T (MFMA 16x16x32 f16):
 //   A = 16 tokens x 32 k-slots of keys, B = 32 k-slots x 16 columns of queries.
@@ -68,6 +68,7 @@ constexpr int NPW = FAST_BLOCKS_PER_WAVE; // compressed blocks per wave
 constexpr int MAXWG = FAST_MAX_WG;        // workgroups per (sequence, kv head)
 constexpr int FROW = 272;                 // LDS row of a staged fp16 token (256 + 16 against bank conflicts)
 constexpr float M_INIT = -1e30f;          // running max before the first block
+constexpr int WF16 = 0;                   // the wave that scores the staged fp16 tokens
 constexpr int NCP = 32;                   // table replicas per entry (lane % 32: one per lane of an LDS pass)
 // A block whose max exceeds the running max m raises m to that max + this
 // margin (base-2 units), so later blocks rarely trigger a rescale; weights
@@ -566,9 +567,9 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     return as_h8(pb);
   };
 
-  // ---- the staged fp16 tokens (sink / residual ring, original space): the
-  // last wave, before its compressed blocks
-  if (w == FW - 1 && nf > 0) {
+  // ---- the staged fp16 tokens (sink / residual ring, original space): wave
+  // WF16, before its compressed blocks
+  if (w == WF16 && nf > 0) {
     half8 qf[4];
     {
       const uint8_t* src = smem + Layout::qfo + ((uint32_t)(hd * 2 + (partf != 0.f ? 1 : 0)) * 4 + q4) * 4 * 16;
@@ -729,9 +730,18 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
 
   // ---- combine the 8 waves of this workgroup through LDS (the table region,
   // free once every wave is past its blocks). The two fp16 parts of a (tile,
-  // head) meet through `partner`; the high-part column of each (tile, head)
-  // then writes row t * G + head (a virtual head: tiles keep separate maxima).
+  // head) meet through `partner`; for TS == 2 the two tiles of a head (columns
+  // r and r ^ 8) are then merged at their common max by a rotation by 8, and
+  // the high-part column of tile 0 writes the head's row.
   l_run = rows_sum(l_run);
+  float tsc = 1.f;  // scale of this lane's tile state to the merged max
+  if constexpr (TS == 2) {
+    const float m2 = fmaxf(m_run, row_ror<8>(m_run));
+    tsc = fexp2(m_run - m2);
+    l_run *= tsc;
+    l_run += row_ror<8>(l_run);
+    m_run = m2;
+  }
   __syncthreads();
   float* cm = reinterpret_cast<float*>(smem + Layout::cmb) + (w * 8) * CMS;  // [wave][head][CMS]
   float* cl = reinterpret_cast<float*>(smem + Layout::cml) + w * 32;        // [wave][head][4]
@@ -739,14 +749,21 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   for (int i = 0; i < 4; ++i) {
     float vr[8];
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) vr[nb] = acc_r[nb][i] + partner<G>(acc_r[nb][i]);
-    if (writer) {
-      float* d = cm + (tile * G + hd) * CMS + 32 * q4 + 8 * i;
+    for (int nb = 0; nb < 8; ++nb) {
+      float x = acc_r[nb][i] + partner<G>(acc_r[nb][i]);
+      if constexpr (TS == 2) {
+        x *= tsc;
+        x += row_ror<8>(x);
+      }
+      vr[nb] = x;
+    }
+    if (writer && tile == 0) {
+      float* d = cm + hd * CMS + 32 * q4 + 8 * i;
       *reinterpret_cast<float4*>(d) = make_float4(vr[0], vr[1], vr[2], vr[3]);
       *reinterpret_cast<float4*>(d + 4) = make_float4(vr[4], vr[5], vr[6], vr[7]);
     }
   }
-  if (q4 == 0 && writer) *reinterpret_cast<float4*>(cl + 4 * (tile * G + hd)) = make_float4(m_run, l_run, m_orig, 0.f);
+  if (q4 == 0 && writer && tile == 0) *reinterpret_cast<float4*>(cl + 4 * hd) = make_float4(m_run, l_run, m_orig, 0.f);
   __syncthreads();
   // thread (head, dim): merge the 8 waves into the workgroup's rotated sum
   // and original-space sum at the workgroup max M, both divided by the
@@ -762,23 +779,19 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
       const int h = e / FD, j = e % FD;
       float M = M_INIT;
 #pragma unroll
-      for (int ww = 0; ww < FW; ++ww)
-#pragma unroll
-        for (int t = 0; t < TS; ++t) M = fmaxf(M, cls[ww * 32 + 4 * (t * G + h)]);
+      for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, cls[ww * 32 + 4 * h]);
       float sr = 0.f, L = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < FW; ++ww)
-#pragma unroll
-        for (int t = 0; t < TS; ++t) {
-          const float4 st = *reinterpret_cast<const float4*>(cls + ww * 32 + 4 * (t * G + h));
-          const float sc = fexp2(st.x - M);
-          sr = fmaf(sc, cms[(ww * 8 + t * G + h) * CMS + j], sr);
-          L = fmaf(sc, st.y, L);
-        }
+      for (int ww = 0; ww < FW; ++ww) {
+        const float4 st = *reinterpret_cast<const float4*>(cls + ww * 32 + 4 * h);
+        const float sc = fexp2(st.x - M);
+        sr = fmaf(sc, cms[(ww * 8 + h) * CMS + j], sr);
+        L = fmaf(sc, st.y, L);
+      }
       float so = 0.f;
       if (wg_has_fp16) {
-        // original-space part of the last wave, parked at its max then
-        const float mo = cls[(FW - 1) * 32 + 4 * h + 2];
+        // original-space part of wave WF16, parked at its max then
+        const float mo = cls[WF16 * 32 + 4 * h + 2];
         so = mo > M_INIT ? fexp2(mo - M) * opk[h * FD + j] : 0.f;
       }
       const float inv = L > 0.f ? 1.f / L : 0.f;

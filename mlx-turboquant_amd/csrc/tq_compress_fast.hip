@@ -24,10 +24,10 @@
 //      so lane (vector n = l & 15, g = l >> 4) ends up holding the 8
 //      consecutive dims 32w + 8g .. 32w + 8g + 7 of vector n;
 //   4. coordinates are scaled and quantized (count of boundaries below, ties
-//      low, NaN -> 0; codebook.py:220-223) through a 64-cell table (cell
-//      width 1/64; with at most one boundary per cell, code = base +
-//      (y > boundary); a codebook that puts two boundaries in one cell is
-//      counted instead);
+//      low, NaN -> 0; codebook.py:220-223) through a cell table (cell width
+//      1/64 over |y| <= 1 plus a margin, so a cell index never needs a clamp;
+//      with at most one boundary per cell, code = base + (y > boundary); a
+//      codebook that puts two boundaries in one cell is counted instead);
 //   5. the lane's 8 codes form 8*BITS consecutive bits of the LSB-first row
 //      bitstream (packing.py); lanes assemble whole dwords and store them.
 
@@ -49,7 +49,11 @@ constexpr int CT = 64;         // vectors per tile
 constexpr int CTHR = 256;      // threads per workgroup (4 waves)
 constexpr int XS = 272;        // LDS row stride of the x tile, bytes (256 + 16: conflict-free b128 reads)
 constexpr float RSC = 256.f;   // scale of R before the fp16 split
-constexpr int NCELL = 64;      // quantizer cells: c = round(64 y + 32) clamped to [0, 63]
+// Quantizer cells c = round(64 y + 32), c in [CELL_LO, CELL_LO + NCELL): y is
+// a coordinate of a unit vector (|y| <= 1 up to rounding, so c in [-32, 96]),
+// or 0 for a vector whose norm is not finite
+constexpr int CELL_LO = -40;
+constexpr int NCELL = 144;
 constexpr float MAGIC = 12582912.f;  // 1.5 * 2^23: fma(y, 64, 32 + MAGIC) holds round(64 y + 32) in its low bits
 constexpr uint32_t MAGIC_BITS = 0x4B400000u;
 
@@ -96,16 +100,21 @@ struct QCell {
   uint32_t base;  // boundaries below every value of the cell
 };
 
-// code of a finite y from the cell table at LDS byte offset `tbl_adj` +
-// 8 * MAGIC_BITS (smem is the kernel's only LDS object, at offset 0; the
-// magic bias is folded into the base so the cell address is one shift-add);
-// non-finite y only occur in vectors with a non-finite norm, whose codes are
-// set to 0 by the caller
+// code of y (|y| <= 1 + 2^-20) from the cell table at LDS byte offset
+// `tbl_adj` + 8 * (MAGIC_BITS + CELL_LO) (smem is the kernel's only LDS
+// object, at offset 0; the magic bias and the first cell are folded into the
+// base so the cell address is one shift-add)
 __device__ inline uint32_t quant_table(float y, const uint8_t* smem, uint32_t tbl_adj) {
-  const int r = (int)__float_as_uint(fmaf(y, 64.f, 32.f + MAGIC));
-  const uint32_t rc = (uint32_t)min(max(r, (int)MAGIC_BITS), (int)MAGIC_BITS + NCELL - 1);
-  const QCell q = *reinterpret_cast<const QCell*>(smem + (tbl_adj + 8u * rc));
+  const uint32_t r = __float_as_uint(fmaf(y, 64.f, 32.f + MAGIC));
+  const QCell q = *reinterpret_cast<const QCell*>(smem + (tbl_adj + 8u * r));
   return q.base + (y > q.bnd ? 1u : 0u);
+}
+
+// a * b with 0 * anything = 0 (also for an infinite or NaN a)
+__device__ inline float mul_zero_wins(float a, float b) {
+  float r;
+  asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
 }
 
 template <int BH, int BL>
@@ -127,13 +136,13 @@ __global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, 
     const int cb = tid >> 4, k = tid & 15;
     reinterpret_cast<float*>(smem + L_BND)[tid] = k < (cb ? NBL : NBH) ? (cb ? a.bnd_lo : a.bnd_hi)[k] : 0.f;
   }
-  if (tid < 2 * NCELL) {
-    const int cb = tid / NCELL, c = tid % NCELL;
+  for (int i = tid; i < 2 * NCELL; i += CTHR) {
+    const int cb = i / NCELL, ci = i % NCELL, c = CELL_LO + ci;
     const float* bp = cb ? a.bnd_lo : a.bnd_hi;
     const int nb = cb ? NBL : NBH;
     const float eps = 0x1p-20f;  // > the rounding of the cell index near a cell edge, in y units
-    const float lo = c == 0 ? -INFINITY : ((float)c - 32.5f) * (1.f / 64.f) - eps;
-    const float hi = c == NCELL - 1 ? INFINITY : ((float)c - 31.5f) * (1.f / 64.f) + eps;
+    const float lo = ci == 0 ? -INFINITY : ((float)c - 32.5f) * (1.f / 64.f) - eps;
+    const float hi = ci == NCELL - 1 ? INFINITY : ((float)c - 31.5f) * (1.f / 64.f) + eps;
     uint32_t base = 0, amb = 0;
     float bnd = INFINITY;
     for (int k = 0; k < nb; ++k) {
@@ -141,7 +150,7 @@ __global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, 
       if (b < lo) ++base;
       else if (b <= hi) { ++amb; bnd = b; }
     }
-    QCell* q = reinterpret_cast<QCell*>(smem + L_QT) + cb * NCELL + c;
+    QCell* q = reinterpret_cast<QCell*>(smem + L_QT) + cb * NCELL + ci;
     q->bnd = bnd;
     q->base = base;
     if (amb > 1) atomicOr(flag, 1u);
@@ -169,7 +178,7 @@ __global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, 
     }
   __syncthreads();
   const bool table = *flag == 0u;
-  const uint32_t qtab_adj = L_QT + (whi ? 0u : NCELL * 8u) - 8u * MAGIC_BITS;  // wraps: see quant_table
+  const uint32_t qtab_adj = L_QT + (whi ? 0u : NCELL * 8u) - 8u * (MAGIC_BITS + (uint32_t)CELL_LO);  // wraps: see quant_table
 
   // next non-empty tile at or after `id` in this workgroup's sequence
   auto make_tile = [&](int id) {
@@ -287,7 +296,7 @@ __global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, 
       for (int n2 = 0; n2 < 2; ++n2)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float y = acc.v[s4][n2][e] * sc;
+          const float y = mul_zero_wins(acc.v[s4][n2][e], sc);  // 0 for a non-finite norm (sc = 0)
           uint32_t c;
           if constexpr (TABLE) {
             c = quant_table(y, smem, qtab_adj);

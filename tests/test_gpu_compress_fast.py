@@ -83,6 +83,26 @@ def test_nan_vector_codes_zero():
     assert not np.any((got != ref.idx) & ~ref.near)
 
 
+@pytest.mark.parametrize("bits", [4, 3, 2, 3.5])
+def test_axis_vectors_and_infinities(bits):
+    """Vectors along rotated axes (x = +-s R_j, so y_j = +-1: the outermost
+    quantizer cells) and vectors holding an infinity (norm inf, codes 0)."""
+    R = O.rotation_matrix(128)
+    rows = [0, 1, 37, 64, 100, 127]
+    x = np.concatenate([np.stack([R[j] * sg * sc for j in rows]) for sg in (1.0, -1.0) for sc in (1.0, 300.0)])
+    x = x.astype(np.float16)[None, None]
+    mism, outside, ulp1, total, norms_eq, _ = code_parity(x, bits)
+    print(f"bits={bits}: axis vectors, mismatches {mism}/{total} (outside band {outside})")
+    assert norms_eq and outside == 0
+    y = _x((1, 1, 8, 128), seed=11)
+    y[0, 0, 2, 7] = np.inf
+    y[0, 0, 5, 0] = -np.inf
+    ch, cl, n, _, _ = gpu_compress(y, bits)
+    assert np.isinf(n[0, 0, 2]) and np.isinf(n[0, 0, 5])
+    for t in (2, 5):
+        assert not ch[0, 0, t].any() and (cl is None or not cl[0, 0, t].any())
+
+
 def test_fast_and_general_kernels_agree():
     """Both kernels against the oracle on the same input, and with each other
     outside the band."""

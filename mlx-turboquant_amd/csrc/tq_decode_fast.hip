@@ -661,11 +661,9 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
     // overlap one block's lookups with the previous block's softmax); a slot
     // past the wave's blocks masks all its tokens. Block k + 2 (or, past the
     // last block, R^T) is requested as slot k starts, so two blocks stay in
-    // flight while slot k computes; the scheduling barrier keeps those loads
-    // ahead of every wait of slot k.
+    // flight while slot k computes.
     if (k + 2 < NPW) load_slot(k + 2);
     if (k + 2 == NPW) load_rt();
-    __builtin_amdgcn_sched_barrier(0);
     const Blk& L = B[k];
     const int t0 = slot_t0(k);
     const int tend = blk0 + w + FW * k < blk1 ? comp : 0;

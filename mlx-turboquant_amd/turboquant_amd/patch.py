@@ -12,6 +12,18 @@ Outlier detection runs the reference's 5-token probe (patch.py:89-133)
 through ``model.turboquant_probe(tokens)`` when the model defines it (it
 returns one (B, H, T, D) key tensor per layer), else through a Hugging Face
 forward with ``use_cache=True``.
+
+Hybrid and sliding-window models (patch.py:228-321): layers whose attention
+is linear (a ``linear_attn`` / ``linear_attention`` module and no
+``self_attn`` / ``attention``, or ``config.layer_types`` entry
+``"linear_attention"``) and layers whose model-default cache is a
+sliding-window one keep the model's default cache. The defaults come from a
+class-level ``make_cache`` when the model class defines one (the reference's
+rule), else from the Hugging Face config (``layer_types`` /
+``sliding_window`` / ``use_sliding_window`` / ``max_window_layers``):
+``SlidingWindowKVCache`` for sliding-window layers, ``None`` for
+linear-attention layers (their state belongs to the model), ``FP16KVCache``
+otherwise.
 """
 
 from __future__ import annotations
@@ -49,6 +61,117 @@ class FP16KVCache:
 
     def size(self):
         return self.offset
+
+
+class SlidingWindowKVCache:
+    """fp16 cache of a sliding-window-attention layer: attention sees the last
+    ``max_size`` tokens (the role of mlx-lm's ``RotatingKVCache``, which the
+    reference leaves on such layers, patch.py:270-321). ``update_and_fetch``
+    returns the kept tokens plus the new ones; ``make_mask`` gives the matching
+    causal window mask."""
+
+    def __init__(self, max_size: int):
+        if max_size <= 0:
+            raise ValueError("max_size must be positive")
+        self.max_size = max_size
+        self.keys = self.values = None
+        self.offset = 0
+
+    def update_and_fetch(self, keys, values):
+        if self.keys is None:
+            k, v = keys, values
+        else:
+            k = torch.cat([self.keys, keys], dim=2)
+            v = torch.cat([self.values, values], dim=2)
+        self.offset += keys.shape[2]
+        self.keys, self.values = k[:, :, -self.max_size:], v[:, :, -self.max_size:]
+        return k, v
+
+    def make_mask(self, N, offset=None, return_array=False, window_size=None):
+        """Mask of N queries starting at absolute position ``offset`` (default
+        the tokens cached so far) over the keys the next ``update_and_fetch``
+        returns: True where query i may see key j (causal, within the
+        window). None when every key is visible to a single query."""
+        off = self.offset if offset is None else offset
+        win = window_size or self.max_size
+        kept = min(off, self.max_size)
+        if N == 1 and kept < win and not return_array:
+            return None
+        q = off + torch.arange(N).unsqueeze(1)                   # absolute query positions
+        kpos = off - kept + torch.arange(kept + N).unsqueeze(0)  # absolute key positions
+        return (kpos <= q) & (q - kpos < win)
+
+    def empty(self):
+        return self.keys is None
+
+    def size(self):
+        return self.offset
+
+
+def _config_of(model):
+    for cand in (model, getattr(model, "model", None), getattr(model, "language_model", None)):
+        if cand is None:
+            continue
+        c = getattr(cand, "config", None) or getattr(cand, "args", None)
+        if c is not None:
+            return c
+    return None
+
+
+def _model_layers(model) -> list:
+    inner = getattr(model, "model", model)
+    layers = getattr(inner, "layers", None)
+    if layers is None:
+        layers = getattr(model, "layers", None)
+    return list(layers or [])
+
+
+def linear_attention_layers(model) -> set[int]:
+    """Layers with linear attention (patch.py:228-260): a ``linear_attn`` /
+    ``linear_attention`` module and no ``self_attn`` / ``attention`` module,
+    or ``"linear_attention"`` in the config's ``layer_types``."""
+    out = set()
+    for i, layer in enumerate(_model_layers(model)):
+        if hasattr(layer, "linear_attn") or hasattr(layer, "linear_attention"):
+            if not (hasattr(layer, "self_attn") or hasattr(layer, "attention")):
+                out.add(i)
+    kinds = getattr(_config_of(model), "layer_types", None)
+    if kinds:
+        out |= {i for i, t in enumerate(kinds) if t == "linear_attention"}
+    return out
+
+
+def _config_default_caches(model, num_layers: int, linear: set[int]) -> list:
+    """The model-default cache of every layer from a Hugging Face config
+    (``linear``: the linear-attention layers)."""
+    cfg = _config_of(model)
+    if cfg is None:
+        raise ValueError("no model config")
+    window = getattr(cfg, "sliding_window", None)
+    kinds = getattr(cfg, "layer_types", None)
+    if not kinds:
+        use = getattr(cfg, "use_sliding_window", None)
+        first = getattr(cfg, "max_window_layers", None)
+        if window and use is not False and (use or first is None):
+            kinds = ["sliding_attention" if first is None or i >= first else "full_attention"
+                     for i in range(num_layers)]
+        else:
+            kinds = ["full_attention"] * num_layers
+    out = []
+    for i in range(num_layers):
+        t = kinds[i] if i < len(kinds) else "full_attention"
+        if i in linear or t == "linear_attention":
+            out.append(None)
+        elif t == "sliding_attention" and window:
+            out.append(SlidingWindowKVCache(int(window)))
+        else:
+            out.append(FP16KVCache())
+    return out
+
+
+def _is_sliding_cache(c) -> bool:
+    """The reference tests for mlx-lm's RotatingKVCache family (patch.py:262-300)."""
+    return isinstance(c, SlidingWindowKVCache) or "Rotating" in type(c).__name__
 
 
 def _get_model_config(model) -> dict:
@@ -148,10 +271,39 @@ def apply_turboquant(model, key_bits: float = 4, value_bits: float = 2, residual
         except Exception:
             pass  # detection failure compresses every layer (patch.py:221-226)
 
+    # hybrid (linear-attention) and sliding-window layers keep the model's own
+    # cache type (patch.py:228-321)
+    linear_layers = linear_attention_layers(model)
+    if linear_layers:
+        warnings.warn(f"Detected {len(linear_layers)} linear-attention layers in model (hybrid architecture, "
+                      f"e.g. Qwen3.5). These layers will use the model's default cache type instead of "
+                      f"TurboQuantKVCache.", UserWarning, stacklevel=2)
+    class_make_cache = getattr(type(model), "make_cache", None)  # captured before the instance attribute
+
+    def default_caches():
+        if class_make_cache is not None:
+            return list(class_make_cache(model))
+        return _config_default_caches(model, nl, linear_layers)
+
+    swa_layers = set()
+    try:
+        for i, c in enumerate(default_caches()):
+            if i not in linear_layers and _is_sliding_cache(c):
+                swa_layers.add(i)
+    except Exception:
+        pass
+    if swa_layers:
+        warnings.warn(f"Detected {len(swa_layers)} sliding-window-attention layers in model. These layers will "
+                      f"use the model's default cache type instead of TurboQuantKVCache.", UserWarning, stacklevel=2)
+    default_layers = linear_layers | swa_layers
+
     def make_cache():
+        defaults = default_caches() if default_layers else None
         caches = []
         for i in range(nl):
-            if i in layers_to_skip:
+            if i in default_layers:
+                caches.append(defaults[i] if i < len(defaults) else None)
+            elif i in layers_to_skip:
                 caches.append(FP16KVCache())
             else:
                 caches.append(TurboQuantKVCache(
@@ -166,7 +318,7 @@ def apply_turboquant(model, key_bits: float = 4, value_bits: float = 2, residual
         "head_dim": hd, "num_kv_heads": nkv, "num_layers": nl, "key_bits": key_bits,
         "value_bits": value_bits, "residual_window": residual_window, "fp16_sink_size": fp16_sink_size,
         "chunk_size": chunk_size, "qjl_correction": qjl_correction, "qjl_n_proj": qjl_n_proj,
-        "skip_layers": sorted(layers_to_skip),
+        "skip_layers": sorted(layers_to_skip), "default_cache_layers": sorted(default_layers),
     }
     return model
 

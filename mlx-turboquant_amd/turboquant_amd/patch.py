@@ -209,6 +209,8 @@ def _probe_layer_keys(model) -> list:
     pkv = getattr(out, "past_key_values", None)
     if pkv is None:
         raise ValueError("model returned no key cache")
+    if hasattr(pkv, "layers"):  # transformers >= 4.56 Cache: one layer object per decoder layer
+        return [getattr(layer, "keys", None) for layer in pkv.layers]
     if hasattr(pkv, "key_cache"):
         return list(pkv.key_cache)
     return [kv[0] for kv in pkv]

@@ -22,8 +22,11 @@ same counters on a copy of known size; read from the committed summary.
 
 Also reported: compress throughput on configs[2] (131072-token prefill drained
 in 4096-token chunks, K3/V2 and K3.5/V3.5), the roofline of the decode
-attention call, and a CPU baseline (float32 numpy restatement of the
-reference's per-step path: dense concat + SDPA) on a bounded sample.
+attention call, the configs[3] 36-layer outlier-stress step (30 packed layers
++ 6 fp16 layers) and the configs[4] ragged layer-step (one-token drains +
+attention over 16 sequences, with and without the QJL sketch), and a CPU
+baseline (float32 numpy restatement of the reference's per-step path: dense
+concat + SDPA) on a bounded sample.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
@@ -133,6 +136,105 @@ def bench_compress(dev, kb, vb, total=131072, chunk=4096, reps=3):
     per_vec = 256 + (c._kc.row_hi + c._kc.row_lo + 4 + c._vc.row_hi + c._vc.row_lo + 4) / 2
     return {"bits": f"K{kb}/V{vb}", "tokens": c._compressed_len, "vectors": n_vec, "ms": round(ms, 4),
             "vectors_per_s": n_vec / (ms * 1e-3), "GBps": n_vec * per_vec / (ms * 1e-3) / 1e9}
+
+
+def bench_config3(dev, reps: int = 5, warmup: int = 2):
+    """one decode step of a 36-layer Qwen3-8B-shaped model
+    (Hq=32, Hkv=8, D=128) at T=65536 where the outlier rule kept 6 seeded
+    layers in fp16: 30 fused K4/V2 attend calls (sink 128, window 128) and 6
+    torch SDPA calls over the fp16 K/V (the reference hands outlier layers a
+    plain KVCache and runs its SDPA on them). Captured in a HIP graph."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+    from turboquant_amd import TurboQuantKVCache
+    layers, T = 36, 65536
+    fp16_layers = set(np.random.RandomState(3).choice(layers, 6, replace=False).tolist())
+    caches, kvs, qs, outs = [], [], [], []
+    for l in range(layers):
+        g = torch.Generator(device=dev).manual_seed(2000 + l)
+        k = torch.randn(1, 8, T, 128, generator=g, device=dev).half()
+        v = torch.randn(1, 8, T, 128, generator=g, device=dev).half()
+        if l in fp16_layers:
+            caches.append(None)
+            kvs.append((k, v))
+        else:
+            c = TurboQuantKVCache(head_dim=128, num_kv_heads=8, key_bits=4, value_bits=2,
+                                  residual_window=128, fp16_sink_size=128)
+            c.update(k, v)
+            del k, v
+            caches.append(c)
+            kvs.append(None)
+        qs.append(torch.randn(1, 32, 1, 128, generator=g, device=dev).half())
+        outs.append(torch.empty(1, 32, 1, 128, dtype=torch.float32, device=dev))
+
+    def run(packed=True, fp16=True):
+        def fn():
+            for c, kv, q, o in zip(caches, kvs, qs, outs):
+                if c is not None and packed:
+                    c.attend(q, out=o)
+                elif kv is not None and fp16:
+                    F.scaled_dot_product_attention(q, kv[0], kv[1], enable_gqa=True)
+        return fn
+
+    ms, _, _ = time_graph(run(), reps, warmup)
+    ms_p, _, _ = time_graph(run(fp16=False), reps, warmup)
+    ms_f, _, _ = time_graph(run(packed=False), reps, warmup)
+    b_packed = sum(decode_bytes_per_layer(c, 32) for c in caches if c is not None)
+    b_fp16 = len(fp16_layers) * (2 * 8 * T * 128 * 2 + 32 * 128 * 2 * 2)
+    return {"workload": "configs[3]: 36 layers, Hq=32 Hkv=8 D=128, T=65536; 30 K4/V2 layers (sink 128, window "
+                        "128) through the fused attend, 6 fp16 outlier layers through torch SDPA; one graph",
+            "ms_per_step": round(ms, 4), "bytes_per_step": b_packed + b_fp16,
+            "GBps": round((b_packed + b_fp16) / (ms * 1e-3) / 1e9, 1),
+            "packed_layers_ms": round(ms_p, 4), "packed_GBps": round(b_packed / (ms_p * 1e-3) / 1e9, 1),
+            "fp16_layers_ms": round(ms_f, 4), "fp16_GBps": round(b_fp16 / (ms_f * 1e-3) / 1e9, 1)}
+
+
+def bench_config4(dev, steps: int = 12):
+    """one layer-step of 16 ragged Llama-3.1-8B-shaped sequences
+    (lengths ~ U[4096, 32768], seeded), K4/V2, the reference's defaults
+    (window 128, no sink): append one token per sequence, drain one per
+    sequence into the packed store (one ragged compress launch per side),
+    fused decode attention over every sequence in one launch. With the QJL
+    sketch (m = 128) attention runs on the general kernel; without it on the
+    K4/V2 kernels. Eager launches, events around each step."""
+    import numpy as np
+    import torch
+    from turboquant_amd.ragged import RaggedKVBatch
+    lens = np.random.RandomState(4).randint(4096, 32769, size=16)
+    res = {"workload": "configs[4]: 16 ragged sequences ~U[4096,32768], Hq=32 Hkv=8 D=128, K4/V2, window 128, "
+                       "no sink; per layer-step: one-token drain per sequence + one attention launch"}
+    for qjl_m in (128, 0):
+        rb = RaggedKVBatch(16, 8, 128, 4, 2, residual_window=128, fp16_sink_size=0, qjl_n_proj=qjl_m, device=dev)
+        g = torch.Generator(device=dev).manual_seed(5)
+        for b, T in enumerate(lens):
+            rb.load(b, torch.randn(8, int(T), 128, generator=g, device=dev).half(),
+                    torch.randn(8, int(T), 128, generator=g, device=dev).half())
+        q = torch.randn(16, 32, 128, generator=g, device=dev).half()
+        out = torch.empty(16, 32, 128, dtype=torch.float32, device=dev)
+        kv = [(torch.randn(16, 8, 128, generator=g, device=dev).half(),
+               torch.randn(16, 8, 128, generator=g, device=dev).half()) for _ in range(steps + 2)]
+        t_step, t_attn = [], []
+        for i, (k, v) in enumerate(kv):
+            e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            e0.record()
+            rb.step(k, v)
+            e1.record()
+            rb.attend(q, out=out)
+            e2.record()
+            torch.cuda.synchronize()
+            if i >= 2:
+                t_step.append(e0.elapsed_time(e2))
+                t_attn.append(e1.elapsed_time(e2))
+        per_tok = sum(c.row_hi + c.row_lo + 4 + (c.row_sign + 4 if qjl_m else 0) for c in (rb.kc, rb.vc))
+        byt = 8 * (int(rb.comp_len.sum()) * per_tok + int(rb.res_len.sum()) * 512) + 16 * 32 * 128 * 6
+        ms_s, ms_a = float(np.median(t_step)), float(np.median(t_attn))
+        res["qjl" if qjl_m else "no_qjl"] = {
+            "kernel": "general (chunk_kernel)" if qjl_m else "K4/V2 (fast_decode_kernel + merge)",
+            "layer_step_us": round(ms_s * 1e3, 1), "attend_us": round(ms_a * 1e3, 1),
+            "attend_bytes": byt, "attend_GBps": round(byt / (ms_a * 1e-3) / 1e9, 1)}
+        del rb
+    return res
 
 
 def cpu_baseline(caches, qs, budget_s: float = 12.0):
@@ -249,6 +351,7 @@ def main():
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compress", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the configs[3] / configs[4] timings")
     ap.add_argument("--pmc-workload", action="store_true", help="short program for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -318,6 +421,12 @@ def main():
         comp = [bench_compress(dev, 3, 2), bench_compress(dev, 3.5, 3.5)]
         result["compress"] = comp
         result["compress_vectors_per_s"] = round(comp[0]["vectors_per_s"], 1)
+    if not args.no_extra:
+        log("timing configs[3] and configs[4]")
+        result["config3"] = bench_config3(dev)
+        torch.cuda.empty_cache()
+        result["config4"] = bench_config4(dev)
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         log("timing CPU baseline")
         per_layer, threads, n, cpu_vps = cpu_baseline(caches, qs)

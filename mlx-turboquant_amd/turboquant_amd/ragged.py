@@ -1,0 +1,183 @@
+"""Ragged decode batches: B sequences of different lengths served by one
+compress launch and one attention launch per step.
+
+The reference's cache holds one length for the whole batch (cache.py:19-116).
+Serving sequences of different lengths together needs per-sequence lengths,
+which the C ABI takes as arrays: ``tq_span`` n_tok_b / src_tok0_b /
+dst_tok0_b for the drain (tq_compress), ``tq_attn_desc`` comp_len / sink_len /
+res_len / res_start for attention (tq_decode_attention).
+
+Each sequence keeps the layout of ``TurboQuantKVCache``: [fp16 sink |
+compressed | fp16 residual window]. The batch shares one packed store per
+side (rows of every sequence at their own lengths), one fp16 sink buffer and
+one residual ring of window + 1 slots per sequence. A step appends one token
+per sequence; a sequence whose window is full drains its oldest residual
+token into the store in the same launch as the others (the reference's
+chunk_size = 1 policy, cache.py:529-533). The first ``fp16_sink_size``
+tokens of a sequence go to the sink (cache.py:577-618).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _codec, _lib
+from .cache import _workspace
+from .rotation import DEFAULT_SEED
+
+
+def _i32(xs, dev) -> torch.Tensor:
+    return torch.tensor(np.asarray(xs, np.int32), dtype=torch.int32, device=dev)
+
+
+class RaggedKVBatch:
+    """``batch`` sequences of one layer, ``num_kv_heads`` kv heads each."""
+
+    def __init__(self, batch: int, num_kv_heads: int, head_dim: int = 128, key_bits: float = 4,
+                 value_bits: float = 2, residual_window: int = 128, fp16_sink_size: int = 0,
+                 qjl_n_proj: int = 0, rotation_seed: int = DEFAULT_SEED, device=None):
+        if residual_window < 1:
+            raise ValueError("residual_window must be >= 1")
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.device = dev
+        self.B, self.H, self.D = batch, num_kv_heads, head_dim
+        self.window, self.sink = residual_window, fp16_sink_size
+        self.cap = residual_window + 1  # ring slots
+        self.qjl = qjl_n_proj > 0
+        self.kc = _codec.get_codec(head_dim, key_bits, rotation_seed, qjl_n_proj, dev)
+        self.vc = _codec.get_codec(head_dim, value_bits, rotation_seed, qjl_n_proj, dev)
+        self.kstore = _codec.PackedStore(self.kc, batch, num_kv_heads, qjl=self.qjl)
+        self.vstore = _codec.PackedStore(self.vc, batch, num_kv_heads, qjl=self.qjl)
+        f16 = dict(dtype=torch.float16, device=dev)
+        self.sink_k = torch.zeros(batch, num_kv_heads, max(fp16_sink_size, 1), head_dim, **f16)
+        self.sink_v = torch.zeros_like(self.sink_k)
+        self.ring_k = torch.zeros(batch, num_kv_heads, self.cap, head_dim, **f16)
+        self.ring_v = torch.zeros_like(self.ring_k)
+        z = lambda: np.zeros(batch, dtype=np.int64)
+        self.sink_len, self.comp_len, self.res_len, self.res_start, self.offset = z(), z(), z(), z(), z()
+        self._keep = []  # per-sequence arrays of launches still in flight
+
+    # ------------------------------------------------------------------ fill
+    def load(self, b: int, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Fill the empty sequence ``b`` from its (H, T, D) keys / values: the
+        first fp16_sink_size tokens to the sink, the last residual_window of the
+        rest to the ring, the tokens between compressed (the state one-token
+        drains leave after T tokens)."""
+        if self.offset[b]:
+            raise ValueError(f"sequence {b} is not empty")
+        H, T, D = keys.shape
+        if (H, D) != (self.H, self.D) or values.shape != keys.shape:
+            raise ValueError("keys / values must be (num_kv_heads, T, head_dim)")
+        k, v = keys.to(self.device, torch.float16), values.to(self.device, torch.float16)
+        s = min(T, self.sink)
+        r = min(T - s, self.window)
+        c = T - s - r
+        self.sink_k[b, :, :s] = k[:, :s]
+        self.sink_v[b, :, :s] = v[:, :s]
+        if c > 0:
+            self.kstore.reserve(c, int(self.comp_len.max()))
+            self.vstore.reserve(c, int(self.comp_len.max()))
+            for codec, x, store in ((self.kc, k, self.kstore), (self.vc, v, self.vstore)):
+                _codec.compress_into(codec, x[None, :, s:s + c].contiguous(), 0, c, self._row_view(store, b), 0)
+        self.ring_k[b, :, :r] = k[:, s + c:]
+        self.ring_v[b, :, :r] = v[:, s + c:]
+        self.sink_len[b], self.comp_len[b], self.res_len[b], self.res_start[b] = s, c, r, 0
+        self.offset[b] = T
+
+    @staticmethod
+    def _row_view(store: _codec.PackedStore, b: int) -> _codec.PackedStore:
+        """Store view of batch row b only (same capacity and strides)."""
+        view = object.__new__(_codec.PackedStore)
+        view.__dict__.update(store.__dict__)
+        view.batch = 1
+        for name in ("codes_hi", "codes_lo", "norms", "signs", "gamma"):
+            t = getattr(store, name)
+            setattr(view, name, None if t is None else t[b:b + 1])
+        return view
+
+    # ------------------------------------------------------------------ step
+    def step(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Append one token per sequence ((B, H, D) keys / values). Sequences
+        still filling their sink write there; the others append to their ring,
+        and a sequence whose ring then holds residual_window + 1 tokens drains
+        its oldest one into the store (one ragged launch per side)."""
+        B, H, D, dev = self.B, self.H, self.D, self.device
+        if keys.shape != (B, H, D) or values.shape != keys.shape:
+            raise ValueError("keys / values must be (batch, num_kv_heads, head_dim)")
+        keys, values = keys.to(dev, torch.float16), values.to(dev, torch.float16)
+        to_sink = self.offset < self.sink
+        if to_sink.any():
+            bi = np.nonzero(to_sink)[0]
+            pos = self.sink_len[bi]
+            bt, pt = torch.as_tensor(bi, device=dev), torch.as_tensor(pos, device=dev)
+            self.sink_k[bt, :, pt] = keys[bt]
+            self.sink_v[bt, :, pt] = values[bt]
+            self.sink_len[bi] += 1
+        bi = np.nonzero(~to_sink)[0]
+        if bi.size:
+            slot = (self.res_start[bi] + self.res_len[bi]) % self.cap
+            bt, st = torch.as_tensor(bi, device=dev), torch.as_tensor(slot, device=dev)
+            self.ring_k[bt, :, st] = keys[bt]
+            self.ring_v[bt, :, st] = values[bt]
+            self.res_len[bi] += 1
+        drain = self.res_len > self.window
+        if drain.any():
+            need = int((self.comp_len + drain).max())
+            self.kstore.reserve(need, int(self.comp_len.max()))
+            self.vstore.reserve(need, int(self.comp_len.max()))
+            n_b, src_b, dst_b = _i32(drain, dev), _i32(self.res_start, dev), _i32(self.comp_len, dev)
+            span = _lib.Span(rows=B * H, heads=H, n_tok=1, reserved=0, n_tok_b=n_b.data_ptr(),
+                             src_tok0_b=src_b.data_ptr(), dst_tok0_b=dst_b.data_ptr())
+            lib = _lib.load()
+            for codec, ring, store in ((self.kc, self.ring_k, self.kstore), (self.vc, self.ring_v, self.vstore)):
+                st = store.struct(0)
+                _lib.check(lib.tq_compress(codec.ref(), ring.data_ptr(), _lib.dtype_code(ring.dtype), self.cap * D,
+                                           ctypes.byref(span), ctypes.byref(st), _lib.stream_ptr(dev)), "tq_compress")
+            self._keep = [n_b, src_b, dst_b]  # freed after the next launch is ordered behind this one
+            self.comp_len += drain
+            self.res_start = np.where(drain, (self.res_start + 1) % self.cap, self.res_start)
+            self.res_len -= drain
+        self.offset += 1
+
+    # ------------------------------------------------------------- attention
+    def descriptor(self, q: torch.Tensor, out: torch.Tensor, scale: float, general: bool = False):
+        """``tq_attn_desc`` of a (B, Hq, D) query against every sequence; the
+        per-sequence arrays live until the next call."""
+        dev = q.device
+        comp, sink = _i32(self.comp_len, dev), _i32(self.sink_len, dev)
+        res, start = _i32(self.res_len, dev), _i32(self.res_start, dev)
+        arrays = [comp, sink, res, start]
+        d = _lib.AttnDesc(
+            batch=self.B, hq=q.shape[1], hkv=self.H, qjl=1 if self.qjl else 0, scale=scale,
+            max_comp=int(self.comp_len.max()), max_sink=int(self.sink_len.max()), max_res=int(self.res_len.max()),
+            q_dtype=_lib.dtype_code(q.dtype), kv_dtype=_lib.dtype_code(self.sink_k.dtype),
+            q=q.data_ptr(), out=out.data_ptr(), kstore=self.kstore.struct(0), vstore=self.vstore.struct(0),
+            comp_len=comp.data_ptr(), sink_k=self.sink_k.data_ptr(), sink_v=self.sink_v.data_ptr(),
+            sink_head_stride=self.sink_k.shape[2] * self.D, sink_len=sink.data_ptr(),
+            res_k=self.ring_k.data_ptr(), res_v=self.ring_v.data_ptr(), res_head_stride=self.cap * self.D,
+            res_cap=self.cap, res_start0=0, res_start=start.data_ptr(), res_len=res.data_ptr(),
+            flags=_lib.TQ_ATTN_GENERAL if general else 0)
+        return d, arrays
+
+    def attend(self, q: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
+               general: bool = False) -> torch.Tensor:
+        """Decode attention of one query per head and sequence: q (B, Hq, D),
+        Hq a multiple of the kv heads; returns float32 (B, Hq, D) over each
+        sequence's own [sink | compressed | residual] tokens."""
+        if q.dim() != 3 or q.shape[0] != self.B or q.shape[2] != self.D:
+            raise ValueError(f"query shape {tuple(q.shape)} does not match the batch")
+        if (self.offset == 0).any():
+            raise ValueError("attend() with an empty sequence in the batch")
+        q = q.contiguous()
+        if out is None:
+            out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+        d, arrays = self.descriptor(q, out, scale if scale is not None else self.D ** -0.5, general)
+        lib = _lib.load()
+        ws = _workspace(q.device, lib.tq_decode_workspace_bytes(self.kc.ref(), ctypes.byref(d)))
+        _lib.check(lib.tq_decode_attention(self.kc.ref(), self.vc.ref(), ctypes.byref(d), ws.data_ptr(), ws.numel(),
+                                           _lib.stream_ptr(q.device)), "tq_decode_attention")
+        self._attn_keep = arrays
+        return out

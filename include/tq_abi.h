@@ -191,6 +191,21 @@ int tq_decode_attention(const tq_codec* kcodec, const tq_codec* vcodec,
                         const tq_attn_desc* desc, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* Decode attention over uncompressed K/V (one query token per head),
+ * head_dim 128, fp16 or bf16 K/V (kv_dtype), q fp16 / bf16 / fp32: the
+ * sink and residual-ring segments of `desc` with no compressed tokens
+ * (desc->max_comp must be 0; kstore, vstore and qjl are not read). A plain
+ * (batch*hkv, T_cap, 128) cache is a sink of length T (sink_len NULL,
+ * max_sink = T, sink_head_stride = T_cap * 128).
+ * Replaces the decode attention of the layers the reference keeps on an
+ * uncompressed mlx-lm KVCache (outlier / skipped layers, patch.py:219-226 and
+ * :337-338, attended by mlx SDPA over the fp16 K/V). tq_decode_attention sends
+ * its calls with max_comp == 0 here too (same kernels). Same workspace rules
+ * as tq_decode_attention. */
+size_t tq_dense_decode_workspace_bytes(const tq_attn_desc* desc, int32_t head_dim);
+int tq_dense_decode_attention(const tq_attn_desc* desc, int32_t head_dim, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -437,6 +437,65 @@ static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_
   return fast_geometry(d, nwg, bpw, fpw);
 }
 
+// Dense (uncompressed fp16 / bf16) calls: head_dim 128, nothing compressed,
+// 16-byte aligned rows. record = false only tests (no error message kept).
+static int dense_check(const tq_attn_desc* d, int D, bool record = true) {
+#define DENSE_FAIL(code, ...) return record ? set_error(code, __VA_ARGS__) : (code)
+  if (D != 128) DENSE_FAIL(TQ_ERR_UNSUPPORTED, "dense decode attention: head_dim %d != 128", D);
+  if (d->max_comp != 0) DENSE_FAIL(TQ_ERR_INVALID, "dense decode attention with compressed tokens (max_comp %d)", d->max_comp);
+  if (d->batch <= 0 || d->hkv <= 0 || d->hq <= 0 || d->hq % d->hkv)
+    DENSE_FAIL(TQ_ERR_INVALID, "bad head counts hq=%d hkv=%d batch=%d", d->hq, d->hkv, d->batch);
+  const int G = d->hq / d->hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    DENSE_FAIL(TQ_ERR_UNSUPPORTED, "query heads per kv head %d not in {1,2,4,8}", G);
+  if (d->batch > 65535 || d->hkv > 65535) DENSE_FAIL(TQ_ERR_UNSUPPORTED, "grid too large");
+  if (d->max_sink < 0 || d->max_res < 0) DENSE_FAIL(TQ_ERR_INVALID, "negative segment length");
+  if (!d->q || !d->out) DENSE_FAIL(TQ_ERR_INVALID, "q/out is NULL");
+  if (!aligned16(d->q)) DENSE_FAIL(TQ_ERR_UNSUPPORTED, "dense decode attention: q must be 16-byte aligned");
+  if (d->q_dtype < TQ_F16 || d->q_dtype > TQ_F32) DENSE_FAIL(TQ_ERR_UNSUPPORTED, "unknown q dtype");
+  if (d->kv_dtype != TQ_F16 && d->kv_dtype != TQ_BF16)
+    DENSE_FAIL(TQ_ERR_UNSUPPORTED, "dense decode attention needs fp16 or bf16 K/V");
+  if (d->max_sink > 0 && (!d->sink_k || !d->sink_v)) DENSE_FAIL(TQ_ERR_INVALID, "sink pointers are NULL");
+  if (d->max_res > 0 && (!d->res_k || !d->res_v || d->res_cap <= 0 || d->max_res > d->res_cap))
+    DENSE_FAIL(TQ_ERR_INVALID, "residual ring pointers / capacity");
+  if (d->max_res > 0 && !d->res_start && (d->res_start0 < 0 || d->res_start0 >= d->res_cap))
+    DENSE_FAIL(TQ_ERR_INVALID, "ring start %d outside [0, %d)", d->res_start0, d->res_cap);
+  if (d->max_sink > 0 && !(aligned16(d->sink_k) && aligned16(d->sink_v) && d->sink_head_stride % 8 == 0))
+    DENSE_FAIL(TQ_ERR_UNSUPPORTED, "sink rows must be 16-byte aligned");
+  if (d->max_res > 0 && !(aligned16(d->res_k) && aligned16(d->res_v) && d->res_head_stride % 8 == 0))
+    DENSE_FAIL(TQ_ERR_UNSUPPORTED, "ring rows must be 16-byte aligned");
+  return TQ_OK;
+#undef DENSE_FAIL
+}
+
+static size_t dense_workspace(const tq_attn_desc* d) {
+  int nwg, bpw;
+  dense_geometry(d->batch, d->hkv, d->max_sink, d->max_res, device_cus(), nwg, bpw);
+  const int G = d->hkv > 0 ? d->hq / d->hkv : 1;
+  return nwg > 1 ? (size_t)d->batch * d->hkv * nwg * G * FAST_PART_FLOATS * 4 : 0;
+}
+
+static int dense_run(const tq_attn_desc* d, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  DenseArgs a;
+  a.sink_k = d->sink_k; a.sink_v = d->sink_v; a.sink_hs = d->sink_head_stride;
+  a.res_k = d->res_k; a.res_v = d->res_v; a.res_hs = d->res_head_stride;
+  a.res_cap = d->res_cap; a.res_start0 = d->res_start0;
+  a.sink_len_b = d->sink_len; a.res_len_b = d->res_len; a.res_start_b = d->res_start;
+  a.max_sink = d->max_sink; a.max_res = d->max_res;
+  a.q = d->q; a.q_dtype = d->q_dtype; a.out = d->out;
+  a.hq = d->hq; a.hkv = d->hkv;
+  a.qscale = d->scale * 1.4426950408889634f;
+  dense_geometry(d->batch, d->hkv, d->max_sink, d->max_res, device_cus(), a.nwg, a.bpw);
+  const size_t need = dense_workspace(d);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return set_error(TQ_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, need);
+  a.part = static_cast<float*>(workspace);
+  const int merge = (d->flags & TQ_ATTN_PARTIALS_ONLY) ? 0 : 1;
+  if (launch_dense_decode(a, d->hq / d->hkv, d->kv_dtype == TQ_BF16, d->batch, merge, s) != 0)
+    TQ_LAUNCH_CHECK("tq_dense_decode_attention");
+  return TQ_OK;
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -456,7 +515,11 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
   size_t fast = 0;
   if (fast_geometry(d, nwg, bpw, fpw))
     fast = (size_t)d->batch * d->hkv * nwg * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
-  const size_t bytes = general > fast ? general : fast;
+  size_t bytes = general > fast ? general : fast;
+  if (d->max_comp == 0 && kcodec->d == 128) {
+    const size_t dense = dense_workspace(d);
+    if (dense > bytes) bytes = dense;
+  }
   return (bytes + 255) & ~(size_t)255;
 }
 
@@ -498,6 +561,10 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     return set_error(TQ_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, need);
 
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // nothing compressed yet: the dense kernel over the sink and ring
+  if (d->max_comp == 0 && !(d->flags & TQ_ATTN_GENERAL) && (d->max_sink > 0 || d->max_res > 0) &&
+      dense_check(d, kc->d, false) == TQ_OK)
+    return dense_run(d, workspace, workspace_bytes, s);
   if (fast_eligible(kc, vc, d) && !(d->flags & TQ_ATTN_GENERAL)) {
     if (fast_set_attributes() != 0)
       return set_error(TQ_ERR_LAUNCH, "cannot raise the LDS limit of the decode kernel");
@@ -571,6 +638,19 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   hipLaunchKernelGGL(combine_kernel, dim3(d->hq, d->batch), dim3(128), cmb_smem, s, a);
   TQ_LAUNCH_CHECK("tq_decode_attention combine");
   return TQ_OK;
+}
+
+size_t tq_dense_decode_workspace_bytes(const tq_attn_desc* d, int32_t head_dim) {
+  if (!d || head_dim != 128 || d->hkv <= 0 || d->batch <= 0) return 0;
+  return (dense_workspace(d) + 255) & ~(size_t)255;
+}
+
+int tq_dense_decode_attention(const tq_attn_desc* d, int32_t head_dim, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (!d) return set_error(TQ_ERR_INVALID, "attention descriptor is NULL");
+  const int rc = dense_check(d, head_dim);
+  if (rc) return rc;
+  return dense_run(d, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -44,4 +44,33 @@ constexpr int FAST_FP16_PER_WG = 16;     // fp16 tokens per workgroup, staged in
 constexpr int FAST_MAX_WG = 256;         // workgroups per (sequence, kv head)
 constexpr int FAST_PART_FLOATS = 132;    // per query head per workgroup: M, L, pad, pad, out[128] (original space, / L)
 
+// Merge of per-workgroup partials (FAST_PART_FLOATS per query head, nwg per
+// (sequence, kv head)) into out (batch, hq, 128) float32.
+int launch_partial_merge(float* part, int nwg, int G, int hq, int hkv, int batch, float* out, hipStream_t s);
+
+// Arguments of the dense (fp16 / bf16 K/V) decode-attention kernel: the
+// fp16 segments of tq_attn_desc, head_dim 128.
+struct DenseArgs {
+  const void* sink_k; const void* sink_v; int64_t sink_hs;   // elements
+  const void* res_k;  const void* res_v;  int64_t res_hs;    // ring
+  int res_cap, res_start0;
+  const int32_t* sink_len_b;
+  const int32_t* res_len_b;
+  const int32_t* res_start_b;
+  int max_sink, max_res;
+  const void* q; int q_dtype;
+  float* out;
+  int hq, hkv;
+  float qscale;          // scale * log2(e)
+  float* part;           // per-workgroup partials (workspace), unused when nwg == 1
+  int nwg;               // workgroups per (sequence, kv head)
+  int bpw;               // 32-token blocks per wave
+};
+
+constexpr int DENSE_WAVES = 4;  // waves per workgroup of the dense kernel
+
+void dense_geometry(int batch, int hkv, int max_sink, int max_res, int cus, int& nwg, int& bpw);
+// bf: bf16 K/V (else fp16); merge 0 skips the merge launch (measurement)
+int launch_dense_decode(const DenseArgs& a, int G, bool bf, int batch, int merge, hipStream_t s);
+
 }  // namespace tq

@@ -846,6 +846,19 @@ int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+int launch_partial_merge(float* part, int nwg, int G, int hq, int hkv, int batch, float* out, hipStream_t s) {
+  FastArgs a{};
+  a.part = part; a.nwg = nwg; a.hq = hq; a.hkv = hkv; a.out = out;
+  const dim3 grid(2, hq, batch);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((fast_merge_kernel<1>), grid, dim3(64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((fast_merge_kernel<2>), grid, dim3(64), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((fast_merge_kernel<4>), grid, dim3(64), 0, s, a); break;
+    default: hipLaunchKernelGGL((fast_merge_kernel<8>), grid, dim3(64), 0, s, a); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // The kernel's LDS is static (Layout::total bytes); nothing to raise.
 int fast_set_attributes() { return 0; }
 

@@ -41,6 +41,45 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def dense_attention(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                    scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention of one query token per head over uncompressed K/V
+    through ``tq_dense_decode_attention``: the attention of the layers kept
+    on an fp16 cache (the reference's outlier / skipped layers, patch.py:337-338).
+
+    ``queries`` (B, Hq, 1, D) or (B, Hq, D); ``keys`` / ``values`` (B, Hkv, T, D)
+    fp16 or bf16 with D = 128, Hq a multiple (1, 2, 4, 8) of Hkv, rows
+    contiguous (a view of a larger (B, Hkv, T_cap, D) buffer is fine).
+    Returns float32 (B, Hq, 1, D) = softmax(scale q K^T) V (default scale
+    D**-0.5)."""
+    _lib.require_device(keys)
+    q = queries[:, :, 0] if queries.dim() == 4 else queries
+    q = q.contiguous()
+    if q.data_ptr() % 16:
+        q = q.clone()  # the kernel reads 16-byte pieces of the query rows
+    B, hkv, T, D = keys.shape
+    if values.shape != keys.shape or values.dtype != keys.dtype or values.stride() != keys.stride():
+        raise ValueError("keys and values must have one shape, dtype and layout")
+    if q.dim() != 3 or q.shape[0] != B or q.shape[2] != D:
+        raise ValueError(f"query shape {tuple(queries.shape)} does not match keys {tuple(keys.shape)}")
+    st = keys.stride()
+    if st[3] != 1 or st[2] != D or st[0] != hkv * st[1]:
+        raise ValueError("keys / values need contiguous rows and heads laid out (B, Hkv) in order")
+    if out is None:
+        out = torch.empty(B, q.shape[1], 1, D, dtype=torch.float32, device=q.device)
+    desc = _lib.AttnDesc(
+        batch=B, hq=q.shape[1], hkv=hkv, qjl=0, scale=D ** -0.5 if scale is None else scale,
+        max_comp=0, max_sink=T, max_res=0, q_dtype=_lib.dtype_code(q.dtype), kv_dtype=_lib.dtype_code(keys.dtype),
+        q=q.data_ptr(), out=out.data_ptr(), comp_len=None, sink_k=keys.data_ptr(), sink_v=values.data_ptr(),
+        sink_head_stride=st[1], sink_len=None, res_k=None, res_v=None, res_head_stride=0, res_cap=0,
+        res_start0=0, res_start=None, res_len=None, flags=0)
+    lib = _lib.load()
+    ws = _workspace(q.device, lib.tq_dense_decode_workspace_bytes(ctypes.byref(desc), D))
+    _lib.check(lib.tq_dense_decode_attention(ctypes.byref(desc), D, ws.data_ptr(), ws.numel(),
+                                             _lib.stream_ptr(q.device)), "tq_dense_decode_attention")
+    return out
+
+
 def drain_schedule(fp16_len: int, window: int, chunk_size: int) -> list[int]:
     """Sizes of the drains the reference performs on an fp16 buffer of
     ``fp16_len`` tokens (cache.py:497-533)."""

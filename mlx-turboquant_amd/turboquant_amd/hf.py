@@ -8,14 +8,15 @@ model the same roles are:
 
 - ``TurboQuantCache(model)``: a ``transformers`` ``Cache`` whose layers are
   the caches ``apply_turboquant`` installed: a ``TurboQuantLayer`` per
-  compressed layer, the model's own default layer (``DynamicCache(config)``)
-  for the layers ``apply_turboquant`` leaves uncompressed (outlier,
-  sliding-window, linear-attention layers);
+  compressed layer and per uncompressed full-attention layer (outlier /
+  skipped, ``FP16KVCache``), the model's own default layer
+  (``DynamicCache(config)``) for sliding-window and linear-attention layers;
 - the attention function registered as ``"turboquant"``: for a one-token
   decode step it runs the fused decode-attention kernel over the packed codes
-  (``TurboQuantKVCache.attend``) and never materialises the dense K/V; every
-  other call (prefill, uncompressed layers) is ``transformers``' SDPA over the
-  dense K/V, as in the reference.
+  (``TurboQuantKVCache.attend``, never materialising the dense K/V) or the
+  dense decode kernel over an ``FP16KVCache`` (fp16 / bf16, head_dim 128);
+  every other call (prefill, the model's default layers) is ``transformers``'
+  SDPA over the dense K/V, as in the reference.
 
     apply_turboquant(model, key_bits=4, value_bits=2, residual_window=128)
     model.set_attn_implementation("turboquant")
@@ -35,15 +36,17 @@ from transformers.cache_utils import Cache, CacheLayerMixin, DynamicCache, Dynam
 from transformers.integrations.sdpa_attention import sdpa_attention_forward
 
 from .cache import TurboQuantKVCache
+from .patch import FP16KVCache
 
 ATTN_IMPLEMENTATION = "turboquant"
 
 
 class TurboQuantLayer(CacheLayerMixin):
-    """One compressed attention layer. ``update`` appends the new tokens
+    """One attention layer over a ``TurboQuantKVCache`` (compressed) or an
+    ``FP16KVCache`` (uncompressed). ``update`` appends the new tokens
     (draining the oldest residual tokens into the packed store) and returns
     the dense K/V in the input dtype, or, for a one-token step with ``fused``,
-    the new tokens themselves tagged for the fused kernel."""
+    the new tokens themselves tagged for the decode kernel."""
 
     is_sliding = False
     is_compileable = False
@@ -56,6 +59,9 @@ class TurboQuantLayer(CacheLayerMixin):
 
     def lazy_initialization(self, key_states, value_states):
         self.dtype, self.device = key_states.dtype, key_states.device
+        if isinstance(self.cache, FP16KVCache):  # the dense kernel's shapes
+            self.fused = self.fused and key_states.is_cuda and key_states.shape[-1] == 128 and \
+                key_states.dtype in (torch.float16, torch.bfloat16)
         self.is_initialized = True
 
     def update(self, key_states, value_states, *args, **kwargs):
@@ -105,7 +111,7 @@ class TurboQuantCache(Cache):
         defaults = DynamicCache(config=model.config).layers
         layers = []
         for i, c in enumerate(caches):
-            if isinstance(c, TurboQuantKVCache):
+            if isinstance(c, (TurboQuantKVCache, FP16KVCache)):
                 layers.append(TurboQuantLayer(c, fused))
             else:
                 layers.append(defaults[i] if i < len(defaults) else DynamicLayer())
@@ -115,8 +121,9 @@ class TurboQuantCache(Cache):
 def turboquant_attention(module, query, key, value, attention_mask, dropout: float = 0.0,
                          scaling: float | None = None, **kwargs):
     """Attention function of ``set_attn_implementation("turboquant")``: the
-    fused K4/V2 / general decode kernel for a one-token step of a compressed
-    layer, ``transformers``' SDPA otherwise. Returns (B, T, Hq, D)."""
+    decode kernels for a one-token step of a ``TurboQuantLayer`` (packed codes
+    or dense fp16 / bf16), ``transformers``' SDPA otherwise. Returns
+    (B, T, Hq, D)."""
     layer = getattr(key, "_turboquant_layer", None)
     if layer is None:
         return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout,

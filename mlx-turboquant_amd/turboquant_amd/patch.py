@@ -38,26 +38,58 @@ from .cache import TurboQuantKVCache
 
 class FP16KVCache:
     """Uncompressed cache used for skipped / outlier layers (the reference
-    hands those layers mlx-lm's ``KVCache``, patch.py:337-338)."""
+    hands those layers mlx-lm's ``KVCache``, patch.py:337-338). Storage grows
+    in steps of ``step`` tokens, as mlx-lm's KVCache does; ``keys`` /
+    ``values`` are views of the first ``offset`` tokens. ``attend`` runs the
+    dense decode-attention kernel over them (fp16 / bf16, head_dim 128)."""
+
+    step = 256
 
     def __init__(self):
-        self.keys = self.values = None
+        self._k = self._v = None
         self.offset = 0
 
+    @property
+    def keys(self):
+        return None if self._k is None else self._k[:, :, :self.offset]
+
+    @property
+    def values(self):
+        return None if self._v is None else self._v[:, :, :self.offset]
+
+    def update(self, keys, values) -> None:
+        """Append (B, H, n, D) keys / values."""
+        n, prev = keys.shape[2], self.offset
+        if self._k is None or prev + n > self._k.shape[2]:
+            B, H, _, D = keys.shape
+            cap = (prev + n + self.step - 1) // self.step * self.step
+            k = keys.new_empty(B, H, cap, D)
+            v = values.new_empty(B, H, cap, values.shape[3])
+            if self._k is not None:
+                k[:, :, :prev] = self._k[:, :, :prev]
+                v[:, :, :prev] = self._v[:, :, :prev]
+            self._k, self._v = k, v
+        self._k[:, :, prev:prev + n] = keys
+        self._v[:, :, prev:prev + n] = values
+        self.offset = prev + n
+
     def update_and_fetch(self, keys, values):
-        if self.keys is None:
-            self.keys, self.values = keys, values
-        else:
-            self.keys = torch.cat([self.keys, keys], dim=2)
-            self.values = torch.cat([self.values, values], dim=2)
-        self.offset += keys.shape[2]
+        self.update(keys, values)
         return self.keys, self.values
+
+    def attend(self, queries, scale=None, out=None):
+        """Decode attention of one query token per head over the cached tokens:
+        float32 (B, Hq, 1, D)."""
+        if self._k is None or self.offset == 0:
+            raise ValueError("attend() on an empty cache")
+        from .cache import dense_attention
+        return dense_attention(queries, self.keys, self.values, scale=scale, out=out)
 
     def make_mask(self, N, offset=0, return_array=False, window_size=None):
         return None if N == 1 and not return_array else "causal"
 
     def empty(self):
-        return self.keys is None
+        return self._k is None
 
     def size(self):
         return self.offset

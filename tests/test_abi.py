@@ -74,3 +74,16 @@ def test_host_side_validation_errors():
     codec = _lib.Codec(d=96, bits_hi=4, bits_lo=4, split=96)
     assert lib.tq_compress(ctypes.byref(codec), None, 0, 0, None, None, None) == _lib.TQ_ERR_UNSUPPORTED
     assert lib.tq_pack_codes(None, 0, 128, 4, None, None) == _lib.TQ_OK  # empty is a no-op
+    # dense decode attention: head_dim, compressed tokens, K/V dtype, group size
+    d = _lib.AttnDesc(batch=1, hq=8, hkv=2, max_sink=4, q_dtype=_lib.TQ_F16, kv_dtype=_lib.TQ_F16,
+                      q=16, out=16, sink_k=16, sink_v=16, sink_head_stride=512)
+    assert lib.tq_dense_decode_attention(ctypes.byref(d), 64, None, 0, None) == _lib.TQ_ERR_UNSUPPORTED
+    assert b"head_dim 64" in lib.tq_last_error()
+    d.max_comp = 5
+    assert lib.tq_dense_decode_attention(ctypes.byref(d), 128, None, 0, None) == _lib.TQ_ERR_INVALID
+    d.max_comp, d.kv_dtype = 0, _lib.TQ_F32
+    assert lib.tq_dense_decode_attention(ctypes.byref(d), 128, None, 0, None) == _lib.TQ_ERR_UNSUPPORTED
+    d.kv_dtype, d.hq = _lib.TQ_F16, 6
+    assert lib.tq_dense_decode_attention(ctypes.byref(d), 128, None, 0, None) == _lib.TQ_ERR_UNSUPPORTED
+    d.hq, d.sink_k = 8, 18  # rows not 16-byte aligned
+    assert lib.tq_dense_decode_attention(ctypes.byref(d), 128, None, 0, None) == _lib.TQ_ERR_UNSUPPORTED

@@ -54,7 +54,9 @@ def test_cache_layers_and_exact_without_compression(cpu_cache):
     m = tiny_llama()
     apply_turboquant(m, key_bits=4, value_bits=2, residual_window=256, skip_layers=[2])
     cache = TurboQuantCache(m, fused=False)
-    assert [type(x).__name__ for x in cache.layers] == ["TurboQuantLayer", "TurboQuantLayer", "DynamicLayer"]
+    assert [type(x).__name__ for x in cache.layers] == ["TurboQuantLayer"] * 3
+    from turboquant_amd.patch import FP16KVCache
+    assert isinstance(cache.layers[2].cache, FP16KVCache)  # the skipped layer: uncompressed
     ids = torch.randint(0, 97, (1, 40), generator=torch.Generator().manual_seed(1))
     with torch.no_grad():
         got = run(m, cache, ids, 8)

@@ -45,6 +45,7 @@ struct AttnArgs {
   float* sq;    // (B, Hq, m)  S @ (scale * q)
   float* part;  // (B, Hq, nch, PS)
   int nc, ns, nr, nch, ps;
+  int c0;  // first chunk of a chunk_kernel launch
 };
 
 __host__ __device__ inline int part_stride(int D, int m) { return ((2 + D + m) + 3) & ~3; }
@@ -85,20 +86,123 @@ __device__ inline uint32_t code_at(const uint8_t* row, int j, int bits) {
   return v & ((1u << bits) - 1u);
 }
 
+// Rows [0, n) of `row_bytes` bytes each, contiguous at src, into LDS rows of
+// `stride` bytes starting at column `col` (dword copies when the rows, the
+// column and the source are 4-byte aligned).
+__device__ inline void stage_rows(uint8_t* dst, int stride, int col, const uint8_t* src, int row_bytes, int n) {
+  if (row_bytes <= 0 || n <= 0) return;
+  const int tid = threadIdx.x;
+  if ((row_bytes & 3) == 0 && (col & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 3) == 0) {
+    const int rw = row_bytes >> 2;
+    const uint32_t* sw = reinterpret_cast<const uint32_t*>(src);
+    for (int e = tid; e < n * rw; e += NT) {
+      const int t = e / rw, k = e - t * rw;
+      *reinterpret_cast<uint32_t*>(dst + t * stride + col + 4 * k) = sw[e];
+    }
+  } else {
+    for (int e = tid; e < n * row_bytes; e += NT) {
+      const int t = e / row_bytes, k = e - t * row_bytes;
+      dst[t * stride + col + k] = src[e];
+    }
+  }
+}
+
+// s[h] += sum_{j < nd} q[h][j0 + j] * lut[code j] for BITS-wide LSB-first
+// codes in a 4-byte-aligned LDS row; nd and j0 multiples of 32. The codes of
+// 32 dims are BITS dwords, read once; shifts are compile-time constants.
+template <int BITS, int D, int G>
+__device__ inline void dot_codes(const uint8_t* row, int nd, const float* lut, const float (*q)[D], int j0,
+                                 float (&s)[G]) {
+  const uint32_t* rw = reinterpret_cast<const uint32_t*>(row);
+  for (int jb = 0; jb < nd; jb += 32) {
+    uint32_t wd[BITS];
+#pragma unroll
+    for (int i = 0; i < BITS; ++i) wd[i] = rw[(jb >> 5) * BITS + i];
+#pragma unroll
+    for (int j4 = 0; j4 < 32; j4 += 4) {
+      float cv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int bit = BITS * (j4 + u);
+        uint32_t v = wd[bit >> 5] >> (bit & 31);
+        if ((bit & 31) + BITS > 32) v |= wd[(bit >> 5) + 1] << (32 - (bit & 31));
+        cv[u] = lut[v & ((1u << BITS) - 1u)];
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float4 qq = *reinterpret_cast<const float4*>(&q[h][j0 + jb + j4]);
+        s[h] = fmaf(qq.x, cv[0], s[h]);
+        s[h] = fmaf(qq.y, cv[1], s[h]);
+        s[h] = fmaf(qq.z, cv[2], s[h]);
+        s[h] = fmaf(qq.w, cv[3], s[h]);
+      }
+    }
+  }
+}
+
+template <int D, int G>
+__device__ inline void dot_codes_bits(int bits, const uint8_t* row, int nd, const float* lut, const float (*q)[D],
+                                      int j0, float (&s)[G]) {
+  switch (bits) {
+    case 1: dot_codes<1, D, G>(row, nd, lut, q, j0, s); break;
+    case 2: dot_codes<2, D, G>(row, nd, lut, q, j0, s); break;
+    case 3: dot_codes<3, D, G>(row, nd, lut, q, j0, s); break;
+    default: dot_codes<4, D, G>(row, nd, lut, q, j0, s); break;
+  }
+}
+
+// zs[h] = sum_{i < m} sq[h][i] * z_i, z_i = +1 where sign bit i is set, else
+// -1 (LSB-first bits in a 4-byte-aligned LDS row; m a multiple of 32)
+template <int G, int MAXM>
+__device__ inline void dot_signs(const uint8_t* row, int m, const float (*sq)[MAXM], float (&zs)[G]) {
+  const uint32_t* rw = reinterpret_cast<const uint32_t*>(row);
+  for (int ib = 0; ib < m; ib += 32) {
+    const uint32_t wd = rw[ib >> 5];
+#pragma unroll
+    for (int i4 = 0; i4 < 32; i4 += 4) {
+      float z[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) z[u] = ((wd >> (i4 + u)) & 1u) ? 1.f : -1.f;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float4 qq = *reinterpret_cast<const float4*>(&sq[h][ib + i4]);
+        zs[h] = fmaf(qq.x, z[0], zs[h]);
+        zs[h] = fmaf(qq.y, z[1], zs[h]);
+        zs[h] = fmaf(qq.z, z[2], zs[h]);
+        zs[h] = fmaf(qq.w, z[3], zs[h]);
+      }
+    }
+  }
+}
+
+// One chunk of CHUNK tokens of one segment for the G query heads of kv head g:
+// thread t scores token t (packed tokens from code rows staged in LDS,
+// fp16 tokens from memory), the chunk's softmax weights go to LDS, then
+// thread (dim j, token slice) accumulates the weighted values of dim j for
+// every head; with QJL the sign sketches are staged too and the value term
+// sum_t p_t gamma_t z_t is accumulated per projection.
 template <int D, int G>
 __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
-  constexpr int HP = NT / D > 0 ? NT / D : 1;  // threads per dim in the PV phase
+  constexpr int TSL = NT / D > 0 ? NT / D : 1;  // token slices of the PV phase (threads per dim)
   constexpr int MAXM = 256;
-  __shared__ float qv[G][D];          // rotated (compressed) or plain (fp16) scaled query
-  __shared__ float w[G][CHUNK];       // p * n_v (or p) per token
-  __shared__ float pg[G][CHUNK];      // p * gamma_v (QJL)
+  // LDS row strides of staged code rows (at most 4 bits per dim) and sign
+  // rows, padded by one dword so that the rows of neighbouring tokens start
+  // in different banks
+  constexpr int KR = D / 2 + 4;
+  constexpr int SR = MAXM / 8 + 4;
+  __shared__ __align__(16) float qv[G][D];   // rotated (compressed) or plain (fp16) scaled query
+  __shared__ __align__(16) float w[G][CHUNK];   // p * n_v (or p) per token
+  __shared__ __align__(16) float pg[G][CHUNK];  // p * gamma_v (QJL)
   __shared__ float red[G][NT / 64];
   __shared__ float mx[G], lsum[G];
   __shared__ float klut[2][16], vlut[2][16];
-  __shared__ float sqv[G][MAXM];
-  __shared__ uint8_t vtile[CHUNK * 128];
-
-  const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  __shared__ __align__(16) float sqv[G][MAXM];
+  __shared__ __align__(16) uint8_t ktile[CHUNK * KR];  // key code rows: hi bytes, then lo bytes
+  __shared__ __align__(16) uint8_t vtile[CHUNK * KR];  // value code rows
+  __shared__ __align__(16) uint8_t ksg[CHUNK * SR];    // key sign rows (QJL)
+  __shared__ __align__(16) uint8_t vsg[CHUNK * SR];    // value sign rows (QJL)
+  __shared__ float slice[G][NT];                       // per-thread partial sums of the PV / QJL phases
+  const int c = blockIdx.x + a.c0, g = blockIdx.y, b = blockIdx.z;
   const int hq = a.d.hq, tid = threadIdx.x;
   const int row = b * a.d.hkv + g;
 
@@ -132,16 +236,25 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
     vlut[0][tid] = tid < (1 << a.vb_hi) ? a.vc_hi[tid] : 0.f;
     vlut[1][tid] = tid < (1 << a.vb_lo) ? a.vc_lo[tid] : 0.f;
   }
-  // stage packed V rows (hi then lo bytes per token) for the PV phase
-  const int vrb = a.v_row_hi + a.v_row_lo;
+  // stage the chunk's code rows (and sign rows) in LDS
   if (packed) {
-    const uint8_t* vh = a.d.vstore.codes_hi + (int64_t)row * a.d.vstore.hi_head_stride + (int64_t)base * a.v_row_hi;
-    for (int e = tid; e < nvalid * a.v_row_hi; e += NT)
-      vtile[(e / a.v_row_hi) * vrb + e % a.v_row_hi] = vh[e];
-    if (a.v_row_lo) {
-      const uint8_t* vl = a.d.vstore.codes_lo + (int64_t)row * a.d.vstore.lo_head_stride + (int64_t)base * a.v_row_lo;
-      for (int e = tid; e < nvalid * a.v_row_lo; e += NT)
-        vtile[(e / a.v_row_lo) * vrb + a.v_row_hi + e % a.v_row_lo] = vl[e];
+    const tq_store& ks = a.d.kstore;
+    const tq_store& vs = a.d.vstore;
+    stage_rows(ktile, KR, 0, ks.codes_hi + (int64_t)row * ks.hi_head_stride + (int64_t)base * a.k_row_hi, a.k_row_hi,
+               nvalid);
+    if (a.k_row_lo)
+      stage_rows(ktile, KR, a.k_row_hi, ks.codes_lo + (int64_t)row * ks.lo_head_stride + (int64_t)base * a.k_row_lo,
+                 a.k_row_lo, nvalid);
+    stage_rows(vtile, KR, 0, vs.codes_hi + (int64_t)row * vs.hi_head_stride + (int64_t)base * a.v_row_hi, a.v_row_hi,
+               nvalid);
+    if (a.v_row_lo)
+      stage_rows(vtile, KR, a.v_row_hi, vs.codes_lo + (int64_t)row * vs.lo_head_stride + (int64_t)base * a.v_row_lo,
+                 a.v_row_lo, nvalid);
+    if (qjl) {
+      stage_rows(ksg, SR, 0, ks.signs + (int64_t)row * ks.sign_head_stride + (int64_t)base * a.row_sign, a.row_sign,
+                 nvalid);
+      stage_rows(vsg, SR, 0, vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base * a.row_sign, a.row_sign,
+                 nvalid);
     }
   }
   __syncthreads();
@@ -155,30 +268,18 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) s[h] = 0.f;
     if (packed) {
-      const uint8_t* kh = a.d.kstore.codes_hi + (int64_t)row * a.d.kstore.hi_head_stride + (int64_t)(base + t) * a.k_row_hi;
-      const uint8_t* kl = a.k_row_lo ? a.d.kstore.codes_lo + (int64_t)row * a.d.kstore.lo_head_stride +
-                                           (int64_t)(base + t) * a.k_row_lo
-                                     : nullptr;
-      for (int j = 0; j < D; ++j) {
-        const bool hi = j < a.ks;
-        const float cv = hi ? klut[0][code_at(kh, j, a.kb_hi)] : klut[1][code_at(kl, j - a.ks, a.kb_lo)];
-#pragma unroll
-        for (int h = 0; h < G; ++h) s[h] = fmaf(qv[h][j], cv, s[h]);
-      }
+      const uint8_t* kr = ktile + t * KR;
+      dot_codes_bits<D, G>(a.kb_hi, kr, a.ks, klut[0], qv, 0, s);
+      if (a.ks < D) dot_codes_bits<D, G>(a.kb_lo, kr + a.k_row_hi, D - a.ks, klut[1], qv, a.ks, s);
       const float nk = a.d.kstore.norms[(int64_t)row * a.d.kstore.norm_head_stride + base + t];
 #pragma unroll
       for (int h = 0; h < G; ++h) s[h] *= nk;
       if (qjl) {
-        const uint8_t* sg = a.d.kstore.signs + (int64_t)row * a.d.kstore.sign_head_stride + (int64_t)(base + t) * a.row_sign;
         const float gk = a.d.kstore.gamma[(int64_t)row * a.d.kstore.gamma_head_stride + base + t];
         float zs[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) zs[h] = 0.f;
-        for (int i = 0; i < a.m; ++i) {
-          const float z = ((sg[i >> 3] >> (i & 7)) & 1u) ? 1.f : -1.f;
-#pragma unroll
-          for (int h = 0; h < G; ++h) zs[h] = fmaf(sqv[h][i], z, zs[h]);
-        }
+        dot_signs<G, MAXM>(ksg + t * SR, a.m, sqv, zs);
         const float coef = SQRT_HALF_PI / (float)D * gk;
 #pragma unroll
         for (int h = 0; h < G; ++h) s[h] = fmaf(coef, zs[h], s[h]);
@@ -249,63 +350,102 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   }
   __syncthreads();
 
-  // ---- PV: thread (j, hp) accumulates dim j for heads hp, hp+HP, ...
+  // ---- PV: thread (j, sl) accumulates dim j of every head over token slice
+  // sl (TSL slices of CHUNK / TSL tokens), so each code is decoded once for
+  // all G heads; the slices are summed through LDS. Weights of 4 tokens per
+  // LDS read (tokens past nvalid have weight 0).
+  const int n4 = (nvalid + 3) & ~3;
   float* outp = a.part;
-  for (int jj = tid; jj < D * HP; jj += NT) {
-    const int j = jj % D, hp = jj / D;
+  {
+    const int j = tid % D, sl = tid / D;
+    const int t_lo = sl * (CHUNK / TSL), t_hi = min(n4, t_lo + CHUNK / TSL);
     float acc[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h] = 0.f;
-    if (packed) {
-      const bool hi = j < a.vs;
-      const int bits = hi ? a.vb_hi : a.vb_lo;
-      const int jl = hi ? j : j - a.vs;
-      const int off = hi ? 0 : a.v_row_hi;
-      const float* lut = vlut[hi ? 0 : 1];
-      for (int tt = 0; tt < nvalid; ++tt) {
-        const float cv = lut[code_at(vtile + tt * vrb + off, jl, bits)];
+    if (tid < D * TSL) {
+      if (packed) {
+        const bool hi = j < a.vs;
+        const int bits = hi ? a.vb_hi : a.vb_lo;
+        const int jl = hi ? j : j - a.vs;
+        const int off = hi ? 0 : a.v_row_hi;
+        const float* lut = vlut[hi ? 0 : 1];
+        for (int tt = t_lo; tt < t_hi; tt += 4) {
+          float cv[4];
 #pragma unroll
-        for (int h = 0; h < G; ++h)
-          if (h % HP == hp) acc[h] = fmaf(w[h][tt], cv, acc[h]);
-      }
-    } else {
-      for (int tt = 0; tt < nvalid; ++tt) {
-        int64_t vo;
-        const void* vp;
-        if (seg == 1) {
-          vp = a.d.sink_v;
-          vo = (int64_t)row * a.d.sink_head_stride + (int64_t)(base + tt) * D;
-        } else {
-          const int st = a.d.res_start ? a.d.res_start[b] : a.d.res_start0;
-          const int pos = (st + base + tt) % a.d.res_cap;
-          vp = a.d.res_v;
-          vo = (int64_t)row * a.d.res_head_stride + (int64_t)pos * D;
+          for (int u = 0; u < 4; ++u) cv[u] = lut[code_at(vtile + (tt + u) * KR + off, jl, bits)];
+#pragma unroll
+          for (int h = 0; h < G; ++h) {
+            const float4 wq = *reinterpret_cast<const float4*>(&w[h][tt]);
+            acc[h] = fmaf(wq.x, cv[0], acc[h]);
+            acc[h] = fmaf(wq.y, cv[1], acc[h]);
+            acc[h] = fmaf(wq.z, cv[2], acc[h]);
+            acc[h] = fmaf(wq.w, cv[3], acc[h]);
+          }
         }
-        const float vv = load_elem(vp, vo + j, a.d.kv_dtype);
+      } else {
+        for (int tt = t_lo; tt < min(t_hi, nvalid); ++tt) {
+          int64_t vo;
+          const void* vp;
+          if (seg == 1) {
+            vp = a.d.sink_v;
+            vo = (int64_t)row * a.d.sink_head_stride + (int64_t)(base + tt) * D;
+          } else {
+            const int st = a.d.res_start ? a.d.res_start[b] : a.d.res_start0;
+            const int pos = (st + base + tt) % a.d.res_cap;
+            vp = a.d.res_v;
+            vo = (int64_t)row * a.d.res_head_stride + (int64_t)pos * D;
+          }
+          const float vv = load_elem(vp, vo + j, a.d.kv_dtype);
 #pragma unroll
-        for (int h = 0; h < G; ++h)
-          if (h % HP == hp) acc[h] = fmaf(w[h][tt], vv, acc[h]);
+          for (int h = 0; h < G; ++h) acc[h] = fmaf(w[h][tt], vv, acc[h]);
+        }
       }
     }
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      if (h % HP != hp) continue;
-      float* pp = outp + (((int64_t)b * hq + g * G + h) * a.nch + c) * a.ps;
-      pp[2 + j] = acc[h];
-    }
+    for (int h = 0; h < G; ++h) slice[h][tid] = acc[h];
   }
-  // QJL value term: az[h][i] = sum_t p_t gamma_t z_t,i
+  __syncthreads();
+  for (int e = tid; e < G * D; e += NT) {
+    const int h = e / D, j = e % D;
+    float v = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < TSL; ++sl) v += slice[h][sl * D + j];
+    outp[(((int64_t)b * hq + g * G + h) * a.nch + c) * a.ps + 2 + j] = v;
+  }
+  // QJL value term az[h][i] = sum_t p_t gamma_t z_t,i: thread (i, sl) over
+  // token slice sl of NT / m, each sign bit read once for all G heads
   if (qjl) {
-    const uint8_t* sgb = a.d.vstore.signs + (int64_t)row * a.d.vstore.sign_head_stride + (int64_t)base * a.row_sign;
-    for (int e = tid; e < G * a.m; e += NT) {
-      const int h = e / a.m, i = e % a.m;
-      float acc = 0.f;
-      for (int tt = 0; tt < nvalid; ++tt) {
-        const float z = ((sgb[tt * a.row_sign + (i >> 3)] >> (i & 7)) & 1u) ? 1.f : -1.f;
-        acc = fmaf(pg[h][tt], z, acc);
+    __syncthreads();
+    const int nsl = NT / a.m;  // m <= 256 = NT
+    const int i = tid % a.m, sl = tid / a.m;
+    const int per = CHUNK / nsl;
+    const int t_lo = sl * per, t_hi = min(n4, t_lo + per);
+    float acc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[h] = 0.f;
+    if (sl < nsl) {
+      for (int tt = t_lo; tt < t_hi; tt += 4) {
+        float z[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) z[u] = ((vsg[(tt + u) * SR + (i >> 3)] >> (i & 7)) & 1u) ? 1.f : -1.f;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const float4 pq = *reinterpret_cast<const float4*>(&pg[h][tt]);
+          acc[h] = fmaf(pq.x, z[0], acc[h]);
+          acc[h] = fmaf(pq.y, z[1], acc[h]);
+          acc[h] = fmaf(pq.z, z[2], acc[h]);
+          acc[h] = fmaf(pq.w, z[3], acc[h]);
+        }
       }
-      float* pp = outp + (((int64_t)b * hq + g * G + h) * a.nch + c) * a.ps;
-      pp[2 + D + i] = acc;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) slice[h][tid] = acc[h];
+    __syncthreads();
+    for (int e = tid; e < G * a.m; e += NT) {
+      const int h = e / a.m, ii = e % a.m;
+      float v = 0.f;
+      for (int q = 0; q < nsl; ++q) v += slice[h][q * a.m + ii];
+      outp[(((int64_t)b * hq + g * G + h) * a.nch + c) * a.ps + 2 + D + ii] = v;
     }
   }
   if (tid < G) {
@@ -315,51 +455,73 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   }
 }
 
-__global__ void combine_kernel(AttnArgs a) {
+// Combine of the chunk partials of query head (b, h): the chunk weights
+// exp(m_c - M) are computed once into LDS, then the weighted sums (rotated
+// dims of the packed chunks, QJL projections, original-space dims of the fp16
+// chunks) and the inverse rotation, with four independent accumulators so the
+// loads of a loop overlap. 128 threads.
+__global__ __launch_bounds__(128) void combine_kernel(AttnArgs a) {
   extern __shared__ float sm[];
-  const int h = blockIdx.x, b = blockIdx.y, D = a.D;
-  const int hq = a.d.hq;
-  const float* pp = a.part + ((int64_t)b * hq + h) * a.nch * a.ps;
+  __shared__ float rmax[2], rsum[2];
+  const int h = blockIdx.x, b = blockIdx.y, D = a.D, tid = threadIdx.x;
+  const int hq = a.d.hq, nch = a.nch;
+  const int64_t ps = a.ps;
+  const float* pp = a.part + ((int64_t)b * hq + h) * nch * ps;
+  float* wc = sm;                       // [nch] chunk weights
+  float* accr = sm + ((nch + 3) & ~3);  // [D] weighted rotated sum
+  float* azs = accr + D;                // [m] weighted QJL projections
   float M = -INFINITY;
-  for (int c = 0; c < a.nch; ++c) M = fmaxf(M, pp[(int64_t)c * a.ps]);
-  float* accr = sm;        // D rotated
-  float* azs = sm + D;     // m
+  for (int c = tid; c < nch; c += 128) M = fmaxf(M, pp[c * ps]);
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  if ((tid & 63) == 0) rmax[tid >> 6] = M;
+  __syncthreads();
+  M = fmaxf(rmax[0], rmax[1]);
   float L = 0.f;
-  for (int c = 0; c < a.nch; ++c) {
-    const float mc = pp[(int64_t)c * a.ps];
-    if (mc > -INFINITY) L += expf(mc - M) * pp[(int64_t)c * a.ps + 1];
+  for (int c = tid; c < nch; c += 128) {
+    const float mc = pp[c * ps];
+    const float wgt = mc > -INFINITY ? expf(mc - M) : 0.f;
+    wc[c] = wgt;
+    L = fmaf(wgt, pp[c * ps + 1], L);
   }
-  for (int j = threadIdx.x; j < D; j += blockDim.x) {
-    float r = 0.f;
-    for (int c = 0; c < a.nc; ++c) {
-      const float mc = pp[(int64_t)c * a.ps];
-      if (mc > -INFINITY) r = fmaf(expf(mc - M), pp[(int64_t)c * a.ps + 2 + j], r);
+  for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
+  if ((tid & 63) == 0) rsum[tid >> 6] = L;
+  __syncthreads();
+  L = rsum[0] + rsum[1];
+  // sum over chunks [c0, c1) of wc[c] * pp[c * ps + col]
+  auto wsum = [&](int c0, int c1, int col) {
+    float r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+    int c = c0;
+    for (; c + 4 <= c1; c += 4) {
+      r0 = fmaf(wc[c], pp[c * ps + col], r0);
+      r1 = fmaf(wc[c + 1], pp[(c + 1) * ps + col], r1);
+      r2 = fmaf(wc[c + 2], pp[(c + 2) * ps + col], r2);
+      r3 = fmaf(wc[c + 3], pp[(c + 3) * ps + col], r3);
     }
-    accr[j] = r;
-  }
-  for (int i = threadIdx.x; i < a.m; i += blockDim.x) {
-    float r = 0.f;
-    for (int c = 0; c < a.nc; ++c) {
-      const float mc = pp[(int64_t)c * a.ps];
-      if (mc > -INFINITY) r = fmaf(expf(mc - M), pp[(int64_t)c * a.ps + 2 + D + i], r);
-    }
-    azs[i] = r;
-  }
+    for (; c < c1; ++c) r0 = fmaf(wc[c], pp[c * ps + col], r0);
+    return (r0 + r1) + (r2 + r3);
+  };
+  for (int j = tid; j < D; j += 128) accr[j] = wsum(0, a.nc, 2 + j);
+  for (int i = tid; i < a.m; i += 128) azs[i] = wsum(0, a.nc, 2 + D + i);
   __syncthreads();
   float* out = a.d.out + ((int64_t)b * hq + h) * D;
-  for (int j = threadIdx.x; j < D; j += blockDim.x) {
-    float o = 0.f;
-    for (int i = 0; i < D; ++i) o = fmaf(accr[i], a.vrot[(int64_t)i * D + j], o);
-    float f = 0.f;
-    for (int c = a.nc; c < a.nch; ++c) {
-      const float mc = pp[(int64_t)c * a.ps];
-      if (mc > -INFINITY) f = fmaf(expf(mc - M), pp[(int64_t)c * a.ps + 2 + j], f);
+  for (int j = tid; j < D; j += 128) {
+    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+    for (int i = 0; i < D; i += 4) {
+      o0 = fmaf(accr[i], a.vrot[(int64_t)i * D + j], o0);
+      o1 = fmaf(accr[i + 1], a.vrot[(int64_t)(i + 1) * D + j], o1);
+      o2 = fmaf(accr[i + 2], a.vrot[(int64_t)(i + 2) * D + j], o2);
+      o3 = fmaf(accr[i + 3], a.vrot[(int64_t)(i + 3) * D + j], o3);
     }
-    o += f;
+    float o = (o0 + o1) + (o2 + o3) + wsum(a.nc, nch, 2 + j);
     if (a.m > 0) {
-      float z = 0.f;
-      for (int i = 0; i < a.m; ++i) z = fmaf(azs[i], a.proj[(int64_t)i * D + j], z);
-      o = fmaf(SQRT_HALF_PI / (float)D, z, o);
+      float z0 = 0.f, z1 = 0.f, z2 = 0.f, z3 = 0.f;
+      for (int i = 0; i < a.m; i += 4) {
+        z0 = fmaf(azs[i], a.proj[(int64_t)i * D + j], z0);
+        z1 = fmaf(azs[i + 1], a.proj[(int64_t)(i + 1) * D + j], z1);
+        z2 = fmaf(azs[i + 2], a.proj[(int64_t)(i + 2) * D + j], z2);
+        z3 = fmaf(azs[i + 3], a.proj[(int64_t)(i + 3) * D + j], z3);
+      }
+      o = fmaf(SQRT_HALF_PI / (float)D, (z0 + z1) + (z2 + z3), o);
     }
     out[j] = (L > 0.f) ? o / L : 0.f;
   }
@@ -615,6 +777,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   chunk_counts(d, a.nc, a.ns, a.nr);
   a.nch = a.nc + a.ns + a.nr;
   a.ps = part_stride(a.D, a.m);
+  a.c0 = 0;
   const size_t heads = (size_t)d->batch * d->hq;
   float* ws = static_cast<float*>(workspace);
   a.qr = ws;
@@ -634,7 +797,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     }
     TQ_LAUNCH_CHECK("tq_decode_attention chunks");
   }
-  const size_t cmb_smem = (size_t)(a.D + a.m) * 4;
+  const size_t cmb_smem = (size_t)(((a.nch + 3) & ~3) + a.D + a.m) * 4;
   hipLaunchKernelGGL(combine_kernel, dim3(d->hq, d->batch), dim3(128), cmb_smem, s, a);
   TQ_LAUNCH_CHECK("tq_decode_attention combine");
   return TQ_OK;

@@ -29,8 +29,38 @@ from .cache import _workspace
 from .rotation import DEFAULT_SEED
 
 
-def _i32(xs, dev) -> torch.Tensor:
-    return torch.tensor(np.asarray(xs, np.int32), dtype=torch.int32, device=dev)
+class _IntStage:
+    """Host int32 arrays to the device in one asynchronous copy per call,
+    through two pinned slots; a slot's host side is rewritten only after its
+    previous copy has completed, and its device side is overwritten by a copy
+    ordered (on the same stream) after the launches that read it."""
+
+    def __init__(self, n: int, dev: torch.device):
+        self.host = [torch.empty(n, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self.dev = [torch.empty(n, dtype=torch.int32, device=dev) for _ in range(2)]
+        self.done = [None, None]
+        self.k = 0
+
+    def put(self, *arrays) -> list[torch.Tensor]:
+        k = self.k
+        self.k ^= 1
+        if self.done[k] is not None:
+            self.done[k].synchronize()
+        h = self.host[k].numpy()
+        n = 0
+        for x in arrays:
+            h[n:n + len(x)] = x
+            n += len(x)
+        d = self.dev[k]
+        d[:n].copy_(self.host[k][:n], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.done[k] = ev
+        views, n = [], 0
+        for x in arrays:
+            views.append(d[n:n + len(x)])
+            n += len(x)
+        return views
 
 
 class RaggedKVBatch:
@@ -58,7 +88,9 @@ class RaggedKVBatch:
         self.ring_v = torch.zeros_like(self.ring_k)
         z = lambda: np.zeros(batch, dtype=np.int64)
         self.sink_len, self.comp_len, self.res_len, self.res_start, self.offset = z(), z(), z(), z(), z()
-        self._keep = []  # per-sequence arrays of launches still in flight
+        self._step_ints = _IntStage(4 * batch, dev)   # ring slots / drain arrays of a step
+        self._attn_ints = _IntStage(4 * batch, dev)   # per-sequence lengths of an attention call
+        self._rows = torch.arange(batch, device=dev)
 
     # ------------------------------------------------------------------ fill
     def load(self, b: int, keys: torch.Tensor, values: torch.Tensor) -> None:
@@ -109,26 +141,32 @@ class RaggedKVBatch:
             raise ValueError("keys / values must be (batch, num_kv_heads, head_dim)")
         keys, values = keys.to(dev, torch.float16), values.to(dev, torch.float16)
         to_sink = self.offset < self.sink
+        # token b goes to sink position sink_len[b] or ring slot (start + len) % cap
+        ring_slot = (self.res_start + self.res_len) % self.cap
+        res_after = self.res_len + ~to_sink
+        drain = res_after > self.window
         if to_sink.any():
             bi = np.nonzero(to_sink)[0]
-            pos = self.sink_len[bi]
-            bt, pt = torch.as_tensor(bi, device=dev), torch.as_tensor(pos, device=dev)
+            bt, pt = self._step_ints.put(bi, self.sink_len[bi])
             self.sink_k[bt, :, pt] = keys[bt]
             self.sink_v[bt, :, pt] = values[bt]
             self.sink_len[bi] += 1
-        bi = np.nonzero(~to_sink)[0]
-        if bi.size:
-            slot = (self.res_start[bi] + self.res_len[bi]) % self.cap
-            bt, st = torch.as_tensor(bi, device=dev), torch.as_tensor(slot, device=dev)
+        # one staged copy: ring slots, then the drain arrays (count, ring start, store position)
+        slot_t, n_b, src_b, dst_b = self._step_ints.put(ring_slot, drain, self.res_start, self.comp_len)
+        if (~to_sink).all():
+            self.ring_k[self._rows, :, slot_t] = keys
+            self.ring_v[self._rows, :, slot_t] = values
+        elif (~to_sink).any():
+            bi = np.nonzero(~to_sink)[0]
+            bt = torch.as_tensor(bi, device=dev)
+            st = slot_t[bt]
             self.ring_k[bt, :, st] = keys[bt]
             self.ring_v[bt, :, st] = values[bt]
-            self.res_len[bi] += 1
-        drain = self.res_len > self.window
+        self.res_len = res_after
         if drain.any():
             need = int((self.comp_len + drain).max())
             self.kstore.reserve(need, int(self.comp_len.max()))
             self.vstore.reserve(need, int(self.comp_len.max()))
-            n_b, src_b, dst_b = _i32(drain, dev), _i32(self.res_start, dev), _i32(self.comp_len, dev)
             span = _lib.Span(rows=B * H, heads=H, n_tok=1, reserved=0, n_tok_b=n_b.data_ptr(),
                              src_tok0_b=src_b.data_ptr(), dst_tok0_b=dst_b.data_ptr())
             lib = _lib.load()
@@ -136,7 +174,6 @@ class RaggedKVBatch:
                 st = store.struct(0)
                 _lib.check(lib.tq_compress(codec.ref(), ring.data_ptr(), _lib.dtype_code(ring.dtype), self.cap * D,
                                            ctypes.byref(span), ctypes.byref(st), _lib.stream_ptr(dev)), "tq_compress")
-            self._keep = [n_b, src_b, dst_b]  # freed after the next launch is ordered behind this one
             self.comp_len += drain
             self.res_start = np.where(drain, (self.res_start + 1) % self.cap, self.res_start)
             self.res_len -= drain
@@ -145,10 +182,8 @@ class RaggedKVBatch:
     # ------------------------------------------------------------- attention
     def descriptor(self, q: torch.Tensor, out: torch.Tensor, scale: float, general: bool = False):
         """``tq_attn_desc`` of a (B, Hq, D) query against every sequence; the
-        per-sequence arrays live until the next call."""
-        dev = q.device
-        comp, sink = _i32(self.comp_len, dev), _i32(self.sink_len, dev)
-        res, start = _i32(self.res_len, dev), _i32(self.res_start, dev)
+        per-sequence arrays are device views valid until the call after next."""
+        comp, sink, res, start = self._attn_ints.put(self.comp_len, self.sink_len, self.res_len, self.res_start)
         arrays = [comp, sink, res, start]
         d = _lib.AttnDesc(
             batch=self.B, hq=q.shape[1], hkv=self.H, qjl=1 if self.qjl else 0, scale=scale,

@@ -200,9 +200,10 @@ def bench_config4(dev, steps: int = 12):
     (lengths ~ U[4096, 32768], seeded), K4/V2, the reference's defaults
     (window 128, no sink): append one token per sequence, drain one per
     sequence into the packed store (one ragged compress launch per side),
-    fused decode attention over every sequence in one launch. With the QJL
-    sketch (m = 128) attention runs on the general kernel; without it on the
-    K4/V2 kernels. Eager launches, events around each step."""
+    fused decode attention over every sequence in one call. With the QJL
+    sketch (m = 128) the K4/V2 kernels run with the sketch's key and value
+    terms around them; without it the K4/V2 kernels alone. Eager launches,
+    events around each step."""
     import numpy as np
     import torch
     from turboquant_amd.ragged import RaggedKVBatch
@@ -235,7 +236,8 @@ def bench_config4(dev, steps: int = 12):
         byt = 8 * (int(rb.comp_len.sum()) * per_tok + int(rb.res_len.sum()) * 512) + 16 * 32 * 128 * 6
         ms_s, ms_a = float(np.median(t_step)), float(np.median(t_attn))
         res["qjl" if qjl_m else "no_qjl"] = {
-            "kernel": "general (chunk_kernel)" if qjl_m else "K4/V2 (fast_decode_kernel + merge)",
+            "kernel": ("K4/V2 + sketch (qjl_bias_kernel, fast_decode_kernel with the key term, merge, qjl_value_kernel, "
+                       "qjl_final_kernel)") if qjl_m else "K4/V2 (fast_decode_kernel + merge)",
             "layer_step_us": round(ms_s * 1e3, 1), "attend_us": round(ms_a * 1e3, 1),
             "attend_bytes": byt, "attend_GBps": round(byt / (ms_a * 1e-3) / 1e9, 1)}
         del rb

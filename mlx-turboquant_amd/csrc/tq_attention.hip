@@ -543,6 +543,145 @@ static void launch_chunks(const AttnArgs& a, int G, dim3 grid, hipStream_t s) {
   }
 }
 
+// ---- QJL sketch terms around the K4/V2 kernels (K4 keys / V2 values with a
+// 1-bit sketch, qjl.py:23-94 as in the general path): a bias kernel adds the
+// key term to each compressed token's score (base 2), the partials kernel
+// stores the final scores, and after the merge a value kernel accumulates
+// u_h = sum_t p_t gamma_t z_t per projection (p the normalised softmax
+// weight of compressed token t) and a final kernel adds sqrt(pi/2)/d S^T u_h to
+// the output, as combine_kernel does for the general path.
+constexpr int QCH = 256;  // tokens per workgroup of the QJL kernels
+
+struct QjlArgs {
+  tq_attn_desc d;
+  const float* sq;      // (batch, hq, m) S (scale q), natural units (prologue_kernel)
+  const float* proj;    // (m, 128)
+  int m;
+  float* bias;          // (batch*hkv*G, qb_hs) key term in base-2 score units
+  const float* scores;  // (batch*hkv*G, qb_hs) final base-2 scores
+  const float* ml;      // (batch, hq, 2) global max and sum of the merge
+  float* upart;         // (batch, hq, nvc, m) per-chunk value terms
+  int64_t qb_hs;
+  int nvc;
+};
+
+template <int G>
+__global__ __launch_bounds__(NT) void qjl_bias_kernel(QjlArgs a) {
+  constexpr int MAXM = 256;
+  __shared__ __align__(16) float sq[G][MAXM];
+  const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int row = b * a.d.hkv + g, m = a.m;
+  for (int e = tid; e < G * m; e += NT) sq[e / m][e % m] = a.sq[((int64_t)b * a.d.hq + g * G + e / m) * m + e % m];
+  __syncthreads();
+  const int comp = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
+  const int t = c * QCH + tid;
+  if (t >= a.qb_hs) return;
+  float zs[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) zs[h] = 0.f;
+  float coef = 0.f;
+  if (t < comp) {
+    const tq_store& ks = a.d.kstore;
+    const float gk = ks.gamma[(int64_t)row * ks.gamma_head_stride + t];
+    dot_signs<G, MAXM>(ks.signs + (int64_t)row * ks.sign_head_stride + (int64_t)t * (m / 8), m, sq, zs);
+    coef = 1.4426950408889634f * SQRT_HALF_PI / 128.f * gk;
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) a.bias[((int64_t)row * G + h) * a.qb_hs + t] = coef * zs[h];
+}
+
+template <int G>
+__global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
+  constexpr int SR = 256 / 8 + 4;  // padded LDS sign row
+  __shared__ __align__(16) float pw[G][QCH];
+  __shared__ __align__(16) uint8_t sg[QCH * SR];
+  __shared__ float slice[G][NT];
+  const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq;
+  const int comp = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
+  const int base = c * QCH, nvalid = max(0, min(QCH, comp - base));
+  const tq_store& vs = a.d.vstore;
+  {
+    const int t = tid;
+    const float gv = t < nvalid ? vs.gamma[(int64_t)row * vs.gamma_head_stride + base + t] : 0.f;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float p = 0.f;
+      if (t < nvalid) {
+        const float M = a.ml[((int64_t)b * hq + g * G + h) * 2], L = a.ml[((int64_t)b * hq + g * G + h) * 2 + 1];
+        const float sc = a.scores[((int64_t)row * G + h) * a.qb_hs + base + t];
+        p = L > 0.f ? exp2f(sc - M) / L : 0.f;
+      }
+      pw[h][t] = p * gv;
+    }
+  }
+  stage_rows(sg, SR, 0, vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base * (m / 8), m / 8, nvalid);
+  __syncthreads();
+  const int nsl = NT / m;
+  const int i = tid % m, sl = tid / m;
+  const int per = QCH / nsl;
+  const int n4 = (nvalid + 3) & ~3;
+  const int t_lo = sl * per, t_hi = min(n4, t_lo + per);
+  float acc[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) acc[h] = 0.f;
+  if (sl < nsl) {
+    for (int tt = t_lo; tt < t_hi; tt += 4) {
+      float z[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) z[u] = ((sg[(tt + u) * SR + (i >> 3)] >> (i & 7)) & 1u) ? 1.f : -1.f;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float4 pq = *reinterpret_cast<const float4*>(&pw[h][tt]);
+        acc[h] = fmaf(pq.x, z[0], acc[h]);
+        acc[h] = fmaf(pq.y, z[1], acc[h]);
+        acc[h] = fmaf(pq.z, z[2], acc[h]);
+        acc[h] = fmaf(pq.w, z[3], acc[h]);
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) slice[h][tid] = acc[h];
+  __syncthreads();
+  for (int e = tid; e < G * m; e += NT) {
+    const int h = e / m, ii = e % m;
+    float v = 0.f;
+    for (int q = 0; q < nsl; ++q) v += slice[h][q * m + ii];
+    a.upart[(((int64_t)b * hq + g * G + h) * a.nvc + c) * m + ii] = v;
+  }
+}
+
+__global__ __launch_bounds__(128) void qjl_final_kernel(QjlArgs a) {
+  __shared__ float u[256];
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, m = a.m;
+  const float* up = a.upart + ((int64_t)b * a.d.hq + h) * a.nvc * m;
+  for (int i = tid; i < m; i += 128) {
+    float v = 0.f;
+    for (int c = 0; c < a.nvc; ++c) v += up[(int64_t)c * m + i];
+    u[i] = v;
+  }
+  __syncthreads();
+  float* out = a.d.out + ((int64_t)b * a.d.hq + h) * 128;
+  const int j = tid;
+  float z0 = 0.f, z1 = 0.f, z2 = 0.f, z3 = 0.f;
+  for (int i = 0; i < m; i += 4) {
+    z0 = fmaf(u[i], a.proj[(int64_t)i * 128 + j], z0);
+    z1 = fmaf(u[i + 1], a.proj[(int64_t)(i + 1) * 128 + j], z1);
+    z2 = fmaf(u[i + 2], a.proj[(int64_t)(i + 2) * 128 + j], z2);
+    z3 = fmaf(u[i + 3], a.proj[(int64_t)(i + 3) * 128 + j], z3);
+  }
+  out[j] += SQRT_HALF_PI / 128.f * ((z0 + z1) + (z2 + z3));
+}
+
+// Workspace of the QJL fast route: [fast partials | qr qs sq | bias | scores | ml | upart], 256-byte pieces.
+struct QjlLayout {
+  size_t part, pro, bias, scores, ml, upart, total;
+  int64_t qb_hs;
+  int nvc;
+};
+
+static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
 static int device_cus() {
   static int cus = 0;
   if (cus == 0) {
@@ -582,10 +721,14 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // The K4/V2 partials kernel reads keys / values / norms / queries in 16-byte
 // pieces: every base and head stride must keep them 16-byte aligned.
-static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
+static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, bool qjl_ok = false) {
   const int G = d->hq / d->hkv;
   if (!(kc->rotation_parts != nullptr && vc->rotation_parts != nullptr && vc->d == 128 && kc->d == 128 && kc->bits_hi == 4 && kc->split == 128 && vc->bits_hi == 2 &&
-        vc->split == 128 && !d->qjl && d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8)))
+        vc->split == 128 && (!d->qjl || qjl_ok) && d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8)))
+    return false;
+  if (d->qjl && d->max_comp > 0 &&
+      !((reinterpret_cast<uintptr_t>(d->kstore.signs) & 3) == 0 && d->kstore.sign_head_stride % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(d->vstore.signs) & 3) == 0 && d->vstore.sign_head_stride % 4 == 0))
     return false;
   if (!aligned16(d->q)) return false;
   if (d->max_comp > 0 &&
@@ -597,6 +740,110 @@ static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_
   if (d->max_res > 0 && !(aligned16(d->res_k) && aligned16(d->res_v) && d->res_head_stride % 8 == 0)) return false;
   int nwg, bpw, fpw;
   return fast_geometry(d, nwg, bpw, fpw);
+}
+
+static QjlLayout qjl_layout(const tq_codec* kc, const tq_attn_desc* d) {
+  QjlLayout L{};
+  int nwg = 1, bpw, fpw;
+  fast_geometry(d, nwg, bpw, fpw);
+  const int G = d->hkv > 0 ? d->hq / d->hkv : 1;
+  const size_t heads = (size_t)d->batch * d->hq;
+  const int m = kc->qjl_m;
+  L.qb_hs = ((int64_t)d->max_comp + 31) / 32 * 32;
+  if (L.qb_hs < 32) L.qb_hs = 32;
+  L.nvc = (d->max_comp + QCH - 1) / QCH;
+  if (L.nvc < 1) L.nvc = 1;
+  size_t off = 0;
+  L.part = off; off += al256((size_t)d->batch * d->hkv * nwg * G * FAST_PART_FLOATS * 4);
+  L.pro = off; off += al256(heads * 128 * 4 * 2 + heads * (size_t)m * 4);
+  L.bias = off; off += al256((size_t)d->batch * d->hkv * G * (size_t)L.qb_hs * 4);
+  L.scores = off; off += al256((size_t)d->batch * d->hkv * G * (size_t)L.qb_hs * 4);
+  L.ml = off; off += al256(heads * 2 * 4);
+  L.upart = off; off += al256(heads * (size_t)L.nvc * m * 4);
+  L.total = off;
+  return L;
+}
+
+// Arguments of the K4/V2 partials + merge kernels for one call.
+static void fill_fast(FastArgs& f, const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part) {
+  f = FastArgs{};
+  f.kc = d->kstore.codes_hi; f.k_hs = d->kstore.hi_head_stride;
+  f.kn = d->kstore.norms; f.kn_hs = d->kstore.norm_head_stride;
+  f.vc = d->vstore.codes_hi; f.v_hs = d->vstore.hi_head_stride;
+  f.vn = d->vstore.norms; f.vn_hs = d->vstore.norm_head_stride;
+  f.sink_k = d->sink_k; f.sink_v = d->sink_v; f.sink_hs = d->sink_head_stride;
+  f.res_k = d->res_k; f.res_v = d->res_v; f.res_hs = d->res_head_stride;
+  f.res_cap = d->res_cap; f.res_start0 = d->res_start0;
+  f.comp_len_b = d->comp_len; f.sink_len_b = d->sink_len; f.res_len_b = d->res_len; f.res_start_b = d->res_start;
+  f.max_comp = d->max_comp; f.max_sink = d->max_sink; f.max_res = d->max_res;
+  f.q = d->q; f.q_dtype = d->q_dtype; f.out = d->out;
+  f.hq = d->hq; f.hkv = d->hkv;
+  f.qscale = d->scale * 1.4426950408889634f;
+  f.rot16 = kc->rotation_parts; f.rotT = vc->rotation_parts + 2 * 128 * 128; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
+  f.part = part;
+  fast_geometry(d, f.nwg, f.bpw, f.fpw);
+  f.merge = (d->flags & TQ_ATTN_PARTIALS_ONLY) ? 0 : 1;
+}
+
+// The QJL route: prologue (S q), key-term bias, K4/V2 partials with the bias
+// (scores stored) + merge (max and sum exported), value term, final S^T add.
+static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace,
+                        size_t workspace_bytes, hipStream_t s) {
+  const QjlLayout QL = qjl_layout(kc, d);
+  if (!workspace || workspace_bytes < QL.total)
+    return set_error(TQ_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, QL.total);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const int G = d->hq / d->hkv;
+  const size_t heads = (size_t)d->batch * d->hq;
+  AttnArgs pa{};
+  pa.d = *d;
+  pa.D = 128;
+  pa.rot = kc->rotation;
+  pa.proj = kc->qjl_proj;
+  pa.m = kc->qjl_m;
+  pa.qr = reinterpret_cast<float*>(ws + QL.pro);
+  pa.qs = pa.qr + heads * 128;
+  pa.sq = pa.qs + heads * 128;
+  hipLaunchKernelGGL(prologue_kernel, dim3(d->hq, d->batch), dim3(128), 128 * 4, s, pa);
+  TQ_LAUNCH_CHECK("tq_decode_attention qjl prologue");
+  QjlArgs qa;
+  qa.d = *d;
+  qa.sq = pa.sq;
+  qa.proj = kc->qjl_proj;
+  qa.m = kc->qjl_m;
+  qa.bias = reinterpret_cast<float*>(ws + QL.bias);
+  qa.scores = reinterpret_cast<float*>(ws + QL.scores);
+  qa.ml = reinterpret_cast<float*>(ws + QL.ml);
+  qa.upart = reinterpret_cast<float*>(ws + QL.upart);
+  qa.qb_hs = QL.qb_hs;
+  qa.nvc = QL.nvc;
+  const dim3 bgrid((unsigned)((QL.qb_hs + QCH - 1) / QCH), d->hkv, d->batch);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((qjl_bias_kernel<1>), bgrid, dim3(NT), 0, s, qa); break;
+    case 2: hipLaunchKernelGGL((qjl_bias_kernel<2>), bgrid, dim3(NT), 0, s, qa); break;
+    case 4: hipLaunchKernelGGL((qjl_bias_kernel<4>), bgrid, dim3(NT), 0, s, qa); break;
+    default: hipLaunchKernelGGL((qjl_bias_kernel<8>), bgrid, dim3(NT), 0, s, qa); break;
+  }
+  TQ_LAUNCH_CHECK("tq_decode_attention qjl bias");
+  FastArgs f;
+  fill_fast(f, kc, vc, d, reinterpret_cast<float*>(ws + QL.part));
+  f.merge = 1;
+  f.qjl_bias = qa.bias;
+  f.scores = const_cast<float*>(qa.scores);
+  f.qb_hs = QL.qb_hs;
+  f.ml = const_cast<float*>(qa.ml);
+  if (launch_fast_decode_qjl(f, G, d->batch, s) != 0) TQ_LAUNCH_CHECK("tq_decode_attention qjl fast");
+  const dim3 vgrid((unsigned)QL.nvc, d->hkv, d->batch);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((qjl_value_kernel<1>), vgrid, dim3(NT), 0, s, qa); break;
+    case 2: hipLaunchKernelGGL((qjl_value_kernel<2>), vgrid, dim3(NT), 0, s, qa); break;
+    case 4: hipLaunchKernelGGL((qjl_value_kernel<4>), vgrid, dim3(NT), 0, s, qa); break;
+    default: hipLaunchKernelGGL((qjl_value_kernel<8>), vgrid, dim3(NT), 0, s, qa); break;
+  }
+  TQ_LAUNCH_CHECK("tq_decode_attention qjl value");
+  hipLaunchKernelGGL(qjl_final_kernel, dim3(d->hq, d->batch), dim3(128), 0, s, qa);
+  TQ_LAUNCH_CHECK("tq_decode_attention qjl final");
+  return TQ_OK;
 }
 
 // Dense (uncompressed fp16 / bf16) calls: head_dim 128, nothing compressed,
@@ -678,6 +925,11 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
   if (fast_geometry(d, nwg, bpw, fpw))
     fast = (size_t)d->batch * d->hkv * nwg * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
   size_t bytes = general > fast ? general : fast;
+  if (d->qjl && kcodec->d == 128 && kcodec->qjl_m > 0 && kcodec->qjl_m <= 256 && d->max_comp > 0 && d->hkv > 0 &&
+      d->hq % d->hkv == 0) {
+    const size_t qf = qjl_layout(kcodec, d).total;
+    if (qf > bytes) bytes = qf;
+  }
   if (d->max_comp == 0 && kcodec->d == 128) {
     const size_t dense = dense_workspace(d);
     if (dense > bytes) bytes = dense;
@@ -727,26 +979,13 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   if (d->max_comp == 0 && !(d->flags & TQ_ATTN_GENERAL) && (d->max_sink > 0 || d->max_res > 0) &&
       dense_check(d, kc->d, false) == TQ_OK)
     return dense_run(d, workspace, workspace_bytes, s);
+  if (qjl && d->max_comp > 0 && fast_eligible(kc, vc, d, true) && !(d->flags & TQ_ATTN_GENERAL))
+    return qjl_fast_run(kc, vc, d, workspace, workspace_bytes, s);
   if (fast_eligible(kc, vc, d) && !(d->flags & TQ_ATTN_GENERAL)) {
     if (fast_set_attributes() != 0)
       return set_error(TQ_ERR_LAUNCH, "cannot raise the LDS limit of the decode kernel");
     FastArgs f;
-    f.kc = d->kstore.codes_hi; f.k_hs = d->kstore.hi_head_stride;
-    f.kn = d->kstore.norms; f.kn_hs = d->kstore.norm_head_stride;
-    f.vc = d->vstore.codes_hi; f.v_hs = d->vstore.hi_head_stride;
-    f.vn = d->vstore.norms; f.vn_hs = d->vstore.norm_head_stride;
-    f.sink_k = d->sink_k; f.sink_v = d->sink_v; f.sink_hs = d->sink_head_stride;
-    f.res_k = d->res_k; f.res_v = d->res_v; f.res_hs = d->res_head_stride;
-    f.res_cap = d->res_cap; f.res_start0 = d->res_start0;
-    f.comp_len_b = d->comp_len; f.sink_len_b = d->sink_len; f.res_len_b = d->res_len; f.res_start_b = d->res_start;
-    f.max_comp = d->max_comp; f.max_sink = d->max_sink; f.max_res = d->max_res;
-    f.q = d->q; f.q_dtype = d->q_dtype; f.out = d->out;
-    f.hq = d->hq; f.hkv = d->hkv;
-    f.qscale = d->scale * 1.4426950408889634f;
-    f.rot16 = kc->rotation_parts; f.rotT = vc->rotation_parts + 2 * 128 * 128; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
-    f.part = static_cast<float*>(workspace);
-    fast_geometry(d, f.nwg, f.bpw, f.fpw);
-    f.merge = (d->flags & TQ_ATTN_PARTIALS_ONLY) ? 0 : 1;
+    fill_fast(f, kc, vc, d, static_cast<float*>(workspace));
     if (launch_fast_decode(f, G, d->batch, s) != 0)
       TQ_LAUNCH_CHECK("tq_decode_attention (fast)");
     return TQ_OK;

@@ -32,11 +32,19 @@ struct FastArgs {
   int bpw;               // compressed 32-token blocks per workgroup (<= FAST_WAVES * FAST_BLOCKS_PER_WAVE)
   int fpw;               // fp16 (sink / residual) tokens per workgroup (<= FAST_FP16_PER_WG)
   int merge;             // 1: launch the merge kernel too; 0: partials only (measurement)
+  // QJL sketch terms (the fast kernel with QB): per (sequence, kv head, query
+  // head) rows of qb_hs floats indexed by compressed token
+  const float* qjl_bias; // added to each compressed token's base-2 score
+  float* scores;         // final base-2 scores of the compressed tokens (written)
+  int64_t qb_hs;
+  float* ml;             // merge output: (batch, hq, 2) global max and sum, or NULL
 };
 
 size_t fast_smem_bytes();
 int fast_set_attributes();
 int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s);
+// the same kernels with the QJL key bias added to the scores and the scores stored (a.qjl_bias, a.scores)
+int launch_fast_decode_qjl(const FastArgs& a, int G, int batch, hipStream_t s);
 
 constexpr int FAST_WAVES = 8;            // waves per workgroup of the decode kernel
 constexpr int FAST_BLOCKS_PER_WAVE = 4;  // compressed blocks per wave (two in flight at a time)

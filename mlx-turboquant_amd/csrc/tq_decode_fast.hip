@@ -253,6 +253,10 @@ __global__ __launch_bounds__(64) void fast_merge_kernel(FastArgs a) {
     for (int i = 0; i < MB; ++i) x[i] = pall[min(p0 + MB + i, np - 1) * pstride + P_OUT + dim];
   }
   a.out[((int64_t)b * a.hq + hqi) * FD + dim] = acc * inv;
+  if (a.ml && half == 0 && lane == 0) {
+    a.ml[((int64_t)b * a.hq + hqi) * 2] = m;
+    a.ml[((int64_t)b * a.hq + hqi) * 2 + 1] = l;
+  }
 }
 
 // The compressed blocks of one wave: loads issued at kernel start (lane r, q4)
@@ -267,7 +271,7 @@ __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
 }
 
-template <int G>
+template <int G, bool QB = false>
 __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
   __shared__ __align__(16) uint8_t smem[Layout::total];
 
@@ -716,10 +720,28 @@ __global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
         sc[4 + i] = (sB[i] + partner<G>(sB[i])) * nk[4 + i];
       }
     }
+    if constexpr (QB) {
+      // QJL key term of the lane's tokens (tile `tile`, or both for TS == 1)
+      const float* qb = a.qjl_bias + ((int64_t)row * G + hd) * a.qb_hs + t0 + 4 * q4;
+#pragma unroll
+      for (int t = 0; t < 2 / TS; ++t) {
+        const float4 bb = *reinterpret_cast<const float4*>(qb + 16 * (t + tile));
+        sc[4 * t] += bb.x; sc[4 * t + 1] += bb.y; sc[4 * t + 2] += bb.z; sc[4 * t + 3] += bb.w;
+      }
+    }
     if (t0 + 32 > tend) {  // uniform: only the last block of a sequence and empty slots mask
 #pragma unroll
       for (int i = 0; i < NS; ++i)
         if (t0 + 16 * (tile + (i >> 2)) + 4 * q4 + (i & 3) >= tend) sc[i] = -INFINITY;
+    }
+    if constexpr (QB) {
+      // the final scores of the compressed tokens, for the QJL value term
+      if (tend > 0 && !lo_part && c8 < G) {
+        float* so = a.scores + ((int64_t)row * G + hd) * a.qb_hs + t0 + 4 * q4;
+#pragma unroll
+        for (int t = 0; t < 2 / TS; ++t)
+          *reinterpret_cast<float4*>(so + 16 * (t + tile)) = make_float4(sc[4 * t], sc[4 * t + 1], sc[4 * t + 2], sc[4 * t + 3]);
+      }
     }
     const half8 pb = softmax_pv(sc, nv, acc_r);
 #pragma unroll
@@ -842,6 +864,22 @@ int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s) {
     case 2: launch_g<2>(a, batch, s); break;
     case 4: launch_g<4>(a, batch, s); break;
     default: launch_g<8>(a, batch, s); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int G>
+static void launch_gq(const FastArgs& a, int batch, hipStream_t s) {
+  hipLaunchKernelGGL((fast_decode_kernel<G, true>), dim3(a.nwg, a.hkv, batch), dim3(FT), 0, s, a);
+  if (a.merge) hipLaunchKernelGGL((fast_merge_kernel<G>), dim3(2, a.hq, batch), dim3(64), 0, s, a);
+}
+
+int launch_fast_decode_qjl(const FastArgs& a, int G, int batch, hipStream_t s) {
+  switch (G) {
+    case 1: launch_gq<1>(a, batch, s); break;
+    case 2: launch_gq<2>(a, batch, s); break;
+    case 4: launch_gq<4>(a, batch, s); break;
+    default: launch_gq<8>(a, batch, s); break;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

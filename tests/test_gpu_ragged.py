@@ -128,10 +128,11 @@ def test_ragged_small(qjl_m):
     assert list(rb.comp_len) == [T - 16 - 32 for T in lens]
     q = torch.randn(rb.B, 2 * HQ_PER_KV, D, generator=rb.g, device=DEV).half()
     check_batch(rb, q, oracle_rows=range(rb.B), label=f"small m={qjl_m}")
-    if not qjl_m:  # the K4/V2 kernels against the general kernel on the same batch
-        a = rb.attend(q).cpu().numpy()
-        b = rb.attend(q, general=True).cpu().numpy()
-        assert rel_err(a, b) < 1e-4
+    # the K4/V2 kernels (with the QJL bias / value kernels when sketched) against
+    # the general kernel on the same batch
+    a = rb.attend(q).cpu().numpy()
+    b = rb.attend(q, general=True).cpu().numpy()
+    assert rel_err(a, b) < 1e-4
     for _ in range(40):  # the rings (33 slots) wrap
         step(rb)
     assert list(rb.comp_len) == [T - 16 - 32 + 40 for T in lens] and (rb.res_len == 32).all()
@@ -184,3 +185,6 @@ def test_config4_ragged_decode(qjl_m):
     assert (rb.comp_len == lens - 128 - 128 + 256).all() and (rb.offset == lens + 256).all()
     q = torch.randn(rb.B, 8 * HQ_PER_KV, D, generator=rb.g, device=DEV).half()
     check_batch(rb, q, oracle_rows=short, label=f"config4 m={qjl_m} step 256")
+    a = rb.attend(q).cpu().numpy()
+    b = rb.attend(q, general=True).cpu().numpy()
+    assert rel_err(a, b) < 1e-4, f"config4 m={qjl_m}: fast route vs general kernel {rel_err(a, b):.3e}"

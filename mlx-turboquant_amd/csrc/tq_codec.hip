@@ -279,6 +279,121 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
   }
 }
 
+// One vector per wave for small spans (d = 128, with or without a sketch of
+// m <= 128): the one-token ragged drains of a decode step, where the tiled
+// kernel above (64 vectors per workgroup) spends its time in a long chain of
+// dependent phases. The same float32 / float64 operations in the same order
+// as compress_kernel, so the outputs are bit-identical: every product is one
+// output per lane (lane and lane + 64) summed over i = 0..127 in order with
+// fmaf, with R and S staged in LDS (rows padded to 129 floats).
+constexpr int DRW = 8;    // waves (vectors) per workgroup
+constexpr int DRP = 129;  // padded LDS row
+
+__global__ __launch_bounds__(DRW * 64) void drain_kernel(CompressArgs a) {
+  __shared__ float rt[128 * DRP];   // R[c][i] at c * DRP + i
+  __shared__ float st[128 * DRP];   // S[k][i] at k * DRP + i
+  __shared__ float vec[DRW][128];
+  __shared__ uint8_t cds[DRW][128];
+  __shared__ float bnd[2][16];
+  __shared__ float cen[2][16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int e = tid; e < 128 * 128; e += DRW * 64) rt[(e >> 7) * DRP + (e & 127)] = a.rot[e];
+  for (int e = tid; e < a.qjl_m * 128; e += DRW * 64) st[(e >> 7) * DRP + (e & 127)] = a.proj[e];
+  if (tid < 16) {
+    const int nbh = (1 << a.bits_hi) - 1, nbl = (1 << a.bits_lo) - 1;
+    bnd[0][tid] = tid < nbh ? a.bnd_hi[tid] : 0.f;
+    bnd[1][tid] = tid < nbl ? a.bnd_lo[tid] : 0.f;
+    cen[0][tid] = tid <= nbh ? a.cen_hi[tid] : 0.f;
+    cen[1][tid] = tid <= nbl ? a.cen_lo[tid] : 0.f;
+  }
+  __syncthreads();  // the only barrier: waves without a vector may leave after it
+
+  const int vid = blockIdx.x * DRW + w;
+  const int r = vid / a.span.n_tok, t = vid % a.span.n_tok;
+  if (r >= a.span.rows) return;
+  const int b = r / a.span.heads;
+  const int n_tok = a.span.n_tok_b ? a.span.n_tok_b[b] : a.span.n_tok;
+  if (t >= n_tok) return;
+  const int src = (a.span.src_tok0_b ? a.span.src_tok0_b[b] : 0) + t;
+  const int dst = (a.span.dst_tok0_b ? a.span.dst_tok0_b[b] : 0) + t;
+  float* xv = vec[w];
+  const int64_t xrow = (int64_t)r * a.x_hs + (int64_t)src * 128;
+  const float x0 = load_elem(a.x, xrow + lane, a.x_dtype);
+  const float x1 = load_elem(a.x, xrow + 64 + lane, a.x_dtype);
+  xv[lane] = x0;
+  xv[64 + lane] = x1;
+  // norm: float64 block sums (every lane, the same value)
+  const float n = (float)sqrt(sumsq_blocks<128>(xv));
+  if (lane == 0) a.dst.norms[(int64_t)r * a.dst.norm_head_stride + dst] = n;
+  xv[lane] = x0 / fmaxf(n, 1e-10f);
+  xv[64 + lane] = x1 / fmaxf(n, 1e-10f);
+  // rotate: y_c = sum_i x_n[i] * R[c][i]
+  float y0 = 0.f, y1 = 0.f;
+#pragma unroll 8
+  for (int i = 0; i < 128; ++i) {
+    const float xi = xv[i];
+    y0 = fmaf(xi, rt[lane * DRP + i], y0);
+    y1 = fmaf(xi, rt[(lane + 64) * DRP + i], y1);
+  }
+  const bool hi0 = lane < a.split, hi1 = lane + 64 < a.split;
+  const uint32_t c0 = quantize_one(y0, bnd[hi0 ? 0 : 1], (1 << (hi0 ? a.bits_hi : a.bits_lo)) - 1);
+  const uint32_t c1 = quantize_one(y1, bnd[hi1 ? 0 : 1], (1 << (hi1 ? a.bits_hi : a.bits_lo)) - 1);
+  cds[w][lane] = (uint8_t)c0;
+  cds[w][64 + lane] = (uint8_t)c1;
+  if (lane < 4) {  // lane q packs the 32 codes of segment q
+    const int q = lane;
+    const bool hi = 32 * q < a.split;
+    const int bits = hi ? a.bits_hi : a.bits_lo;
+    uint32_t code[32];
+#pragma unroll
+    for (int c = 0; c < 32; ++c) code[c] = cds[w][32 * q + c];
+    uint8_t* d = hi ? a.dst.codes_hi + (int64_t)r * a.dst.hi_head_stride + (int64_t)dst * a.row_hi + (32 * q) * bits / 8
+                    : a.dst.codes_lo + (int64_t)r * a.dst.lo_head_stride + (int64_t)dst * a.row_lo +
+                          (32 * q - a.split) * bits / 8;
+    store_codes_dyn(bits, d, code);
+  }
+  if (!a.proj) return;
+  // QJL sketch of the residual r = x - n * (c[idx] @ R)
+  xv[lane] = cen[hi0 ? 0 : 1][c0];
+  xv[64 + lane] = cen[hi1 ? 0 : 1][c1];
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll 8
+  for (int i = 0; i < 128; ++i) {
+    const float ci = xv[i];
+    a0 = fmaf(ci, rt[i * DRP + lane], a0);
+    a1 = fmaf(ci, rt[i * DRP + lane + 64], a1);
+  }
+  const float r0 = x0 - n * a0;
+  const float r1 = x1 - n * a1;
+  xv[lane] = r0;
+  xv[64 + lane] = r1;
+  double s2 = 0.0;
+#pragma unroll 8
+  for (int i = 0; i < 128; ++i) {
+    const double ri = (double)xv[i];
+    s2 = fma(ri, ri, s2);
+  }
+  if (lane == 0) a.dst.gamma[(int64_t)r * a.dst.gamma_head_stride + dst] = (float)sqrt(s2);
+  float p0 = 0.f, p1 = 0.f;
+  const int k1 = min(lane + 64, a.qjl_m - 1);
+#pragma unroll 8
+  for (int i = 0; i < 128; ++i) {
+    const float ri = xv[i];
+    p0 = fmaf(ri, st[lane * DRP + i], p0);
+    p1 = fmaf(ri, st[k1 * DRP + i], p1);
+  }
+  const uint64_t s_lo = __ballot(p0 >= 0.f), s_hi = __ballot(p1 >= 0.f);
+  if (lane == 0) {
+    uint32_t* sd = reinterpret_cast<uint32_t*>(a.dst.signs + (int64_t)r * a.dst.sign_head_stride + (int64_t)dst * a.row_sign);
+    const int nw = a.qjl_m / 32;
+    sd[0] = (uint32_t)s_lo;
+    if (nw > 1) sd[1] = (uint32_t)(s_lo >> 32);
+    if (nw > 2) sd[2] = (uint32_t)s_hi;
+    if (nw > 3) sd[3] = (uint32_t)(s_hi >> 32);
+  }
+}
+
 struct DequantArgs {
   tq_store src;
   tq_span span;
@@ -494,6 +609,14 @@ int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x
   a.row_lo = row_bytes(codec->d - codec->split, a.bits_lo);
   a.row_sign = a.qjl_m / 8;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // small spans with the QJL sketch (one-token decode drains): one vector per
+  // wave (without a sketch the MFMA kernel below is as fast on such spans)
+  if (codec->d == 128 && qjl && codec->qjl_m <= 128 && span->n_tok <= 8 && !g_force_general) {
+    const int64_t nvec = (int64_t)span->rows * span->n_tok;
+    hipLaunchKernelGGL(drain_kernel, dim3((unsigned)((nvec + DRW - 1) / DRW)), dim3(DRW * 64), 0, s, a);
+    TQ_LAUNCH_CHECK("tq_compress (drain)");
+    return TQ_OK;
+  }
   // fp16, head_dim 128, no QJL sketch: the MFMA kernel (tq_compress_fast.hip)
   if (codec->d == 128 && !g_force_general && launch_compress_fast(a, s)) {
     TQ_LAUNCH_CHECK("tq_compress");

@@ -656,9 +656,16 @@ __global__ __launch_bounds__(128) void qjl_final_kernel(QjlArgs a) {
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, m = a.m;
   const float* up = a.upart + ((int64_t)b * a.d.hq + h) * a.nvc * m;
   for (int i = tid; i < m; i += 128) {
-    float v = 0.f;
-    for (int c = 0; c < a.nvc; ++c) v += up[(int64_t)c * m + i];
-    u[i] = v;
+    float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+    int c = 0;
+    for (; c + 4 <= a.nvc; c += 4) {
+      v0 += up[(int64_t)c * m + i];
+      v1 += up[(int64_t)(c + 1) * m + i];
+      v2 += up[(int64_t)(c + 2) * m + i];
+      v3 += up[(int64_t)(c + 3) * m + i];
+    }
+    for (; c < a.nvc; ++c) v0 += up[(int64_t)c * m + i];
+    u[i] = (v0 + v1) + (v2 + v3);
   }
   __syncthreads();
   float* out = a.d.out + ((int64_t)b * a.d.hq + h) * 128;

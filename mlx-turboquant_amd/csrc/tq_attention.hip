@@ -571,9 +571,12 @@ __global__ __launch_bounds__(NT) void qjl_bias_kernel(QjlArgs a) {
   __shared__ __align__(16) float sq[G][MAXM];
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m;
+  const int comp = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
+  // past the sequence's last 32-token block the bias is never read (those
+  // scores are masked after it is added)
+  if (c * QCH >= ((comp + 31) & ~31)) return;
   for (int e = tid; e < G * m; e += NT) sq[e / m][e % m] = a.sq[((int64_t)b * a.d.hq + g * G + e / m) * m + e % m];
   __syncthreads();
-  const int comp = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
   const int t = c * QCH + tid;
   if (t >= a.qb_hs) return;
   float zs[G];
@@ -600,6 +603,11 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq;
   const int comp = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
   const int base = c * QCH, nvalid = max(0, min(QCH, comp - base));
+  if (nvalid == 0) {  // past the sequence: a zero partial (the final kernel sums every chunk)
+    for (int e = tid; e < G * m; e += NT)
+      a.upart[(((int64_t)b * hq + g * G + e / m) * a.nvc + c) * m + e % m] = 0.f;
+    return;
+  }
   const tq_store& vs = a.d.vstore;
   {
     const int t = tid;

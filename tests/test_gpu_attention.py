@@ -132,6 +132,22 @@ def test_attention_qjl():
     check(c, o, q, "qjl")
 
 
+@pytest.mark.parametrize("G,m", [(1, 32), (2, 96), (4, 64), (8, 256)])
+def test_attention_qjl_k4v2_route(G, m):
+    """K4/V2 with a sketch runs the K4/V2 kernels with the sketch's key and
+    value terms (bias, value and final kernels): float64 over the stored codes
+    and the general kernel on the same cache agree with it, for every query
+    group size and sketch sizes 32-256, two sequences, a sink."""
+    k, v = _kv(2, 2, 700, 128, seed=30 + G)
+    c, o = build(dict(head_dim=128, num_kv_heads=2, residual_window=64, fp16_sink_size=16, qjl_correction=True,
+                      qjl_n_proj=m), k, v)
+    q = np.random.RandomState(31).randn(2, 2 * G, 1, 128).astype(np.float16)
+    check(c, o, q, f"qjl G={G} m={m}")
+    a = c.attend(to_dev(q)).cpu().numpy()
+    b = c.attend(to_dev(q), general_kernel=True).cpu().numpy()
+    assert rel_err(a, b) < 1e-4, f"K4/V2 sketch route vs general kernel: {rel_err(a, b):.3e}"
+
+
 def test_attention_float32_inputs_and_scale():
     rng = np.random.RandomState(31)
     k = rng.randn(1, 2, 400, 128).astype(np.float32)

@@ -593,12 +593,20 @@ __global__ __launch_bounds__(NT) void qjl_bias_kernel(QjlArgs a) {
   for (int h = 0; h < G; ++h) a.bias[((int64_t)row * G + h) * a.qb_hs + t] = coef * zs[h];
 }
 
+typedef _Float16 qh8 __attribute__((ext_vector_type(8)));
+typedef float qf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t qu4 __attribute__((ext_vector_type(4)));
+
+// u = sum_t w_t z_t (w_t = p_t gamma_t per head) by MFMA 16x16x32 f16:
+// A = W (row h: the fp16 high part of head h's weights, row h + 8 the
+// remainder; k = 32 tokens of a block), B = Z (k = the same tokens, columns =
+// 16 projections, exact +-1 built from the staged sign rows), so output rows h
+// and h + 8 added give head h. Wave w takes the projection tiles w, w + 4, ...
 template <int G>
 __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
-  constexpr int SR = 256 / 8 + 4;  // padded LDS sign row
+  constexpr int SR = 256 / 8 + 4;  // padded LDS sign row (bytes)
   __shared__ __align__(16) float pw[G][QCH];
   __shared__ __align__(16) uint8_t sg[QCH * SR];
-  __shared__ float slice[G][NT];
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq;
   const int comp = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
@@ -625,37 +633,48 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   }
   stage_rows(sg, SR, 0, vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base * (m / 8), m / 8, nvalid);
   __syncthreads();
-  const int nsl = NT / m;
-  const int i = tid % m, sl = tid / m;
-  const int per = QCH / nsl;
-  const int n4 = (nvalid + 3) & ~3;
-  const int t_lo = sl * per, t_hi = min(n4, t_lo + per);
-  float acc[G];
+  const int lane = tid & 63, w = tid >> 6, r = lane & 15, q4 = lane >> 4;
+  const int h = r & 7;
+  const bool lo_row = r >= 8;
+  const int nblk = (nvalid + 31) >> 5;
+  for (int ct = w; ct < m / 16; ct += NT / 64) {
+    qf4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int bk = 0; bk < nblk; ++bk) {
+      const int t0 = 32 * bk + 8 * q4;  // the lane's 8 tokens (k-slots 8 q4 .. 8 q4 + 7)
+      // A: weights of head h (zero past G and past nvalid: pw is zero there)
+      qu4 av;
 #pragma unroll
-  for (int h = 0; h < G; ++h) acc[h] = 0.f;
-  if (sl < nsl) {
-    for (int tt = t_lo; tt < t_hi; tt += 4) {
-      float z[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) z[u] = ((sg[(tt + u) * SR + (i >> 3)] >> (i & 7)) & 1u) ? 1.f : -1.f;
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float4 pq = *reinterpret_cast<const float4*>(&pw[h][tt]);
-        acc[h] = fmaf(pq.x, z[0], acc[h]);
-        acc[h] = fmaf(pq.y, z[1], acc[h]);
-        acc[h] = fmaf(pq.z, z[2], acc[h]);
-        acc[h] = fmaf(pq.w, z[3], acc[h]);
+      for (int e = 0; e < 4; ++e) {
+        float w0 = 0.f, w1 = 0.f;
+        if (h < G) {
+          w0 = pw[h][t0 + 2 * e];
+          w1 = pw[h][t0 + 2 * e + 1];
+        }
+        const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
+        const _Float16 l0 = (_Float16)(w0 - (float)h0), l1 = (_Float16)(w1 - (float)h1);
+        const _Float16 x0 = lo_row ? l0 : h0, x1 = lo_row ? l1 : h1;
+        av[e] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
       }
-    }
-  }
+      // B: +-1 of projection 16 ct + r for the lane's 8 tokens (bit set -> +1)
+      const int pj = 16 * ct + r;
+      qu4 bv;
 #pragma unroll
-  for (int h = 0; h < G; ++h) slice[h][tid] = acc[h];
-  __syncthreads();
-  for (int e = tid; e < G * m; e += NT) {
-    const int h = e / m, ii = e % m;
-    float v = 0.f;
-    for (int q = 0; q < nsl; ++q) v += slice[h][q * m + ii];
-    a.upart[(((int64_t)b * hq + g * G + h) * a.nvc + c) * m + ii] = v;
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t s0 = (sg[(t0 + 2 * e) * SR + (pj >> 3)] >> (pj & 7)) & 1u;
+        const uint32_t s1 = (sg[(t0 + 2 * e + 1) * SR + (pj >> 3)] >> (pj & 7)) & 1u;
+        bv[e] = 0xBC00BC00u ^ (s0 << 15) ^ (s1 << 31);
+      }
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qh8, av), __builtin_bit_cast(qh8, bv), acc, 0, 0,
+                                                   0);
+    }
+    // rows 4 q4 + i: add the remainder rows (lane ^ 32 holds rows + 8)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
+      const float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      const int hh = 4 * q4 + i;
+      if (q4 < 2 && hh < G) a.upart[(((int64_t)b * hq + g * G + hh) * a.nvc + c) * m + 16 * ct + r] = v;
+    }
   }
 }
 

@@ -79,12 +79,17 @@ def test_fused_decode_in_model(prompt_len, window, sink):
     assert (c_fr - c_dr).abs().max().item() < 5e-3
 
 
-def test_fused_matches_sdpa_before_compression():
+@pytest.mark.parametrize("skip", [None, [1]], ids=["all_turboquant", "layer1_fp16"])
+def test_fused_matches_sdpa_before_compression(skip):
+    """Nothing compressed yet (and, with a skipped layer, an uncompressed
+    FP16KVCache layer): the one-token steps run the dense decode kernel
+    inside the model and match SDPA."""
     from transformers import DynamicCache
     from turboquant_amd import apply_turboquant
-    from turboquant_amd.hf import TurboQuantCache
+    from turboquant_amd.hf import TurboQuantCache, TurboQuantLayer
+    from turboquant_amd.patch import FP16KVCache
     m = tiny_llama(seed=4)
-    apply_turboquant(m, key_bits=4, value_bits=2, residual_window=512, auto_detect_outliers=False)
+    apply_turboquant(m, key_bits=4, value_bits=2, residual_window=512, auto_detect_outliers=False, skip_layers=skip)
     prompt, steps = _tokens(200, 5), _tokens(20, 6)
     m.set_attn_implementation("sdpa")
     ref = run(m, DynamicCache(), prompt, steps)
@@ -92,6 +97,9 @@ def test_fused_matches_sdpa_before_compression():
     cache = TurboQuantCache(m, fused=True)
     got = run(m, cache, prompt, steps)
     assert cache.layers[0].cache._compressed_len == 0
+    if skip:
+        assert isinstance(cache.layers[1], TurboQuantLayer) and isinstance(cache.layers[1].cache, FP16KVCache)
+        assert cache.layers[1].fused and cache.layers[1].cache.offset == 220
     e = ((got - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item()
-    print(f"fp16 residual only: fused vs SDPA rel {e:.2e}")
+    print(f"fp16 residual only (skip={skip}): fused vs SDPA rel {e:.2e}")
     assert e < 5e-3

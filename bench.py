@@ -330,7 +330,8 @@ def read_traffic():
 
 def pmc_workload(ctx: int):
     """Short program for the counter runs: a copy of known size (the scale of
-    FETCH_SIZE / WRITE_SIZE), then 20 partials-kernel launches of layer 0."""
+    FETCH_SIZE / WRITE_SIZE), then 20 partials-kernel launches of layer 0, then
+    10 dense decode calls over a configs[3] fp16 layer (65536 tokens)."""
     import torch
     from turboquant_amd import _lib
     _lib.load()
@@ -345,8 +346,18 @@ def pmc_workload(ctx: int):
     for _ in range(20):
         call_partials_only(caches[0], qs[0], out)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_bytes": n, "partials_launches": 20,
-                      "algorithmic_bytes_per_launch": decode_bytes_per_layer(caches[0], 32)}), flush=True)
+    del caches
+    from turboquant_amd.patch import FP16KVCache
+    g = torch.Generator(device=dev).manual_seed(2000)
+    f = FP16KVCache()
+    f.update(torch.randn(1, 8, 65536, 128, generator=g, device=dev).half(),
+             torch.randn(1, 8, 65536, 128, generator=g, device=dev).half())
+    q = torch.randn(1, 32, 1, 128, generator=g, device=dev).half()
+    for _ in range(10):
+        f.attend(q, out=out)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "partials_launches": 20, "dense_launches": 10,
+                      "dense_bytes_per_launch": 8 * 65536 * 512 + 32 * 128 * 2}), flush=True)
 
 
 def main():

@@ -626,7 +626,7 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
       if (t < nvalid) {
         const float M = a.ml[((int64_t)b * hq + g * G + h) * 2], L = a.ml[((int64_t)b * hq + g * G + h) * 2 + 1];
         const float sc = a.scores[((int64_t)row * G + h) * a.qb_hs + base + t];
-        p = L > 0.f ? exp2f(sc - M) / L : 0.f;
+        p = L > 0.f ? __builtin_amdgcn_exp2f(sc - M) * (1.f / L) : 0.f;
       }
       pw[h][t] = p * gv;
     }
@@ -637,24 +637,32 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   const int h = r & 7;
   const bool lo_row = r >= 8;
   const int nblk = (nvalid + 31) >> 5;
+  // A operands of the (at most 8) blocks: weights of head h, the fp16 high
+  // part (rows < 8) or remainder (rows >= 8); zero past G and past nvalid
+  qu4 aw[QCH / 32];
+#pragma unroll
+  for (int bk = 0; bk < QCH / 32; ++bk) {
+    const int t0 = 32 * bk + 8 * q4;  // the lane's 8 tokens (k-slots 8 q4 .. 8 q4 + 7)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float w0 = 0.f, w1 = 0.f;
+      if (h < G) {
+        w0 = pw[h][t0 + 2 * e];
+        w1 = pw[h][t0 + 2 * e + 1];
+      }
+      const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
+      const _Float16 l0 = (_Float16)(w0 - (float)h0), l1 = (_Float16)(w1 - (float)h1);
+      const _Float16 x0 = lo_row ? l0 : h0, x1 = lo_row ? l1 : h1;
+      aw[bk][e] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
+    }
+  }
   for (int ct = w; ct < m / 16; ct += NT / 64) {
     qf4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int bk = 0; bk < nblk; ++bk) {
-      const int t0 = 32 * bk + 8 * q4;  // the lane's 8 tokens (k-slots 8 q4 .. 8 q4 + 7)
-      // A: weights of head h (zero past G and past nvalid: pw is zero there)
-      qu4 av;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float w0 = 0.f, w1 = 0.f;
-        if (h < G) {
-          w0 = pw[h][t0 + 2 * e];
-          w1 = pw[h][t0 + 2 * e + 1];
-        }
-        const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
-        const _Float16 l0 = (_Float16)(w0 - (float)h0), l1 = (_Float16)(w1 - (float)h1);
-        const _Float16 x0 = lo_row ? l0 : h0, x1 = lo_row ? l1 : h1;
-        av[e] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
-      }
+    for (int bk = 0; bk < QCH / 32; ++bk) {
+      if (bk >= nblk) break;
+      const int t0 = 32 * bk + 8 * q4;
+      const qu4 av = aw[bk];
       // B: +-1 of projection 16 ct + r for the lane's 8 tokens (bit set -> +1)
       const int pj = 16 * ct + r;
       qu4 bv;

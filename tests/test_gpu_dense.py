@@ -84,9 +84,9 @@ def test_dense_sink_ring_ragged(kv_dtype):
     """Per-sequence sink lengths, ring starts and ring lengths (wrapping and
     not, empty sink, empty ring)."""
     H, G, cap, scap = 3, 4, 70, 48
-    sink_len = [0, 5, 40, 48, 17]
-    res_start = [60, 3, 0, 69, 10]
-    res_len = [50, 70, 0, 33, 1]
+    sink_len = [0, 5, 40, 48, 17, 0]
+    res_start = [60, 3, 0, 69, 10, 5]
+    res_len = [50, 70, 0, 33, 1, 0]   # the last sequence is empty: its output is zero
     B = len(sink_len)
     g = torch.Generator(device=DEV).manual_seed(7)
     sk = torch.randn(B, H, scap, D, generator=g, device=DEV).to(kv_dtype)
@@ -99,7 +99,8 @@ def test_dense_sink_ring_ragged(kv_dtype):
     run_desc(q, out, B, H, sink_k=sk, sink_v=sv, sink_len=i32(sink_len), max_sink=max(sink_len), sink_hs=scap * D,
              res_k=rk, res_v=rv, res_len=i32(res_len), res_start=i32(res_start), max_res=max(res_len), cap=cap,
              kv_dtype=kv_dtype)
-    for b in range(B):
+    assert (out[B - 1] == 0).all()
+    for b in range(B - 1):
         slots = (res_start[b] + np.arange(res_len[b])) % cap
         kk = np.concatenate([sk[b, :, :sink_len[b]].double().cpu().numpy(),
                              rk[b][:, torch.as_tensor(slots, device=DEV)].double().cpu().numpy()], axis=1)

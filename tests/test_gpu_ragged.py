@@ -139,21 +139,27 @@ def test_ragged_small(qjl_m):
     check_batch(rb, q, oracle_rows=range(rb.B), label=f"small m={qjl_m} +40")
 
 
-def test_ragged_short_sequences_fill_sink_and_ring():
+@pytest.mark.parametrize("qjl_m", [0, 64], ids=["k4v2", "k4v2_qjl"])
+def test_ragged_short_sequences_fill_sink_and_ring(qjl_m):
     """Sequences shorter than sink + window: steps fill the sink first, then
-    the ring, and drain only once a ring holds window + 1 tokens."""
+    the ring, and drain only once a ring holds window + 1 tokens. With the
+    sketch, most sequences have nothing compressed while one does (the QJL
+    kernels skip or zero those sequences)."""
     lens = [3, 10, 24, 60]
-    rb = make_batch(lens, H=2, sink=8, window=16, seed=11)
+    rb = make_batch(lens, H=2, sink=8, window=16, seed=11, qjl_m=qjl_m)
     assert list(rb.sink_len) == [3, 8, 8, 8] and list(rb.res_len) == [0, 2, 16, 16]
     assert list(rb.comp_len) == [0, 0, 0, 36]
     q = torch.randn(rb.B, 2 * HQ_PER_KV, D, generator=rb.g, device=DEV).half()
-    check_batch(rb, q, oracle_rows=range(rb.B), label="short")
+    check_batch(rb, q, oracle_rows=range(rb.B), label=f"short m={qjl_m}")
     for _ in range(20):
         step(rb)
     assert list(rb.sink_len) == [8] * 4
     assert list(rb.res_len) == [15, 16, 16, 16] and list(rb.comp_len) == [0, 6, 20, 56]
-    check_batch(rb, q, oracle_rows=range(rb.B), label="short +20")
+    check_batch(rb, q, oracle_rows=range(rb.B), label=f"short +20 m={qjl_m}")
     check_batch(rb, q, general=True, label="short +20 general")
+    a = rb.attend(q).cpu().numpy()
+    b = rb.attend(q, general=True).cpu().numpy()
+    assert rel_err(a, b) < 1e-4
 
 
 def test_ragged_errors():

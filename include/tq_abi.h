@@ -191,6 +191,24 @@ int tq_decode_attention(const tq_codec* kcodec, const tq_codec* vcodec,
                         const tq_attn_desc* desc, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* Decode attention that allocates nothing: tq_decode_attention with the
+ * workspace taken from a scratch array the library holds in device memory,
+ * one copy per GPU, TQ_NOALLOC_SCRATCH_BYTES bytes, kept until the process
+ * ends. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It calls no hipMalloc / hipFree; the
+ * caller still passes q, out and the cache buffers through `desc`.
+ * Calls whose tq_decode_workspace_bytes exceeds TQ_NOALLOC_SCRATCH_BYTES
+ * return TQ_ERR_WORKSPACE. Every call on one GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (different streams, no ordering between them)
+ * race; calls ordered on one stream do not. Nothing is carried from one call
+ * to the next (the scratch needs no initial contents). The first call on a
+ * device looks up that device's copy of the array. */
+#define TQ_NOALLOC_SCRATCH_BYTES (64u << 20)
+size_t tq_decode_noalloc_scratch_bytes(void);
+int tq_decode_attention_noalloc(const tq_codec* kcodec, const tq_codec* vcodec,
+                                const tq_attn_desc* desc, void* stream);
+
 /* Decode attention over uncompressed K/V (one query token per head),
  * head_dim 128, fp16 or bf16 K/V (kv_dtype), q fp16 / bf16 / fp32: the
  * sink and residual-ring segments of `desc` with no compressed tokens

@@ -18,6 +18,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 #include "tq_common.h"
 #include "tq_decode_fast.h"
 
@@ -947,6 +949,36 @@ static int dense_run(const tq_attn_desc* d, void* workspace, size_t workspace_by
   return TQ_OK;
 }
 
+// Scratch of tq_decode_attention_noalloc: a file-scope device array, one copy
+// per GPU the library runs on, held until the process ends. Host code never
+// passes `scratch` itself to a kernel (in host code the name is a host-side
+// stand-in, not a device address): the address of each device's copy is
+// looked up once per device with hipGetSymbolAddress and kept in
+// g_scratch_addr.
+static __device__ __align__(256) uint8_t scratch[TQ_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static void* g_scratch_addr[MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch` (looked up on the first call on
+// that device, with that device current).
+static int noalloc_scratch(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return set_error(TQ_ERR_LAUNCH, "no current HIP device (or device id >= %d)", MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(TQ_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return TQ_OK;
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -1082,6 +1114,20 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   hipLaunchKernelGGL(combine_kernel, dim3(d->hq, d->batch), dim3(128), cmb_smem, s, a);
   TQ_LAUNCH_CHECK("tq_decode_attention combine");
   return TQ_OK;
+}
+
+size_t tq_decode_noalloc_scratch_bytes(void) { return TQ_NOALLOC_SCRATCH_BYTES; }
+
+int tq_decode_attention_noalloc(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* stream) {
+  if (!kc || !d) return set_error(TQ_ERR_INVALID, "codec / attention descriptor is NULL");
+  const size_t need = tq_decode_workspace_bytes(kc, d);
+  if (need > TQ_NOALLOC_SCRATCH_BYTES)
+    return set_error(TQ_ERR_WORKSPACE, "call needs %zu bytes of scratch; the no-allocation entry point holds %zu",
+                     need, (size_t)TQ_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  return tq_decode_attention(kc, vc, d, ws, TQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 size_t tq_dense_decode_workspace_bytes(const tq_attn_desc* d, int32_t head_dim) {

@@ -13,9 +13,9 @@ value = algorithmic bytes read per step / time per step (GB/s): packed codes +
 norms of every compressed token, the fp16 sink/residual tokens, q and out.
 
 roofline: the dominant kernel is the partials kernel of the two-kernel
-K4/V2 path (fast_decode_kernel); its average duration is timed with events on
+K4/V2 path for uniform batches (uniform_decode_kernel<4>); its average duration is timed with events on
 the launch stream around graph replays of one partials-only call
-(TQ_ATTN_PARTIALS_ONLY) per layer, so its bytes stream from HBM as in the
+(tq_measure_decode_partials) per layer, so its bytes stream from HBM as in the
 step (one layer's 28 MB would otherwise stay in the 256 MB last-level cache). traffic = HBM bytes per launch from rocprofv3
 FETCH_SIZE / WRITE_SIZE runs of `bench.py --pmc-workload`, scaled by the
 same counters on a copy of known size; read from the committed summary.
@@ -43,7 +43,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "mlx-turboquant_amd")]
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fast_decode_kernel_k4v2_32k_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "uniform_decode_kernel_k4v2_32k_traffic.md")
 METRIC = "fused decode-attn GB/s over packed KV (% HBM peak) + compress vectors/s"
 
 
@@ -236,8 +236,8 @@ def bench_config4(dev, steps: int = 12):
         byt = 8 * (int(rb.comp_len.sum()) * per_tok + int(rb.res_len.sum()) * 512) + 16 * 32 * 128 * 6
         ms_s, ms_a = float(np.median(t_step)), float(np.median(t_attn))
         res["qjl" if qjl_m else "no_qjl"] = {
-            "kernel": ("K4/V2 + sketch (qjl_bias_kernel, fast_decode_kernel with the key term, merge, qjl_value_kernel, "
-                       "qjl_final_kernel)") if qjl_m else "K4/V2 (fast_decode_kernel + merge)",
+            "kernel": ("K4/V2 + sketch (qjl_bias_kernel, decode_partials_kernel with the key term, merge, "
+                       "qjl_value_kernel, qjl_final_kernel)") if qjl_m else "K4/V2 (decode_partials_kernel + merge)",
             "layer_step_us": round(ms_s * 1e3, 1), "attend_us": round(ms_a * 1e3, 1),
             "attend_bytes": byt, "attend_GBps": round(byt / (ms_a * 1e-3) / 1e9, 1)}
         del rb
@@ -290,13 +290,15 @@ def call_partials_only(c, q, out):
     from turboquant_amd import _lib
     from turboquant_amd.cache import _workspace
     lib = _lib.load()
+    fn = lib.tq_measure_decode_partials  # measurement hook of the library (not in include/tq_abi.h)
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_size_t, ctypes.c_void_p]
     qq = q[:, :, 0].contiguous()
     desc = c.attention_descriptor(qq, out, q.shape[-1] ** -0.5)
-    desc.flags = _lib.TQ_ATTN_PARTIALS_ONLY
     need = lib.tq_decode_workspace_bytes(c._kc.ref(), ctypes.byref(desc))
     ws = _workspace(q.device, need)
-    _lib.check(lib.tq_decode_attention(c._kc.ref(), c._vc.ref(), ctypes.byref(desc), ws.data_ptr(), ws.numel(),
-                                       _lib.stream_ptr(q.device)), "tq_decode_attention")
+    _lib.check(fn(ctypes.addressof(c._kc.struct), ctypes.addressof(c._vc.struct), ctypes.addressof(desc),
+                  ws.data_ptr(), ws.numel(), _lib.stream_ptr(q.device)), "tq_measure_decode_partials")
 
 
 def time_partials_kernel(caches, qs, outs, reps: int, warmup: int):
@@ -425,8 +427,8 @@ def main():
         "decode_steps_per_s": round(1e3 / ms_step, 2),
         "wall_ms_per_step": round(wall_step, 5),
         "bytes_per_step": bytes_step,
-        "roofline": {"kernel": "fast_decode_kernel<4> (partials of one layer: q rotation, packed K4/V2 + fp16 "
-                               "blocks, workgroup combine)",
+        "roofline": {"kernel": "uniform_decode_kernel<4> (partials of one layer: q rotation, packed K4/V2 + fp16 "
+                               "blocks, workgroup combine, inverse rotation)",
                      "bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if traffic else None,

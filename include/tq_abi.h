@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TQ_ABI_VERSION 2
+#define TQ_ABI_VERSION 3
 
 /* Element types of floating-point inputs. */
 enum { TQ_F16 = 0, TQ_BF16 = 1, TQ_F32 = 2 };
@@ -47,10 +47,10 @@ enum {
  * [split, d) use bits_lo with split == d/2 (mlx_turboquant/cache.py:63-84).
  * Both codebooks are the d-dimensional Lloyd-Max tables (codebook.py:146-174). */
 typedef struct tq_codec {
-  int32_t d;                   /* head_dim: 64, 128 or 256 */
+  int32_t d;                   /* head_dim: 64, 96, 128 or 256 */
   int32_t bits_hi;             /* 1..4 */
   int32_t bits_lo;             /* 1..4 */
-  int32_t split;               /* multiple of 32 */
+  int32_t split;               /* multiple of 16 */
   const float* rotation;       /* (d, d) row-major orthogonal R (rotation.py:17-36) */
   const float* centroids_hi;   /* (2^bits_hi,) */
   const float* boundaries_hi;  /* (2^bits_hi - 1,) */
@@ -58,15 +58,52 @@ typedef struct tq_codec {
   const float* boundaries_lo;  /* (2^bits_lo - 1,) */
   const float* qjl_proj;       /* (qjl_m, d) Gaussian S (qjl.py:23-36) or NULL */
   int32_t qjl_m;               /* number of projections (multiple of 32) or 0 */
-  int32_t reserved;
+  int32_t flags;               /* TQ_CODEC_* bits */
   const uint16_t* rotation_parts; /* (4, d, d) 16-bit words, row-major, or NULL:
                                      [0] = fp16(R), [1] = fp16(R - [0]),
-                                     [2] = bf16(R^T), [3] = bf16(R^T - [2]).
-                                     The K4/V2 decode kernels need it (query
-                                     rotation from the key codec's [0..1],
-                                     inverse rotation of the output from the
-                                     value codec's [2..3]); others ignore it. */
+                                     [2] = fp16(R^T), [3] = fp16(R^T - [2]).
+                                     The K4/V2 decode kernels rotate the query
+                                     with the key codec's [0, 1] and rotate the
+                                     output back with the value codec's [2, 3];
+                                     others ignore it. */
+  /* Host-side tables, filled by tq_codec_prepare() from a host copy of
+   * centroids_hi (codebooks of at most 16 entries; passed to kernels by value):
+   * host_centroids = centroids_hi, n_host_centroids entries; and for 2-bit
+   * codebooks an exact fp16 copy for the K4/V2 decode kernels (value side):
+   * centroids_hi[i] == value_scale * fp16 value_table[i] to within
+   * value_table_err (relative). The K4/V2 route runs only when the key
+   * codec's host_centroids are set and the value codec's value_table_err <=
+   * 2e-7 (else the general kernels). */
+  float host_centroids[16];
+  int32_t n_host_centroids;
+  uint16_t value_table[4];
+  float value_scale;
+  float value_table_err;
+  /* (256,) 8-byte entries in device memory, or NULL: the decode table of the
+   * K4/V2 kernels for code byte e. 4-bit codecs: fp16 bits of (c_hi[e & 15],
+   * c_hi[e >> 4], c_lo[e & 15], c_lo[e >> 4]) in 16-bit lanes 0..3, c_hi =
+   * fp16(c), c_lo = fp16(c - c_hi); 2-bit codecs: value_table[(e >> 2i) & 3]
+   * in lane i. tq_codec_decode_table() computes it on the host. */
+  const uint64_t* decode_table;
 } tq_codec;
+
+/* tq_codec.flags: route tq_compress calls with this codec through the
+ * general compress kernel instead of the MFMA kernel (no reference
+ * counterpart; lets tests compare the two kernels, per call). */
+#define TQ_CODEC_GENERAL_COMPRESS 1
+
+/* Fills the host-side tables of `codec` (host_centroids, value_table,
+ * value_scale, value_table_err) from a host copy of centroids_hi
+ * (n_centroids entries; the value table needs 4, other sizes set its error
+ * to infinity; more than 16 leave host_centroids unset). Host only, no
+ * device work. Returns TQ_OK. */
+int tq_codec_prepare(tq_codec* codec, const float* centroids_host, int32_t n_centroids);
+
+/* The 256 entries of decode_table for a prepared codec (host only, no device
+ * work): the 4-bit form for n_host_centroids == 16, the 2-bit form for 4.
+ * Returns TQ_ERR_UNSUPPORTED for other codebooks. The caller copies them to
+ * device memory and sets codec->decode_table. */
+int tq_codec_decode_table(const tq_codec* codec, uint64_t* table_host);
 
 /* A compressed store: packed codes, norms and optional QJL sketch.
  * codes_hi rows are split*bits_hi/8 bytes, codes_lo rows (d-split)*bits_lo/8
@@ -117,11 +154,6 @@ int tq_device_supported(void);
 int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x_head_stride,
                 const tq_span* span, const tq_store* dst, void* stream);
 
-/* Testing aid, no reference counterpart: route every tq_compress call of the
- * process through the general (VALU) kernel (on != 0) instead of the MFMA
- * kernel that fp16 / head_dim 128 / no-QJL calls use, so tests can compare the
- * two. Not thread-safe; default 0. */
-void tq_compress_force_general(int32_t on);
 
 /* Dequantize: out = n * (c[idx] @ R) (+ QJL correction when apply_qjl and
  * the store holds a sketch), float32, element (r, t, i) at
@@ -178,10 +210,6 @@ typedef struct tq_attn_desc {
 /* tq_attn_desc.flags: force the general kernel (every width / QJL) even where
  * the K4/V2 partials + merge kernels apply. */
 #define TQ_ATTN_GENERAL 1
-/* Measurement only: on the K4/V2 path, launch the partials kernel and skip
- * the merge kernel (out is not written). Lets a caller time the dominant
- * kernel alone with events on its stream; no reference counterpart. */
-#define TQ_ATTN_PARTIALS_ONLY 2
 
 /* Workspace: scratch for the per-workgroup partials of one call (no state is
  * kept between calls, no initial contents are needed). Calls sharing a

@@ -738,19 +738,36 @@ static int device_cus() {
   return cus;
 }
 
-// Workgroups per (sequence, kv head) for the K4/V2 partials kernel, its
-// compressed blocks and fp16 tokens per workgroup: about one workgroup per CU
-// in total, at most 4 compressed blocks per wave and 32 fp16 tokens per
-// workgroup. Returns false when the context needs more than FAST_MAX_WG
-// workgroups (the general kernel takes it).
-static bool fast_geometry(const tq_attn_desc* d, int& nwg, int& bpw, int& fpw) {
+// Plan of the K4/V2 path for a call (tq_decode_fast.h): workgroups, chunks
+// per workgroup and partial slots.
+struct FastPlan {
+  int nwg, chunks, vmax;
+};
+
+static FastPlan fast_plan(const tq_attn_desc* d) {
+  FastPlan p;
+  const bool uniform = !d->comp_len && !d->sink_len && !d->res_len;
+  fast_plan_host(d->batch, d->hkv, d->max_comp, d->max_sink, d->max_res, uniform, device_cus(), p.nwg, p.chunks,
+                 p.vmax);
+  return p;
+}
+
+// Workgroups per (sequence, kv head) of the uniform-batch kernels, their
+// compressed blocks and fp16 tokens per workgroup: about one workgroup per
+// CU in total, at most UNI_BLOCKS_PER_WAVE compressed blocks per wave and
+// UNI_FP16_PER_WG fp16 tokens per workgroup. False when the call is not
+// uniform (per-sequence lengths given) or needs more than UNI_MAX_WG
+// workgroups: the persistent kernel takes it.
+static bool uniform_geometry(const tq_attn_desc* d, int& nwg, int& bpw, int& fpw) {
+  nwg = bpw = fpw = 0;
+  if (d->comp_len || d->sink_len || d->res_len) return false;
   const int nbc = (d->max_comp + 31) / 32;
   const int n16 = d->max_sink + d->max_res;
   const int groups = d->batch * d->hkv > 0 ? d->batch * d->hkv : 1;
   const int target = (device_cus() + groups - 1) / groups;
-  const int per_wg = FAST_WAVES * FAST_BLOCKS_PER_WAVE;
+  const int per_wg = FAST_WAVES * UNI_BLOCKS_PER_WAVE;
   int lo = (nbc + per_wg - 1) / per_wg;
-  const int lo16 = (n16 + FAST_FP16_PER_WG - 1) / FAST_FP16_PER_WG;
+  const int lo16 = (n16 + UNI_FP16_PER_WG - 1) / UNI_FP16_PER_WG;
   if (lo16 > lo) lo = lo16;
   if (lo < 1) lo = 1;
   int hi = (nbc + FAST_WAVES - 1) / FAST_WAVES;  // at least one block per wave
@@ -758,17 +775,41 @@ static bool fast_geometry(const tq_attn_desc* d, int& nwg, int& bpw, int& fpw) {
   nwg = target < lo ? lo : (target > hi ? hi : target);
   bpw = (nbc + nwg - 1) / nwg;
   fpw = (n16 + nwg - 1) / nwg;
-  return nwg <= FAST_MAX_WG;
+  return nwg <= UNI_MAX_WG;
+}
+
+// The uniform-batch kernels take a uniform call when the value codec has its
+// R^T parts.
+static bool uniform_route(const tq_codec* vc, const tq_attn_desc* d, int& nwg, int& bpw, int& fpw) {
+  return vc->rotation_parts != nullptr && uniform_geometry(d, nwg, bpw, fpw);
+}
+
+// Partials workspace of the K4/V2 routes of a call: the larger of the uniform
+// kernels' (nwg per (b, g), original space) and the persistent kernel's slots
+// (the route also depends on the value codec, which the sizing does not see).
+static size_t fast_part_bytes(const tq_attn_desc* d) {
+  const int G = d->hkv > 0 ? d->hq / d->hkv : 1;
+  int nwg, bpw, fpw;
+  size_t b = (size_t)fast_plan(d).vmax * G * PACKED_PART_FLOATS * 4;
+  if (uniform_geometry(d, nwg, bpw, fpw)) {
+    const size_t u = (size_t)d->batch * d->hkv * nwg * G * FAST_PART_FLOATS * 4;
+    if (u > b) b = u;
+  }
+  return b;
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // The K4/V2 partials kernel reads keys / values / norms / queries in 16-byte
-// pieces: every base and head stride must keep them 16-byte aligned.
+// pieces: every base and head stride must keep them 16-byte aligned. The value
+// codec needs its exact fp16 table (value_table_err).
 static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, bool qjl_ok = false) {
   const int G = d->hq / d->hkv;
-  if (!(kc->rotation_parts != nullptr && vc->rotation_parts != nullptr && vc->d == 128 && kc->d == 128 && kc->bits_hi == 4 && kc->split == 128 && vc->bits_hi == 2 &&
-        vc->split == 128 && (!d->qjl || qjl_ok) && d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8)))
+  if (!(kc->rotation_parts != nullptr && kc->decode_table != nullptr && vc->decode_table != nullptr &&
+        kc->n_host_centroids == 16 && vc->n_host_centroids == 4 && vc->d == 128 && kc->d == 128 &&
+        kc->bits_hi == 4 && kc->split == 128 &&
+        vc->bits_hi == 2 && vc->split == 128 && vc->value_table_err <= 2e-7f && (!d->qjl || qjl_ok) &&
+        d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8)))
     return false;
   if (d->qjl && d->max_comp > 0 &&
       !((reinterpret_cast<uintptr_t>(d->kstore.signs) & 3) == 0 && d->kstore.sign_head_stride % 4 == 0 &&
@@ -782,14 +823,11 @@ static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_
     return false;
   if (d->max_sink > 0 && !(aligned16(d->sink_k) && aligned16(d->sink_v) && d->sink_head_stride % 8 == 0)) return false;
   if (d->max_res > 0 && !(aligned16(d->res_k) && aligned16(d->res_v) && d->res_head_stride % 8 == 0)) return false;
-  int nwg, bpw, fpw;
-  return fast_geometry(d, nwg, bpw, fpw);
+  return true;
 }
 
 static QjlLayout qjl_layout(const tq_codec* kc, const tq_attn_desc* d) {
   QjlLayout L{};
-  int nwg = 1, bpw, fpw;
-  fast_geometry(d, nwg, bpw, fpw);
   const int G = d->hkv > 0 ? d->hq / d->hkv : 1;
   const size_t heads = (size_t)d->batch * d->hq;
   const int m = kc->qjl_m;
@@ -798,7 +836,7 @@ static QjlLayout qjl_layout(const tq_codec* kc, const tq_attn_desc* d) {
   L.nvc = (d->max_comp + QCH - 1) / QCH;
   if (L.nvc < 1) L.nvc = 1;
   size_t off = 0;
-  L.part = off; off += al256((size_t)d->batch * d->hkv * nwg * G * FAST_PART_FLOATS * 4);
+  L.part = off; off += al256(fast_part_bytes(d));
   L.pro = off; off += al256(heads * 128 * 4 * 2 + heads * (size_t)m * 4);
   L.bias = off; off += al256((size_t)d->batch * d->hkv * G * (size_t)L.qb_hs * 4);
   L.scores = off; off += al256((size_t)d->batch * d->hkv * G * (size_t)L.qb_hs * 4);
@@ -815,18 +853,60 @@ static void fill_fast(FastArgs& f, const tq_codec* kc, const tq_codec* vc, const
   f.kn = d->kstore.norms; f.kn_hs = d->kstore.norm_head_stride;
   f.vc = d->vstore.codes_hi; f.v_hs = d->vstore.hi_head_stride;
   f.vn = d->vstore.norms; f.vn_hs = d->vstore.norm_head_stride;
-  f.sink_k = d->sink_k; f.sink_v = d->sink_v; f.sink_hs = d->sink_head_stride;
-  f.res_k = d->res_k; f.res_v = d->res_v; f.res_hs = d->res_head_stride;
+  f.sink_k = static_cast<const uint16_t*>(d->sink_k); f.sink_v = static_cast<const uint16_t*>(d->sink_v);
+  f.sink_hs = d->sink_head_stride;
+  f.res_k = static_cast<const uint16_t*>(d->res_k); f.res_v = static_cast<const uint16_t*>(d->res_v);
+  f.res_hs = d->res_head_stride;
   f.res_cap = d->res_cap; f.res_start0 = d->res_start0;
   f.comp_len_b = d->comp_len; f.sink_len_b = d->sink_len; f.res_len_b = d->res_len; f.res_start_b = d->res_start;
   f.max_comp = d->max_comp; f.max_sink = d->max_sink; f.max_res = d->max_res;
   f.q = d->q; f.q_dtype = d->q_dtype; f.out = d->out;
-  f.hq = d->hq; f.hkv = d->hkv;
+  f.batch = d->batch; f.hq = d->hq; f.hkv = d->hkv;
   f.qscale = d->scale * 1.4426950408889634f;
-  f.rot16 = kc->rotation_parts; f.rotT = vc->rotation_parts + 2 * 128 * 128; f.kcen = kc->centroids_hi; f.vcen = vc->centroids_hi;
+  f.rot16 = kc->rotation_parts; f.vrot = vc->rotation;
+  f.klut = kc->decode_table; f.vlut = vc->decode_table;
+  f.vscale = vc->value_scale;
   f.part = part;
-  fast_geometry(d, f.nwg, f.bpw, f.fpw);
-  f.merge = (d->flags & TQ_ATTN_PARTIALS_ONLY) ? 0 : 1;
+  const FastPlan p = fast_plan(d);
+  f.nwg = p.nwg; f.chunks = p.chunks; f.vmax = p.vmax;
+  f.uni = !d->comp_len && !d->sink_len && !d->res_len;
+  if (f.uni) fast_uniform_plan(d->batch, d->hkv, d->max_comp, d->max_sink, d->max_res, f.nwg, f.chunks, f.plan_T,
+                               f.plan_nu, f.plan_V);
+}
+
+// The K4/V2 partials (+ merge when merge != 0) of a call into `part`: the
+// uniform-batch kernels when the call is uniform and fits their grid, else
+// the persistent kernel. qb: the QJL key term is added (qjl_bias) and the
+// scores stored; ml receives the merge's global max and sum when not NULL.
+static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part, bool qb,
+                       float* qjl_bias, float* scores, int64_t qb_hs, float* ml, int merge, hipStream_t s) {
+  const int G = d->hq / d->hkv;
+  UniformArgs u{};
+  if (uniform_route(vc, d, u.nwg, u.bpw, u.fpw)) {
+    u.kc = d->kstore.codes_hi; u.k_hs = d->kstore.hi_head_stride;
+    u.kn = d->kstore.norms; u.kn_hs = d->kstore.norm_head_stride;
+    u.vc = d->vstore.codes_hi; u.v_hs = d->vstore.hi_head_stride;
+    u.vn = d->vstore.norms; u.vn_hs = d->vstore.norm_head_stride;
+    u.sink_k = d->sink_k; u.sink_v = d->sink_v; u.sink_hs = d->sink_head_stride;
+    u.res_k = d->res_k; u.res_v = d->res_v; u.res_hs = d->res_head_stride;
+    u.res_cap = d->res_cap; u.res_start0 = d->res_start0;
+    u.res_start_b = d->res_start;  // the lengths are the maximal ones
+    u.max_comp = d->max_comp; u.max_sink = d->max_sink; u.max_res = d->max_res;
+    u.q = d->q; u.q_dtype = d->q_dtype; u.out = d->out;
+    u.batch = d->batch; u.hq = d->hq; u.hkv = d->hkv;
+    u.qscale = d->scale * 1.4426950408889634f;
+    u.rot16 = kc->rotation_parts; u.rotT = vc->rotation_parts + 2 * 128 * 128;
+    for (int i = 0; i < 16; ++i) u.kcent[i] = kc->host_centroids[i];
+    for (int i = 0; i < 4; ++i) u.vtab[i] = vc->value_table[i];
+    u.vscale = vc->value_scale;
+    u.part = part;
+    u.qjl_bias = qjl_bias; u.scores = scores; u.qb_hs = qb_hs; u.ml = ml;
+    return launch_uniform_decode(u, G, qb, merge, s);
+  }
+  FastArgs f;
+  fill_fast(f, kc, vc, d, part);
+  f.qjl_bias = qjl_bias; f.scores = scores; f.qb_hs = qb_hs; f.ml = ml;
+  return launch_fast_decode(f, G, qb, merge, s);
 }
 
 // The QJL route: prologue (S q), key-term bias, K4/V2 partials with the bias
@@ -869,14 +949,9 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     default: hipLaunchKernelGGL((qjl_bias_kernel<8>), bgrid, dim3(NT), 0, s, qa); break;
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl bias");
-  FastArgs f;
-  fill_fast(f, kc, vc, d, reinterpret_cast<float*>(ws + QL.part));
-  f.merge = 1;
-  f.qjl_bias = qa.bias;
-  f.scores = const_cast<float*>(qa.scores);
-  f.qb_hs = QL.qb_hs;
-  f.ml = const_cast<float*>(qa.ml);
-  if (launch_fast_decode_qjl(f, G, d->batch, s) != 0) TQ_LAUNCH_CHECK("tq_decode_attention qjl fast");
+  if (launch_k4v2(kc, vc, d, reinterpret_cast<float*>(ws + QL.part), true, qa.bias, const_cast<float*>(qa.scores),
+                  QL.qb_hs, const_cast<float*>(qa.ml), 1, s) != 0)
+    TQ_LAUNCH_CHECK("tq_decode_attention qjl fast");
   const dim3 vgrid((unsigned)QL.nvc, d->hkv, d->batch);
   switch (G) {
     case 1: hipLaunchKernelGGL((qjl_value_kernel<1>), vgrid, dim3(NT), 0, s, qa); break;
@@ -943,8 +1018,7 @@ static int dense_run(const tq_attn_desc* d, void* workspace, size_t workspace_by
   if (need > 0 && (!workspace || workspace_bytes < need))
     return set_error(TQ_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, need);
   a.part = static_cast<float*>(workspace);
-  const int merge = (d->flags & TQ_ATTN_PARTIALS_ONLY) ? 0 : 1;
-  if (launch_dense_decode(a, d->hq / d->hkv, d->kv_dtype == TQ_BF16, d->batch, merge, s) != 0)
+  if (launch_dense_decode(a, d->hq / d->hkv, d->kv_dtype == TQ_BF16, d->batch, 1, s) != 0)
     TQ_LAUNCH_CHECK("tq_dense_decode_attention");
   return TQ_OK;
 }
@@ -994,10 +1068,7 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
   const size_t nch = (size_t)(nc + ns + nr);
   const size_t heads = (size_t)d->batch * d->hq;
   size_t general = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
-  int nwg, bpw, fpw;
-  size_t fast = 0;
-  if (fast_geometry(d, nwg, bpw, fpw))
-    fast = (size_t)d->batch * d->hkv * nwg * (d->hkv > 0 ? d->hq / d->hkv : 1) * FAST_PART_FLOATS * 4;
+  const size_t fast = d->hkv > 0 && d->hq % d->hkv == 0 ? fast_part_bytes(d) : 0;
   size_t bytes = general > fast ? general : fast;
   if (d->qjl && kcodec->d == 128 && kcodec->qjl_m > 0 && kcodec->qjl_m <= 256 && d->max_comp > 0 && d->hkv > 0 &&
       d->hq % d->hkv == 0) {
@@ -1032,8 +1103,10 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   if (d->max_comp > 0 && (!d->kstore.codes_hi || !d->kstore.norms || !d->vstore.codes_hi || !d->vstore.norms))
     return set_error(TQ_ERR_INVALID, "compressed store pointers are NULL");
   if (d->max_sink > 0 && (!d->sink_k || !d->sink_v)) return set_error(TQ_ERR_INVALID, "sink pointers are NULL");
-  if (d->max_res > 0 && (!d->res_k || !d->res_v || d->res_cap <= 0))
-    return set_error(TQ_ERR_INVALID, "residual pointers are NULL");
+  if (d->max_res > 0 && (!d->res_k || !d->res_v || d->res_cap <= 0 || d->max_res > d->res_cap))
+    return set_error(TQ_ERR_INVALID, "residual ring pointers / capacity");
+  if (d->max_res > 0 && !d->res_start && (d->res_start0 < 0 || d->res_start0 >= d->res_cap))
+    return set_error(TQ_ERR_INVALID, "ring start %d outside [0, %d)", d->res_start0, d->res_cap);
   const int row_v = row_bytes(vc->split, vc->bits_hi) + row_bytes(vc->d - vc->split, vc->bits_lo);
   if (row_v > 128) return set_error(TQ_ERR_UNSUPPORTED, "value row of %d bytes > 128", row_v);
   const bool qjl = d->qjl != 0;
@@ -1056,11 +1129,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   if (qjl && d->max_comp > 0 && fast_eligible(kc, vc, d, true) && !(d->flags & TQ_ATTN_GENERAL))
     return qjl_fast_run(kc, vc, d, workspace, workspace_bytes, s);
   if (fast_eligible(kc, vc, d) && !(d->flags & TQ_ATTN_GENERAL)) {
-    if (fast_set_attributes() != 0)
-      return set_error(TQ_ERR_LAUNCH, "cannot raise the LDS limit of the decode kernel");
-    FastArgs f;
-    fill_fast(f, kc, vc, d, static_cast<float*>(workspace));
-    if (launch_fast_decode(f, G, d->batch, s) != 0)
+    if (launch_k4v2(kc, vc, d, static_cast<float*>(workspace), false, nullptr, nullptr, 0, nullptr, 1, s) != 0)
       TQ_LAUNCH_CHECK("tq_decode_attention (fast)");
     return TQ_OK;
   }
@@ -1113,6 +1182,20 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   const size_t cmb_smem = (size_t)(((a.nch + 3) & ~3) + a.D + a.m) * 4;
   hipLaunchKernelGGL(combine_kernel, dim3(d->hq, d->batch), dim3(128), cmb_smem, s, a);
   TQ_LAUNCH_CHECK("tq_decode_attention combine");
+  return TQ_OK;
+}
+
+// Measurement hook of bench.py, not part of the ABI (include/tq_abi.h does not
+// declare it): the partials kernel of the K4/V2 route alone (no merge, `out`
+// not written), so its launches can be timed with events on their stream.
+int tq_measure_decode_partials(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (!kc || !vc || !d || d->hkv <= 0 || d->hq % d->hkv || !fast_eligible(kc, vc, d) || d->qjl)
+    return set_error(TQ_ERR_UNSUPPORTED, "measurement: not a K4/V2 call");
+  if (!workspace || workspace_bytes < fast_part_bytes(d)) return set_error(TQ_ERR_WORKSPACE, "workspace too small");
+  if (launch_k4v2(kc, vc, d, static_cast<float*>(workspace), false, nullptr, nullptr, 0, nullptr, 0,
+                  static_cast<hipStream_t>(stream)) != 0)
+    TQ_LAUNCH_CHECK("measurement partials");
   return TQ_OK;
 }
 

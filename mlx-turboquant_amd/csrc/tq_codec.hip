@@ -10,6 +10,7 @@
 //   idx = #{k : y > b_k} (codebook.py:220-223);
 //   codes packed as an LSB-first bitstream per row (packing.py:9-173).
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -20,7 +21,6 @@
 namespace tq {
 
 static thread_local char g_err[512] = "";
-static bool g_force_general = false;  // tq_compress_force_general(1): tests cross-check the two kernels
 
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
@@ -559,7 +559,74 @@ extern "C" {
 
 int tq_abi_version(void) { return TQ_ABI_VERSION; }
 
-void tq_compress_force_general(int32_t on) { tq::g_force_general = on != 0; }
+int tq_codec_decode_table(const tq_codec* c, uint64_t* t) {
+  if (!c || !t) return set_error(TQ_ERR_INVALID, "codec / table is NULL");
+  auto h16 = [](float x) { return (uint64_t)__builtin_bit_cast(uint16_t, (_Float16)x); };
+  if (c->n_host_centroids == 16) {
+    uint64_t hi[16], lo[16];
+    for (int i = 0; i < 16; ++i) {
+      const float x = c->host_centroids[i];
+      const _Float16 xh = (_Float16)x;
+      hi[i] = __builtin_bit_cast(uint16_t, xh);
+      lo[i] = h16(x - (float)xh);
+    }
+    for (int e = 0; e < 256; ++e) t[e] = hi[e & 15] | (hi[e >> 4] << 16) | (lo[e & 15] << 32) | (lo[e >> 4] << 48);
+    return TQ_OK;
+  }
+  if (c->n_host_centroids == 4) {
+    for (int e = 0; e < 256; ++e) {
+      uint64_t v = 0;
+      for (int i = 0; i < 4; ++i) v |= (uint64_t)c->value_table[(e >> (2 * i)) & 3] << (16 * i);
+      t[e] = v;
+    }
+    return TQ_OK;
+  }
+  return set_error(TQ_ERR_UNSUPPORTED, "decode table: codebook of %d entries", c->n_host_centroids);
+}
+
+int tq_codec_prepare(tq_codec* c, const float* cen, int32_t n) {
+  if (!c) return set_error(TQ_ERR_INVALID, "codec is NULL");
+  c->n_host_centroids = 0;
+  for (int i = 0; i < 16; ++i) c->host_centroids[i] = 0.f;
+  if (cen && n > 0 && n <= 16) {
+    for (int i = 0; i < n; ++i) c->host_centroids[i] = cen[i];
+    c->n_host_centroids = n;
+  }
+  c->value_table[0] = c->value_table[1] = c->value_table[2] = c->value_table[3] = 0;
+  c->value_scale = 0.f;
+  c->value_table_err = INFINITY;
+  if (!cen || n != 4) return TQ_OK;
+  // The largest centroid is anchored at an fp16 number m * 2^-14 (m an
+  // 11-bit significand); the others are the nearest fp16 numbers of c_i /
+  // scale. Of the 1024 anchors the one with the smallest worst relative error
+  // (scale rounded to float32 included) is kept.
+  int a = 0;
+  for (int i = 1; i < 4; ++i)
+    if (fabs((double)cen[i]) > fabs((double)cen[a])) a = i;
+  const double ca = cen[a];
+  if (!(fabs(ca) > 0.0) || !std::isfinite(ca)) return TQ_OK;
+  double best = INFINITY;
+  for (int m = 1024; m < 2048; ++m) {
+    const double ta = (ca < 0 ? -m : m) * 0x1p-14;
+    const float scale = (float)(ca / ta);
+    uint16_t tab[4];
+    double err = 0.0;
+    for (int i = 0; i < 4; ++i) {
+      const _Float16 t = (_Float16)((double)cen[i] / (double)scale);
+      tab[i] = __builtin_bit_cast(uint16_t, t);
+      const double got = (double)scale * (double)(float)t;
+      const double e = cen[i] == 0.f ? fabs(got) : fabs(got - (double)cen[i]) / fabs((double)cen[i]);
+      err = e > err ? e : err;
+    }
+    if (err < best) {
+      best = err;
+      for (int i = 0; i < 4; ++i) c->value_table[i] = tab[i];
+      c->value_scale = scale;
+    }
+  }
+  c->value_table_err = (float)best;
+  return TQ_OK;
+}
 
 const char* tq_last_error(void) { return tq::g_err; }
 
@@ -611,14 +678,14 @@ int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x
   hipStream_t s = static_cast<hipStream_t>(stream);
   // small spans with the QJL sketch (one-token decode drains): one vector per
   // wave (without a sketch the MFMA kernel below is as fast on such spans)
-  if (codec->d == 128 && qjl && codec->qjl_m <= 128 && span->n_tok <= 8 && !g_force_general) {
+  if (codec->d == 128 && qjl && codec->qjl_m <= 128 && span->n_tok <= 8 && !(codec->flags & TQ_CODEC_GENERAL_COMPRESS)) {
     const int64_t nvec = (int64_t)span->rows * span->n_tok;
     hipLaunchKernelGGL(drain_kernel, dim3((unsigned)((nvec + DRW - 1) / DRW)), dim3(DRW * 64), 0, s, a);
     TQ_LAUNCH_CHECK("tq_compress (drain)");
     return TQ_OK;
   }
   // fp16, head_dim 128, no QJL sketch: the MFMA kernel (tq_compress_fast.hip)
-  if (codec->d == 128 && !g_force_general && launch_compress_fast(a, s)) {
+  if (codec->d == 128 && !(codec->flags & TQ_CODEC_GENERAL_COMPRESS) && launch_compress_fast(a, s)) {
     TQ_LAUNCH_CHECK("tq_compress");
     return TQ_OK;
   }

@@ -1,4 +1,6 @@
-// Arguments of the K4/V2 decode-attention kernels (per-workgroup partials, then a merge).
+// Arguments of the decode-attention kernels: the K4/V2 partials + merge
+// kernels (tq_decode_fast.hip) and the dense fp16 / bf16 kernel
+// (tq_decode_dense.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -6,13 +8,30 @@
 
 namespace tq {
 
+constexpr int FAST_WAVES = 8;          // waves per workgroup of the K4/V2 partials kernel
+constexpr int FAST_PART_FLOATS = 132;  // per query head per dense-kernel partial: M, L, pad, pad, out[128]
+// per query head per K4/V2 partial: M, L, has_orig, pad, rotated out[128],
+// original-space out[128] (both / L)
+constexpr int PACKED_PART_FLOATS = 260;
+constexpr int FAST_MAX_WG = 256;       // partials per (sequence, kv head) of the dense kernel
+
+// Per-call arguments of the K4/V2 partials kernel and its merge kernel.
+// Work plan: sequence b has P_b = ceil(comp_b / 32) packed blocks and
+// ntl_b = ceil((sink_b + res_b) / 16) fp16 tiles; W_b = max(P_b, [ntl_b > 0])
+// units per kv head. With U = hkv sum_b W_b the units of (b, g) are cut into
+// n_b = ceil(W_b / T) chunks of T = ceil(U / (chunks nwg)) units (rounded up to
+// a multiple of 8, the waves of a workgroup); chunk j takes packed blocks
+// [j T, (j + 1) T) and fp16 tiles [j tpc, (j + 1) tpc), tpc = ceil(ntl_b / n_b),
+// and is partial slot N_b + g n_b + j (N_b = hkv sum_{b' < b} n_b').
+// Workgroup p of the nwg takes the chunks [p V / nwg, (p + 1) V / nwg) of
+// the V = N_batch in total.
 struct FastArgs {
   const uint8_t* kc;  int64_t k_hs;    // 4-bit key codes, 64-byte rows
   const float* kn;    int64_t kn_hs;   // key norms
   const uint8_t* vc;  int64_t v_hs;    // 2-bit value codes, 32-byte rows
   const float* vn;    int64_t vn_hs;   // value norms
-  const void* sink_k; const void* sink_v; int64_t sink_hs;   // fp16, elements
-  const void* res_k;  const void* res_v;  int64_t res_hs;    // fp16 ring
+  const uint16_t* sink_k; const uint16_t* sink_v; int64_t sink_hs;   // fp16, elements
+  const uint16_t* res_k;  const uint16_t* res_v;  int64_t res_hs;    // fp16 ring
   int res_cap, res_start0;
   const int32_t* comp_len_b;
   const int32_t* sink_len_b;
@@ -21,18 +40,20 @@ struct FastArgs {
   int max_comp, max_sink, max_res;
   const void* q; int q_dtype;
   float* out;
-  int hq, hkv;
+  int batch, hq, hkv;
   float qscale;          // scale * log2(e)
-  const uint16_t* rot16; // (2, 128, 128) fp16 high part / remainder of R (key codec)
-  const uint16_t* rotT;  // (2, 128, 128) bf16 high part / remainder of R^T (value codec)
-  const float* kcen;     // 16 key centroids
-  const float* vcen;     // 4 value centroids
-  float* part;           // per-workgroup partials (workspace)
-  int nwg;               // workgroups per (sequence, kv head)
-  int bpw;               // compressed 32-token blocks per workgroup (<= FAST_WAVES * FAST_BLOCKS_PER_WAVE)
-  int fpw;               // fp16 (sink / residual) tokens per workgroup (<= FAST_FP16_PER_WG)
-  int merge;             // 1: launch the merge kernel too; 0: partials only (measurement)
-  // QJL sketch terms (the fast kernel with QB): per (sequence, kv head, query
+  const uint16_t* rot16; // (2, 128, 128) fp16 high part / remainder of R (key codec): query rotation
+  const float* vrot;     // (128, 128) R float32, row-major (value codec): inverse rotation in the merge
+  const uint64_t* klut;  // (256,) key decode table of the key codec (tq_codec.decode_table)
+  const uint64_t* vlut;  // (256,) value decode table of the value codec
+  float vscale;          // value centroid i = vscale * table value i
+  float* part;           // (vmax, G, PACKED_PART_FLOATS) partials
+  int nwg;               // workgroups of the partials kernel
+  int chunks;            // target chunks per workgroup (1 when every sequence has the maximal lengths)
+  int vmax;              // partial slots (upper bound of V)
+  int uni;               // 1: every sequence has the maximal lengths; the plan below is set
+  int plan_T, plan_nu, plan_V;  // uniform plan: units per chunk, chunks per (b, g), chunks
+  // QJL sketch terms (partials kernel with QB): per (sequence, kv head, query
   // head) rows of qb_hs floats indexed by compressed token
   const float* qjl_bias; // added to each compressed token's base-2 score
   float* scores;         // final base-2 scores of the compressed tokens (written)
@@ -40,21 +61,63 @@ struct FastArgs {
   float* ml;             // merge output: (batch, hq, 2) global max and sum, or NULL
 };
 
-size_t fast_smem_bytes();
-int fast_set_attributes();
-int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s);
-// the same kernels with the QJL key bias added to the scores and the scores stored (a.qjl_bias, a.scores)
-int launch_fast_decode_qjl(const FastArgs& a, int G, int batch, hipStream_t s);
+// Host-side sizing of the K4/V2 path for a call: workgroups, chunks per
+// workgroup and the partial slots the workspace must hold.
+void fast_plan_host(int batch, int hkv, int max_comp, int max_sink, int max_res, bool uniform, int cus,
+                    int& nwg, int& chunks, int& vmax);
+// The uniform plan (every sequence at the maximal lengths): T, n and V.
+void fast_uniform_plan(int batch, int hkv, int max_comp, int max_sink, int max_res, int nwg, int chunks, int& T,
+                       int& nu, int& V);
+// Launches the partials kernel (QB: with the QJL key bias, scores stored)
+// and, when merge != 0, the merge kernel. G in {1, 2, 4, 8}.
+int launch_fast_decode(const FastArgs& a, int G, bool qb, int merge, hipStream_t s);
 
-constexpr int FAST_WAVES = 8;            // waves per workgroup of the decode kernel
-constexpr int FAST_BLOCKS_PER_WAVE = 4;  // compressed blocks per wave (two in flight at a time)
-constexpr int FAST_FP16_PER_WG = 16;     // fp16 tokens per workgroup, staged in LDS
-constexpr int FAST_MAX_WG = 256;         // workgroups per (sequence, kv head)
-constexpr int FAST_PART_FLOATS = 132;    // per query head per workgroup: M, L, pad, pad, out[128] (original space, / L)
-
-// Merge of per-workgroup partials (FAST_PART_FLOATS per query head, nwg per
-// (sequence, kv head)) into out (batch, hq, 128) float32.
+// Merge of per-workgroup partials in original space ([M, L, pad, pad,
+// out[128] / L] per query head, nwg per (sequence, kv head)) into out
+// (batch, hq, 128) float32: the dense kernel's partials.
 int launch_partial_merge(float* part, int nwg, int G, int hq, int hkv, int batch, float* out, hipStream_t s);
+
+// Arguments of the K4/V2 kernels for uniform batches (tq_decode_uniform.hip):
+// grid (nwg, hkv, batch), workgroup c of (b, g) takes the compressed blocks
+// [c bpw, (c + 1) bpw) and the fp16 tokens [c fpw, (c + 1) fpw) of the
+// [sink | ring] list; partials in original space (FAST_PART_FLOATS per query
+// head, nwg per (b, g)).
+constexpr int UNI_BLOCKS_PER_WAVE = 4;  // compressed blocks per wave
+constexpr int UNI_FP16_PER_WG = 16;     // fp16 tokens per workgroup, staged in LDS
+constexpr int UNI_MAX_WG = 256;         // workgroups per (sequence, kv head)
+
+struct UniformArgs {
+  const uint8_t* kc;  int64_t k_hs;    // 4-bit key codes, 64-byte rows
+  const float* kn;    int64_t kn_hs;   // key norms
+  const uint8_t* vc;  int64_t v_hs;    // 2-bit value codes, 32-byte rows
+  const float* vn;    int64_t vn_hs;   // value norms
+  const void* sink_k; const void* sink_v; int64_t sink_hs;   // fp16, elements
+  const void* res_k;  const void* res_v;  int64_t res_hs;    // fp16 ring
+  int res_cap, res_start0;
+  const int32_t* comp_len_b;   // per-sequence lengths (NULL: the maximal ones)
+  const int32_t* sink_len_b;
+  const int32_t* res_len_b;
+  const int32_t* res_start_b;
+  int max_comp, max_sink, max_res;
+  const void* q; int q_dtype;
+  float* out;
+  int batch, hq, hkv;
+  float qscale;          // scale * log2(e)
+  const uint16_t* rot16; // (2, 128, 128) fp16 high part / remainder of R (key codec): query rotation
+  const uint16_t* rotT;  // (2, 128, 128) fp16 high part / remainder of R^T (value codec): inverse rotation
+  float kcent[16];       // key centroids (tq_codec.host_centroids)
+  uint32_t vtab[4];      // value table: fp16 bits of entry i (tq_codec.value_table)
+  float vscale;          // value centroid i = vscale * table value i
+  float* part;           // per-workgroup partials (workspace)
+  int nwg, bpw, fpw;
+  const float* qjl_bias; // QJL key term (partials kernel with QB), rows of qb_hs floats
+  float* scores;         // final base-2 scores of the compressed tokens (written with QB)
+  int64_t qb_hs;
+  float* ml;             // merge output: (batch, hq, 2) global max and sum, or NULL
+};
+// Launches the uniform-batch partials kernel (qb: with the QJL key bias,
+// scores stored) and, when merge != 0, its merge kernel. G in {1, 2, 4, 8}.
+int launch_uniform_decode(const UniformArgs& a, int G, bool qb, int merge, hipStream_t s);
 
 // Arguments of the dense (fp16 / bf16 K/V) decode-attention kernel: the
 // fp16 segments of tq_attn_desc, head_dim 128.

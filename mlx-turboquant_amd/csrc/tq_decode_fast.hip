@@ -1,13 +1,16 @@
-// Fused decode attention for K4/V2 TurboQuant caches on gfx950: a partials
-// kernel over the compressed / fp16 tokens and a small merge kernel.
+// Fused decode attention for K4/V2 TurboQuant caches on gfx950: a persistent
+// partials kernel over the compressed and fp16 tokens, and a merge kernel that
+// combines the partials and applies the inverse rotation once per query head.
 //
-// Grid (nwg, hkv, batch): workgroup c of (sequence b, kv head g) owns
-//  - the compressed 32-token blocks [c*bpw, (c+1)*bpw) of the sequence (bpw <=
-//    32): wave w takes blocks c*bpw + w + 8k, k < 4, with two blocks' loads in
-//    flight while it computes;
-//  - the fp16 tokens [c*fpw, (c+1)*fpw) (fpw <= 16) of the sequence's [sink |
-//    residual ring] list, staged in LDS during set-up and scored by wave 0
-//    (the first to be issued on its SIMD) before its compressed blocks.
+// Work (plan in tq_decode_fast.h): the tokens of (sequence b, kv head g) are
+// weighted units, its fp16 blocks (32 tokens of the [sink | residual ring]
+// list) first, then its packed 32-token blocks. The units of (b, g) are cut
+// into chunks; workgroup p (one per CU, 8 waves) takes a contiguous run of
+// chunks. A run of chunks of one (b, g) is a segment: the waves take its fp16
+// blocks, then its packed blocks, round robin, and the workgroup writes one
+// partial per segment (max, sum, rotated-space output / sum per query head)
+// and empty partials (sum 0) for the other chunks of the run. The lookup tables
+// are built once per workgroup; the query is rotated once per segment.
 //
 // Scores are computed transposed, S^T = K q^T (MFMA 16x16x32 f16):
 //   A = 16 tokens x 32 k-slots of keys, B = 32 k-slots x 16 columns of queries.
@@ -17,35 +20,32 @@
 // (7 - c8) % G, so a DPP row half-mirror (c8 <-> 7 - c8) adds the two parts,
 // and each lane goes on with the 4 scores of its own tile only. For G = 8
 // column r holds part r >> 3 of head r & 7 (a rotation by 8 pairs them) and
-// every lane sees both tiles. In rotated space (compressed tokens, docs/FUSED_ATTENTION_DESIGN.md
-// :62-67) each key code byte (two 4-bit codes) is looked up in an LDS table
-// whose 8-byte entry is (c_hi[a], c_hi[b], c_lo[a], c_lo[b]); two lookups fill
-// one A operand, and the matching B k-slots repeat the two query values, so
+// every lane sees both tiles. In rotated space (compressed tokens,
+// docs/FUSED_ATTENTION_DESIGN.md:62-67) each key code byte (two 4-bit codes)
+// is looked up in an LDS table whose 8-byte entry is (c_hi[a], c_hi[b],
+// c_lo[a], c_lo[b]); two lookups fill one A operand, and the matching B
+// k-slots repeat the two query values, so
 //   sum_k A B = sum_d (c_hi + c_lo)[idx_d] q_d   with c_lo = c - fp16(c).
 // Scaled by the key norm and run through an online softmax in base 2.
 // Output, transposed too: O^T += V^T P^T with A = 16 dims x 32 tokens of
 // values decoded from an LDS table indexed by one 2-bit-code byte (4 dims of
 // one token) and paired across tokens with v_perm, and B = p * n_v split into
 // fp16 high part / remainder along the same columns as the scores (zero in
-// the k-slots of the other tile).
+// the k-slots of the other tile). The value table holds an exact fp16 copy of
+// the codebook scaled by 1 / vscale (chosen on the host so that both
+// magnitudes of the 2-bit codebook are fp16 numbers to within 5e-8), and
+// vscale is folded into n_v.
 // fp16 tokens (original space) use the same MFMAs with exact fp16 keys /
-// values, accumulated separately.
+// values and the query in original space; their normalised sum is rotated
+// into the segment's partial (MFMA, R high part / remainder) at the end of
+// their phase.
 //
-// Lane (column r, group q4) of a score tile holds tokens 4*q4 + i of the
-// tile, which is exactly the k-slot order (8*q4 + i, tile 1 at + 4) the P^T
-// operand needs, so softmax weights never leave their lane. The running max
-// is raised with a margin, so most blocks need no rescale. The accumulator of lane
-// (column r, q4), MFMA nb, register i is rotated dim 32*q4 + 8*i + nb.
-//
-// The 8 waves of a workgroup are combined through LDS; the workgroup applies
-// the inverse rotation to its rotated sum (MFMA 16x16x32 bf16, high part /
-// remainder of both operands), adds the original-space sum, and writes
-// (max, sum, output / sum) per query head. The merge kernel combines the
-// partials of each (b, g) with their softmax weights.
+// The merge kernel (one workgroup per query head and 32-dim output slice)
+// combines the partials of (b, g) with their softmax weights
+// (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40) and applies out = sum @ R in
+// float32 (rotation.py:68-78).
 
 #include <math.h>
-
-#include <type_traits>
 
 #include "tq_common.h"
 #include "tq_decode_fast.h"
@@ -53,69 +53,57 @@
 namespace tq {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef __fp16 hx2 __attribute__((ext_vector_type(2)));
 
 constexpr int FD = 128;
-constexpr int FW = FAST_WAVES;            // waves per workgroup (FW * 16 == FD)
-constexpr int FT = FW * 64;               // threads
-constexpr int PS = FAST_PART_FLOATS;      // floats per (workgroup, head) partial
-constexpr int P_OUT = 4;                  // partial: [M, L, pad, pad, out[128]]
-constexpr int NPW = FAST_BLOCKS_PER_WAVE; // compressed blocks per wave
-constexpr int MAXWG = FAST_MAX_WG;        // workgroups per (sequence, kv head)
-constexpr int FROW = 272;                 // LDS row of a staged fp16 token (256 + 16 against bank conflicts)
-constexpr float M_INIT = -1e30f;          // running max before the first block
-constexpr int WF16 = 0;                   // the wave that scores the staged fp16 tokens
-constexpr int NCP = 32;                   // table replicas per entry (lane % 32: one per lane of an LDS pass)
+constexpr int FW = FAST_WAVES;       // waves per workgroup (FW * 16 == FD)
+constexpr int FT = FW * 64;          // threads
+constexpr int PS = FAST_PART_FLOATS; // floats per (slot, head) partial
+constexpr int P_OUT = 4;             // partial: [M, L, pad, pad, out[128]]
+constexpr int PPS = PACKED_PART_FLOATS;  // floats per (slot, head) K4/V2 partial
+constexpr float M_INIT = -1e30f;     // running max before the first block
 // A block whose max exceeds the running max m raises m to that max + this
 // margin (base-2 units), so later blocks rarely trigger a rescale; weights
 // stay <= 1.
 constexpr float RESCALE_MARGIN = 3.f;
+// p * n_v above this is scaled down by a power of two (fp16 operand range);
+// the column's exponent is applied at the combine.
+constexpr float PV_LIMIT = 32768.f;
+// |scale * (R q)_j| <= scale * ||q|| must stay below this for the fp16 query
+// operands; larger queries are scaled by a power of two per head.
+constexpr float Q_LIMIT = 16384.f;
+constexpr int MERGE_SLOTS = 2112;    // partial slots of one (b, g) the merge kernel holds weights for (a multiple of 32)
 
-struct Layout {
-  // Lookup tables: value entry e (four 2-bit codes) and key entry e (two
-  // 4-bit codes) each in a 256-byte row of 32 replicas, replica c at 8*c, so
-  // the LDS address of an entry is one byte permute of the code word. Once
-  // every wave is past its blocks the table region holds the combine buffers.
-  static constexpr uint32_t vlut = 0;            // 256 rows x 256 B
-  static constexpr uint32_t klut = 65536;        // 256 rows x 256 B
-  static constexpr uint32_t cmb = 0;             // [8 waves][8 heads][CMS] f32
-  static constexpr uint32_t aop = 34816;         // [8 heads][AOPS bytes: 2 parts x 128 bf16] normalised rotated sum
-  static constexpr uint32_t onr = aop + 8 * 576; // [8 heads][128] f32 normalised original-space sum
-  static constexpr uint32_t cml = 131072;        // [8 waves][8 heads][4] f32 max, sum, max of the orig part
-  static constexpr uint32_t qop = cml + 1024;    // [8 heads][2 parts][QOPS bytes: 4][8][8] fp16 rotated-q B operands
-  static constexpr uint32_t qfo = qop + 16 * 528; // [8 heads][2 parts][4][4][8] fp16 original-space q B operands
-  static constexpr uint32_t opk = qfo + 4096;    // [8 heads][128] f32 parked original-space partial
-  static constexpr uint32_t nst = opk + 4096;    // [8 waves][64] f32 norm staging
-  static constexpr uint32_t qst = nst + 2048;    // [8 heads][128] q as given (up to 4 bytes per element)
-  static constexpr uint32_t f16s = qst + 4096;   // [16 tokens][keys, values][FROW] staged fp16 tokens
-  static constexpr uint32_t total = f16s + FAST_FP16_PER_WG * 2 * FROW;
+// LDS layout. Lookup tables: key entry of code byte e (two 4-bit codes) and
+// value entry of byte e (four 2-bit codes), NCP replicas of 8 bytes each in
+// rows of 256 bytes, so the LDS address of an entry is one byte permute of
+// the code word (code byte as address bits 8-15). NCP = 32: two tables of
+// 64 KB; NCP = 16: one table whose row e holds the 16 key replicas, then the
+// 16 value replicas.
+template <int G>
+struct Lay {
+  static constexpr int NCP = G <= 4 ? 32 : 16;
+  static constexpr uint32_t tabs = NCP == 32 ? 0x20000u : 0x10000u;  // bytes of the tables
+  static constexpr int CMS = FD + 4;                                  // floats per combine row: 128 sums, m, l
+  static constexpr uint32_t cmb = tabs;                               // [FW][G][CMS] f32
+  static constexpr uint32_t QOPS = 528;                               // bytes per (head, part) of qop (512 + 16)
+  static constexpr uint32_t qop = cmb + FW * G * CMS * 4;             // [G][2 parts][QOPS] rotated-q B operands
+  static constexpr uint32_t qfo = qop + G * 2 * QOPS;                 // [G][2 parts][4 q4][4 kb][16 B] original-space q
+  static constexpr uint32_t nst = qfo + G * 2 * 256;                  // [FW][64] f32 norm staging
+  static constexpr uint32_t pre = nst + FW * 256;                     // [G][CMS] parked fp16 tiles: sums, m, l
+  static constexpr uint32_t total = pre + G * CMS * 4;
+  static constexpr uint32_t qstage = G * FD * 4;                      // bytes of the query rows as given (own array)
 };
-// Row strides padded so that rows read by different lanes of one LDS
-// instruction start in different banks: the rotated-q operand rows of the 8
-// (head, part) columns, the combine rows of the G heads, the inverse-rotation
-// operand rows of the G heads.
-constexpr uint32_t QOPS = 528;  // bytes per (head, part) of qop (512 + 16)
-constexpr int CMS = FD + 4;     // floats per (wave, head) of cmb
-constexpr uint32_t AOPS = 576;  // bytes per head of aop (2 x 256 + 64)
-static_assert(FW * 8 * CMS * 4 <= Layout::aop && Layout::onr == Layout::aop + 8 * AOPS &&
-              Layout::onr + 8 * FD * 4 <= Layout::cml, "combine buffers fit the table region");
-static_assert(Layout::total <= 160 * 1024, "LDS of one workgroup");
-static_assert(FAST_FP16_PER_WG == 16, "fp16 tokens: one 16-token score tile, one staging pass");
+static_assert(Lay<4>::total + Lay<4>::qstage <= 160 * 1024 && Lay<8>::total + Lay<8>::qstage <= 160 * 1024,
+              "LDS of one workgroup");
 
 __device__ inline half8 as_h8(u4 v) { return __builtin_bit_cast(half8, v); }
 
 __device__ inline f4 mfma(half8 a, half8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ inline bf8 as_b8(u4 v) { return __builtin_bit_cast(bf8, v); }
-
-__device__ inline f4 mfma_bf(bf8 a, bf8 b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 __device__ inline float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -155,34 +143,935 @@ __device__ inline uint32_t pk_rtz(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
 
-__device__ inline uint32_t pack_h2(float lo, float hi) {
-  const _Float16 a = (_Float16)lo, b = (_Float16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+__device__ inline uint32_t h16(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+
+// A value at a uniform address, read through the scalar cache (constant
+// address space: the value is not written during the kernel).
+template <typename T>
+__device__ inline T ld_uniform(const T* p, int i) {
+  return ((const __attribute__((address_space(4))) T*)(p))[i];
 }
 
-// A float at a uniform address, read through the scalar cache (constant
-// address space: the value is not written during the kernel).
-__device__ inline float ld_uniform(const float* p, int i) {
-  return ((const __attribute__((address_space(4))) float*)(p))[i];
+// Global -> LDS copy of 16 bytes per lane (the active lanes of the wave fill
+// consecutive 16-byte pieces from `lds`). The builtin exists in the device
+// pass only; the host pass of this file only needs the kernel's declaration.
+__device__ inline void load_lds16(const void* g, uint8_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+#endif
 }
 
 __device__ inline u2 lds_u2(const uint8_t* smem, uint32_t addr) {
   return *reinterpret_cast<const u2*>(smem + addr);
 }
 
+__device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// Merge of the partials of (sequence b, kv head g), a second launch on the
-// same stream (the kernel boundary makes the partials visible), in float32
-// (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40). Each partial p holds its max
-// M_p, its sum L_p and its output x_p in original space, normalised by L_p:
-//   out = sum_p w_p x_p,  w_p = 2^(M_p - M) L_p / L,
-//   M = max_p M_p,  L = sum_p 2^(M_p - M) L_p.
-// One wave per (query head, half of the dims): lane p + 64k holds the
-// header of partial p + 64k, lane j sums dim 64 * half + j.
+// ---------------------------------------------------------------- work plan
+struct SeqLen {
+  int comp, sink, res, rstart;
+};
+
+// lengths of sequence b clamped to the bounds the host checked, so every read
+// stays inside the stores, the sink and the ring; the four loads are issued
+// together (an absent array is read through another valid pointer and its
+// value replaced)
+__device__ inline SeqLen seq_len(const FastArgs& a, int b) {
+  const int32_t* any = a.comp_len_b ? a.comp_len_b : a.sink_len_b ? a.sink_len_b : a.res_len_b ? a.res_len_b : a.res_start_b;
+  SeqLen s;
+  if (!any) {
+    s.comp = a.max_comp; s.sink = a.max_sink; s.res = a.max_res; s.rstart = a.res_start0;
+    return s;
+  }
+  const int c = (a.comp_len_b ? a.comp_len_b : any)[b];
+  const int k = (a.sink_len_b ? a.sink_len_b : any)[b];
+  const int e = (a.res_len_b ? a.res_len_b : any)[b];
+  const int t = (a.res_start_b ? a.res_start_b : any)[b];
+  s.comp = a.comp_len_b ? min(max(c, 0), a.max_comp) : a.max_comp;
+  s.sink = a.sink_len_b ? min(max(k, 0), a.max_sink) : a.max_sink;
+  s.res = a.res_len_b ? min(max(e, 0), a.max_res) : a.max_res;
+  s.rstart = a.res_start_b ? min(max(t, 0), max(a.res_cap - 1, 0)) : a.res_start0;
+  return s;
+}
+
+__device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// work units of one (sequence, kv head): its packed blocks, at least one when
+// it has fp16 tokens only
+__device__ inline int units_of(int comp, int nf) { return max((comp + 31) >> 5, nf > 0 ? 1 : 0); }
+
+struct Plan {
+  int T;        // units per chunk (a multiple of FW)
+  int V;        // chunks of the call
+  bool uni;     // every sequence has the maximal lengths
+  int Wu, nu;   // uniform: units and chunks per (b, g)
+};
+
+__device__ inline int round8(int64_t t) { return (int)((max<int64_t>(t, 1) + FW - 1) / FW * FW); }
+
+// Identical in every wave of both kernels (wave-uniform results).
+__device__ Plan make_plan(const FastArgs& a) {
+  Plan p{};
+  const int lane = threadIdx.x & 63;
+  p.uni = a.uni != 0;
+  if (p.uni) {  // computed on the host (fast_uniform_plan)
+    p.Wu = units_of(a.max_comp, a.max_sink + a.max_res);
+    p.T = a.plan_T;
+    p.nu = a.plan_nu;
+    p.V = a.plan_V;
+    return p;
+  }
+  const int64_t div = (int64_t)a.chunks * a.nwg;
+  // lane b - base holds W_b of this 64-sequence batch; sums through readlane
+  int64_t U = 0;
+  int w0 = 0;  // lane b's units of the first 64 sequences
+  for (int base = 0; base < a.batch; base += 64) {
+    const int b = base + lane;
+    SeqLen s{};
+    if (b < a.batch) s = seq_len(a, b);
+    const int w = b < a.batch ? units_of(s.comp, s.sink + s.res) : 0;
+    if (base == 0) w0 = w;
+    const int nb = min(64, a.batch - base);
+    for (int k = 0; k < nb; ++k) U += __builtin_amdgcn_readlane(w, k);
+  }
+  U *= a.hkv;
+  p.T = round8((U + div - 1) / div);
+  int V = 0;
+  for (int base = 0; base < a.batch; base += 64) {
+    int w = w0;
+    if (base > 0) {
+      const int b = base + lane;
+      SeqLen s{};
+      if (b < a.batch) s = seq_len(a, b);
+      w = b < a.batch ? units_of(s.comp, s.sink + s.res) : 0;
+    }
+    const int nb = min(64, a.batch - base);
+    for (int k = 0; k < nb; ++k) V += cdiv(__builtin_amdgcn_readlane(w, k), p.T);
+  }
+  p.V = V * a.hkv;
+  return p;
+}
+
+// Sequence of chunk `key` (or sequence `key` when by_seq): its first chunk
+// N_b, chunks per kv head n_b, units W_b and lengths.
+struct Loc {
+  int b, Nb, nb, W;
+  SeqLen s;
+};
+
+__device__ Loc locate(const FastArgs& a, const Plan& p, int key, bool by_seq) {
+  Loc L{};
+  if (p.uni) {
+    const int per = a.hkv * p.nu;
+    L.b = by_seq ? key : key / per;
+    L.Nb = L.b * per;
+    L.nb = p.nu;
+    L.W = p.Wu;
+    L.s = seq_len(a, L.b);
+    return L;
+  }
+  const int lane = threadIdx.x & 63;
+  int carry = 0;  // chunks of the sequences before the current one
+  bool found = false;
+  for (int base = 0; base < a.batch && !found; base += 64) {
+    const int b = base + lane;
+    SeqLen s{};
+    if (b < a.batch) s = seq_len(a, b);
+    const int w = b < a.batch ? units_of(s.comp, s.sink + s.res) : 0;
+    const int nb = min(64, a.batch - base);
+    for (int k = 0; k < nb; ++k) {
+      const int wk = __builtin_amdgcn_readlane(w, k);
+      const int n = a.hkv * cdiv(wk, p.T);
+      if (by_seq ? base + k == key : key < carry + n) {
+        L.b = base + k;
+        L.Nb = carry;
+        L.nb = n / a.hkv;
+        L.W = wk;
+        L.s.comp = __builtin_amdgcn_readlane(s.comp, k);
+        L.s.sink = __builtin_amdgcn_readlane(s.sink, k);
+        L.s.res = __builtin_amdgcn_readlane(s.res, k);
+        L.s.rstart = __builtin_amdgcn_readlane(s.rstart, k);
+        found = true;
+        break;
+      }
+      carry += n;
+    }
+  }
+  return L;
+}
+
+// One segment of a workgroup: chunks [v, vend) of (b, g), their packed blocks
+// [k0, k1) and fp16 tiles [t0, t1).
+struct Seg {
+  int b, g, row, vend;
+  int k0, k1, t0, t1;
+  int comp, sink, nf, rstart;
+};
+
+__device__ inline Seg segment(const FastArgs& a, const Plan& P, int v, int v1) {
+  const Loc L = locate(a, P, v, false);
+  Seg S;
+  const int rel = v - L.Nb;
+  S.b = L.b;
+  S.g = uni(rel / L.nb);
+  const int jc = uni(rel % L.nb);
+  S.vend = uni(min(v1, L.Nb + (S.g + 1) * L.nb));
+  const int cnt = S.vend - v;
+  S.row = S.b * a.hkv + S.g;
+  S.comp = L.s.comp;
+  S.sink = L.s.sink;
+  S.nf = L.s.sink + L.s.res;
+  S.rstart = L.s.rstart;
+  const int Pb = (S.comp + 31) >> 5;
+  S.k0 = min(Pb, jc * P.T);
+  S.k1 = min(Pb, (jc + cnt) * P.T);
+  const int ntl = (S.nf + 15) >> 4;
+  const int tpc = cdiv(ntl, L.nb);
+  S.t0 = min(ntl, jc * tpc);
+  S.t1 = min(ntl, (jc + cnt) * tpc);
+  return S;
+}
+
+// ------------------------------------------------------------ partials kernel
+// One packed block of a wave, loaded from HBM (lane r, q4)
+struct Blk {
+  u4 k0, k1;      // key codes of tokens t0 + r and t0 + 16 + r, bytes 16*q4 ..
+  uint32_t v[8];  // value code halfword r of tokens A0..A3 (t0 + 4q4 + i), B0..B3 (t0 + 16 + 4q4 + i)
+  float nk, nv;   // key / value norm of token t0 + (lane & 31)
+  float4 qb[2];   // QJL key term of the lane's tokens (tile `tile`, and tile 1 for G = 8)
+};
+
+// One fp16 tile (16 tokens of the [sink | ring] list) of wave FW - 1 (lane r, q4)
+struct Tile16 {
+  u4 k[4];  // key row of token r, dims 32 q4 + 8 kb .. + 8
+  u4 v[4];  // value rows of tokens 4 q4 + i, dims 8 r .. 8 r + 7
+};
+
+// Raw buffer over `bytes` bytes at p (stride 0): loads past the end read zero.
+__device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+constexpr int WF16 = FW - 1;  // the wave that takes the fp16 tiles (it has the fewest packed blocks)
+
+template <int G, bool QB>
+__global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
+  using LY = Lay<G>;
+  __shared__ __align__(16) uint8_t smem[LY::total];
+  // the G query rows of the segment as given, written by direct global->LDS
+  // loads (an array of its own, so those loads are not ordered with smem)
+  __shared__ __align__(16) uint8_t qst[LY::qstage];
+
+  constexpr int TS = G <= 4 ? 2 : 1;  // tiles sharing the columns
+  constexpr int NS = 8 / TS;           // scores per lane per block
+  const int w = uni(threadIdx.x >> 6);
+  const int j0 = 16 * w;  // rotated dims of this wave in the query rotation
+  const int esz = a.q_dtype == TQ_F32 ? 4 : 2;
+  // Lane-derived values, recomputed at the start of every phase from an opaque
+  // copy of the thread id: otherwise the compiler computes them once and keeps
+  // them live through the block loop, where they do not fit beside its
+  // registers.
+  int tid, lane, r, q4, tile, c8, hd, ko, vo, no;
+  bool lo_part, writer;
+  float partf;
+  auto rederive = [&]() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    tid = t;
+    lane = t & 63;
+    r = lane & 15;
+    q4 = lane >> 4;
+    tile = TS == 2 ? r >> 3 : 0;  // tile of column r (TS == 2)
+    c8 = r & 7;
+    hd = TS == 2 ? (c8 < 4 ? c8 : 7 - c8) % G : c8;  // query head of column r
+    lo_part = TS == 2 ? c8 >= 4 : r >= 8;          // column holds the fp16 remainder
+    partf = lo_part ? 1.f : 0.f;
+    writer = !lo_part && c8 < G;  // one column per (tile, head) writes the combine rows
+    // lane byte offsets within a block: key bytes 16*q4 .. of token r (token
+    // 16 + r at +1024); value halfword r of token 4*q4 (token 4*q4 + i at
+    // +32 i, token 16 + 4*q4 + i at +512 + 32 i); norm of token lane & 31
+    ko = r * 64 + 16 * q4;
+    vo = q4 * 128 + 2 * r;
+    no = (lane & 31) * 4;
+  };
+  rederive();
+
+  // Every kernel argument the set-up needs, loaded in one batch of scalar
+  // loads and waited for once (first uses spread over the set-up would
+  // otherwise wait one by one).
+  asm volatile("" ::"s"(a.kc), "s"(a.kn), "s"(a.vc), "s"(a.vn), "s"(a.q), "s"(a.rot16), "s"(a.sink_k),
+               "s"(a.sink_v), "s"(a.res_k), "s"(a.res_v), "s"(a.k_hs), "s"(a.kn_hs), "s"(a.v_hs), "s"(a.vn_hs),
+               "s"(a.sink_hs), "s"(a.res_hs), "s"(a.max_comp), "s"(a.max_sink), "s"(a.max_res), "s"(a.res_start0),
+               "s"(a.res_cap), "s"(a.hq), "s"(a.hkv), "s"(a.q_dtype), "s"(a.uni), "s"(a.plan_T), "s"(a.plan_nu),
+               "s"(a.plan_V), "s"(a.nwg), "s"(a.batch));
+  asm volatile("" ::"s"(a.klut), "s"(a.vlut), "s"(a.qscale), "s"(a.vscale), "s"(a.comp_len_b), "s"(a.sink_len_b),
+               "s"(a.res_len_b), "s"(a.res_start_b), "s"(a.part));
+  // the decode-table entries of this lane's rows of the LDS tables (row e =
+  // 32 w + 4 k + lane / 16, k < 8), requested before anything else
+  uint64_t ke[8], ve[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int e = 32 * w + 4 * k + (lane >> 4);
+    ke[k] = a.klut[e];
+    ve[k] = a.vlut[e];
+  }
+  const Plan P = make_plan(a);
+  const int v0 = (int)((int64_t)blockIdx.x * P.V / a.nwg);
+  const int v1 = (int)((int64_t)(blockIdx.x + 1) * P.V / a.nwg);
+
+  // ---- per-segment loads, issued at the end of the previous segment (for
+  // the first segment before the lookup tables are built): the query rows,
+  // the R rows j0 + n of this wave as MFMA B operands (fp16 high part and
+  // remainder; k-slot (q4, i) of step kb = dim 32 kb + 8 q4 + i), then the
+  // first two packed blocks of the wave.
+  Seg S{};
+  const int qchunks = G * FD * esz / 16;  // 16-byte chunks of the G query rows
+  u4 rqh[4], rql[4];
+  Tile16 T16;
+  Blk B0, B1, B2;
+  int nkw = 0;
+  const uint8_t *kcodes = nullptr, *vcodes = nullptr;
+  const float *knorm = nullptr, *vnorm = nullptr;
+  auto slot_t0 = [&](int m) { return (S.k0 + w + FW * m) << 5; };
+  auto load_slot = [&](Blk& B, int m) {
+    const bool live = m < nkw;
+    const int t0 = live ? slot_t0(m) : 0;
+    const int n = live ? S.comp - t0 : 0;  // tokens readable from t0 on
+    const __amdgpu_buffer_rsrc_t rk = rsrc(kcodes + (int64_t)t0 * 64, n * 64);
+    const __amdgpu_buffer_rsrc_t rv = rsrc(vcodes + (int64_t)t0 * 32, n * 32);
+    const __amdgpu_buffer_rsrc_t rkn = rsrc(knorm + t0, n * 4);
+    const __amdgpu_buffer_rsrc_t rvn = rsrc(vnorm + t0, n * 4);
+    // constant offsets as the scalar offset operand (no per-offset VGPRs)
+    B.k0 = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0);
+    B.k1 = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 1024, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      B.v[i] = __builtin_amdgcn_raw_buffer_load_b16(rv, vo, i < 4 ? 32 * i : 512 + 32 * (i - 4), 0);
+    B.nk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rkn, no, 0, 0));
+    B.nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvn, no, 0, 0));
+    if constexpr (QB) {
+      const float* qbr = a.qjl_bias + ((int64_t)S.row * G + hd) * a.qb_hs + t0;
+      const __amdgpu_buffer_rsrc_t rb = rsrc(qbr, live ? min(32, (int)(a.qb_hs - t0)) * 4 : 0);
+#pragma unroll
+      for (int t = 0; t < 2 / TS; ++t) {
+        const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rb, (16 * (t + tile) + 4 * q4) * 4, 0, 0);
+        B.qb[t] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
+      }
+    }
+  };
+  // row of token u of the [sink | ring] list (u clamped into the list)
+  auto tok = [&](const uint16_t* s_base, const uint16_t* r_base, int u) {
+    u = min(u, S.nf - 1);
+    if (u < S.sink) return s_base + (int64_t)u * FD;
+    int sl = S.rstart + (u - S.sink);
+    sl = sl >= a.res_cap ? sl - a.res_cap : sl;
+    return r_base + (int64_t)sl * FD;
+  };
+  auto load_tile = [&](int t) {
+    const uint16_t* sk = a.sink_k + (int64_t)S.row * a.sink_hs;
+    const uint16_t* sv = a.sink_v + (int64_t)S.row * a.sink_hs;
+    const uint16_t* rk = a.res_k + (int64_t)S.row * a.res_hs;
+    const uint16_t* rv = a.res_v + (int64_t)S.row * a.res_hs;
+    const uint16_t* pk = tok(sk, rk, 16 * t + r) + 32 * q4;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) T16.k[kb] = *reinterpret_cast<const u4*>(pk + 8 * kb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) T16.v[i] = *reinterpret_cast<const u4*>(tok(sv, rv, 16 * t + 4 * q4 + i) + 8 * r);
+  };
+  auto issue = [&](int v) {
+    S = segment(a, P, v, v1);
+    {
+      // the G query rows of (b, g), 16-byte chunk e by thread e, straight into
+      // LDS (wave w fills bytes [1024 w, 1024 w + 1024))
+      const uint8_t* qp = static_cast<const uint8_t*>(a.q) + ((int64_t)S.b * a.hq + S.g * G) * FD * esz;
+      if (tid < qchunks)
+        load_lds16(qp + 16 * tid, qst + 1024 * w);
+    }
+    {
+      const uint16_t* rh = a.rot16 + (j0 + r) * FD + 8 * q4;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        rqh[kb] = *reinterpret_cast<const u4*>(rh + 32 * kb);
+        rql[kb] = *reinterpret_cast<const u4*>(rh + FD * FD + 32 * kb);
+      }
+    }
+    nkw = S.k1 - S.k0 > w ? (S.k1 - S.k0 - w + FW - 1) / FW : 0;
+    kcodes = a.kc + (int64_t)S.row * a.k_hs;
+    vcodes = a.vc + (int64_t)S.row * a.v_hs;
+    knorm = a.kn + (int64_t)S.row * a.kn_hs;
+    vnorm = a.vn + (int64_t)S.row * a.vn_hs;
+    // wave WF16 requests its packed blocks after its fp16 tiles (their
+    // registers do not overlap)
+    if (!(w == WF16 && S.t1 > S.t0)) {
+      load_slot(B0, 0);
+      load_slot(B1, 1);
+    }
+  };
+  if (v0 < v1) issue(v0);
+
+  // ---- lookup tables (once per workgroup): each lane stores two replicas of
+  // its rows' entries per 16-byte store, lane-linear (a wave's store fills 4
+  // consecutive rows)
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t off = (uint32_t)(32 * w + 4 * k + (lane >> 4)) * 256 + 16 * (lane & 15);
+    const u4 kv = u4{(uint32_t)ke[k], (uint32_t)(ke[k] >> 32), (uint32_t)ke[k], (uint32_t)(ke[k] >> 32)};
+    const u4 vv = u4{(uint32_t)ve[k], (uint32_t)(ve[k] >> 32), (uint32_t)ve[k], (uint32_t)(ve[k] >> 32)};
+    if constexpr (LY::NCP == 32) {
+      *reinterpret_cast<u4*>(smem + 0x10000u + off) = kv;
+      *reinterpret_cast<u4*>(smem + off) = vv;
+    } else {
+      *reinterpret_cast<u4*>(smem + off) = (lane & 15) >= 8 ? vv : kv;
+    }
+  }
+  // per-lane table address constants: byte 0 the replica offset, byte 2 the
+  // key table's base bit (NCP = 32)
+  uint32_t ck, cv;
+  constexpr uint32_t selk = LY::NCP == 32 ? 0x0C020000u : 0x0C0C0000u;
+  auto table_consts = [&]() {
+    if constexpr (LY::NCP == 32) {
+      ck = (uint32_t)(lane & 31) * 8 | 0x10000u;
+      cv = (uint32_t)(lane & 31) * 8;
+    } else {
+      ck = (uint32_t)(lane & 15) * 8;
+      cv = (uint32_t)(lane & 15) * 8 + 128;
+    }
+  };
+  auto kaddr = [&](uint32_t word, int byte) { return __builtin_amdgcn_perm(word, ck, selk | ((4u + byte) << 8)); };
+  auto vaddr = [&](uint32_t word, int byte) { return __builtin_amdgcn_perm(word, cv, 0x0C0C0000u | ((4u + byte) << 8)); };
+
+  // Online softmax of the NS scores of this lane (tokens A0..A3 and / or
+  // B0..B3 of the block, column r); returns the P^T operand (p * nv, high
+  // part or remainder by column, zero in the k-slots of the other tile) and
+  // rescales `acc` when a block's max exceeds the running max, or when p *
+  // nv would leave the fp16 range (the column exponent vx then grows).
+  auto softmax_pv = [&](float (&s)[NS], const float (&nv)[NS], f4 (&acc)[8], float& m_run, float& l_run,
+                        int& vx) {
+    float bm = s[0];
+#pragma unroll
+    for (int i = 1; i < NS; ++i) bm = fmaxf(bm, s[i]);
+    bm = rows_max(bm);
+    if (__builtin_amdgcn_ballot_w64(bm > m_run) != 0) {
+      const float mnew = bm > m_run ? bm + RESCALE_MARGIN : m_run;
+      const float corr = fexp2(m_run - mnew);
+      l_run *= corr;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc[nb] *= corr;
+      m_run = mnew;
+    }
+    float pv[NS];
+    float pm = 0.f;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const float p = fexp2(s[i] - m_run);
+      l_run += p;
+      pv[i] = p * nv[i];
+      pm = fmaxf(pm, pv[i]);
+    }
+    if (__builtin_amdgcn_ballot_w64(pm * __builtin_amdgcn_ldexpf(1.f, -vx) > PV_LIMIT) != 0) {
+      const float cm = rows_max(pm * __builtin_amdgcn_ldexpf(1.f, -vx));
+      const int d = cm > PV_LIMIT ? (int)ceilf(log2f(cm / PV_LIMIT)) : 0;
+      const float f = __builtin_amdgcn_ldexpf(1.f, -d);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc[nb] *= f;
+      vx += d;
+    }
+    const float down = __builtin_amdgcn_ldexpf(1.f, -vx);
+    uint32_t dd[NS / 2];
+#pragma unroll
+    for (int j = 0; j < NS / 2; ++j) {
+      const float p0 = pv[2 * j] * down, p1 = pv[2 * j + 1] * down;
+      const hx2 h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
+      const float e0 = fmaf(-partf, (float)h[0], p0);
+      const float e1 = fmaf(-partf, (float)h[1], p1);
+      dd[j] = pk_rtz(e0, e1);
+    }
+    u4 pb;
+    if constexpr (TS == 2) {
+      pb[0] = tile ? 0u : dd[0];
+      pb[1] = tile ? 0u : dd[1];
+      pb[2] = tile ? dd[0] : 0u;
+      pb[3] = tile ? dd[1] : 0u;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pb[j] = dd[j];
+    }
+    return as_h8(pb);
+  };
+
+  // A wave's state -> one LDS row per head [sums 128 | m | l]: the two fp16
+  // parts of a (tile, head) meet through `partner`; for TS == 2 the two tiles
+  // of a head (columns r and r ^ 8) are merged at their common max by a
+  // rotation by 8, and the high-part column of tile 0 writes the row.
+  auto to_rows = [&](f4 (&acc)[8], float m_run, float l_run, int vx, float* rows) {
+    l_run = rows_sum(l_run);
+    float tsc = __builtin_amdgcn_ldexpf(1.f, vx);
+    if constexpr (TS == 2) {
+      const float m2 = fmaxf(m_run, row_ror<8>(m_run));
+      const float t = fexp2(m_run - m2);
+      tsc *= t;
+      l_run *= t;
+      l_run += row_ror<8>(l_run);
+      m_run = m2;
+    }
+    float* cm = rows + hd * LY::CMS;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float vr[8];
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        float x = (acc[nb][i] + partner<G>(acc[nb][i])) * tsc;
+        if constexpr (TS == 2) x += row_ror<8>(x);
+        vr[nb] = x;
+      }
+      if (writer && tile == 0) {
+        float* d = cm + 32 * q4 + 8 * i;
+        *reinterpret_cast<float4*>(d) = make_float4(vr[0], vr[1], vr[2], vr[3]);
+        *reinterpret_cast<float4*>(d + 4) = make_float4(vr[4], vr[5], vr[6], vr[7]);
+      }
+    }
+    if (q4 == 0 && writer && tile == 0) *reinterpret_cast<float2*>(cm + FD) = make_float2(m_run, l_run);
+  };
+
+  const float vsc = a.vscale;
+  uint8_t* nst = smem + LY::nst + w * 256;  // this wave's norm staging: [key norms 32][value norms 32]
+
+  for (int v = v0; v < v1;) {
+    rederive();
+    const bool has16 = S.t1 > S.t0;
+    __syncthreads();
+
+    // ---- query rotation: D[h][n] = sum_i q[h][i] R[j0 + n][i] on MFMA (q
+    // high part x R high part + q high x R remainder + q remainder x R high),
+    // written (times qscale, and 2^-qe per head for very large queries) as
+    // fp16 high part / remainder straight into the score B-operand layout
+    // [head][part][q4][s][8 halves]: dim j = 32*q4 + 4*s + e sits at halves
+    // (e & 1) + 4*(e >> 1) and + 2
+    float qe_scale;  // 2^qe of this lane's column head: multiplies its scores
+    {
+      // dims 32 kb + 8 q4 .. + 8 of query head min(r, G - 1) (the A operand
+      // rows), as float
+      float x[4][8];
+      {
+        const uint8_t* qr = qst + (uint32_t)min(r, G - 1) * FD * esz;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const int d = 32 * kb + 8 * q4;
+          if (a.q_dtype == TQ_F32) {
+            const float4 u0 = *reinterpret_cast<const float4*>(qr + 4 * d);
+            const float4 u1 = *reinterpret_cast<const float4*>(qr + 4 * d + 16);
+            x[kb][0] = u0.x; x[kb][1] = u0.y; x[kb][2] = u0.z; x[kb][3] = u0.w;
+            x[kb][4] = u1.x; x[kb][5] = u1.y; x[kb][6] = u1.z; x[kb][7] = u1.w;
+          } else {
+            const u4 u = *reinterpret_cast<const u4*>(qr + 2 * d);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const uint32_t hb = (u[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+              x[kb][i] = a.q_dtype == TQ_BF16 ? __uint_as_float(hb << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+            }
+          }
+        }
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fmaf(x[kb][i], x[kb][i], ss);
+      // the query norm of head r (4 lanes hold its 128 dims) bounds every
+      // rotated coordinate: the power of two that keeps the operands in fp16
+      // range
+      ss = rows_sum(ss);
+      const float qn = sqrtf(ss) * a.qscale;
+      const int qe = qn > Q_LIMIT ? (int)ceilf(log2f(qn / Q_LIMIT)) : 0;  // lanes r: head r
+      const float qdown = __builtin_amdgcn_ldexpf(1.f, -qe);
+      half8 qo_hi[4], qo_lo[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float xs = x[kb][i] * qdown;
+          qo_hi[kb][i] = (_Float16)xs;
+          qo_lo[kb][i] = (_Float16)(xs - (float)qo_hi[kb][i]);
+        }
+      f4 dq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        dq = mfma(qo_hi[kb], as_h8(rqh[kb]), dq);
+        dq = mfma(qo_hi[kb], as_h8(rql[kb]), dq);
+        dq = mfma(qo_lo[kb], as_h8(rqh[kb]), dq);
+      }
+      // the first fp16 tile of wave WF16, requested once the rotation's
+      // registers are free (its latency overlaps the barrier)
+      if (has16 && w == WF16) load_tile(S.t0);
+      const int j = j0 + r, e = j & 3;
+      const uint32_t off = ((uint32_t)(j >> 5) * 8 + ((j >> 2) & 7)) * 16 + 2 * ((e & 1) + 4 * (e >> 1));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * q4 + i;
+        if (h < G) {
+          const float vq = dq[i] * a.qscale;
+          const _Float16 hi = (_Float16)vq, lo = (_Float16)(vq - (float)hi);
+          uint8_t* dh = smem + LY::qop + (uint32_t)(h * 2) * LY::QOPS + off;
+          *reinterpret_cast<_Float16*>(dh) = hi;
+          *reinterpret_cast<_Float16*>(dh + 4) = hi;
+          *reinterpret_cast<_Float16*>(dh + LY::QOPS) = lo;
+          *reinterpret_cast<_Float16*>(dh + LY::QOPS + 4) = lo;
+        }
+      }
+      // fp16 tokens: the (unscaled, 2^-qe) query in original space, step kb
+      // k-slot (q4, i) = dim 32*q4 + 8*kb + i, high part / remainder in
+      // [head][part][q4][kb][8 halves]; the lane holding dims 32*kb + 8*q4 ..
+      // of head r copies its operand halves there
+      if (has16 && w == 0 && r < G) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          uint8_t* dd = smem + LY::qfo + ((uint32_t)(r * 2 * 4 + kb) * 4 + q4) * 16;
+          *reinterpret_cast<half8*>(dd) = qo_hi[kb];
+          *reinterpret_cast<half8*>(dd + 4 * 4 * 16) = qo_lo[kb];
+        }
+      }
+      // lane h (column h, group 0) holds the exponent of head h
+      int qeh = 0;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const int xh = __builtin_amdgcn_readlane(qe, h);
+        qeh = hd == h ? xh : qeh;
+      }
+      qe_scale = __builtin_amdgcn_ldexpf(1.f, qeh);
+    }
+    __syncthreads();
+
+    // ---- fp16 tiles (wave WF16, original space): parked in LDS (`pre`) as
+    // [sums | m | l] per head
+    rederive();
+    if (has16 && w == WF16) {
+      half8 qf[4];
+      {
+        const uint8_t* src = smem + LY::qfo + ((uint32_t)(hd * 2 + (lo_part ? 1 : 0)) * 4 + q4) * 4 * 16;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) qf[kb] = *reinterpret_cast<const half8*>(src + 16 * kb);
+      }
+      f4 acc_o[8];
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc_o[nb] = f4{0.f, 0.f, 0.f, 0.f};
+      float m_o = M_INIT, l_o = 0.f;
+      int vx_o = 0;
+      const float sf = a.qscale * qe_scale;
+      for (int t = S.t0; t < S.t1; ++t) {
+        if (t != S.t0) load_tile(t);
+        // one 16-token score tile (tokens r); the k-slots of tokens 16.. of
+        // the P^T operand stay empty
+        f4 sA = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) sA = mfma(as_h8(T16.k[kb]), qf[kb], sA);
+        float sc[NS], ones[NS];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float full = (sA[i] + partner<G>(sA[i])) * sf;
+          sc[i] = tile == 0 && 16 * t + 4 * q4 + i < S.nf ? full : -INFINITY;  // the tile-1 columns see no fp16 token
+          if constexpr (NS == 8) sc[4 + i] = -INFINITY;
+        }
+#pragma unroll
+        for (int i = 0; i < NS; ++i) ones[i] = 1.f;
+        const half8 pb = softmax_pv(sc, ones, acc_o, m_o, l_o, vx_o);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
+          u4 bv;
+          bv[0] = __builtin_amdgcn_perm(T16.v[1][nb >> 1], T16.v[0][nb >> 1], sel);
+          bv[1] = __builtin_amdgcn_perm(T16.v[3][nb >> 1], T16.v[2][nb >> 1], sel);
+          bv[2] = 0u;
+          bv[3] = 0u;
+          acc_o[nb] = mfma(as_h8(bv), pb, acc_o[nb]);
+        }
+      }
+      to_rows(acc_o, m_o, l_o, vx_o, reinterpret_cast<float*>(smem + LY::pre));
+      load_slot(B0, 0);
+      load_slot(B1, 1);
+    }
+
+    // ---- packed blocks (rotated space)
+    rederive();
+    table_consts();
+    half8 qop[8];
+    {
+      const uint8_t* src = smem + LY::qop + (uint32_t)(hd * 2 + (lo_part ? 1 : 0)) * LY::QOPS + (uint32_t)q4 * 128;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) qop[s] = *reinterpret_cast<const half8*>(src + 16 * s);
+    }
+    f4 acc[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[nb] = f4{0.f, 0.f, 0.f, 0.f};
+    float m_run = M_INIT, l_run = 0.f;
+    int vx = 0;
+
+    // The norms go to the wave's staging row first, for every slot (also the
+    // skipped ones): the wait for a slot's loads then sits before the branch
+    // on both paths, and the counts of loads in flight stay exact.
+    auto stage = [&](const Blk& Bk) { *reinterpret_cast<float*>(nst + 4 * lane) = lane < 32 ? Bk.nk : Bk.nv * vsc; };
+    auto compute = [&](const Blk& Bk, int m) {
+      const int t0 = slot_t0(m);
+      const int tend = m < nkw ? S.comp : 0;
+      // key / value norms of the lane's tokens: tile `tile` (TS == 2) or both
+      float nk[NS], nv[NS];
+#pragma unroll
+      for (int t = 0; t < 2 / TS; ++t) {
+        const float4 k4 = *reinterpret_cast<const float4*>(nst + 64 * (t + tile) + 16 * q4);
+        const float4 v4 = *reinterpret_cast<const float4*>(nst + 128 + 64 * (t + tile) + 16 * q4);
+        nk[4 * t] = k4.x; nk[4 * t + 1] = k4.y; nk[4 * t + 2] = k4.z; nk[4 * t + 3] = k4.w;
+        nv[4 * t] = v4.x; nv[4 * t + 1] = v4.y; nv[4 * t + 2] = v4.z; nv[4 * t + 3] = v4.w;
+      }
+      // V^T operands (row = dim 8r + nb, k-slot pairs = token pairs of the
+      // lane), looked up first: they depend only on the codes, and their LDS
+      // latency then overlaps the scores and the softmax
+      u4 va[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t px = Bk.v[2 * j], py = Bk.v[2 * j + 1];  // token pair j
+        const u2 x0 = lds_u2(smem, vaddr(px, 0)), x1 = lds_u2(smem, vaddr(px, 1));
+        const u2 y0 = lds_u2(smem, vaddr(py, 0)), y1 = lds_u2(smem, vaddr(py, 1));
+        va[0][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x05040100u);
+        va[1][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x07060302u);
+        va[2][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x05040100u);
+        va[3][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x07060302u);
+        va[4][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x05040100u);
+        va[5][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x07060302u);
+        va[6][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x05040100u);
+        va[7][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x07060302u);
+      }
+      f4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const uint32_t wa = Bk.k0[s >> 1], wb = Bk.k1[s >> 1];
+        const int by = 2 * (s & 1);
+        const u2 ea0 = lds_u2(smem, kaddr(wa, by)), ea1 = lds_u2(smem, kaddr(wa, by + 1));
+        const u2 eb0 = lds_u2(smem, kaddr(wb, by)), eb1 = lds_u2(smem, kaddr(wb, by + 1));
+        sA = mfma(as_h8(u4{ea0[0], ea0[1], ea1[0], ea1[1]}), qop[s], sA);
+        sB = mfma(as_h8(u4{eb0[0], eb0[1], eb1[0], eb1[1]}), qop[s], sB);
+      }
+      float sc[NS];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (TS == 2) {
+          const float sv = tile ? sB[i] : sA[i];
+          sc[i] = (sv + partner<G>(sv)) * (nk[i] * qe_scale);
+        } else {
+          sc[i] = (sA[i] + partner<G>(sA[i])) * (nk[i] * qe_scale);
+          sc[4 + i] = (sB[i] + partner<G>(sB[i])) * (nk[4 + i] * qe_scale);
+        }
+      }
+      if constexpr (QB) {
+        // QJL key term of the lane's tokens (tile `tile`, or both for TS == 1)
+#pragma unroll
+        for (int t = 0; t < 2 / TS; ++t) {
+          sc[4 * t] += Bk.qb[t].x; sc[4 * t + 1] += Bk.qb[t].y; sc[4 * t + 2] += Bk.qb[t].z; sc[4 * t + 3] += Bk.qb[t].w;
+        }
+      }
+      if (t0 + 32 > tend) {  // uniform: only the last block of a sequence and empty slots mask
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+          if (t0 + 16 * (tile + (i >> 2)) + 4 * q4 + (i & 3) >= tend) sc[i] = -INFINITY;
+      }
+      if constexpr (QB) {
+        // the final scores of the compressed tokens, for the QJL value term
+        if (tend > 0 && !lo_part && c8 < G) {
+          float* so = a.scores + ((int64_t)S.row * G + hd) * a.qb_hs + t0 + 4 * q4;
+#pragma unroll
+          for (int t = 0; t < 2 / TS; ++t)
+            *reinterpret_cast<float4*>(so + 16 * (t + tile)) =
+                make_float4(sc[4 * t], sc[4 * t + 1], sc[4 * t + 2], sc[4 * t + 3]);
+        }
+      }
+      const half8 pb = softmax_pv(sc, nv, acc, m_run, l_run, vx);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc[nb] = mfma(as_h8(va[nb]), pb, acc[nb]);
+    };
+
+    // three blocks in registers: block m + 2 is requested as block m starts;
+    // slots past the wave's blocks read nothing (empty buffer ranges) and are
+    // skipped
+    for (int m = 0; m < nkw; m += 3) {
+      load_slot(B2, m + 2);
+      stage(B0);
+      compute(B0, m);
+      load_slot(B0, m + 3);
+      stage(B1);
+      if (m + 1 < nkw) compute(B1, m + 1);
+      load_slot(B1, m + 4);
+      stage(B2);
+      if (m + 2 < nkw) compute(B2, m + 2);
+    }
+
+    // ---- combine the waves (and the parked fp16 tiles) into the segment's
+    // partial: [M, L, has_orig, 0, rotated sum / L, original-space sum / L]
+    rederive();
+    to_rows(acc, m_run, l_run, vx, reinterpret_cast<float*>(smem + LY::cmb) + w * G * LY::CMS);
+    __syncthreads();
+    {
+      const float* cms = reinterpret_cast<const float*>(smem + LY::cmb);
+      const float* pr = reinterpret_cast<const float*>(smem + LY::pre);
+      float* part = a.part + (int64_t)v * G * PPS;
+      for (int e = tid; e < G * FD; e += FT) {
+        const int h = e / FD, jj = e % FD;
+        float M = has16 ? pr[h * LY::CMS + FD] : M_INIT;
+#pragma unroll
+        for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, cms[(ww * G + h) * LY::CMS + FD]);
+        float O = 0.f, Lt = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < FW; ++ww) {
+          const float* rw = cms + (ww * G + h) * LY::CMS;
+          const float sc = fexp2(rw[FD] - M);
+          O = fmaf(sc, rw[jj], O);
+          Lt = fmaf(sc, rw[FD + 1], Lt);
+        }
+        float Oo = 0.f;
+        if (has16) {
+          const float so = fexp2(pr[h * LY::CMS + FD] - M);
+          Oo = so * pr[h * LY::CMS + jj];
+          Lt = fmaf(so, pr[h * LY::CMS + FD + 1], Lt);
+        }
+        const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+        part[h * PPS + P_OUT + jj] = O * inv;
+        if (has16) part[h * PPS + P_OUT + FD + jj] = Oo * inv;
+        if (jj == 0) *reinterpret_cast<float4*>(part + h * PPS) = make_float4(M, Lt, has16 ? 1.f : 0.f, 0.f);
+      }
+      // the other chunks of the run: empty partials (sum 0, skipped by the merge)
+      for (int e = tid; e < (S.vend - v - 1) * G; e += FT)
+        *reinterpret_cast<float4*>(a.part + ((int64_t)(v + 1) * G + e) * PPS) = make_float4(M_INIT, 0.f, 0.f, 0.f);
+    }
+    // the next segment's loads (its query rotation waits for them)
+    const int vn = S.vend;
+    rederive();
+    if (vn < v1) issue(vn);
+    v = vn;
+  }
+}
+
+// ---------------------------------------------------------------- merge kernel
+// Query head hqi of sequence b, output dims [32 sl, 32 sl + 32): the partials
+// of (b, g) combined with w_p = 2^(M_p - M) L_p / L (M = max_p M_p, L = sum_p
+// 2^(M_p - M) L_p), then out = (sum_p w_p rot_p) @ R + sum_p w_p orig_p
+// (float32, R of the value codec). Thread t holds rotated dim t and, for
+// t < 32, original-space dim 32 sl + t; the loads of the first MB partials
+// are issued together with the headers and the R column slice.
 constexpr int MB = 32;  // partials per batch of loads
 
-// max / sum over the wave: DPP rotations within each 16-lane row, then the
-// four rows
+__device__ inline float block_max128(float v, float* sh) {
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  v = fmaxf(v, row_ror<1>(v));
+  v = rows_max(v);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(sh[0], sh[1]);
+}
+
+__device__ inline float block_sum128(float v, float* sh) {
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  v = rows_sum(v);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return sh[0] + sh[1];
+}
+
+template <int G>
+__global__ __launch_bounds__(128) void decode_merge_kernel(FastArgs a) {
+  __shared__ float wsh[MERGE_SLOTS];  // w_p (0 for empty partials)
+  __shared__ float hsh[MERGE_SLOTS];  // has_orig_p
+  __shared__ float rs[FD];
+  __shared__ float red[4][32];
+  __shared__ float rm[2], rl[2];
+  const int sl = blockIdx.x, hqi = blockIdx.y, b = blockIdx.z;
+  const int g = hqi / G, h = hqi % G;
+  const int tid = threadIdx.x;
+  const int jj = tid & 31, qq = tid >> 5;
+
+  // R[i][32 sl + jj] for the 32 rows i of this thread's quarter
+  float rv[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) rv[i] = a.vrot[(32 * qq + i) * FD + 32 * sl + jj];
+
+  const Plan P = make_plan(a);
+  const Loc L = locate(a, P, b, true);
+  const int s0 = L.Nb + g * L.nb, cnt = L.nb;
+  const float* pp = a.part + ((int64_t)s0 * G + h) * PPS;  // partial p at pp + p * G * PPS
+  const int64_t pst = (int64_t)G * PPS;
+  const int last = max(cnt - 1, 0);
+  float x[MB], xo[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    x[i] = pp[min(i, last) * pst + P_OUT + tid];
+    xo[i] = pp[min(i, last) * pst + P_OUT + FD + 32 * sl + jj];
+  }
+  float4 hd0 = make_float4(M_INIT, 0.f, 0.f, 0.f);
+  if (tid < cnt) hd0 = *reinterpret_cast<const float4*>(pp + tid * pst);
+
+  // the global max over the partials with a sum (headers past 128 in a loop)
+  float m = hd0.y > 0.f ? hd0.x : M_INIT;
+  for (int p = tid + 128; p < cnt; p += 128) {
+    const float2 hh = *reinterpret_cast<const float2*>(pp + p * pst);
+    if (hh.y > 0.f) m = fmaxf(m, hh.x);
+  }
+  const float M = block_max128(m, rm);
+  float ls = 0.f;
+  const int cpad = (cnt + MB - 1) / MB * MB;  // weights past cnt are zero
+  for (int p = tid; p < cpad; p += 128) {
+    float4 hh = make_float4(M_INIT, 0.f, 0.f, 0.f);
+    if (p < cnt) hh = p == tid ? hd0 : *reinterpret_cast<const float4*>(pp + p * pst);
+    const float wp = hh.y > 0.f ? fexp2(hh.x - M) * hh.y : 0.f;
+    wsh[p] = wp;
+    hsh[p] = hh.y > 0.f ? hh.z : 0.f;
+    ls += wp;
+  }
+  const float Ls = block_sum128(ls, rl);  // its barrier also publishes wsh / hsh
+  const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+  float acc = 0.f, acco = 0.f;
+  for (int p0 = 0; p0 < cnt; p0 += MB) {
+    if (p0 > 0) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        x[i] = pp[min(p0 + i, last) * pst + P_OUT + tid];
+        xo[i] = pp[min(p0 + i, last) * pst + P_OUT + FD + 32 * sl + jj];
+      }
+    }
+    // branch-free: values of empty partials (weight 0) and of partials
+    // without an original-space part are replaced by 0 (they may hold
+    // anything, NaN included)
+#pragma unroll
+    for (int i = 0; i < MB; i += 4) {
+      const float4 w4 = *reinterpret_cast<const float4*>(wsh + p0 + i);
+      const float4 h4 = *reinterpret_cast<const float4*>(hsh + p0 + i);
+      const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, hv[4] = {h4.x, h4.y, h4.z, h4.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc = fmaf(wv[u], wv[u] != 0.f ? x[i + u] : 0.f, acc);
+        acco = fmaf(wv[u], hv[u] != 0.f ? xo[i + u] : 0.f, acco);
+      }
+    }
+  }
+  rs[tid] = acc * inv;
+  __syncthreads();
+  float o = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) o = fmaf(rs[32 * qq + i], rv[i], o);
+  red[qq][jj] = o;
+  __syncthreads();
+  if (tid < 32)
+    a.out[((int64_t)b * a.hq + hqi) * FD + 32 * sl + tid] =
+        (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]) + acco * inv;
+  if (a.ml && sl == 0 && tid == 0) {
+    a.ml[((int64_t)b * a.hq + hqi) * 2] = M;
+    a.ml[((int64_t)b * a.hq + hqi) * 2 + 1] = Ls;
+  }
+}
+
+// ------------------------------------------------ merge of original-space partials
+// (the dense kernel's): one wave per (query head, half of the dims); lane p +
+// 64k holds the header of partial p + 64k, lane j sums dim 64 * half + j.
 __device__ inline float wave_max(float v) {
   v = fmaxf(v, row_ror<8>(v));
   v = fmaxf(v, row_ror<4>(v));
@@ -199,9 +1088,15 @@ __device__ inline float wave_sum(float v) {
   return rows_sum(v);
 }
 
+struct OrigMergeArgs {
+  const float* part;
+  float* out;
+  int nwg, hq, hkv;
+};
+
 template <int G>
-__global__ __launch_bounds__(64) void fast_merge_kernel(FastArgs a) {
-  __shared__ __align__(16) float wsh[MAXWG];  // w_p, written and read back by the one wave
+__global__ __launch_bounds__(64) void orig_merge_kernel(OrigMergeArgs a) {
+  __shared__ __align__(16) float wsh[FAST_MAX_WG];  // w_p, written and read back by the one wave
   const int half = blockIdx.x, hqi = blockIdx.y, b = blockIdx.z;
   const int g = hqi / G, h = hqi % G;
   const int lane = threadIdx.x;
@@ -210,12 +1105,10 @@ __global__ __launch_bounds__(64) void fast_merge_kernel(FastArgs a) {
   const float* pall = a.part + (int64_t)(b * a.hkv + g) * np * pstride + h * PS;  // partial p at pall + p*pstride
   const int dim = 64 * half + lane;
 
-  // headers (partials past np re-read the last one and are masked), then the
-  // first batch of outputs
-  static_assert(MAXWG == 256 && MB == 32, "merge register layout");
-  float2 hd[MAXWG / 64];
+  static_assert(FAST_MAX_WG == 256 && MB == 32, "merge register layout");
+  float2 hd[FAST_MAX_WG / 64];
 #pragma unroll
-  for (int k = 0; k < MAXWG / 64; ++k)
+  for (int k = 0; k < FAST_MAX_WG / 64; ++k)
     hd[k] = *reinterpret_cast<const float2*>(pall + min(lane + 64 * k, np - 1) * pstride);
   float x[MB];
 #pragma unroll
@@ -223,20 +1116,20 @@ __global__ __launch_bounds__(64) void fast_merge_kernel(FastArgs a) {
 
   float m = M_INIT;
 #pragma unroll
-  for (int k = 0; k < MAXWG / 64; ++k)
+  for (int k = 0; k < FAST_MAX_WG / 64; ++k)
     if (lane + 64 * k < np) m = fmaxf(m, hd[k].x);
   m = wave_max(m);
-  float w[MAXWG / 64];
+  float wgt[FAST_MAX_WG / 64];
   float l = 0.f;
 #pragma unroll
-  for (int k = 0; k < MAXWG / 64; ++k) {
-    w[k] = lane + 64 * k < np ? fexp2(hd[k].x - m) * hd[k].y : 0.f;
-    l += w[k];
+  for (int k = 0; k < FAST_MAX_WG / 64; ++k) {
+    wgt[k] = lane + 64 * k < np ? fexp2(hd[k].x - m) * hd[k].y : 0.f;
+    l += wgt[k];
   }
   l = wave_sum(l);
   const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-  for (int k = 0; k < MAXWG / 64; ++k) wsh[lane + 64 * k] = w[k];  // zero past np
+  for (int k = 0; k < FAST_MAX_WG / 64; ++k) wsh[lane + 64 * k] = wgt[k];  // zero past np
 
   float acc = 0.f;
   for (int p0 = 0;; p0 += MB) {
@@ -253,651 +1146,67 @@ __global__ __launch_bounds__(64) void fast_merge_kernel(FastArgs a) {
     for (int i = 0; i < MB; ++i) x[i] = pall[min(p0 + MB + i, np - 1) * pstride + P_OUT + dim];
   }
   a.out[((int64_t)b * a.hq + hqi) * FD + dim] = acc * inv;
-  if (a.ml && half == 0 && lane == 0) {
-    a.ml[((int64_t)b * a.hq + hqi) * 2] = m;
-    a.ml[((int64_t)b * a.hq + hqi) * 2 + 1] = l;
-  }
 }
 
-// The compressed blocks of one wave: loads issued at kernel start (lane r, q4)
-struct Blk {
-  u4 k0, k1;      // key codes of tokens t0 + r and t0 + 16 + r, bytes 16*q4 ..
-  uint32_t v[8];  // value code halfword r of tokens A0..A3 (t0 + 4q4 + i), B0..B3 (t0 + 16 + 4q4 + i)
-  float nk, nv;   // key / value norm of token t0 + (lane & 31)
-};
-
-// Raw buffer over `bytes` bytes at p (stride 0): loads past the end read zero.
-__device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+// ---------------------------------------------------------------- host side
+void fast_plan_host(int batch, int hkv, int max_comp, int max_sink, int max_res, bool uniform, int cus, int& nwg,
+                    int& chunks, int& vmax) {
+  const int64_t pb = (max_comp + 31) / 32;
+  const int64_t W = pb > 0 ? pb : (max_sink + max_res > 0 ? 1 : 0);
+  const int64_t U = (int64_t)batch * hkv * W;
+  int64_t n = (U + 7) / 8;  // at least one unit per wave
+  if (n < 1) n = 1;
+  if (n > cus) n = cus;
+  nwg = (int)n;
+  chunks = uniform ? 1 : 8;
+  vmax = chunks * nwg + batch * hkv;
 }
 
-template <int G, bool QB = false>
-__global__ __launch_bounds__(FT) void fast_decode_kernel(FastArgs a) {
-  __shared__ __align__(16) uint8_t smem[Layout::total];
-
-  const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 15, q4 = lane >> 4;
-  const int row = b * a.hkv + g;
-  const int j0 = 16 * w;  // output-dim tile of this wave for the query rotation
-  constexpr int TS = G <= 4 ? 2 : 1;  // tiles sharing the columns
-  constexpr int NS = 8 / TS;           // scores per lane per block
-  const int tile = TS == 2 ? r >> 3 : 0;  // tile of column r (TS == 2)
-  const int c8 = r & 7;
-  const int hd = TS == 2 ? (c8 < 4 ? c8 : 7 - c8) % G : c8;  // query head of column r
-  const bool lo_part = TS == 2 ? c8 >= 4 : r >= 8;          // column holds the fp16 remainder
-  const float partf = lo_part ? 1.f : 0.f;
-  const bool writer = !lo_part && c8 < G;  // one column per (tile, head) writes the combine rows
-
-  // All kernel arguments the set-up needs are loaded in one batch of scalar
-  // loads and waited for once (a branch on an argument would otherwise split
-  // them into dependent round trips).
-  {
-    const void* p0 = a.comp_len_b; const void* p1 = a.sink_len_b;
-    const void* p2 = a.res_len_b; const void* p3 = a.res_start_b;
-    const void* p4 = a.kc; const void* p5 = a.kn; const void* p6 = a.vc; const void* p7 = a.vn;
-    const void* p8 = a.q; const void* p9 = a.rot16; const void* p10 = a.kcen; const void* p11 = a.vcen;
-    const void* p12 = a.sink_k; const void* p13 = a.sink_v; const void* p14 = a.res_k; const void* p15 = a.res_v;
-    const int64_t s0 = a.k_hs, s1 = a.kn_hs, s2 = a.v_hs, s3 = a.vn_hs, s4 = a.sink_hs, s5 = a.res_hs;
-    const int i0 = a.max_comp, i1 = a.max_sink, i2 = a.max_res, i3 = a.res_start0, i4 = a.bpw, i5 = a.hkv,
-              i6 = a.hq, i7 = a.q_dtype, i8 = a.fpw, i9 = a.res_cap;
-    asm volatile("" ::"s"(p0), "s"(p1), "s"(p2), "s"(p3), "s"(p4), "s"(p5), "s"(p6), "s"(p7), "s"(p8), "s"(p9),
-                 "s"(p10), "s"(p11), "s"(p12), "s"(p13), "s"(p14), "s"(p15), "s"(s0), "s"(s1), "s"(s2), "s"(s3),
-                 "s"(s4), "s"(s5), "s"(i0), "s"(i1), "s"(i2), "s"(i3), "s"(i4), "s"(i5), "s"(i6), "s"(i7), "s"(i8),
-                 "s"(i9));
-  }
-  const int comp = a.comp_len_b ? a.comp_len_b[b] : a.max_comp;
-  const int sink = a.sink_len_b ? a.sink_len_b[b] : a.max_sink;
-  const int res = a.res_len_b ? a.res_len_b[b] : a.max_res;
-  const int rstart = a.res_start_b ? a.res_start_b[b] : a.res_start0;
-  const int nbc = (comp + 31) >> 5;
-  const int blk0 = c * a.bpw, blk1 = min(blk0 + a.bpw, nbc);
-  const int f0 = c * a.fpw, nf = max(0, min(a.fpw, sink + res - f0));  // fp16 tokens [f0, f0 + nf)
-
-  // ---- set-up loads: centroids, R rows, q and the staged fp16 tokens, issued
-  // before any compressed block so this small set-up data is not queued
-  // behind a GPU-wide flood of block loads. All loads are issued
-  // unconditionally (past the data, from valid addresses) so the compiler's
-  // memory-counter waits stay exact.
-  // table centroids of this lane (lane group qg of the table build): key
-  // centroids 4m + qg, value centroid qg; the others the build needs are
-  // uniform
-  const int qg = lane >> 4;
-  float kcq[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) kcq[m] = a.kcen[4 * m + qg];
-  const float vcq = a.vcen[qg];
-  // R rows j0 + n as MFMA B operands (k-slot (q4, i) of step kb = dim 32*kb + 8*q4 + i),
-  // fp16 high part and remainder precomputed by the codec
-  u4 rqh[4], rql[4];
-  {
-    const uint16_t* rh = a.rot16 + (j0 + r) * FD + 8 * q4;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      rqh[kb] = *reinterpret_cast<const u4*>(rh + 32 * kb);
-      rql[kb] = *reinterpret_cast<const u4*>(rh + FD * FD + 32 * kb);
-    }
-  }
-  // the G query rows of this kv head, staged in LDS as given: 16-byte chunk e
-  // (threads past the rows re-read chunk 0)
-  const int esz = a.q_dtype == TQ_F32 ? 4 : 2;
-  const int qchunks = G * FD * esz / 16;
-  u4 qld;
-  {
-    const uint8_t* qp = static_cast<const uint8_t*>(a.q) + ((int64_t)b * a.hq + g * G) * FD * esz;
-    const int e = tid < qchunks ? tid : 0;
-    qld = *reinterpret_cast<const u4*>(qp + 16 * e);
-  }
-  // fp16 tokens of this workgroup: 512 chunks of 16 bytes, chunk e = tid =
-  // token slot e >> 5, keys ((e >> 4) & 1 == 0) or values, bytes 16*(e & 15)
-  // of the row
-  u4 fst;
-  {
-    {
-      const int e = tid;
-      const int u = f0 + min(e >> 5, max(nf - 1, 0));  // token of the [sink | residual] list
-      const bool is_v = (e >> 4) & 1;
-      const uint16_t* src;
-      if (nf == 0) {
-        src = a.rot16;  // nothing staged: a dummy read
-      } else if (u < sink) {
-        src = static_cast<const uint16_t*>(is_v ? a.sink_v : a.sink_k) + (int64_t)row * a.sink_hs + (int64_t)u * FD;
-      } else {
-        int sl = rstart + (u - sink);  // ring slot (rstart + t < 2 * res_cap)
-        sl = sl >= a.res_cap ? sl - a.res_cap : sl;
-        src = static_cast<const uint16_t*>(is_v ? a.res_v : a.res_k) + (int64_t)row * a.res_hs + (int64_t)sl * FD;
-      }
-      fst = *reinterpret_cast<const u4*>(src + 8 * (e & 15));
-    }
-  }
-  // ---- loads of the compressed blocks of this wave: blocks blk0 + w + 8k.
-  // Buffer loads over the tokens [t0, comp) of the row: bytes past the
-  // sequence read as zero (those tokens are masked), slots past the wave's
-  // blocks re-read block 0 and are masked.
-  const bool has_comp = comp > 0;
-  const uint8_t* kcodes = has_comp ? a.kc + (int64_t)row * a.k_hs : nullptr;
-  const uint8_t* vcodes = has_comp ? a.vc + (int64_t)row * a.v_hs : nullptr;
-  const float* knorm = has_comp ? a.kn + (int64_t)row * a.kn_hs : nullptr;
-  const float* vnorm = has_comp ? a.vn + (int64_t)row * a.vn_hs : nullptr;
-  auto slot_t0 = [&](int k) {
-    const int blk = blk0 + w + FW * k;
-    return blk < blk1 ? blk << 5 : 0;
-  };
-  // lane byte offsets within a block: key bytes 16*q4 .. of token r (token
-  // 16 + r at +1024); value halfword r of token 4*q4 (token 4*q4 + i at
-  // +32 i, token 16 + 4*q4 + i at +512 + 32 i); norm of token lane & 31
-  const int ko = r * 64 + 16 * q4;
-  const int vo = q4 * 128 + 2 * r;
-  const int no = (lane & 31) * 4;
-  Blk B[NPW];
-  auto load_slot = [&](int k) {
-    const int t0 = slot_t0(k);
-    const int n = has_comp ? comp - t0 : 0;  // tokens readable from t0 on
-    const __amdgpu_buffer_rsrc_t rk = rsrc(kcodes + (int64_t)t0 * 64, n * 64);
-    const __amdgpu_buffer_rsrc_t rv = rsrc(vcodes + (int64_t)t0 * 32, n * 32);
-    const __amdgpu_buffer_rsrc_t rkn = rsrc(knorm + t0, n * 4);
-    const __amdgpu_buffer_rsrc_t rvn = rsrc(vnorm + t0, n * 4);
-    B[k].k0 = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0);
-    B[k].k1 = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 1024, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      B[k].v[i] = __builtin_amdgcn_raw_buffer_load_b16(rv, vo + (i < 4 ? 32 * i : 512 + 32 * (i - 4)), 0, 0);
-    B[k].nk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rkn, no, 0, 0));
-    B[k].nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvn, no, 0, 0));
-  };
-  // block 0 is requested right behind the set-up loads: waiting for those
-  // does not wait for it
-  load_slot(0);
-  // ---- tables:
-  // key byte e -> (c_hi[e&15], c_hi[e>>4], c_lo[e&15], c_lo[e>>4]) fp16
-  // value byte e -> (c[e&3], c[(e>>2)&3], c[(e>>4)&3], c[(e>>6)&3]) fp16
-  // Store k of wave w fills rows 4s .. 4s + 3 (s = 8w + k) of a table with one
-  // 16-byte store (two replicas) per lane, lane-linear and so conflict-free:
-  // lane l writes entry e = 4s + (l >> 4), replicas 2(l & 15) and 2(l & 15) + 1.
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int sx = 8 * w + k;             // uniform
-    const float ca = kcq[k & 3];           // c[e & 15], e & 15 = 4 (k & 3) + qg
-    const float cb = ld_uniform(a.kcen, sx >> 2);  // c[e >> 4]
-    const float ha = (float)(_Float16)ca, hb = (float)(_Float16)cb;
-    u4 ke;
-    ke[0] = pack_h2(ca, cb);
-    ke[1] = pack_h2(ca - ha, cb - hb);
-    ke[2] = ke[0];
-    ke[3] = ke[1];
-    *reinterpret_cast<u4*>(smem + Layout::klut + sx * 1024 + lane * 16) = ke;
-    u4 ve;
-    ve[0] = pack_h2(vcq, ld_uniform(a.vcen, k & 3));
-    ve[1] = pack_h2(ld_uniform(a.vcen, (sx >> 2) & 3), ld_uniform(a.vcen, sx >> 4));
-    ve[2] = ve[0];
-    ve[3] = ve[1];
-    *reinterpret_cast<u4*>(smem + Layout::vlut + sx * 1024 + lane * 16) = ve;
-  }
-  if (tid < qchunks) *reinterpret_cast<u4*>(smem + Layout::qst + 16 * tid) = qld;
-  // staged fp16 tokens: [slot][keys | values][272-byte row]
-  *reinterpret_cast<u4*>(smem + Layout::f16s + (tid >> 5) * (2 * FROW) + ((tid >> 4) & 1) * FROW + 16 * (tid & 15)) = fst;
-  __syncthreads();
-
-  // block 1 once the tables are built; block k + 2 as slot k starts
-  load_slot(1);
-
-
-  // q rows as MFMA A operands (row r = query head min(r, G-1), k-slots = dims
-  // 32*kb + 8*q4 ..): fp16 high part and remainder
-  half8 qo_hi[4], qo_lo[4];
-  {
-    const uint8_t* qr = smem + Layout::qst + (uint32_t)min(r, G - 1) * FD * esz;
-    if (a.q_dtype == TQ_F16) {
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        qo_hi[kb] = *reinterpret_cast<const half8*>(qr + (32 * kb + 8 * q4) * 2);
-        qo_lo[kb] = half8{};
-      }
-    } else {
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int d = 32 * kb + 8 * q4 + i;
-          const float x = a.q_dtype == TQ_F32 ? *reinterpret_cast<const float*>(qr + 4 * d)
-                                              : __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(qr + 2 * d) << 16);
-          const _Float16 hx = (_Float16)x;
-          qo_hi[kb][i] = hx;
-          qo_lo[kb][i] = (_Float16)(x - (float)hx);
-        }
-      }
-    }
-  }
-  // ---- q_rot tile: D[h][n] = sum_i q[h][i] R[j0+n][i]   (B[k=i][n] = R[j0+n][i]),
-  // written (times qscale) as fp16 high part / remainder straight into the
-  // score B-operand layout [head][part][q4][s][8 halves]: dim j = 32*q4 + 4*s + e
-  // sits at halves (e & 1) + 4*(e >> 1) and + 2 (see the operand layout below)
-  {
-    f4 dq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      dq = mfma(qo_hi[kb], as_h8(rqh[kb]), dq);
-      dq = mfma(qo_hi[kb], as_h8(rql[kb]), dq);
-      dq = mfma(qo_lo[kb], as_h8(rqh[kb]), dq);
-    }
-    const int j = j0 + r, e = j & 3;
-    const uint32_t off = ((uint32_t)(j >> 5) * 8 + ((j >> 2) & 7)) * 16 + 2 * ((e & 1) + 4 * (e >> 1));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * q4 + i;
-      if (h < G) {
-        const float v = dq[i] * a.qscale;
-        const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
-        uint8_t* dh = smem + Layout::qop + (uint32_t)(h * 2) * QOPS + off;
-        *reinterpret_cast<_Float16*>(dh) = hi;
-        *reinterpret_cast<_Float16*>(dh + 4) = hi;
-        *reinterpret_cast<_Float16*>(dh + QOPS) = lo;
-        *reinterpret_cast<_Float16*>(dh + QOPS + 4) = lo;
-      }
-    }
-  }
-  // fp16 tokens use the (unscaled) q in original space as score B operands,
-  // step kb k-slot (q4, i) = dim 32*q4 + 8*kb + i: fp16 high part / remainder
-  // in [head][part][q4][kb][8 halves]; the lane holding dims 32*kb + 8*q4 ..
-  // of head r copies its operand halves there
-  if (w == 0 && r < G && nf > 0) {
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      uint8_t* d = smem + Layout::qfo + ((uint32_t)(r * 2 * 4 + kb) * 4 + q4) * 16;
-      *reinterpret_cast<half8*>(d) = qo_hi[kb];
-      *reinterpret_cast<half8*>(d + 4 * 4 * 16) = qo_lo[kb];
-    }
-  }
-  __syncthreads();
-
-  // ---- per-lane online softmax state of column r (head hd)
-  float m_run = M_INIT, l_run = 0.f;
-  float m_orig = M_INIT;  // running max the parked original-space partial refers to
-  f4 acc_r[8];            // rotated-space output accumulators
-
-  const uint32_t cp = (uint32_t)(lane & (NCP - 1)) * 8;  // replica offset within a table row
-  static_assert(Layout::klut == 0x10000 && Layout::vlut == 0, "table addresses are byte permutes");
-  const uint32_t cpk = cp | Layout::klut;
-  auto kaddr = [&](uint32_t word, int byte) {      // klut + (byte of word) * 256 + cp: bytes (cp, code byte, 1, 0)
-    return __builtin_amdgcn_perm(word, cpk, 0x0C020000u | ((4u + byte) << 8));
-  };
-  auto vaddr = [&](uint32_t word, int byte) {      // vlut + (byte of word) * 256 + cp
-    return Layout::vlut + __builtin_amdgcn_perm(word, cp, 0x0C0C0000u | ((4u + byte) << 8));
-  };
-
-  // Online softmax of the NS scores of this lane (tokens A0..A3 and / or
-  // B0..B3 of the block, column r), returns the P^T operand (p * nv, high
-  // part or remainder by column, zero in the k-slots of the other tile) and
-  // rescales `acc` when a block's max exceeds the running max.
-  auto softmax_pv = [&](float (&s)[NS], const float (&nv)[NS], f4 (&acc)[8]) {
-    float bm = s[0];
-#pragma unroll
-    for (int i = 1; i < NS; ++i) bm = fmaxf(bm, s[i]);
-    bm = rows_max(bm);
-    if (__builtin_amdgcn_ballot_w64(bm > m_run) != 0) {
-      const float mnew = bm > m_run ? bm + RESCALE_MARGIN : m_run;
-      const float corr = fexp2(m_run - mnew);
-      l_run *= corr;
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) acc[nb] *= corr;
-      m_run = mnew;
-    }
-    float pv[NS];
-#pragma unroll
-    for (int i = 0; i < NS; ++i) {
-      const float p = fexp2(s[i] - m_run);
-      l_run += p;
-      pv[i] = p * nv[i];
-    }
-    uint32_t d[NS / 2];
-#pragma unroll
-    for (int j = 0; j < NS / 2; ++j) {
-      const hx2 h = __builtin_amdgcn_cvt_pkrtz(pv[2 * j], pv[2 * j + 1]);
-      const float t0 = fmaf(-partf, (float)h[0], pv[2 * j]);
-      const float t1 = fmaf(-partf, (float)h[1], pv[2 * j + 1]);
-      d[j] = pk_rtz(t0, t1);
-    }
-    u4 pb;
-    if constexpr (TS == 2) {
-      pb[0] = tile ? 0u : d[0];
-      pb[1] = tile ? 0u : d[1];
-      pb[2] = tile ? d[0] : 0u;
-      pb[3] = tile ? d[1] : 0u;
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pb[j] = d[j];
-    }
-    return as_h8(pb);
-  };
-
-  // ---- the staged fp16 tokens (sink / residual ring, original space): wave
-  // WF16, before its compressed blocks
-  if (w == WF16 && nf > 0) {
-    half8 qf[4];
-    {
-      const uint8_t* src = smem + Layout::qfo + ((uint32_t)(hd * 2 + (partf != 0.f ? 1 : 0)) * 4 + q4) * 4 * 16;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) qf[kb] = *reinterpret_cast<const half8*>(src + 16 * kb);
-    }
-    f4 acc_o[8];
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc_o[nb] = f4{0.f, 0.f, 0.f, 0.f};
-    const uint8_t* fs = smem + Layout::f16s;
-    // one 16-token score tile (tokens r); the k-slots of tokens 16.. of the
-    // P^T operand stay empty
-    f4 sA = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const u4 kA = *reinterpret_cast<const u4*>(fs + r * (2 * FROW) + 64 * q4 + 16 * kb);
-      sA = mfma(as_h8(kA), qf[kb], sA);
-    }
-    float sc[NS], ones[NS];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float full = (sA[i] + partner<G>(sA[i])) * a.qscale;
-      sc[i] = tile == 0 && 4 * q4 + i < nf ? full : -INFINITY;  // the tile-1 columns see no fp16 token
-      if constexpr (NS == 8) sc[4 + i] = -INFINITY;
-    }
-#pragma unroll
-    for (int i = 0; i < NS; ++i) ones[i] = 1.f;
-    const half8 pb = softmax_pv(sc, ones, acc_o);
-    u4 vv[8];  // values: dims 8r .. 8r+7 of tokens A0..A3 (k-slots of B0..B3 zero)
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      vv[i] = i < 4 ? *reinterpret_cast<const u4*>(fs + (4 * q4 + i) * (2 * FROW) + FROW + 16 * r) : u4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
-      u4 bv;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = __builtin_amdgcn_perm(vv[2 * j + 1][nb >> 1], vv[2 * j][nb >> 1], sel);
-      acc_o[nb] = mfma(as_h8(bv), pb, acc_o[nb]);
-    }
-    // park the original-space partial (hi + lo columns summed) in LDS with the
-    // running max it refers to; later blocks only rescale it at the combine
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float vo[8];
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) vo[nb] = acc_o[nb][i] + partner<G>(acc_o[nb][i]);
-      if (writer && tile == 0) {
-        float* d = reinterpret_cast<float*>(smem + Layout::opk) + hd * FD + 32 * q4 + 8 * i;
-        *reinterpret_cast<float4*>(d) = make_float4(vo[0], vo[1], vo[2], vo[3]);
-        *reinterpret_cast<float4*>(d + 4) = make_float4(vo[4], vo[5], vo[6], vo[7]);
-      }
-    }
-    m_orig = m_run;
-  }
-
-  // B operands of the rotated-space scores, step s: k-slots (q4, i) hold
-  // q[d], q[d+1], q[d], q[d+1], q[d+2], q[d+3], q[d+2], q[d+3], d = 32*q4 + 4*s,
-  // matching the key table entry layout (hi pair, lo pair) of two code bytes;
-  // column r reads the high part (even r / G) or the remainder of head r % G.
-  half8 qop[8];
-  {
-    const uint8_t* src = smem + Layout::qop + (uint32_t)(hd * 2 + (partf != 0.f ? 1 : 0)) * QOPS + (uint32_t)q4 * 128;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qop[s] = *reinterpret_cast<const half8*>(src + 16 * s);
-  }
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) acc_r[nb] = f4{0.f, 0.f, 0.f, 0.f};
-
-  // R^T rows 16w + r as bf16 MFMA B operands of the inverse rotation (k-slot
-  // (q4, i) of step kb = rotated dim 32*kb + 8*q4 + i), high part and
-  // remainder; requested as the wave's last-but-one slot starts
-  u4 rth[4], rtl[4];
-  auto load_rt = [&]() {
-    const uint16_t* rt = a.rotT + (16 * w + r) * FD + 8 * q4;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      rth[kb] = *reinterpret_cast<const u4*>(rt + 32 * kb);
-      rtl[kb] = *reinterpret_cast<const u4*>(rt + FD * FD + 32 * kb);
-    }
-  };
-  static_assert(NPW >= 2, "two blocks in flight");
-
-  // ---- the compressed blocks of this wave (rotated space)
-  uint8_t* nst = smem + Layout::nst + w * 256;  // this wave's norm staging: [key norms 32][value norms 32]
-#pragma unroll
-  for (int k = 0; k < NPW; ++k) {
-    // every slot is computed (no branch between them, so the scheduler can
-    // overlap one block's lookups with the previous block's softmax); a slot
-    // past the wave's blocks masks all its tokens. Block k + 2 (or, past the
-    // last block, R^T) is requested as slot k starts, so two blocks stay in
-    // flight while slot k computes.
-    if (k + 2 < NPW) load_slot(k + 2);
-    if (k + 2 == NPW) load_rt();
-    const Blk& L = B[k];
-    const int t0 = slot_t0(k);
-    const int tend = blk0 + w + FW * k < blk1 ? comp : 0;
-    *reinterpret_cast<float*>(nst + 4 * lane) = lane < 32 ? L.nk : L.nv;
-    // key / value norms of the lane's tokens: tile `tile` (TS == 2) or both
-    float nk[NS], nv[NS];
-#pragma unroll
-    for (int t = 0; t < 2 / TS; ++t) {
-      const float4 k4 = *reinterpret_cast<const float4*>(nst + 64 * (t + tile) + 16 * q4);
-      const float4 v4 = *reinterpret_cast<const float4*>(nst + 128 + 64 * (t + tile) + 16 * q4);
-      nk[4 * t] = k4.x; nk[4 * t + 1] = k4.y; nk[4 * t + 2] = k4.z; nk[4 * t + 3] = k4.w;
-      nv[4 * t] = v4.x; nv[4 * t + 1] = v4.y; nv[4 * t + 2] = v4.z; nv[4 * t + 3] = v4.w;
-    }
-    // V^T operands (row = dim 8r + nb, k-slot pairs = token pairs of the
-    // lane), looked up first: they depend only on the codes, and their LDS
-    // latency then overlaps the scores and the softmax
-    u4 va[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t px = L.v[2 * j], py = L.v[2 * j + 1];  // token pair j
-      const u2 x0 = lds_u2(smem, vaddr(px, 0)), x1 = lds_u2(smem, vaddr(px, 1));
-      const u2 y0 = lds_u2(smem, vaddr(py, 0)), y1 = lds_u2(smem, vaddr(py, 1));
-      va[0][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x05040100u);
-      va[1][j] = __builtin_amdgcn_perm(y0[0], x0[0], 0x07060302u);
-      va[2][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x05040100u);
-      va[3][j] = __builtin_amdgcn_perm(y0[1], x0[1], 0x07060302u);
-      va[4][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x05040100u);
-      va[5][j] = __builtin_amdgcn_perm(y1[0], x1[0], 0x07060302u);
-      va[6][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x05040100u);
-      va[7][j] = __builtin_amdgcn_perm(y1[1], x1[1], 0x07060302u);
-    }
-    f4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const uint32_t wa = L.k0[s >> 1], wb = L.k1[s >> 1];
-      const int by = 2 * (s & 1);
-      const u2 ea0 = lds_u2(smem, kaddr(wa, by)), ea1 = lds_u2(smem, kaddr(wa, by + 1));
-      const u2 eb0 = lds_u2(smem, kaddr(wb, by)), eb1 = lds_u2(smem, kaddr(wb, by + 1));
-      sA = mfma(as_h8(u4{ea0[0], ea0[1], ea1[0], ea1[1]}), qop[s], sA);
-      sB = mfma(as_h8(u4{eb0[0], eb0[1], eb1[0], eb1[1]}), qop[s], sB);
-    }
-    float sc[NS];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (TS == 2) {
-        const float sv = tile ? sB[i] : sA[i];
-        sc[i] = (sv + partner<G>(sv)) * nk[i];
-      } else {
-        sc[i] = (sA[i] + partner<G>(sA[i])) * nk[i];
-        sc[4 + i] = (sB[i] + partner<G>(sB[i])) * nk[4 + i];
-      }
-    }
-    if constexpr (QB) {
-      // QJL key term of the lane's tokens (tile `tile`, or both for TS == 1)
-      const float* qb = a.qjl_bias + ((int64_t)row * G + hd) * a.qb_hs + t0 + 4 * q4;
-#pragma unroll
-      for (int t = 0; t < 2 / TS; ++t) {
-        const float4 bb = *reinterpret_cast<const float4*>(qb + 16 * (t + tile));
-        sc[4 * t] += bb.x; sc[4 * t + 1] += bb.y; sc[4 * t + 2] += bb.z; sc[4 * t + 3] += bb.w;
-      }
-    }
-    if (t0 + 32 > tend) {  // uniform: only the last block of a sequence and empty slots mask
-#pragma unroll
-      for (int i = 0; i < NS; ++i)
-        if (t0 + 16 * (tile + (i >> 2)) + 4 * q4 + (i & 3) >= tend) sc[i] = -INFINITY;
-    }
-    if constexpr (QB) {
-      // the final scores of the compressed tokens, for the QJL value term
-      if (tend > 0 && !lo_part && c8 < G) {
-        float* so = a.scores + ((int64_t)row * G + hd) * a.qb_hs + t0 + 4 * q4;
-#pragma unroll
-        for (int t = 0; t < 2 / TS; ++t)
-          *reinterpret_cast<float4*>(so + 16 * (t + tile)) = make_float4(sc[4 * t], sc[4 * t + 1], sc[4 * t + 2], sc[4 * t + 3]);
-      }
-    }
-    const half8 pb = softmax_pv(sc, nv, acc_r);
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc_r[nb] = mfma(as_h8(va[nb]), pb, acc_r[nb]);
-  }
-
-  // ---- combine the 8 waves of this workgroup through LDS (the table region,
-  // free once every wave is past its blocks). The two fp16 parts of a (tile,
-  // head) meet through `partner`; for TS == 2 the two tiles of a head (columns
-  // r and r ^ 8) are then merged at their common max by a rotation by 8, and
-  // the high-part column of tile 0 writes the head's row.
-  l_run = rows_sum(l_run);
-  float tsc = 1.f;  // scale of this lane's tile state to the merged max
-  if constexpr (TS == 2) {
-    const float m2 = fmaxf(m_run, row_ror<8>(m_run));
-    tsc = fexp2(m_run - m2);
-    l_run *= tsc;
-    l_run += row_ror<8>(l_run);
-    m_run = m2;
-  }
-  __syncthreads();
-  float* cm = reinterpret_cast<float*>(smem + Layout::cmb) + (w * 8) * CMS;  // [wave][head][CMS]
-  float* cl = reinterpret_cast<float*>(smem + Layout::cml) + w * 32;        // [wave][head][4]
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float vr[8];
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      float x = acc_r[nb][i] + partner<G>(acc_r[nb][i]);
-      if constexpr (TS == 2) {
-        x *= tsc;
-        x += row_ror<8>(x);
-      }
-      vr[nb] = x;
-    }
-    if (writer && tile == 0) {
-      float* d = cm + hd * CMS + 32 * q4 + 8 * i;
-      *reinterpret_cast<float4*>(d) = make_float4(vr[0], vr[1], vr[2], vr[3]);
-      *reinterpret_cast<float4*>(d + 4) = make_float4(vr[4], vr[5], vr[6], vr[7]);
-    }
-  }
-  if (q4 == 0 && writer && tile == 0) *reinterpret_cast<float4*>(cl + 4 * hd) = make_float4(m_run, l_run, m_orig, 0.f);
-  __syncthreads();
-  // thread (head, dim): merge the 8 waves into the workgroup's rotated sum
-  // and original-space sum at the workgroup max M, both divided by the
-  // workgroup sum L; the rotated one goes to LDS as bf16 high part /
-  // remainder (A operand of the inverse rotation), the other as float
-  float* part = a.part + ((int64_t)row * a.nwg + c) * G * PS;
-  const bool wg_has_fp16 = nf > 0;
-  {
-    const float* cms = reinterpret_cast<const float*>(smem + Layout::cmb);
-    const float* cls = reinterpret_cast<const float*>(smem + Layout::cml);
-    const float* opk = reinterpret_cast<const float*>(smem + Layout::opk);
-    for (int e = tid; e < G * FD; e += FT) {
-      const int h = e / FD, j = e % FD;
-      float M = M_INIT;
-#pragma unroll
-      for (int ww = 0; ww < FW; ++ww) M = fmaxf(M, cls[ww * 32 + 4 * h]);
-      float sr = 0.f, L = 0.f;
-#pragma unroll
-      for (int ww = 0; ww < FW; ++ww) {
-        const float4 st = *reinterpret_cast<const float4*>(cls + ww * 32 + 4 * h);
-        const float sc = fexp2(st.x - M);
-        sr = fmaf(sc, cms[(ww * 8 + h) * CMS + j], sr);
-        L = fmaf(sc, st.y, L);
-      }
-      float so = 0.f;
-      if (wg_has_fp16) {
-        // original-space part of wave WF16, parked at its max then
-        const float mo = cls[WF16 * 32 + 4 * h + 2];
-        so = mo > M_INIT ? fexp2(mo - M) * opk[h * FD + j] : 0.f;
-      }
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      const float rn = sr * inv;
-      const __bf16 bh = (__bf16)rn;
-      const __bf16 bl = (__bf16)(rn - (float)bh);
-      uint16_t* ao = reinterpret_cast<uint16_t*>(smem + Layout::aop + h * AOPS) + j;
-      ao[0] = __builtin_bit_cast(uint16_t, bh);
-      ao[FD] = __builtin_bit_cast(uint16_t, bl);
-      reinterpret_cast<float*>(smem + Layout::onr)[h * FD + j] = so * inv;
-      if (j == 0) *reinterpret_cast<float4*>(part + h * PS) = make_float4(M, L, 0.f, 0.f);
-    }
-  }
-  __syncthreads();
-  // ---- inverse rotation, wave w: out[h][j] = sum_i rn[h][i] R[i][j] + on[h][j]
-  // for j in [16w, 16w + 16): A = rn (row = head min(r, G-1)), B = R^T rows
-  {
-    const uint8_t* src = smem + Layout::aop + (uint32_t)min(r, G - 1) * AOPS + (uint32_t)(8 * q4) * 2;
-    f4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0, d2 = d0;  // three independent MFMA chains
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const bf8 ah = *reinterpret_cast<const bf8*>(src + 64 * kb);
-      const bf8 al = *reinterpret_cast<const bf8*>(src + FD * 2 + 64 * kb);
-      d0 = mfma_bf(ah, as_b8(rth[kb]), d0);
-      d1 = mfma_bf(ah, as_b8(rtl[kb]), d1);
-      d2 = mfma_bf(al, as_b8(rth[kb]), d2);
-    }
-    const f4 d = d0 + (d1 + d2);
-    const int j = 16 * w + r;
-    const float* onr = reinterpret_cast<const float*>(smem + Layout::onr);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * q4 + i;
-      if (h < G) part[h * PS + P_OUT + j] = d[i] + onr[h * FD + j];
-    }
-  }
+void fast_uniform_plan(int batch, int hkv, int max_comp, int max_sink, int max_res, int nwg, int chunks, int& T,
+                       int& nu, int& V) {
+  const int64_t pb = (max_comp + 31) / 32;
+  const int64_t W = pb > 0 ? pb : (max_sink + max_res > 0 ? 1 : 0);
+  const int64_t U = (int64_t)batch * hkv * W;
+  const int64_t div = (int64_t)chunks * nwg;
+  int64_t t = (U + div - 1) / div;
+  if (t < 1) t = 1;
+  T = (int)((t + FW - 1) / FW * FW);
+  nu = (int)((W + T - 1) / T);
+  V = batch * hkv * nu;
 }
 
-size_t fast_smem_bytes() { return Layout::total; }
-
-template <int G>
-static void launch_g(const FastArgs& a, int batch, hipStream_t s) {
-  hipLaunchKernelGGL((fast_decode_kernel<G>), dim3(a.nwg, a.hkv, batch), dim3(FT), 0, s, a);
-  if (a.merge) hipLaunchKernelGGL((fast_merge_kernel<G>), dim3(2, a.hq, batch), dim3(64), 0, s, a);
+template <int G, bool QB>
+static void launch_g(const FastArgs& a, int merge, hipStream_t s) {
+  hipLaunchKernelGGL((decode_partials_kernel<G, QB>), dim3(a.nwg), dim3(FT), 0, s, a);
+  if (merge) hipLaunchKernelGGL((decode_merge_kernel<G>), dim3(4, a.hq, a.batch), dim3(128), 0, s, a);
 }
 
-int launch_fast_decode(const FastArgs& a, int G, int batch, hipStream_t s) {
-  switch (G) {
-    case 1: launch_g<1>(a, batch, s); break;
-    case 2: launch_g<2>(a, batch, s); break;
-    case 4: launch_g<4>(a, batch, s); break;
-    default: launch_g<8>(a, batch, s); break;
-  }
-  return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
-template <int G>
-static void launch_gq(const FastArgs& a, int batch, hipStream_t s) {
-  hipLaunchKernelGGL((fast_decode_kernel<G, true>), dim3(a.nwg, a.hkv, batch), dim3(FT), 0, s, a);
-  if (a.merge) hipLaunchKernelGGL((fast_merge_kernel<G>), dim3(2, a.hq, batch), dim3(64), 0, s, a);
-}
-
-int launch_fast_decode_qjl(const FastArgs& a, int G, int batch, hipStream_t s) {
-  switch (G) {
-    case 1: launch_gq<1>(a, batch, s); break;
-    case 2: launch_gq<2>(a, batch, s); break;
-    case 4: launch_gq<4>(a, batch, s); break;
-    default: launch_gq<8>(a, batch, s); break;
+int launch_fast_decode(const FastArgs& a, int G, bool qb, int merge, hipStream_t s) {
+  if (a.chunks * a.nwg + 1 > MERGE_SLOTS) return -1;
+  switch (G * 2 + (qb ? 1 : 0)) {
+    case 2: launch_g<1, false>(a, merge, s); break;
+    case 3: launch_g<1, true>(a, merge, s); break;
+    case 4: launch_g<2, false>(a, merge, s); break;
+    case 5: launch_g<2, true>(a, merge, s); break;
+    case 8: launch_g<4, false>(a, merge, s); break;
+    case 9: launch_g<4, true>(a, merge, s); break;
+    case 16: launch_g<8, false>(a, merge, s); break;
+    case 17: launch_g<8, true>(a, merge, s); break;
+    default: return -1;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_partial_merge(float* part, int nwg, int G, int hq, int hkv, int batch, float* out, hipStream_t s) {
-  FastArgs a{};
-  a.part = part; a.nwg = nwg; a.hq = hq; a.hkv = hkv; a.out = out;
+  OrigMergeArgs a{part, out, nwg, hq, hkv};
   const dim3 grid(2, hq, batch);
   switch (G) {
-    case 1: hipLaunchKernelGGL((fast_merge_kernel<1>), grid, dim3(64), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((fast_merge_kernel<2>), grid, dim3(64), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((fast_merge_kernel<4>), grid, dim3(64), 0, s, a); break;
-    default: hipLaunchKernelGGL((fast_merge_kernel<8>), grid, dim3(64), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((orig_merge_kernel<1>), grid, dim3(64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((orig_merge_kernel<2>), grid, dim3(64), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((orig_merge_kernel<4>), grid, dim3(64), 0, s, a); break;
+    default: hipLaunchKernelGGL((orig_merge_kernel<8>), grid, dim3(64), 0, s, a); break;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
-
-// The kernel's LDS is static (Layout::total bytes); nothing to raise.
-int fast_set_attributes() { return 0; }
 
 }  // namespace tq

@@ -37,15 +37,14 @@ class DeviceCodec:
             raise ValueError(f"Unsupported bit-width: {bits}. Use 1, 2, 3, or 4.")
         self.device = device
         self.rotation = get_rotation_matrix(d, seed, device)
-        # MFMA operands of the decode kernels: fp16 high part and remainder of
-        # R (query rotation), bf16 high part and remainder of R^T (inverse
-        # rotation of the output), as 16-bit words
-        hi = self.rotation.half()
+        # MFMA operands of the K4/V2 decode kernels: fp16 high part and
+        # remainder of R (query rotation) and of R^T (inverse rotation), as
+        # 16-bit words
         rt = self.rotation.t().contiguous()
-        bhi = rt.bfloat16()
+        hi, hit = self.rotation.half(), rt.half()
         self.rotation_parts = torch.stack([
             hi.view(torch.int16), (self.rotation - hi.float()).half().view(torch.int16),
-            bhi.view(torch.int16), (rt - bhi.float()).bfloat16().view(torch.int16)]).contiguous()
+            hit.view(torch.int16), (rt - hit.float()).half().view(torch.int16)]).contiguous()
         self.c_hi, self.b_hi = get_codebook(d, self.bits_hi, device)
         self.c_lo, self.b_lo = get_codebook(d, self.bits_lo, device)
         self.qjl_m = qjl_m
@@ -59,14 +58,34 @@ class DeviceCodec:
             boundaries_hi=self.b_hi.data_ptr(), centroids_lo=self.c_lo.data_ptr(),
             boundaries_lo=self.b_lo.data_ptr(),
             qjl_proj=self.proj.data_ptr() if self.proj is not None else None,
-            qjl_m=qjl_m, reserved=0, rotation_parts=self.rotation_parts.data_ptr())
+            qjl_m=qjl_m, flags=0, rotation_parts=self.rotation_parts.data_ptr())
+        # host-side tables: the codebook by value and, for 2-bit codebooks,
+        # its exact fp16 copy (the K4/V2 decode kernels' value table)
+        cen = self.c_hi.detach().cpu().numpy().astype("float32")
+        lib = _lib.load()
+        _lib.check(lib.tq_codec_prepare(ctypes.byref(self.struct), cen.ctypes.data, len(cen)), "tq_codec_prepare")
+        # decode table of the K4/V2 kernels (4-bit keys / 2-bit values), in device memory
+        self.decode_table = None
+        if len(cen) in (4, 16):
+            import numpy as np
+            tab = np.zeros(256, np.uint64)
+            _lib.check(lib.tq_codec_decode_table(ctypes.byref(self.struct), tab.ctypes.data), "tq_codec_decode_table")
+            self.decode_table = torch.from_numpy(tab.view(np.int64)).to(device)
+            self.struct.decode_table = self.decode_table.data_ptr()
+        self._cen_host = cen
 
     @property
     def fractional(self) -> bool:
         return self.split < self.d
 
-    def ref(self):
-        return ctypes.byref(self.struct)
+    def ref(self, general_compress: bool = False):
+        """``tq_codec*`` of this codec; ``general_compress`` routes tq_compress
+        through the general kernel (a copy of the struct with the flag set)."""
+        if not general_compress:
+            return ctypes.byref(self.struct)
+        c = _lib.Codec.from_buffer_copy(self.struct)
+        c.flags |= _lib.TQ_CODEC_GENERAL_COMPRESS
+        return ctypes.byref(c)
 
 
 _codecs: dict[tuple, DeviceCodec] = {}
@@ -152,10 +171,11 @@ class PackedStore:
 
 
 def compress_into(codec: DeviceCodec, x: torch.Tensor, x_tok0: int, n_tok: int,
-                  store: PackedStore, dst_tok0: int) -> None:
+                  store: PackedStore, dst_tok0: int, general: bool = False) -> None:
     """Compress tokens [x_tok0, x_tok0 + n_tok) of x (B, H, T, D), contiguous in
     its last two dims with head stride x.stride(1), into store tokens
-    [dst_tok0, dst_tok0 + n_tok)."""
+    [dst_tok0, dst_tok0 + n_tok). ``general`` selects the general compress
+    kernel (tests compare it with the MFMA kernel)."""
     if n_tok <= 0:
         return
     B, H, T, D = x.shape
@@ -164,7 +184,7 @@ def compress_into(codec: DeviceCodec, x: torch.Tensor, x_tok0: int, n_tok: int,
     st = store.struct(dst_tok0)
     xp = x.data_ptr() + x_tok0 * D * x.element_size()
     lib = _lib.load()
-    _lib.check(lib.tq_compress(codec.ref(), xp, _lib.dtype_code(x.dtype), x.stride(1), ctypes.byref(span),
+    _lib.check(lib.tq_compress(codec.ref(general), xp, _lib.dtype_code(x.dtype), x.stride(1), ctypes.byref(span),
                                ctypes.byref(st), _lib.stream_ptr(x.device)), "tq_compress")
 
 

@@ -35,7 +35,12 @@ class Codec(ctypes.Structure):
     _fields_ = [("d", _i32), ("bits_hi", _i32), ("bits_lo", _i32), ("split", _i32),
                 ("rotation", _p), ("centroids_hi", _p), ("boundaries_hi", _p),
                 ("centroids_lo", _p), ("boundaries_lo", _p), ("qjl_proj", _p),
-                ("qjl_m", _i32), ("reserved", _i32), ("rotation_parts", _p)]
+                ("qjl_m", _i32), ("flags", _i32), ("rotation_parts", _p),
+                ("host_centroids", ctypes.c_float * 16), ("n_host_centroids", _i32),
+                ("value_table", ctypes.c_uint16 * 4), ("value_scale", ctypes.c_float),
+                ("value_table_err", ctypes.c_float), ("decode_table", _p)]
+
+TQ_CODEC_GENERAL_COMPRESS = 1
 
 
 class Store(ctypes.Structure):
@@ -65,7 +70,6 @@ class AttnDesc(ctypes.Structure):
                 ("res_start", _p), ("res_len", _p), ("flags", _i32), ("reserved2", _i32)]
 
 TQ_ATTN_GENERAL = 1
-TQ_ATTN_PARTIALS_ONLY = 2
 
 
 _PC = ctypes.POINTER(Codec)
@@ -79,7 +83,8 @@ SIGNATURES = {
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_device_supported": (_i32, []),
     "tq_compress": (_i32, [_PC, _p, _i32, _i64, _PSp, _PS, _p]),
-    "tq_compress_force_general": (None, [_i32]),
+    "tq_codec_prepare": (_i32, [_PC, _p, _i32]),
+    "tq_codec_decode_table": (_i32, [_PC, _p]),
     "tq_dequantize": (_i32, [_PC, _PS, _PSp, _p, _i64, _i32, _p]),
     "tq_pack_codes": (_i32, [_p, _i64, _i32, _i32, _p, _p]),
     "tq_unpack_codes": (_i32, [_p, _i64, _i32, _i32, _p, _p]),
@@ -113,7 +118,7 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.tq_abi_version() != 2:
+    if lib.tq_abi_version() != 3:
         raise TurboQuantLibraryError("turboquant_amd: ABI version mismatch")
     _lib = lib
     return lib

@@ -13,8 +13,9 @@ def to_dev(a: np.ndarray) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-def gpu_compress(x: np.ndarray, bits: float, qjl_m: int = 0, seed: int = 42):
-    """Compress (B, H, T, D) on the GPU; returns numpy (codes_hi, codes_lo, norms, signs, gamma)."""
+def gpu_compress(x: np.ndarray, bits: float, qjl_m: int = 0, seed: int = 42, general: bool = False):
+    """Compress (B, H, T, D) on the GPU; returns numpy (codes_hi, codes_lo, norms, signs, gamma).
+    ``general`` routes the call through the general compress kernel."""
     from turboquant_amd import _codec
 
     xt = to_dev(x)
@@ -22,7 +23,7 @@ def gpu_compress(x: np.ndarray, bits: float, qjl_m: int = 0, seed: int = 42):
     codec = _codec.get_codec(D, bits, seed, qjl_m, xt.device)
     st = _codec.PackedStore(codec, B, H, qjl=qjl_m > 0)
     st.reserve(max(T, 1), 0)
-    _codec.compress_into(codec, xt, 0, T, st, 0)
+    _codec.compress_into(codec, xt, 0, T, st, 0, general=general)
     torch.cuda.synchronize()
 
     def np_(t):

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} not bound in _lib.SIGNATURES"
-    assert lib.tq_abi_version() == 2
+    assert lib.tq_abi_version() == 3
 
 
 def test_struct_layouts_match_header():
@@ -87,3 +87,28 @@ def test_host_side_validation_errors():
     assert lib.tq_dense_decode_attention(ctypes.byref(d), 128, None, 0, None) == _lib.TQ_ERR_UNSUPPORTED
     d.hq, d.sink_k = 8, 18  # rows not 16-byte aligned
     assert lib.tq_dense_decode_attention(ctypes.byref(d), 128, None, 0, None) == _lib.TQ_ERR_UNSUPPORTED
+
+
+def test_value_table_is_an_exact_fp16_copy_of_the_2bit_codebook():
+    """tq_codec_prepare (host only): centroid i == value_scale *
+    fp16(value_table[i]) for the shipped d=128 2-bit codebook to within 2e-7,
+    the bar of the K4/V2 decode route; other sizes are refused (error inf)."""
+    import numpy as np
+    from turboquant_amd import _lib
+    from turboquant_amd.codebook import codebook_arrays
+    lib = _lib.load()
+    cen, _ = codebook_arrays(128, 2)
+    cen = np.ascontiguousarray(cen, np.float32)
+    c = _lib.Codec()
+    assert lib.tq_codec_prepare(ctypes.byref(c), cen.ctypes.data, 4) == _lib.TQ_OK
+    assert c.n_host_centroids == 4 and np.array_equal(np.array(list(c.host_centroids))[:4], cen)
+    tab = np.array(list(c.value_table), np.uint16).view(np.float16).astype(np.float64)
+    got = float(np.float32(c.value_scale)) * tab
+    rel = np.abs(got - cen) / np.abs(cen)
+    assert rel.max() <= 2e-7 and c.value_table_err <= 2e-7, rel
+    assert np.isclose(rel.max(), c.value_table_err, rtol=1e-3, atol=1e-12)
+    # the table entries are fp16 numbers in the normal range, antisymmetric like the codebook
+    assert np.all(np.abs(tab) >= 2.0 ** -14) and np.array_equal(tab[::-1], -tab)
+    c16 = np.linspace(-1, 1, 16, dtype=np.float32)
+    assert lib.tq_codec_prepare(ctypes.byref(c), c16.ctypes.data, 16) == _lib.TQ_OK
+    assert c.value_table_err == float("inf")

@@ -30,18 +30,6 @@ def _x(shape, seed, scale=None, vec_scale=None):
     return np.clip(x, -6e4, 6e4).astype(np.float16)
 
 
-class force_general:
-    """Route tq_compress through the general kernel inside the block."""
-
-    def __enter__(self):
-        from turboquant_amd import _lib
-        _lib.load().tq_compress_force_general(1)
-
-    def __exit__(self, *exc):
-        from turboquant_amd import _lib
-        _lib.load().tq_compress_force_general(0)
-
-
 @pytest.mark.parametrize("T", [1, 17, 63, 64, 65, 200, 1000])
 def test_partial_tiles(T):
     x = _x((1, 3, T, 128), seed=T, scale=0.5)
@@ -108,8 +96,7 @@ def test_fast_and_general_kernels_agree():
     outside the band."""
     x = _x((1, 8, 512, 128), seed=9, scale=0.5)
     fast = gpu_compress(x, 3.5)
-    with force_general():
-        gen = gpu_compress(x, 3.5)
+    gen = gpu_compress(x, 3.5, general=True)
     r_fast = code_parity(x, 3.5, gpu=fast)
     r_gen = code_parity(x, 3.5, gpu=gen, ref=r_fast[5])
     assert r_fast[4] and r_gen[4] and r_fast[1] == 0 and r_gen[1] == 0

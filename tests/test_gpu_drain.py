@@ -1,7 +1,7 @@
 """The one-vector drain kernel of tq_compress (spans of at most 8 tokens per
 row, head_dim 128, with the QJL sketch: the one-token ragged drains of a
 decode step, cache.py:529-533 with qjl_correction) against the tiled general
-compress kernel (tq_compress_force_general): both compute the same float32 /
+compress kernel (TQ_CODEC_GENERAL_COMPRESS): both compute the same float32 /
 float64 operations in the same order, so codes, norms, residual norms and
 sign words must be bit-identical. The general kernel itself is checked
 against the oracle in test_gpu_codec.py / test_gpu_ragged.py.
@@ -33,14 +33,10 @@ def drain(codec, ring, n_b, src_b, dst_b, heads, general):
     span = _lib.Span(rows=B * heads, heads=heads, n_tok=int(max(n_b)), reserved=0, n_tok_b=nb.data_ptr(),
                      src_tok0_b=sb.data_ptr(), dst_tok0_b=db.data_ptr())
     lib = _lib.load()
-    lib.tq_compress_force_general(1 if general else 0)
-    try:
-        st = store.struct(0)
-        _lib.check(lib.tq_compress(codec.ref(), ring.data_ptr(), _lib.dtype_code(ring.dtype), ring.shape[2] * D,
-                                   ctypes.byref(span), ctypes.byref(st), _lib.stream_ptr(DEV)), "tq_compress")
-        torch.cuda.synchronize()
-    finally:
-        lib.tq_compress_force_general(0)
+    st = store.struct(0)
+    _lib.check(lib.tq_compress(codec.ref(general), ring.data_ptr(), _lib.dtype_code(ring.dtype), ring.shape[2] * D,
+                               ctypes.byref(span), ctypes.byref(st), _lib.stream_ptr(DEV)), "tq_compress")
+    torch.cuda.synchronize()
     return {n: getattr(store, n).cpu().numpy() for n in ("codes_hi", "codes_lo", "norms", "signs", "gamma")
             if getattr(store, n) is not None}
 

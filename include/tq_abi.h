@@ -192,17 +192,20 @@ typedef struct tq_attn_desc {
   const void* q;                        /* (batch, hq, d) */
   float* out;                           /* (batch, hq, d) float32 */
   tq_store kstore, vstore;              /* rows = batch * hkv */
-  const int32_t* comp_len;              /* (batch,) or NULL = max_comp */
+  const int32_t* comp_len;              /* (batch,) device, 0 <= comp_len[b] <= max_comp, or NULL = max_comp */
   const void* sink_k;                   /* kv_dtype (batch*hkv, sink_cap, d) or NULL */
   const void* sink_v;
   int64_t sink_head_stride;             /* elements */
-  const int32_t* sink_len;              /* (batch,) or NULL = max_sink */
+  const int32_t* sink_len;              /* (batch,) device, 0 <= sink_len[b] <= max_sink, or NULL = max_sink */
   const void* res_k;                    /* kv_dtype ring (batch*hkv, res_cap, d) or NULL */
   const void* res_v;
   int64_t res_head_stride;              /* elements */
   int32_t res_cap, res_start0;          /* ring capacity; ring start when res_start == NULL */
-  const int32_t* res_start;             /* (batch,) ring start, or NULL = res_start0 */
-  const int32_t* res_len;               /* (batch,) or NULL = max_res */
+  const int32_t* res_start;             /* (batch,) device ring start in [0, res_cap), or NULL = res_start0 */
+  const int32_t* res_len;               /* (batch,) device, 0 <= res_len[b] <= max_res, or NULL = max_res.
+                                           Kernels clamp every entry into these bounds (an out-of-range
+                                           entry gives a wrong result for its sequence, never an access
+                                           outside the stores, sink or ring). */
   int32_t flags;                        /* TQ_ATTN_* bits */
   int32_t reserved2;
 } tq_attn_desc;

@@ -29,6 +29,17 @@ constexpr int CHUNK = 256;   // tokens per partial
 constexpr int NT = 256;      // threads per workgroup
 constexpr float SQRT_HALF_PI = 1.2533141373155003f;
 
+// Per-sequence lengths read from device arrays are clamped to the bounds the
+// host checked (tq_abi.h: 0 <= len_b <= max_*, 0 <= res_start_b < res_cap), so
+// an inconsistent array cannot send a kernel past the stores, sink or ring.
+__device__ inline int clamp_len(int v, int mx) { return min(max(v, 0), mx); }
+__device__ inline int seq_comp(const tq_attn_desc& d, int b) {
+  return d.comp_len ? clamp_len(d.comp_len[b], d.max_comp) : d.max_comp;
+}
+__device__ inline int seq_ring_start(const tq_attn_desc& d, int b) {
+  return d.res_start ? clamp_len(d.res_start[b], max(d.res_cap - 1, 0)) : d.res_start0;
+}
+
 struct AttnArgs {
   tq_attn_desc d;
   int D;
@@ -214,9 +225,9 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   else if (c < a.nc + a.ns) { seg = 1; base = (c - a.nc) * CHUNK; }
   else { seg = 2; base = (c - a.nc - a.ns) * CHUNK; }
   int len;
-  if (seg == 0) len = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
-  else if (seg == 1) len = a.d.sink_len ? a.d.sink_len[b] : a.d.max_sink;
-  else len = a.d.res_len ? a.d.res_len[b] : a.d.max_res;
+  if (seg == 0) len = seq_comp(a.d, b);
+  else if (seg == 1) len = a.d.sink_len ? clamp_len(a.d.sink_len[b], a.d.max_sink) : a.d.max_sink;
+  else len = a.d.res_len ? clamp_len(a.d.res_len[b], a.d.max_res) : a.d.max_res;
   const int nvalid = max(0, min(CHUNK, len - base));
 
   const bool packed = seg == 0;
@@ -293,7 +304,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
         kp = a.d.sink_k;
         ko = (int64_t)row * a.d.sink_head_stride + (int64_t)(base + t) * D;
       } else {
-        const int st = a.d.res_start ? a.d.res_start[b] : a.d.res_start0;
+        const int st = seq_ring_start(a.d, b);
         const int pos = (st + base + t) % a.d.res_cap;
         kp = a.d.res_k;
         ko = (int64_t)row * a.d.res_head_stride + (int64_t)pos * D;
@@ -392,7 +403,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
             vp = a.d.sink_v;
             vo = (int64_t)row * a.d.sink_head_stride + (int64_t)(base + tt) * D;
           } else {
-            const int st = a.d.res_start ? a.d.res_start[b] : a.d.res_start0;
+            const int st = seq_ring_start(a.d, b);
             const int pos = (st + base + tt) % a.d.res_cap;
             vp = a.d.res_v;
             vo = (int64_t)row * a.d.res_head_stride + (int64_t)pos * D;
@@ -573,7 +584,7 @@ __global__ __launch_bounds__(NT) void qjl_bias_kernel(QjlArgs a) {
   __shared__ __align__(16) float sq[G][MAXM];
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m;
-  const int comp = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
+  const int comp = seq_comp(a.d, b);
   // past the sequence's last 32-token block the bias is never read (those
   // scores are masked after it is added)
   if (c * QCH >= ((comp + 31) & ~31)) return;
@@ -609,9 +620,10 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   constexpr int SR = 256 / 8 + 4;  // padded LDS sign row (bytes)
   __shared__ __align__(16) float pw[G][QCH];
   __shared__ __align__(16) uint8_t sg[QCH * SR];
+  __shared__ uint32_t wmx[G];  // per head: the chunk's max weight (float bits; weights are >= 0)
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq;
-  const int comp = a.d.comp_len ? a.d.comp_len[b] : a.d.max_comp;
+  const int comp = seq_comp(a.d, b);
   const int base = c * QCH, nvalid = max(0, min(QCH, comp - base));
   if (nvalid == 0) {  // past the sequence: a zero partial (the final kernel sums every chunk)
     for (int e = tid; e < G * m; e += NT)
@@ -619,6 +631,10 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
     return;
   }
   const tq_store& vs = a.d.vstore;
+  if (tid < G) wmx[tid] = 0u;
+  __syncthreads();
+  // unnormalised weights w = 2^(s - M) gamma (O(gamma), whatever the context
+  // length); 1 / L is applied in float32 to the sums
   {
     const int t = tid;
     const float gv = t < nvalid ? vs.gamma[(int64_t)row * vs.gamma_head_stride + base + t] : 0.f;
@@ -628,13 +644,24 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
       if (t < nvalid) {
         const float M = a.ml[((int64_t)b * hq + g * G + h) * 2], L = a.ml[((int64_t)b * hq + g * G + h) * 2 + 1];
         const float sc = a.scores[((int64_t)row * G + h) * a.qb_hs + base + t];
-        p = L > 0.f ? __builtin_amdgcn_exp2f(sc - M) * (1.f / L) : 0.f;
+        p = L > 0.f ? __builtin_amdgcn_exp2f(sc - M) : 0.f;
       }
-      pw[h][t] = p * gv;
+      const float wt = p * gv;
+      pw[h][t] = wt;
+      float mx = wt;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      if ((tid & 63) == 0) atomicMax(&wmx[h], __float_as_uint(mx));
     }
   }
   stage_rows(sg, SR, 0, vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base * (m / 8), m / 8, nvalid);
   __syncthreads();
+  // head h's weights enter fp16 as w 2^(14 - E_h) (E_h the exponent of the
+  // chunk's max weight: operands below 2^15, none subnormal but the tiny)
+  auto head_exp = [&](int hh) {
+    const uint32_t mb = wmx[hh];
+    return mb == 0u ? 0 : max((int)((mb >> 23) & 0xFFu), 1) - 127;
+  };
   const int lane = tid & 63, w = tid >> 6, r = lane & 15, q4 = lane >> 4;
   const int h = r & 7;
   const bool lo_row = r >= 8;
@@ -649,8 +676,9 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
     for (int e = 0; e < 4; ++e) {
       float w0 = 0.f, w1 = 0.f;
       if (h < G) {
-        w0 = pw[h][t0 + 2 * e];
-        w1 = pw[h][t0 + 2 * e + 1];
+        const float up = __builtin_amdgcn_ldexpf(1.f, 14 - head_exp(h));
+        w0 = pw[h][t0 + 2 * e] * up;
+        w1 = pw[h][t0 + 2 * e + 1] * up;
       }
       const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
       const _Float16 l0 = (_Float16)(w0 - (float)h0), l1 = (_Float16)(w1 - (float)h1);
@@ -683,7 +711,11 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
       const float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
       const int hh = 4 * q4 + i;
-      if (q4 < 2 && hh < G) a.upart[(((int64_t)b * hq + g * G + hh) * a.nvc + c) * m + 16 * ct + r] = v;
+      if (q4 < 2 && hh < G) {
+        const float L = a.ml[((int64_t)b * hq + g * G + hh) * 2 + 1];
+        const float down = L > 0.f ? __builtin_amdgcn_ldexpf(1.f, head_exp(hh) - 14) / L : 0.f;
+        a.upart[(((int64_t)b * hq + g * G + hh) * a.nvc + c) * m + 16 * ct + r] = v * down;
+      }
     }
   }
 }

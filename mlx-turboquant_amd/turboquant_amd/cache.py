@@ -41,6 +41,10 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+# query heads per kv head the decode-attention kernels serve
+ATTEND_GROUPS = (1, 2, 4, 8)
+
+
 def dense_attention(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                     scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """Decode attention of one query token per head over uncompressed K/V
@@ -93,6 +97,7 @@ class TurboQuantKVCache:
     """TurboQuant-compressed KV cache (cache.py:19-116)."""
 
     step = 256
+    ATTEND_HEAD_DIMS = (64, 128, 256)  # head_dims of the codecs and the decode-attention kernels
 
     def __init__(self, head_dim: int = 128, num_kv_heads: int = 1, key_bits: float = 4,
                  value_bits: float = 2, residual_window: int = 128, rotation_seed: int = DEFAULT_SEED,

@@ -29,3 +29,23 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Code-parity accounting of the GPU codec tests: per call, the
+    coordinates compared, the code mismatches against the oracle, how many of
+    them lie inside the float32 boundary band (all must), and how many lie
+    within 1 float32 ulp of a boundary. Printed under -q too."""
+    helpers = sys.modules.get("gpu_helpers")
+    log = getattr(helpers, "PARITY_LOG", None)
+    if not log:
+        return
+    tr = terminalreporter
+    tr.write_sep("=", "code parity against the oracle (mismatches: all / in band / within 1 ulp / outside band)")
+    tot = [0, 0, 0, 0, 0]
+    for test, bits, n, m, inb, ulp, out in log:
+        tr.write_line(f"{test} bits={bits}: {n} coords, mismatches {m} / {inb} / {ulp} / {out}")
+        for i, x in enumerate((n, m, inb, ulp, out)):
+            tot[i] += x
+    tr.write_line(f"TOTAL: {tot[0]} coords, mismatches {tot[1]} / in band {tot[2]} / within 1 ulp {tot[3]} / "
+                  f"outside band {tot[4]} ({len(log)} comparisons)")

@@ -3,6 +3,8 @@ and compare with the numpy oracle (test infrastructure)."""
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import torch
 
@@ -42,9 +44,17 @@ def unpack_codes(codes_hi, codes_lo, bits: float, d: int) -> np.ndarray:
     return idx
 
 
+# Every code_parity call of the session: (test, bits, coordinates compared,
+# mismatches, mismatches inside the float32 band, of those within 1 ulp of a
+# boundary, mismatches outside the band), printed by conftest's terminal
+# summary (also under -q).
+PARITY_LOG: list[tuple] = []
+
+
 def code_parity(x: np.ndarray, bits: float, gpu=None, ref=None):
     """Compare GPU codes/norms with the oracle (``ref``: a precomputed
-    ``O.compress`` result of the same input).
+    ``O.compress`` result of the same input). Records the counts in
+    PARITY_LOG and asserts that every mismatch lies inside the band.
 
     Returns (n_mismatch, n_outside_band, n_within_1ulp, total, norms_equal, ref)."""
     D = x.shape[-1]
@@ -68,7 +78,11 @@ def code_parity(x: np.ndarray, bits: float, gpu=None, ref=None):
         ulp = np.spacing(np.abs(yy).astype(np.float32)).astype(np.float64)
         ulp1[..., sl] = dist <= ulp
     norms_equal = np.array_equal(nrm.view(np.uint32), ref.norms.view(np.uint32))
-    return int(mism.sum()), int(outside.sum()), int((mism & ulp1).sum()), mism.size, norms_equal, ref
+    n_m, n_out, n_ulp = int(mism.sum()), int(outside.sum()), int((mism & ulp1).sum())
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    PARITY_LOG.append((test, bits, int(mism.size), n_m, n_m - n_out, n_ulp, n_out))
+    assert n_out == 0, f"{n_out} code mismatches outside the float32 boundary band ({n_m} in all)"
+    return n_m, n_out, n_ulp, int(mism.size), norms_equal, ref
 
 
 def rel_err(a: np.ndarray, b: np.ndarray) -> float:

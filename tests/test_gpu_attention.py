@@ -18,6 +18,7 @@ pytestmark = pytest.mark.gpu
 
 REL_TOL = 1e-3
 COS_TOL = 0.9999
+FAST_REL_TOL = 5e-6  # the K4/V2 kernels (fp16 high part + remainder operands, exact value table) vs float64
 
 
 def build(kw, k, v, steps=()):
@@ -161,21 +162,43 @@ def test_attention_float32_inputs_and_scale():
 
 
 def test_attention_golden_small():
+    """The fixture is the oracle's attention over the oracle's own codes. The
+    kernel is held to 1e-3 / cos 0.9999 against the oracle evaluated on the
+    codes the cache stores; those codes differ from the oracle's only inside
+    the float32 boundary band (counted by code_parity), and with no such flip
+    the same bound holds against the fixture itself. Any remaining gap to the
+    fixture is the flips' own: the oracle over the stored codes shows it."""
     import sys
     sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
     from make_golden import attn_small_case
+    from gpu_helpers import code_parity
     from turboquant_amd import TurboQuantKVCache
-    rng_case = attn_small_case()
-    k, v = rng_case[0], rng_case[1]
+    k, v, _, _ = attn_small_case()
     g = np.load(os.path.join(os.path.dirname(__file__), "golden", "attn_small.npz"))
-    c = TurboQuantKVCache(head_dim=128, num_kv_heads=2, key_bits=4, value_bits=2, residual_window=32,
-                          fp16_sink_size=16)
+    kw = dict(head_dim=128, num_kv_heads=2, key_bits=4, value_bits=2, residual_window=32, fp16_sink_size=16)
+    c = TurboQuantKVCache(**kw)
     c.update(to_dev(k), to_dev(v))
+    o = O.CacheOracle(**kw)
+    o.update(k, v)
+    assert rel_err(o.attend(g["q"]), g["out"]) < 1e-12  # the oracle reproduces the fixture
     out = c.attend(to_dev(g["q"])).cpu().numpy()
-    # the fixture uses the oracle's codes; an in-band code flip moves a
-    # 252-token attention by up to ~1e-3, hence the looser bound here (the
-    # strict bound against the stored codes is checked in the other tests)
-    assert rel_err(out, g["out"]) < 5e-3 and min_cos(out, g["out"]) >= 0.999
+    kk, vv = dense_from_gpu_codes(c, o)
+    ref = O.attention(g["q"], kk, vv)
+    e, cs = rel_err(out, ref), min_cos(out, ref)
+    assert e < 1e-3 and cs >= 0.9999, (e, cs)
+    S, C = c._sink_len, c._compressed_len
+    flips = 0
+    for side, bits, x in (("k", 4, k), ("v", 2, v)):
+        hi, lo, n = c.packed(side)
+        gpu = (hi.cpu().numpy(), None if lo is None else lo.cpu().numpy(), n.cpu().numpy(), None, None)
+        flips += code_parity(x[:, :, S:S + C], bits, gpu=gpu)[0]  # asserts every flip is in band
+    e_fix, cs_fix = rel_err(out, g["out"]), min_cos(out, g["out"])
+    print(f"golden: kernel vs oracle on stored codes rel {e:.2e} cos {cs:.7f}; vs fixture rel {e_fix:.2e} "
+          f"cos {cs_fix:.7f}; in-band code flips {flips}")
+    if flips == 0:
+        assert e_fix < 1e-3 and cs_fix >= 0.9999
+    else:  # the gap to the fixture is the flips': the oracle over the stored codes is as far from it
+        assert abs(rel_err(ref, g["out"]) - e_fix) < 1e-3
 
 
 def test_update_and_fetch_dense_matches_oracle():
@@ -272,8 +295,42 @@ def test_fast_kernel_matches_general_and_oracle(G, T, sink, window, chunk):
     ref = O.attention(q, kk, vv)
     e_f, e_g = rel_err(fast, ref), rel_err(gen, ref)
     print(f"G={G} T={T}: fast rel {e_f:.3e} general rel {e_g:.3e} fast-vs-general {rel_err(fast, gen):.3e}")
-    assert e_f < REL_TOL and min_cos(fast, ref) >= COS_TOL
+    assert e_f < FAST_REL_TOL and min_cos(fast, ref) >= COS_TOL
     assert e_g < REL_TOL
+
+
+def test_fast_kernel_large_value_norms():
+    """Values of norm ~6e5 (fp16 entries near 5e4): p * n_v passes the fp16
+    range, so the kernels scale the P^T operand of such columns by a power of
+    two (applied back at the combine). Against float64 at the fast bound."""
+    k, v = _kv(1, 2, 3000, 128, seed=95)
+    v = np.clip(v.astype(np.float32) * 2e4, -6e4, 6e4).astype(np.float16)
+    c, o = build(dict(head_dim=128, num_kv_heads=2, key_bits=4, value_bits=2, residual_window=64,
+                      fp16_sink_size=16), k, v)
+    q = np.random.RandomState(96).randn(1, 8, 1, 128).astype(np.float16)
+    fast = c.attend(to_dev(q)).cpu().numpy()
+    kk, vv = dense_from_gpu_codes(c, o)
+    ref = O.attention(q, kk, vv)
+    assert np.isfinite(fast).all()
+    assert rel_err(fast, ref) < FAST_REL_TOL and min_cos(fast, ref) >= COS_TOL, rel_err(fast, ref)
+
+
+def test_qjl_fast_route_small_values_long_context():
+    """Value entries of scale 0.02 over ~33,000 compressed tokens (softmax
+    weights of order gamma / N): the K4/V2 sketch route against the general
+    kernel (float32 weights throughout) at 1e-4."""
+    from turboquant_amd import TurboQuantKVCache
+    k, v = _kv(1, 2, 33024, 128, seed=91)
+    v = (v.astype(np.float32) * 0.02).astype(np.float16)
+    c = TurboQuantKVCache(head_dim=128, num_kv_heads=2, key_bits=4, value_bits=2, residual_window=128,
+                          fp16_sink_size=0, qjl_correction=True, qjl_n_proj=128)
+    c.update(to_dev(k), to_dev(v))
+    assert c._compressed_len >= 32768
+    q = to_dev(np.random.RandomState(92).randn(1, 8, 1, 128).astype(np.float16))
+    a = c.attend(q).cpu().numpy()
+    b = c.attend(q, general_kernel=True).cpu().numpy()
+    print(f"QJL K4/V2 vs general, values x0.02, {c._compressed_len} compressed: rel {rel_err(a, b):.3e}")
+    assert rel_err(a, b) < 1e-4
 
 
 def test_fast_kernel_repeat_calls_identical():

@@ -175,22 +175,24 @@ def test_ragged_errors():
         rb.step(torch.zeros(2, 2, 64, device=DEV), torch.zeros(2, 2, 64, device=DEV))
 
 
-@pytest.mark.parametrize("qjl_m", [0, 128], ids=["k4v2", "k4v2_qjl"])
-def test_config4_ragged_decode(qjl_m):
+@pytest.mark.parametrize("qjl_m,sink", [(0, 128), (128, 128), (0, 0), (128, 0)],
+                         ids=["k4v2", "k4v2_qjl", "k4v2_sink0", "k4v2_qjl_sink0"])
+def test_config4_ragged_decode(qjl_m, sink):
     """configs[4] at size: 16 Llama-3.1-8B-shaped sequences (H_kv = 8,
     H_q = 32), lengths ~ Uniform[4096, 32768] (seeded), K4/V2 (with the QJL
     sketch through a 128 x 128 projection), 256 decode steps of one new token
-    per sequence, each draining one token per sequence into the store."""
+    per sequence, each draining one token per sequence into the store. Sink
+    0 is the reference default and the benched configuration."""
     lens = np.random.RandomState(4).randint(4096, 32769, size=16)
-    rb = make_batch(lens, H=8, qjl_m=qjl_m, seed=5)
+    rb = make_batch(lens, H=8, qjl_m=qjl_m, sink=sink, seed=5)
     q = torch.randn(rb.B, 8 * HQ_PER_KV, D, generator=rb.g, device=DEV).half()
     short = [int(i) for i in np.argsort(lens)[:2]]
-    check_batch(rb, q, oracle_rows=short, label=f"config4 m={qjl_m} step 0")
+    check_batch(rb, q, oracle_rows=short, label=f"config4 m={qjl_m} sink={sink} step 0")
     for _ in range(256):
         step(rb)
-    assert (rb.comp_len == lens - 128 - 128 + 256).all() and (rb.offset == lens + 256).all()
+    assert (rb.comp_len == lens - sink - 128 + 256).all() and (rb.offset == lens + 256).all()
     q = torch.randn(rb.B, 8 * HQ_PER_KV, D, generator=rb.g, device=DEV).half()
-    check_batch(rb, q, oracle_rows=short, label=f"config4 m={qjl_m} step 256")
+    check_batch(rb, q, oracle_rows=short, label=f"config4 m={qjl_m} sink={sink} step 256")
     a = rb.attend(q).cpu().numpy()
     b = rb.attend(q, general=True).cpu().numpy()
     assert rel_err(a, b) < 1e-4, f"config4 m={qjl_m}: fast route vs general kernel {rel_err(a, b):.3e}"

@@ -58,7 +58,8 @@ struct AttnArgs {
   float* sq;    // (B, Hq, m)  S @ (scale * q)
   float* part;  // (B, Hq, nch, PS)
   int nc, ns, nr, nch, ps;
-  int c0;  // first chunk of a chunk_kernel launch
+  int c0;    // first chunk of a chunk_kernel launch
+  int gsub;  // launch groups per kv head: a chunk_kernel<D, G> group holds G = (hq / hkv) / gsub query heads
 };
 
 __host__ __device__ inline int part_stride(int D, int m) { return ((2 + D + m) + 3) & ~3; }
@@ -121,8 +122,11 @@ __device__ inline void stage_rows(uint8_t* dst, int stride, int col, const uint8
 }
 
 // s[h] += sum_{j < nd} q[h][j0 + j] * lut[code j] for BITS-wide LSB-first
-// codes in a 4-byte-aligned LDS row; nd and j0 multiples of 32. The codes of
-// 32 dims are BITS dwords, read once; shifts are compile-time constants.
+// codes in a 4-byte-aligned LDS row; nd and j0 multiples of 16. The codes of
+// 32 dims are BITS dwords, read once; shifts are compile-time constants. A
+// trailing group of 16 codes (head_dim 96 split in halves of 48) reads the
+// BITS dwords of a full group, of which it uses the first 2 BITS bytes (the
+// row stride leaves room for the rest).
 template <int BITS, int D, int G>
 __device__ inline void dot_codes(const uint8_t* row, int nd, const float* lut, const float (*q)[D], int j0,
                                  float (&s)[G]) {
@@ -131,8 +135,10 @@ __device__ inline void dot_codes(const uint8_t* row, int nd, const float* lut, c
     uint32_t wd[BITS];
 #pragma unroll
     for (int i = 0; i < BITS; ++i) wd[i] = rw[(jb >> 5) * BITS + i];
+    const bool half = nd - jb < 32;
 #pragma unroll
     for (int j4 = 0; j4 < 32; j4 += 4) {
+      if (j4 >= 16 && half) break;
       float cv[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -215,9 +221,10 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   __shared__ __align__(16) uint8_t ksg[CHUNK * SR];    // key sign rows (QJL)
   __shared__ __align__(16) uint8_t vsg[CHUNK * SR];    // value sign rows (QJL)
   __shared__ float slice[G][NT];                       // per-thread partial sums of the PV / QJL phases
+  // group g: query heads [g G, g G + G) of kv head g / gsub
   const int c = blockIdx.x + a.c0, g = blockIdx.y, b = blockIdx.z;
   const int hq = a.d.hq, tid = threadIdx.x;
-  const int row = b * a.d.hkv + g;
+  const int row = b * a.d.hkv + g / a.gsub;
 
   // segment of this chunk
   int seg, base;
@@ -546,14 +553,27 @@ static void chunk_counts(const tq_attn_desc* d, int& nc, int& ns, int& nr) {
   nr = (d->max_res + CHUNK - 1) / CHUNK;
 }
 
+// G: query heads per launch group (1 .. 8)
 template <int D>
 static void launch_chunks(const AttnArgs& a, int G, dim3 grid, hipStream_t s) {
   switch (G) {
     case 1: hipLaunchKernelGGL((chunk_kernel<D, 1>), grid, dim3(NT), 0, s, a); break;
     case 2: hipLaunchKernelGGL((chunk_kernel<D, 2>), grid, dim3(NT), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((chunk_kernel<D, 3>), grid, dim3(NT), 0, s, a); break;
     case 4: hipLaunchKernelGGL((chunk_kernel<D, 4>), grid, dim3(NT), 0, s, a); break;
+    case 5: hipLaunchKernelGGL((chunk_kernel<D, 5>), grid, dim3(NT), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((chunk_kernel<D, 6>), grid, dim3(NT), 0, s, a); break;
+    case 7: hipLaunchKernelGGL((chunk_kernel<D, 7>), grid, dim3(NT), 0, s, a); break;
     default: hipLaunchKernelGGL((chunk_kernel<D, 8>), grid, dim3(NT), 0, s, a); break;
   }
+}
+
+// Query heads per launch group of the general kernel for G query heads per
+// kv head: the largest divisor of G that is at most 8.
+static int group_heads(int G) {
+  for (int k = 8; k > 1; --k)
+    if (G % k == 0) return k;
+  return 1;
 }
 
 // ---- QJL sketch terms around the K4/V2 kernels (K4 keys / V2 values with a
@@ -1123,10 +1143,9 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   if (kc->d != vc->d) return set_error(TQ_ERR_INVALID, "key/value head_dim differ");
   if (d->batch <= 0 || d->hkv <= 0 || d->hq <= 0 || d->hq % d->hkv)
     return set_error(TQ_ERR_INVALID, "bad head counts hq=%d hkv=%d batch=%d", d->hq, d->hkv, d->batch);
-  const int G = d->hq / d->hkv;
-  if (G != 1 && G != 2 && G != 4 && G != 8)
-    return set_error(TQ_ERR_UNSUPPORTED, "query heads per kv head %d not in {1,2,4,8}", G);
-  if (d->batch > 65535 || d->hkv > 65535) return set_error(TQ_ERR_UNSUPPORTED, "grid too large");
+  const int G = d->hq / d->hkv;  // any integer ratio: the general kernel groups the heads by group_heads(G)
+  if (d->batch > 65535 || (int64_t)d->hkv * (G / group_heads(G)) > 65535 || d->hq > 65535)
+    return set_error(TQ_ERR_UNSUPPORTED, "grid too large");
   if (d->max_comp < 0 || d->max_sink < 0 || d->max_res < 0)
     return set_error(TQ_ERR_INVALID, "negative segment length");
   if (!d->q || !d->out) return set_error(TQ_ERR_INVALID, "q/out is NULL");
@@ -1192,6 +1211,8 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   a.nch = a.nc + a.ns + a.nr;
   a.ps = part_stride(a.D, a.m);
   a.c0 = 0;
+  const int gh = group_heads(G);
+  a.gsub = G / gh;
   const size_t heads = (size_t)d->batch * d->hq;
   float* ws = static_cast<float*>(workspace);
   a.qr = ws;
@@ -1203,11 +1224,12 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   hipLaunchKernelGGL(prologue_kernel, dim3(d->hq, d->batch), dim3(128), pro_smem, s, a);
   TQ_LAUNCH_CHECK("tq_decode_attention prologue");
   if (a.nch > 0) {
-    dim3 grid(a.nch, d->hkv, d->batch);
+    dim3 grid(a.nch, d->hkv * a.gsub, d->batch);
     switch (a.D) {
-      case 64: launch_chunks<64>(a, G, grid, s); break;
-      case 128: launch_chunks<128>(a, G, grid, s); break;
-      default: launch_chunks<256>(a, G, grid, s); break;
+      case 64: launch_chunks<64>(a, gh, grid, s); break;
+      case 96: launch_chunks<96>(a, gh, grid, s); break;
+      case 128: launch_chunks<128>(a, gh, grid, s); break;
+      default: launch_chunks<256>(a, gh, grid, s); break;
     }
     TQ_LAUNCH_CHECK("tq_decode_attention chunks");
   }

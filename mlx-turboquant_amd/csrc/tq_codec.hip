@@ -32,13 +32,13 @@ int set_error(int code, const char* fmt, ...) {
 
 int check_codec(const tq_codec* c) {
   if (!c) return set_error(TQ_ERR_INVALID, "codec is NULL");
-  if (c->d != 64 && c->d != 128 && c->d != 256)
-    return set_error(TQ_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, 256)", c->d);
+  if (c->d != 64 && c->d != 96 && c->d != 128 && c->d != 256)
+    return set_error(TQ_ERR_UNSUPPORTED, "head_dim %d not supported (64, 96, 128, 256)", c->d);
   if (c->bits_hi < 1 || c->bits_hi > 4 || c->bits_lo < 1 || c->bits_lo > 4)
     return set_error(TQ_ERR_UNSUPPORTED, "Unsupported bit-width: %d/%d. Use 1, 2, 3, or 4.",
                      c->bits_hi, c->bits_lo);
-  if (c->split <= 0 || c->split > c->d || (c->split % 32) != 0)
-    return set_error(TQ_ERR_UNSUPPORTED, "split %d must be a positive multiple of 32 <= d", c->split);
+  if (c->split <= 0 || c->split > c->d || (c->split % 16) != 0)
+    return set_error(TQ_ERR_UNSUPPORTED, "split %d must be a positive multiple of 16 <= d", c->split);
   if (!c->rotation || !c->centroids_hi || !c->boundaries_hi)
     return set_error(TQ_ERR_INVALID, "codec rotation / codebook pointer is NULL");
   if (c->split < c->d && (!c->centroids_lo || !c->boundaries_lo))
@@ -54,6 +54,8 @@ int check_codec(const tq_codec* c) {
 // is staged in LDS with each 32-column segment padded to 36 floats so that the
 // NSEG segments of a wave read distinct LDS banks.
 // ---------------------------------------------------------------------------
+// Thread (v, q) = (tid / NSEG, tid % NSEG); for D = 96 the last thread of the
+// 256 has no vector (v == VPW): it reads vector VPW - 1 and writes nothing.
 template <int D>
 struct Geo {
   static constexpr int NSEG = D / 32;          // 32-column segments
@@ -89,6 +91,24 @@ __device__ inline void load_codes_dyn(int bits, const uint8_t* src, uint32_t (&c
     case 3: load_codes<3>(src, code); break;
     default: load_codes<4>(src, code); break;
   }
+}
+
+// Codes c0 .. c0 + 15 of a segment as 2 BITS bytes of the LSB-first
+// bitstream, written / read byte by byte (rows whose byte offsets are not
+// dword multiples: head_dim 96 split in halves of 48 codes).
+__device__ inline void store_half(int bits, uint8_t* dst, const uint32_t (&code)[32], int c0) {
+  uint64_t w = 0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) w |= (uint64_t)code[c0 + k] << (bits * k);
+  for (int i = 0; i < 2 * bits; ++i) dst[i] = (uint8_t)(w >> (8 * i));
+}
+
+__device__ inline void load_half(int bits, const uint8_t* src, uint32_t (&code)[32], int c0) {
+  uint64_t w = 0;
+  for (int i = 0; i < 2 * bits; ++i) w |= (uint64_t)src[i] << (8 * i);
+  const uint32_t mask = (1u << bits) - 1u;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) code[c0 + k] = (uint32_t)(w >> (bits * k)) & mask;
 }
 
 // count of boundaries strictly below y (ties go low, NaN -> 0)
@@ -181,6 +201,8 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
 
   // Rotate: y = x_n @ R^T.
   const int v = tid / G::NSEG, q = tid % G::NSEG;
+  const bool vok = v < G::VPW;            // false only for the spare thread of D = 96
+  const int vr = vok ? v : G::VPW - 1;    // the vector row it reads
   float acc[32];
 #pragma unroll
   for (int c = 0; c < 32; ++c) acc[c] = 0.f;
@@ -188,27 +210,43 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
     __syncthreads();
     stage_tile<D, true>(a.rot, i0, mt);
     __syncthreads();
-    tile_madd<D>(xs + v * G::XS, mt, i0, q, acc);
+    tile_madd<D>(xs + vr * G::XS, mt, i0, q, acc);
   }
 
-  // Quantize + pack this thread's 32 coordinates.
-  const bool hi = 32 * q < a.split;
-  const int bits = hi ? a.bits_hi : a.bits_lo;
-  const float* bk = bnd[hi ? 0 : 1];
-  const int nb = (1 << bits) - 1;
+  // Quantize + pack this thread's 32 coordinates (columns 32q + c; column j
+  // uses the high-width codebook when j < split).
+  const bool split16 = (a.split & 31) != 0;  // a segment holds 16 codes of each width
   uint32_t code[32];
 #pragma unroll
-  for (int c = 0; c < 32; ++c) code[c] = quantize_one(acc[c], bk, nb);
+  for (int c = 0; c < 32; ++c) {
+    const bool hc = 32 * q + c < a.split;
+    code[c] = quantize_one(acc[c], bnd[hc ? 0 : 1], (1 << (hc ? a.bits_hi : a.bits_lo)) - 1);
+  }
   if (v < nv) {
-    uint8_t* dst;
-    if (hi) {
-      dst = a.dst.codes_hi + (int64_t)r * a.dst.hi_head_stride + (int64_t)(dst0 + v) * a.row_hi +
-            (32 * q) * bits / 8;
+    if (!split16) {
+      const bool hi = 32 * q < a.split;
+      const int bits = hi ? a.bits_hi : a.bits_lo;
+      uint8_t* dst;
+      if (hi) {
+        dst = a.dst.codes_hi + (int64_t)r * a.dst.hi_head_stride + (int64_t)(dst0 + v) * a.row_hi +
+              (32 * q) * bits / 8;
+      } else {
+        dst = a.dst.codes_lo + (int64_t)r * a.dst.lo_head_stride + (int64_t)(dst0 + v) * a.row_lo +
+              (32 * q - a.split) * bits / 8;
+      }
+      store_codes_dyn(bits, dst, code);
     } else {
-      dst = a.dst.codes_lo + (int64_t)r * a.dst.lo_head_stride + (int64_t)(dst0 + v) * a.row_lo +
-            (32 * q - a.split) * bits / 8;
+      for (int hh = 0; hh < 2; ++hh) {
+        const int j = 32 * q + 16 * hh;
+        const bool hi = j < a.split;
+        const int bits = hi ? a.bits_hi : a.bits_lo;
+        uint8_t* dst = hi ? a.dst.codes_hi + (int64_t)r * a.dst.hi_head_stride + (int64_t)(dst0 + v) * a.row_hi +
+                                j * bits / 8
+                          : a.dst.codes_lo + (int64_t)r * a.dst.lo_head_stride + (int64_t)(dst0 + v) * a.row_lo +
+                                (j - a.split) * bits / 8;
+        store_half(bits, dst, code, 16 * hh);
+      }
     }
-    store_codes_dyn(bits, dst, code);
   }
 
   if (!a.proj) return;
@@ -216,10 +254,9 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
   // QJL sketch of the residual r = x - n * (c[idx] @ R) (cache.py:396-427).
   // Reconstruct in rotated space first: xs[v][j] <- c[idx_j] (overwrites x_n).
   __syncthreads();
-  {
-    const float* ck = cen[hi ? 0 : 1];
+  if (vok) {
 #pragma unroll
-    for (int c = 0; c < 32; ++c) xs[v * G::XS + 32 * q + c] = ck[code[c]];
+    for (int c = 0; c < 32; ++c) xs[v * G::XS + 32 * q + c] = cen[32 * q + c < a.split ? 0 : 1][code[c]];
   }
 #pragma unroll
   for (int c = 0; c < 32; ++c) acc[c] = 0.f;
@@ -227,11 +264,11 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
     __syncthreads();
     stage_tile<D, false>(a.rot, i0, mt);
     __syncthreads();
-    tile_madd<D>(xs + v * G::XS, mt, i0, q, acc);
+    tile_madd<D>(xs + vr * G::XS, mt, i0, q, acc);
   }
   __syncthreads();
   // residual in xs (float32: x - n * acc)
-  {
+  if (vok) {
     const float n = nrm[v];
 #pragma unroll
     for (int c = 0; c < 32; ++c) {
@@ -266,7 +303,7 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
             mrow < a.qjl_m ? a.proj[(int64_t)mrow * D + i0 + ii] : 0.f;
       }
       __syncthreads();
-      tile_madd<D>(xs + v * G::XS, mt, i0, q, acc);
+      tile_madd<D>(xs + vr * G::XS, mt, i0, q, acc);
     }
     if (v < nv && qs < nseg_m) {
       uint32_t word = 0;
@@ -428,22 +465,38 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
   }
   __syncthreads();
   const int v = tid / G::NSEG, q = tid % G::NSEG;
-  const bool hi = 32 * q < a.split;
-  const int bits = hi ? a.bits_hi : a.bits_lo;
+  const bool vok = v < G::VPW;            // false only for the spare thread of D = 96
+  const int vr = vok ? v : G::VPW - 1;
   uint32_t code[32];
   if (v < nv) {
-    const uint8_t* src = hi ? a.src.codes_hi + (int64_t)r * a.src.hi_head_stride +
-                                  (int64_t)(src0 + v) * a.row_hi + (32 * q) * bits / 8
-                            : a.src.codes_lo + (int64_t)r * a.src.lo_head_stride +
-                                  (int64_t)(src0 + v) * a.row_lo + (32 * q - a.split) * bits / 8;
-    load_codes_dyn(bits, src, code);
+    if ((a.split & 31) == 0) {
+      const bool hi = 32 * q < a.split;
+      const int bits = hi ? a.bits_hi : a.bits_lo;
+      const uint8_t* src = hi ? a.src.codes_hi + (int64_t)r * a.src.hi_head_stride +
+                                    (int64_t)(src0 + v) * a.row_hi + (32 * q) * bits / 8
+                              : a.src.codes_lo + (int64_t)r * a.src.lo_head_stride +
+                                    (int64_t)(src0 + v) * a.row_lo + (32 * q - a.split) * bits / 8;
+      load_codes_dyn(bits, src, code);
+    } else {  // halves of 16 codes, byte loads
+      for (int hh = 0; hh < 2; ++hh) {
+        const int j = 32 * q + 16 * hh;
+        const bool hi = j < a.split;
+        const int bits = hi ? a.bits_hi : a.bits_lo;
+        const uint8_t* src = hi ? a.src.codes_hi + (int64_t)r * a.src.hi_head_stride +
+                                      (int64_t)(src0 + v) * a.row_hi + j * bits / 8
+                                : a.src.codes_lo + (int64_t)r * a.src.lo_head_stride +
+                                      (int64_t)(src0 + v) * a.row_lo + (j - a.split) * bits / 8;
+        load_half(bits, src, code, 16 * hh);
+      }
+    }
   } else {
 #pragma unroll
     for (int c = 0; c < 32; ++c) code[c] = 0;
   }
-  const float* ck = cen[hi ? 0 : 1];
+  if (vok) {
 #pragma unroll
-  for (int c = 0; c < 32; ++c) ys[v * G::XS + 32 * q + c] = ck[code[c]];
+    for (int c = 0; c < 32; ++c) ys[v * G::XS + 32 * q + c] = cen[32 * q + c < a.split ? 0 : 1][code[c]];
+  }
   float acc[32];
 #pragma unroll
   for (int c = 0; c < 32; ++c) acc[c] = 0.f;
@@ -451,7 +504,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
     __syncthreads();
     stage_tile<D, false>(a.rot, i0, mt);
     __syncthreads();
-    tile_madd<D>(ys + v * G::XS, mt, i0, q, acc);
+    tile_madd<D>(ys + vr * G::XS, mt, i0, q, acc);
   }
   const float n = v < nv ? a.src.norms[(int64_t)r * a.src.norm_head_stride + src0 + v] : 0.f;
 #pragma unroll
@@ -476,7 +529,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
 #pragma unroll
         for (int c = 0; c < 32; ++c)
           ys[v * G::XS + 32 * q + c] = seg < nseg_m ? (((w >> c) & 1u) ? 1.f : -1.f) : 0.f;
-      } else {
+      } else if (vok) {
 #pragma unroll
         for (int c = 0; c < 32; ++c) ys[v * G::XS + 32 * q + c] = 0.f;
       }
@@ -485,7 +538,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
         __syncthreads();
         stage_tile<D, false>(a.proj + (int64_t)m0 * D, i0, mt);
         __syncthreads();
-        tile_madd<D>(ys + v * G::XS, mt, i0, q, corr);
+        tile_madd<D>(ys + vr * G::XS, mt, i0, q, corr);
       }
     }
     if (v < nv) {
@@ -695,6 +748,11 @@ int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x
       hipLaunchKernelGGL(compress_kernel<64>, g, dim3(256), 0, s, a);
       break;
     }
+    case 96: {
+      dim3 g((span->n_tok + Geo<96>::VPW - 1) / Geo<96>::VPW, span->rows);
+      hipLaunchKernelGGL(compress_kernel<96>, g, dim3(256), 0, s, a);
+      break;
+    }
     case 128: {
       dim3 g((span->n_tok + Geo<128>::VPW - 1) / Geo<128>::VPW, span->rows);
       hipLaunchKernelGGL(compress_kernel<128>, g, dim3(256), 0, s, a);
@@ -746,6 +804,11 @@ int tq_dequantize(const tq_codec* codec, const tq_store* src, const tq_span* spa
     case 64: {
       dim3 g((span->n_tok + Geo<64>::VPW - 1) / Geo<64>::VPW, span->rows);
       hipLaunchKernelGGL(dequant_kernel<64>, g, dim3(256), 0, s, a);
+      break;
+    }
+    case 96: {
+      dim3 g((span->n_tok + Geo<96>::VPW - 1) / Geo<96>::VPW, span->rows);
+      hipLaunchKernelGGL(dequant_kernel<96>, g, dim3(256), 0, s, a);
       break;
     }
     case 128: {

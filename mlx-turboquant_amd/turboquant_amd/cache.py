@@ -41,7 +41,8 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
-# query heads per kv head the decode-attention kernels serve
+# query heads per kv head of the dense fp16 / bf16 decode kernel (the packed
+# route, TurboQuantKVCache.attend, takes any integer ratio)
 ATTEND_GROUPS = (1, 2, 4, 8)
 
 
@@ -97,7 +98,7 @@ class TurboQuantKVCache:
     """TurboQuant-compressed KV cache (cache.py:19-116)."""
 
     step = 256
-    ATTEND_HEAD_DIMS = (64, 128, 256)  # head_dims of the codecs and the decode-attention kernels
+    ATTEND_HEAD_DIMS = (64, 96, 128, 256)  # head_dims of the codecs and the decode-attention kernels
 
     def __init__(self, head_dim: int = 128, num_kv_heads: int = 1, key_bits: float = 4,
                  value_bits: float = 2, residual_window: int = 128, rotation_seed: int = DEFAULT_SEED,
@@ -369,8 +370,8 @@ class TurboQuantKVCache:
         """Decode attention of one query token per head over the whole cache,
         scoring compressed tokens directly from packed codes.
 
-        ``queries``: (B, Hq, 1, D) or (B, Hq, D); Hq a multiple (1, 2, 4, 8) of
-        the kv heads, query head h reads kv head h // (Hq / Hkv). Returns
+        ``queries``: (B, Hq, 1, D) or (B, Hq, D); Hq any multiple of the kv
+        heads, query head h reads kv head h // (Hq / Hkv). Returns
         float32 (B, Hq, 1, D): softmax(scale * q K^T) V over the same tokens
         update_and_fetch would return (default scale D**-0.5).
         ``general_kernel`` forces the general kernel where the K4/V2 fast

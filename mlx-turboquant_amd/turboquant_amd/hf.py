@@ -64,12 +64,13 @@ def model_heads(config) -> tuple[int, int, int]:
 
 def fused_supported(cache, hq: int, hkv: int, head_dim: int) -> bool:
     """Whether the decode kernels serve a layer of this shape: the packed
-    route (``TurboQuantKVCache.attend``) or the dense fp16 / bf16 kernel
-    (``FP16KVCache.attend``, head_dim 128)."""
-    if hkv <= 0 or hq % hkv or hq // hkv not in ATTEND_GROUPS:
+    route (``TurboQuantKVCache.attend``: any integer query-head ratio) or the
+    dense fp16 / bf16 kernel (``FP16KVCache.attend``: head_dim 128, ratios
+    1, 2, 4, 8)."""
+    if hkv <= 0 or hq % hkv:
         return False
     if isinstance(cache, FP16KVCache):
-        return head_dim == 128
+        return head_dim == 128 and hq // hkv in ATTEND_GROUPS
     return head_dim in TurboQuantKVCache.ATTEND_HEAD_DIMS
 
 

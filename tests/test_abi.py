@@ -71,8 +71,13 @@ def test_host_side_validation_errors():
     assert lib.tq_pack_codes(None, 1, 128, 5, None, None) == _lib.TQ_ERR_UNSUPPORTED
     assert b"Unsupported bit-width" in lib.tq_last_error()
     assert lib.tq_unpack_codes(None, 1, 5, 3, None, None) == _lib.TQ_ERR_INVALID
-    codec = _lib.Codec(d=96, bits_hi=4, bits_lo=4, split=96)
+    codec = _lib.Codec(d=80, bits_hi=4, bits_lo=4, split=80)
     assert lib.tq_compress(ctypes.byref(codec), None, 0, 0, None, None, None) == _lib.TQ_ERR_UNSUPPORTED
+    assert b"head_dim 80" in lib.tq_last_error()
+    codec = _lib.Codec(d=96, bits_hi=4, bits_lo=3, split=40)  # halves of 16 codes at most
+    assert lib.tq_compress(ctypes.byref(codec), None, 0, 0, None, None, None) == _lib.TQ_ERR_UNSUPPORTED
+    codec = _lib.Codec(d=96, bits_hi=4, bits_lo=3, split=48)  # a valid shape: the NULL rotation is refused
+    assert lib.tq_compress(ctypes.byref(codec), None, 0, 0, None, None, None) == _lib.TQ_ERR_INVALID
     assert lib.tq_pack_codes(None, 0, 128, 4, None, None) == _lib.TQ_OK  # empty is a no-op
     # dense decode attention: head_dim, compressed tokens, K/V dtype, group size
     d = _lib.AttnDesc(batch=1, hq=8, hkv=2, max_sink=4, q_dtype=_lib.TQ_F16, kv_dtype=_lib.TQ_F16,

@@ -94,9 +94,12 @@ def test_compressed_decode_loop(cpu_cache):
 
 def test_fused_cache_under_sdpa_and_unsupported_groups(cpu_cache):
     """A fused cache never takes the kernel route unless the model's
-    attention is "turboquant" and the layer shape is served: under SDPA, and
-    for 3 query heads per kv head, every step returns the dense K/V (the
-    kernels cannot run on this CPU-only box, so a fused step would raise)."""
+    attention is "turboquant" and the layer shape is served: under SDPA every
+    step returns the dense K/V, and so does an uncompressed (FP16KVCache)
+    layer with 3 query heads per kv head, which the dense decode kernel does
+    not serve (the kernels cannot run on this CPU-only box, so a fused step
+    would raise). A compressed layer of that shape is fused: the packed
+    route takes any ratio."""
     from transformers import LlamaConfig, LlamaForCausalLM
     from turboquant_amd import apply_turboquant
     from turboquant_amd.hf import TurboQuantCache
@@ -115,6 +118,9 @@ def test_fused_cache_under_sdpa_and_unsupported_groups(cpu_cache):
     m3 = LlamaForCausalLM(cfg).eval()
     apply_turboquant(m3, key_bits=4, value_bits=2, residual_window=16, auto_detect_outliers=False)
     m3.set_attn_implementation("turboquant")
+    assert all(layer.fused for layer in TurboQuantCache(m3, fused=True).layers)
+    apply_turboquant(m3, key_bits=4, value_bits=2, residual_window=16, auto_detect_outliers=False,
+                     skip_layers=[0, 1])
     cache = TurboQuantCache(m3, fused=True)
     assert not any(layer.fused for layer in cache.layers)
     with torch.no_grad():

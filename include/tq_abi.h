@@ -207,7 +207,10 @@ typedef struct tq_attn_desc {
                                            entry gives a wrong result for its sequence, never an access
                                            outside the stores, sink or ring). */
   int32_t flags;                        /* TQ_ATTN_* bits */
-  int32_t reserved2;
+  int32_t n_q;                          /* query tokens per sequence: 0 / 1 decode; > 1 the last n_q
+                                           tokens of each sequence attend causally (query i sees
+                                           positions <= total - n_q + i), q and out (batch, hq, n_q, d),
+                                           general kernel (cache.py:722-724 "causal" prefill mask) */
 } tq_attn_desc;
 
 /* tq_attn_desc.flags: force the general kernel (every width / QJL) even where

@@ -64,13 +64,20 @@ struct AttnArgs {
 
 __host__ __device__ inline int part_stride(int D, int m) { return ((2 + D + m) + 3) & ~3; }
 
+// Query row (b, h, query token qi) of the call: q is (batch, hq, n_q, d).
+// The general path treats query token qi of sequence b as its own row vb =
+// b n_q + qi of the workspace (qr / qs / sq / partials are (batch n_q, hq, .)).
+__device__ inline int nq_of(const tq_attn_desc& d) { return d.n_q > 1 ? d.n_q : 1; }
+
 __global__ void prologue_kernel(AttnArgs a) {
   extern __shared__ float sm[];
-  const int h = blockIdx.x, b = blockIdx.y, D = a.D;
-  const int64_t qo = ((int64_t)b * a.d.hq + h) * D;
+  const int h = blockIdx.x, vb = blockIdx.y, D = a.D;
+  const int nq = nq_of(a.d), b = vb / nq, qi = vb % nq;
+  const int64_t qin = (((int64_t)b * a.d.hq + h) * nq + qi) * D;
+  const int64_t qo = ((int64_t)vb * a.d.hq + h) * D;
   float* qsm = sm;
   for (int i = threadIdx.x; i < D; i += blockDim.x) {
-    const float v = a.d.scale * load_elem(a.d.q, qo + i, a.d.q_dtype);
+    const float v = a.d.scale * load_elem(a.d.q, qin + i, a.d.q_dtype);
     qsm[i] = v;
     a.qs[qo + i] = v;
   }
@@ -82,7 +89,7 @@ __global__ void prologue_kernel(AttnArgs a) {
     a.qr[qo + j] = acc;
   }
   if (a.m > 0) {
-    const int64_t so = ((int64_t)b * a.d.hq + h) * a.m;
+    const int64_t so = ((int64_t)vb * a.d.hq + h) * a.m;
     for (int i = threadIdx.x; i < a.m; i += blockDim.x) {
       const float* si = a.proj + (int64_t)i * D;
       float acc = 0.f;
@@ -221,8 +228,10 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   __shared__ __align__(16) uint8_t ksg[CHUNK * SR];    // key sign rows (QJL)
   __shared__ __align__(16) uint8_t vsg[CHUNK * SR];    // value sign rows (QJL)
   __shared__ float slice[G][NT];                       // per-thread partial sums of the PV / QJL phases
-  // group g: query heads [g G, g G + G) of kv head g / gsub
-  const int c = blockIdx.x + a.c0, g = blockIdx.y, b = blockIdx.z;
+  // group g: query heads [g G, g G + G) of kv head g / gsub; query token qi
+  // of sequence b (row vb of the workspace)
+  const int c = blockIdx.x + a.c0, g = blockIdx.y, vb = blockIdx.z;
+  const int nq = nq_of(a.d), b = vb / nq, qi = vb % nq;
   const int hq = a.d.hq, tid = threadIdx.x;
   const int row = b * a.d.hkv + g / a.gsub;
 
@@ -231,23 +240,27 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   if (c < a.nc) { seg = 0; base = c * CHUNK; }
   else if (c < a.nc + a.ns) { seg = 1; base = (c - a.nc) * CHUNK; }
   else { seg = 2; base = (c - a.nc - a.ns) * CHUNK; }
-  int len;
-  if (seg == 0) len = seq_comp(a.d, b);
-  else if (seg == 1) len = a.d.sink_len ? clamp_len(a.d.sink_len[b], a.d.max_sink) : a.d.max_sink;
-  else len = a.d.res_len ? clamp_len(a.d.res_len[b], a.d.max_res) : a.d.max_res;
+  const int len_c = seq_comp(a.d, b);
+  const int len_s = a.d.sink_len ? clamp_len(a.d.sink_len[b], a.d.max_sink) : a.d.max_sink;
+  const int len_r = a.d.res_len ? clamp_len(a.d.res_len[b], a.d.max_res) : a.d.max_res;
+  const int len = seg == 0 ? len_c : seg == 1 ? len_s : len_r;
   const int nvalid = max(0, min(CHUNK, len - base));
+  // causal: the n_q queries are the last n_q tokens of [sink | compressed |
+  // residual]; query qi sees positions <= total - n_q + qi (cache.py:722-724)
+  const int pos0 = (seg == 0 ? len_s : seg == 1 ? 0 : len_s + len_c) + base;  // position of token base
+  const int lim = len_s + len_c + len_r - nq + qi;
 
   const bool packed = seg == 0;
   const bool qjl = packed && a.m > 0;
   for (int e = tid; e < G * D; e += NT) {
     const int h = e / D, j = e % D;
-    const int64_t qo = ((int64_t)b * hq + g * G + h) * D + j;
+    const int64_t qo = ((int64_t)vb * hq + g * G + h) * D + j;
     qv[h][j] = packed ? a.qr[qo] : a.qs[qo];
   }
   if (qjl) {
     for (int e = tid; e < G * a.m; e += NT) {
       const int h = e / a.m, i = e % a.m;
-      sqv[h][i] = a.sq[((int64_t)b * hq + g * G + h) * a.m + i];
+      sqv[h][i] = a.sq[((int64_t)vb * hq + g * G + h) * a.m + i];
     }
   }
   if (tid < 16) {
@@ -284,7 +297,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
 #pragma unroll
   for (int h = 0; h < G; ++h) s[h] = -INFINITY;
   const int t = tid;
-  if (t < nvalid) {
+  if (t < nvalid && pos0 + t <= lim) {
 #pragma unroll
     for (int h = 0; h < G; ++h) s[h] = 0.f;
     if (packed) {
@@ -430,7 +443,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
     float v = 0.f;
 #pragma unroll
     for (int sl = 0; sl < TSL; ++sl) v += slice[h][sl * D + j];
-    outp[(((int64_t)b * hq + g * G + h) * a.nch + c) * a.ps + 2 + j] = v;
+    outp[(((int64_t)vb * hq + g * G + h) * a.nch + c) * a.ps + 2 + j] = v;
   }
   // QJL value term az[h][i] = sum_t p_t gamma_t z_t,i: thread (i, sl) over
   // token slice sl of NT / m, each sign bit read once for all G heads
@@ -465,11 +478,11 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
       const int h = e / a.m, ii = e % a.m;
       float v = 0.f;
       for (int q = 0; q < nsl; ++q) v += slice[h][q * a.m + ii];
-      outp[(((int64_t)b * hq + g * G + h) * a.nch + c) * a.ps + 2 + D + ii] = v;
+      outp[(((int64_t)vb * hq + g * G + h) * a.nch + c) * a.ps + 2 + D + ii] = v;
     }
   }
   if (tid < G) {
-    float* pp = outp + (((int64_t)b * hq + g * G + tid) * a.nch + c) * a.ps;
+    float* pp = outp + (((int64_t)vb * hq + g * G + tid) * a.nch + c) * a.ps;
     pp[0] = mx[tid];
     pp[1] = lsum[tid];
   }
@@ -483,10 +496,11 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
 __global__ __launch_bounds__(128) void combine_kernel(AttnArgs a) {
   extern __shared__ float sm[];
   __shared__ float rmax[2], rsum[2];
-  const int h = blockIdx.x, b = blockIdx.y, D = a.D, tid = threadIdx.x;
+  const int h = blockIdx.x, vb = blockIdx.y, D = a.D, tid = threadIdx.x;
+  const int nq = nq_of(a.d), b = vb / nq, qi = vb % nq;
   const int hq = a.d.hq, nch = a.nch;
   const int64_t ps = a.ps;
-  const float* pp = a.part + ((int64_t)b * hq + h) * nch * ps;
+  const float* pp = a.part + ((int64_t)vb * hq + h) * nch * ps;
   float* wc = sm;                       // [nch] chunk weights
   float* accr = sm + ((nch + 3) & ~3);  // [D] weighted rotated sum
   float* azs = accr + D;                // [m] weighted QJL projections
@@ -523,7 +537,7 @@ __global__ __launch_bounds__(128) void combine_kernel(AttnArgs a) {
   for (int j = tid; j < D; j += 128) accr[j] = wsum(0, a.nc, 2 + j);
   for (int i = tid; i < a.m; i += 128) azs[i] = wsum(0, a.nc, 2 + D + i);
   __syncthreads();
-  float* out = a.d.out + ((int64_t)b * hq + h) * D;
+  float* out = a.d.out + (((int64_t)b * hq + h) * nq + qi) * D;
   for (int j = tid; j < D; j += 128) {
     float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
     for (int i = 0; i < D; i += 4) {
@@ -857,6 +871,7 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // codec needs its exact fp16 table (value_table_err).
 static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, bool qjl_ok = false) {
   const int G = d->hq / d->hkv;
+  if (d->n_q > 1) return false;  // one query token per sequence
   if (!(kc->rotation_parts != nullptr && kc->decode_table != nullptr && vc->decode_table != nullptr &&
         kc->n_host_centroids == 16 && vc->n_host_centroids == 4 && vc->d == 128 && kc->d == 128 &&
         kc->bits_hi == 4 && kc->split == 128 &&
@@ -1023,6 +1038,7 @@ static int dense_check(const tq_attn_desc* d, int D, bool record = true) {
 #define DENSE_FAIL(code, ...) return record ? set_error(code, __VA_ARGS__) : (code)
   if (D != 128) DENSE_FAIL(TQ_ERR_UNSUPPORTED, "dense decode attention: head_dim %d != 128", D);
   if (d->max_comp != 0) DENSE_FAIL(TQ_ERR_INVALID, "dense decode attention with compressed tokens (max_comp %d)", d->max_comp);
+  if (d->n_q > 1) DENSE_FAIL(TQ_ERR_UNSUPPORTED, "dense decode attention: one query token (n_q %d)", d->n_q);
   if (d->batch <= 0 || d->hkv <= 0 || d->hq <= 0 || d->hq % d->hkv)
     DENSE_FAIL(TQ_ERR_INVALID, "bad head counts hq=%d hkv=%d batch=%d", d->hq, d->hkv, d->batch);
   const int G = d->hq / d->hkv;
@@ -1118,7 +1134,7 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
   const int D = kcodec->d;
   const int m = d->qjl ? kcodec->qjl_m : 0;
   const size_t nch = (size_t)(nc + ns + nr);
-  const size_t heads = (size_t)d->batch * d->hq;
+  const size_t heads = (size_t)d->batch * d->hq * (d->n_q > 1 ? d->n_q : 1);  // query rows
   size_t general = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
   const size_t fast = d->hkv > 0 && d->hq % d->hkv == 0 ? fast_part_bytes(d) : 0;
   size_t bytes = general > fast ? general : fast;
@@ -1144,8 +1160,13 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   if (d->batch <= 0 || d->hkv <= 0 || d->hq <= 0 || d->hq % d->hkv)
     return set_error(TQ_ERR_INVALID, "bad head counts hq=%d hkv=%d batch=%d", d->hq, d->hkv, d->batch);
   const int G = d->hq / d->hkv;  // any integer ratio: the general kernel groups the heads by group_heads(G)
-  if (d->batch > 65535 || (int64_t)d->hkv * (G / group_heads(G)) > 65535 || d->hq > 65535)
+  if (d->n_q < 0) return set_error(TQ_ERR_INVALID, "n_q %d < 0", d->n_q);
+  if ((int64_t)d->batch * (d->n_q > 1 ? d->n_q : 1) > 65535 || (int64_t)d->hkv * (G / group_heads(G)) > 65535 ||
+      d->hq > 65535)
     return set_error(TQ_ERR_UNSUPPORTED, "grid too large");
+  if (d->n_q > 1 && d->n_q > d->max_sink + d->max_comp + d->max_res)
+    return set_error(TQ_ERR_INVALID, "n_q %d query tokens > the %d cached tokens", d->n_q,
+                     d->max_sink + d->max_comp + d->max_res);
   if (d->max_comp < 0 || d->max_sink < 0 || d->max_res < 0)
     return set_error(TQ_ERR_INVALID, "negative segment length");
   if (!d->q || !d->out) return set_error(TQ_ERR_INVALID, "q/out is NULL");
@@ -1213,7 +1234,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   a.c0 = 0;
   const int gh = group_heads(G);
   a.gsub = G / gh;
-  const size_t heads = (size_t)d->batch * d->hq;
+  const size_t heads = (size_t)d->batch * d->hq * (d->n_q > 1 ? d->n_q : 1);  // query rows
   float* ws = static_cast<float*>(workspace);
   a.qr = ws;
   a.qs = a.qr + heads * a.D;
@@ -1221,10 +1242,11 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   a.part = a.sq + heads * a.m;
 
   const size_t pro_smem = (size_t)a.D * 4;
-  hipLaunchKernelGGL(prologue_kernel, dim3(d->hq, d->batch), dim3(128), pro_smem, s, a);
+  const int nq = d->n_q > 1 ? d->n_q : 1;
+  hipLaunchKernelGGL(prologue_kernel, dim3(d->hq, d->batch * nq), dim3(128), pro_smem, s, a);
   TQ_LAUNCH_CHECK("tq_decode_attention prologue");
   if (a.nch > 0) {
-    dim3 grid(a.nch, d->hkv * a.gsub, d->batch);
+    dim3 grid(a.nch, d->hkv * a.gsub, d->batch * nq);
     switch (a.D) {
       case 64: launch_chunks<64>(a, gh, grid, s); break;
       case 96: launch_chunks<96>(a, gh, grid, s); break;
@@ -1234,7 +1256,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     TQ_LAUNCH_CHECK("tq_decode_attention chunks");
   }
   const size_t cmb_smem = (size_t)(((a.nch + 3) & ~3) + a.D + a.m) * 4;
-  hipLaunchKernelGGL(combine_kernel, dim3(d->hq, d->batch), dim3(128), cmb_smem, s, a);
+  hipLaunchKernelGGL(combine_kernel, dim3(d->hq, d->batch * nq), dim3(128), cmb_smem, s, a);
   TQ_LAUNCH_CHECK("tq_decode_attention combine");
   return TQ_OK;
 }

@@ -67,7 +67,7 @@ class AttnDesc(ctypes.Structure):
                 ("sink_k", _p), ("sink_v", _p), ("sink_head_stride", _i64), ("sink_len", _p),
                 ("res_k", _p), ("res_v", _p), ("res_head_stride", _i64),
                 ("res_cap", _i32), ("res_start0", _i32),
-                ("res_start", _p), ("res_len", _p), ("flags", _i32), ("reserved2", _i32)]
+                ("res_start", _p), ("res_len", _p), ("flags", _i32), ("n_q", _i32)]
 
 TQ_ATTN_GENERAL = 1
 

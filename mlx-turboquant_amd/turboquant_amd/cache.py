@@ -367,31 +367,33 @@ class TurboQuantKVCache:
 
     def attend(self, queries: torch.Tensor, scale: float | None = None,
                out: torch.Tensor | None = None, general_kernel: bool = False) -> torch.Tensor:
-        """Decode attention of one query token per head over the whole cache,
-        scoring compressed tokens directly from packed codes.
+        """Attention of the query tokens over the whole cache, scoring
+        compressed tokens directly from packed codes.
 
-        ``queries``: (B, Hq, 1, D) or (B, Hq, D); Hq any multiple of the kv
-        heads, query head h reads kv head h // (Hq / Hkv). Returns
-        float32 (B, Hq, 1, D): softmax(scale * q K^T) V over the same tokens
+        ``queries``: (B, Hq, T_q, D) or (B, Hq, D) (T_q = 1); Hq any multiple
+        of the kv heads, query head h reads kv head h // (Hq / Hkv). With T_q
+        > 1 the queries are the cache's last T_q tokens and attend causally:
+        query i sees the first offset - T_q + i + 1 tokens (the reference's
+        "causal" prefill mask, cache.py:722-724). Returns float32
+        (B, Hq, T_q, D): softmax(scale * q K^T) V over the same tokens
         update_and_fetch would return (default scale D**-0.5).
         ``general_kernel`` forces the general kernel where the K4/V2 fast
         kernels would run (used to cross-check the two)."""
         if self._B is None or self.offset == 0:
             raise ValueError("attend() on an empty cache")
-        q = queries
-        if q.dim() == 4:
-            if q.shape[2] != 1:
-                raise ValueError("attend() handles one query token per head")
-            q = q[:, :, 0]
+        q = queries if queries.dim() == 4 else queries[:, :, None]
         q = q.contiguous()
-        B, hq, D = q.shape
+        B, hq, tq, D = q.shape
         if B != self._B or D != self.head_dim:
             raise ValueError(f"query shape {tuple(queries.shape)} does not match the cache")
+        if tq > self.offset:
+            raise ValueError(f"{tq} query tokens > the {self.offset} cached tokens")
         if scale is None:
             scale = D ** -0.5
         if out is None:
-            out = torch.empty(B, hq, 1, D, dtype=torch.float32, device=q.device)
+            out = torch.empty(B, hq, tq, D, dtype=torch.float32, device=q.device)
         desc = self.attention_descriptor(q, out, scale, general_kernel)
+        desc.n_q = tq
         lib = _lib.load()
         need = lib.tq_decode_workspace_bytes(self._kc.ref(), ctypes.byref(desc))
         ws = _workspace(q.device, need)

@@ -150,19 +150,11 @@ struct Tile {
   u4 v[8];
 };
 
-// Tile loads are issued as inline asm and waited for explicitly
-// (wait_tile): the two-tile rotation keeps exactly 16 loads (the other tile)
-// issued after the ones being waited for, a count the compiler's own wait
-// insertion loses at the loop's control-flow merges (it then waits for the
-// other tile too, which serialises the pipeline). The compiler does not see
-// these loads, so a wait it inserts for its own loads can only be longer than
-// needed, never shorter. The wait asm names the tile registers as in/out
-// operands, so no use of them moves above it.
+// Tile loads: 16-byte non-temporal loads the compiler sees (it inserts
+// every wait itself).
 template <int OFF>
 __device__ inline u4 gload(const void* p) {
-  u4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off offset:%2 nt" : "=v"(v) : "v"(p), "i"(OFF));
-  return v;
+  return __builtin_nontemporal_load(reinterpret_cast<const u4*>(static_cast<const uint8_t*>(p) + OFF));
 }
 
 __device__ inline void load_tile(Tile& t, const Blk& bk, int r, int q4) {
@@ -178,18 +170,6 @@ __device__ inline void load_tile(Tile& t, const Blk& bk, int r, int q4) {
 #pragma unroll
   for (int j = 0; j < 8; ++j)
     t.v[j] = gload<0>(bk.v + (int64_t)min(bk.off + slot_token(q4, j), last) * DD + 8 * r);
-}
-
-// Waits until at most N vector-memory loads are outstanding; the tile's
-// registers are then valid.
-template <int N>
-__device__ inline void wait_tile(Tile& t) {
-  asm volatile("s_waitcnt vmcnt(%16)"
-               : "+v"(t.k[0][0]), "+v"(t.k[0][1]), "+v"(t.k[0][2]), "+v"(t.k[0][3]),
-                 "+v"(t.k[1][0]), "+v"(t.k[1][1]), "+v"(t.k[1][2]), "+v"(t.k[1][3]),
-                 "+v"(t.v[0]), "+v"(t.v[1]), "+v"(t.v[2]), "+v"(t.v[3]),
-                 "+v"(t.v[4]), "+v"(t.v[5]), "+v"(t.v[6]), "+v"(t.v[7])
-               : "i"(N));
 }
 
 template <int G, bool BF>
@@ -253,9 +233,6 @@ __global__ __launch_bounds__(DT) __attribute__((amdgpu_waves_per_eu(2))) void de
     load_tile(t0, first, r, q4);
     load_tile(t1, second, r, q4);
   }
-  asm volatile("s_waitcnt vmcnt(32)"
-               : "+v"(qr[0]), "+v"(qr[1]), "+v"(qr[2]), "+v"(qr[3]), "+v"(qr[4]), "+v"(qr[5]), "+v"(qr[6]),
-                 "+v"(qr[7]));
 
   u4 qop[4];
   {
@@ -358,10 +335,8 @@ __global__ __launch_bounds__(DT) __attribute__((amdgpu_waves_per_eu(2))) void de
     const int npair = ((jend - jbeg + DW - 1) / DW + 1) / 2;
     for (int it = 0; it < npair; ++it) {
       const int j = jbeg + 2 * DW * it;
-      wait_tile<16>(t0);
       compute(t0, block_at(sq, j));
       load_tile(t0, block_at(sq, min(j + 2 * DW, jend - 1)), r, q4);
-      wait_tile<16>(t1);
       compute(t1, j + DW < jend ? block_at(sq, j + DW) : Blk{nullptr, nullptr, 0, 0});
       load_tile(t1, block_at(sq, min(j + 3 * DW, jend - 1)), r, q4);
     }
@@ -413,10 +388,6 @@ __global__ __launch_bounds__(DT) __attribute__((amdgpu_waves_per_eu(2))) void de
       }
     }
   }
-  // the last refills (and, for a wave without blocks, the first two) are
-  // still in flight: keep their registers reserved until they have landed
-  wait_tile<0>(t0);
-  wait_tile<0>(t1);
 }
 
 template <int G>

@@ -649,12 +649,27 @@ typedef uint32_t qu4 __attribute__((ext_vector_type(4)));
 // remainder; k = 32 tokens of a block), B = Z (k = the same tokens, columns =
 // 16 projections, exact +-1 built from the staged sign rows), so output rows h
 // and h + 8 added give head h. Wave w takes the projection tiles w, w + 4, ...
+// max over the 64 lanes of a wave in VALU cross-lane moves: DPP rotations
+// within each 16-lane row, then the four rows (every lane gets the result)
+__device__ inline float wave_max_dpp(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xF, 0xF, true)));
+  const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+  const auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
+}
+
 template <int G>
 __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
-  constexpr int SR = 256 / 8 + 4;  // padded LDS sign row (bytes)
   __shared__ __align__(16) float pw[G][QCH];
-  __shared__ __align__(16) uint8_t sg[QCH * SR];
+  // sign words transposed: sgw[k][t] = projections 32k .. 32k + 31 of token
+  // t, so a lane reads its 8 consecutive tokens' words in two 16-byte loads
+  __shared__ __align__(16) uint32_t sgw[256 / 32][QCH];
   __shared__ uint32_t wmx[G];  // per head: the chunk's max weight (float bits; weights are >= 0)
+  __shared__ float invl[G];    // per head: 1 / L
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq;
   const int comp = seq_comp(a.d, b);
@@ -679,16 +694,23 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
         const float M = a.ml[((int64_t)b * hq + g * G + h) * 2], L = a.ml[((int64_t)b * hq + g * G + h) * 2 + 1];
         const float sc = a.scores[((int64_t)row * G + h) * a.qb_hs + base + t];
         p = L > 0.f ? __builtin_amdgcn_exp2f(sc - M) : 0.f;
+        if (t == 0) invl[h] = L > 0.f ? 1.f / L : 0.f;
       }
       const float wt = p * gv;
       pw[h][t] = wt;
-      float mx = wt;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      const float mx = wave_max_dpp(wt);
       if ((tid & 63) == 0) atomicMax(&wmx[h], __float_as_uint(mx));
     }
   }
-  stage_rows(sg, SR, 0, vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base * (m / 8), m / 8, nvalid);
+  {
+    const uint32_t* gs = reinterpret_cast<const uint32_t*>(vs.signs + (int64_t)row * vs.sign_head_stride +
+                                                           (int64_t)base * (m / 8));
+    const int nw = m / 32;
+    for (int e = tid; e < nvalid * nw; e += NT) {
+      const int t = e / nw, k = e - t * nw;
+      sgw[k][t] = gs[e];
+    }
+  }
   __syncthreads();
   // head h's weights enter fp16 as w 2^(14 - E_h) (E_h the exponent of the
   // chunk's max weight: operands below 2^15, none subnormal but the tiny)
@@ -703,6 +725,7 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   // A operands of the (at most 8) blocks: weights of head h, the fp16 high
   // part (rows < 8) or remainder (rows >= 8); zero past G and past nvalid
   qu4 aw[QCH / 32];
+  const float up_h = h < G ? __builtin_amdgcn_ldexpf(1.f, 14 - head_exp(h)) : 0.f;
 #pragma unroll
   for (int bk = 0; bk < QCH / 32; ++bk) {
     const int t0 = 32 * bk + 8 * q4;  // the lane's 8 tokens (k-slots 8 q4 .. 8 q4 + 7)
@@ -710,9 +733,8 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
     for (int e = 0; e < 4; ++e) {
       float w0 = 0.f, w1 = 0.f;
       if (h < G) {
-        const float up = __builtin_amdgcn_ldexpf(1.f, 14 - head_exp(h));
-        w0 = pw[h][t0 + 2 * e] * up;
-        w1 = pw[h][t0 + 2 * e + 1] * up;
+        w0 = pw[h][t0 + 2 * e] * up_h;
+        w1 = pw[h][t0 + 2 * e + 1] * up_h;
       }
       const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
       const _Float16 l0 = (_Float16)(w0 - (float)h0), l1 = (_Float16)(w1 - (float)h1);
@@ -728,12 +750,15 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
       const int t0 = 32 * bk + 8 * q4;
       const qu4 av = aw[bk];
       // B: +-1 of projection 16 ct + r for the lane's 8 tokens (bit set -> +1)
-      const int pj = 16 * ct + r;
+      const int pj = 16 * ct + r, bit = pj & 31;
+      const qu4 x0 = *reinterpret_cast<const qu4*>(&sgw[pj >> 5][t0]);
+      const qu4 x1 = *reinterpret_cast<const qu4*>(&sgw[pj >> 5][t0 + 4]);
+      const uint32_t xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
       qu4 bv;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t s0 = (sg[(t0 + 2 * e) * SR + (pj >> 3)] >> (pj & 7)) & 1u;
-        const uint32_t s1 = (sg[(t0 + 2 * e + 1) * SR + (pj >> 3)] >> (pj & 7)) & 1u;
+        const uint32_t s0 = (xs[2 * e] >> bit) & 1u;
+        const uint32_t s1 = (xs[2 * e + 1] >> bit) & 1u;
         bv[e] = 0xBC00BC00u ^ (s0 << 15) ^ (s1 << 31);
       }
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qh8, av), __builtin_bit_cast(qh8, bv), acc, 0, 0,
@@ -746,8 +771,7 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
       const float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
       const int hh = 4 * q4 + i;
       if (q4 < 2 && hh < G) {
-        const float L = a.ml[((int64_t)b * hq + g * G + hh) * 2 + 1];
-        const float down = L > 0.f ? __builtin_amdgcn_ldexpf(1.f, head_exp(hh) - 14) / L : 0.f;
+        const float down = __builtin_amdgcn_ldexpf(invl[hh], head_exp(hh) - 14);
         a.upart[(((int64_t)b * hq + g * G + hh) * a.nvc + c) * m + 16 * ct + r] = v * down;
       }
     }

@@ -110,6 +110,34 @@ def time_graph(fn, reps: int, warmup: int):
     return st.elapsed_time(en) / reps, wall, g
 
 
+def bench_layer_batched(dev, layers: int, ctx: int, reps: int, warmup: int):
+    """The 32 layers' decode attention as ONE launch: a cache whose batch
+    holds one configs[1]-shaped layer per sequence (same per-layer shapes and
+    bytes), attended with one call. Not a decode step a model can take (layer
+    l + 1's query needs layer l's output); it shows the per-launch fixed cost
+    the per-layer figure pays."""
+    import torch
+    from turboquant_amd import TurboQuantKVCache
+    g = torch.Generator(device=dev).manual_seed(3000)
+    scale = torch.exp(torch.randn(128, generator=g, device=dev) * 0.5)
+    c = TurboQuantKVCache(head_dim=128, num_kv_heads=8, key_bits=4, value_bits=2, residual_window=128,
+                          fp16_sink_size=128)
+    k = (torch.randn(layers, 8, ctx, 128, generator=g, device=dev) * scale).half()
+    v = torch.randn(layers, 8, ctx, 128, generator=g, device=dev).half()
+    c.update(k, v)
+    del k, v
+    q = torch.randn(layers, 32, 1, 128, generator=g, device=dev).half()
+    out = torch.empty(layers, 32, 1, 128, dtype=torch.float32, device=dev)
+    ms, _, _ = time_graph(lambda: c.attend(q, out=out), reps, warmup)
+    nbytes = decode_bytes_per_layer(c, 32)
+    del c
+    torch.cuda.empty_cache()
+    return {"layers": layers, "us_per_launch": round(ms * 1e3, 3), "bytes": nbytes,
+            "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel": "uniform_decode_kernel<4> + uniform_merge_kernel<4>, batch = layers"}
+
+
 def bench_compress(dev, kb, vb, total=131072, chunk=4096, reps=3):
     import torch
     from turboquant_amd import TurboQuantKVCache
@@ -435,6 +463,9 @@ def main():
                      "bytes_per_launch": bytes_layer[0], "avg_launch_us": round(ms_kernel * 1e3, 3),
                      "whole_call_us": round(ms_step * 1e3 / len(caches), 3)},
     }
+    if not args.no_extra:
+        log("timing the layer-batched launch")
+        result["layer_batched"] = bench_layer_batched(dev, args.layers, args.ctx, args.steps, args.warmup)
     if not args.no_compress:
         log("timing compress")
         del outs

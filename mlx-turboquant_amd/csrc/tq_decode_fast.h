@@ -82,7 +82,7 @@ int launch_partial_merge(float* part, int nwg, int G, int hq, int hkv, int batch
 // [c bpw, (c + 1) bpw) and the fp16 tokens [c fpw, (c + 1) fpw) of the
 // [sink | ring] list; partials in original space (FAST_PART_FLOATS per query
 // head, nwg per (b, g)).
-constexpr int UNI_BLOCKS_PER_WAVE = 4;  // compressed blocks per wave
+constexpr int UNI_BLOCKS_PER_WAVE = 8;  // compressed blocks per wave at most (kernels for 4 and 8)
 constexpr int UNI_FP16_PER_WG = 16;     // fp16 tokens per workgroup, staged in LDS
 constexpr int UNI_MAX_WG = 256;         // workgroups per (sequence, kv head)
 

@@ -5,8 +5,8 @@
 //
 // Grid (nwg, hkv, batch): workgroup c of (sequence b, kv head g) owns
 //  - the compressed 32-token blocks [c*bpw, (c+1)*bpw) of the sequence (bpw <=
-//    32): wave w takes blocks c*bpw + w + 8k, k < 4, with two blocks' loads in
-//    flight while it computes;
+//    8 NPW, NPW = 4 or 8): wave w takes blocks c*bpw + w + 8k, k < NPW, with
+//    two blocks' loads in flight while it computes;
 //  - the fp16 tokens [c*fpw, (c+1)*fpw) (fpw <= 16) of the sequence's [sink |
 //    residual ring] list, staged in LDS during set-up and scored by wave 0
 //    (the first to be issued on its SIMD) before its compressed blocks.
@@ -71,7 +71,6 @@ constexpr int FW = FAST_WAVES;            // waves per workgroup (FW * 16 == FD)
 constexpr int FT = FW * 64;               // threads
 constexpr int PS = FAST_PART_FLOATS;      // floats per (workgroup, head) partial
 constexpr int P_OUT = 4;                  // partial: [M, L, pad, pad, out[128]]
-constexpr int NPW = UNI_BLOCKS_PER_WAVE;  // compressed blocks per wave
 constexpr int MAXWG = UNI_MAX_WG;         // workgroups per (sequence, kv head)
 constexpr int FROW = 272;                 // LDS row of a staged fp16 token (256 + 16 against bank conflicts)
 constexpr float M_INIT = -1e30f;          // running max before the first block
@@ -268,7 +267,9 @@ __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
 }
 
-template <int G, bool QB = false>
+// NPW: compressed blocks per wave (4, or 8 for long contexts and large
+// batches, where fewer workgroups pay the set-up and combine)
+template <int G, bool QB, int NPW>
 __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   __shared__ __align__(16) uint8_t smem[Layout::total];
 
@@ -915,7 +916,10 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
 
 template <int G, bool QB>
 static void launch_u(const UniformArgs& a, int merge, hipStream_t s) {
-  hipLaunchKernelGGL((uk::uniform_decode_kernel<G, QB>), dim3(a.nwg, a.hkv, a.batch), dim3(uk::FT), 0, s, a);
+  if (a.bpw > FAST_WAVES * 4)
+    hipLaunchKernelGGL((uk::uniform_decode_kernel<G, QB, 8>), dim3(a.nwg, a.hkv, a.batch), dim3(uk::FT), 0, s, a);
+  else
+    hipLaunchKernelGGL((uk::uniform_decode_kernel<G, QB, 4>), dim3(a.nwg, a.hkv, a.batch), dim3(uk::FT), 0, s, a);
   if (merge) hipLaunchKernelGGL((uk::uniform_merge_kernel<G>), dim3(2, a.hq, a.batch), dim3(64), 0, s, a);
 }
 

@@ -72,8 +72,11 @@ typedef struct tq_codec {
    * codebooks an exact fp16 copy for the K4/V2 decode kernels (value side):
    * centroids_hi[i] == value_scale * fp16 value_table[i] to within
    * value_table_err (relative). The K4/V2 route runs only when the key
-   * codec's host_centroids are set and the value codec's value_table_err <=
-   * 2e-7 (else the general kernels). */
+   * codec has rotation_parts, 16 host_centroids and its decode_table, and the
+   * value codec its decode_table with value_table_err <= 2e-7 (else the
+   * general kernels); a uniform batch (no per-sequence lengths) also uses
+   * the value codec's rotation_parts [2, 3] (without them the persistent
+   * kernel of ragged batches takes it). */
   float host_centroids[16];
   int32_t n_host_centroids;
   uint16_t value_table[4];

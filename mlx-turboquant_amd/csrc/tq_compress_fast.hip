@@ -110,12 +110,10 @@ __device__ inline uint32_t quant_table(float y, const uint8_t* smem, uint32_t tb
   return q.base + (y > q.bnd ? 1u : 0u);
 }
 
-// a * b with 0 * anything = 0 (also for an infinite or NaN a)
-__device__ inline float mul_zero_wins(float a, float b) {
-  float r;
-  asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
+// a * b with 0 * anything = 0 (also for an infinite or NaN a): the legacy
+// multiply, through its LLVM intrinsic (clang has no builtin for it)
+extern "C" __device__ float tq_fmul_legacy(float, float) __asm("llvm.amdgcn.fmul.legacy");
+__device__ inline float mul_zero_wins(float a, float b) { return tq_fmul_legacy(a, b); }
 
 template <int BH, int BL>
 __global__ __launch_bounds__(CTHR, 3) void compress_fast_kernel(CompressArgs a, Div tiles_per_row, Div heads,

@@ -196,3 +196,27 @@ def test_config4_ragged_decode(qjl_m, sink):
     a = rb.attend(q).cpu().numpy()
     b = rb.attend(q, general=True).cpu().numpy()
     assert rel_err(a, b) < 1e-4, f"config4 m={qjl_m}: fast route vs general kernel {rel_err(a, b):.3e}"
+
+
+def test_uniform_batch_with_ring_starts():
+    """Equal lengths with only the per-sequence ring starts given (no length
+    arrays): the uniform-batch kernels, which read res_start per sequence,
+    against the persistent kernel fed every array, and against float64."""
+    from turboquant_amd import _lib
+    from turboquant_amd.cache import _workspace
+    rb = make_batch([900, 900, 900], H=2, sink=16, window=32, seed=12)
+    for _ in range(45):  # the 33-slot rings wrap
+        step(rb)
+    assert len(set(rb.comp_len.tolist())) == 1 and len(set(rb.res_start.tolist())) == 1
+    q = torch.randn(rb.B, 2 * HQ_PER_KV, D, generator=rb.g, device=DEV).half()
+    ref = check_batch(rb, q, oracle_rows=[1], label="uniform ring starts (arrays)")
+    out = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+    d, arrays = rb.descriptor(q.contiguous(), out, D ** -0.5, False)
+    d.comp_len = d.sink_len = d.res_len = None  # uniform: only the ring starts per sequence
+    lib = _lib.load()
+    ws = _workspace(DEV, lib.tq_decode_workspace_bytes(rb.kc.ref(), ctypes.byref(d)))
+    _lib.check(lib.tq_decode_attention(rb.kc.ref(), rb.vc.ref(), ctypes.byref(d), ws.data_ptr(), ws.numel(),
+                                       _lib.stream_ptr(DEV)), "tq_decode_attention")
+    torch.cuda.synchronize()
+    del arrays
+    assert rel_err(out.cpu().numpy(), ref.cpu().numpy()) < 1e-5

@@ -390,6 +390,25 @@ def pmc_workload(ctx: int):
                       "dense_bytes_per_launch": 8 * 65536 * 512 + 32 * 128 * 2}), flush=True)
 
 
+def pmc_compress_workload():
+    """Short program for the compress counter runs: the copy of known size,
+    then the configs[2] K3/V2 prefill (131,072 tokens in 4096-token chunks)
+    twice, the second on warm codecs."""
+    import torch
+    from turboquant_amd import _lib
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    del src, dst
+    r = bench_compress(dev, 3, 2, reps=1)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "compress": r}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -401,6 +420,7 @@ def main():
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the configs[3] / configs[4] timings")
     ap.add_argument("--pmc-workload", action="store_true", help="short program for rocprofv3 --pmc runs")
+    ap.add_argument("--pmc-compress", action="store_true", help="short compress program for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -409,6 +429,9 @@ def main():
 
     if args.pmc_workload:
         pmc_workload(args.ctx)
+        return
+    if args.pmc_compress:
+        pmc_compress_workload()
         return
 
     import torch

@@ -479,7 +479,7 @@ def main():
         "wall_ms_per_step": round(wall_step, 5),
         "bytes_per_step": bytes_step,
         "roofline": {"kernel": "uniform_decode_kernel<4> (partials of one layer: q rotation, packed K4/V2 + fp16 "
-                               "blocks, workgroup combine, inverse rotation)",
+                               "blocks, workgroup combine; the merge kernel applies the inverse rotation)",
                      "bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if traffic else None,

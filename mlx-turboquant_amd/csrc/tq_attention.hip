@@ -868,10 +868,10 @@ static bool uniform_geometry(const tq_attn_desc* d, int& nwg, int& bpw, int& fpw
   return nwg <= UNI_MAX_WG;
 }
 
-// The uniform-batch kernels take a uniform call when the value codec has its
-// R^T parts.
+// The uniform-batch kernels take a uniform call (their merge applies the
+// value codec's float32 rotation).
 static bool uniform_route(const tq_codec* vc, const tq_attn_desc* d, int& nwg, int& bpw, int& fpw) {
-  return vc->rotation_parts != nullptr && uniform_geometry(d, nwg, bpw, fpw);
+  return vc->rotation != nullptr && uniform_geometry(d, nwg, bpw, fpw);
 }
 
 // Partials workspace of the K4/V2 routes of a call: the larger of the uniform
@@ -882,7 +882,7 @@ static size_t fast_part_bytes(const tq_attn_desc* d) {
   int nwg, bpw, fpw;
   size_t b = (size_t)fast_plan(d).vmax * G * PACKED_PART_FLOATS * 4;
   if (uniform_geometry(d, nwg, bpw, fpw)) {
-    const size_t u = (size_t)d->batch * d->hkv * nwg * G * FAST_PART_FLOATS * 4;
+    const size_t u = (size_t)d->batch * d->hkv * nwg * G * PACKED_PART_FLOATS * 4;
     if (u > b) b = u;
   }
   return b;
@@ -986,8 +986,13 @@ static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_des
     u.q = d->q; u.q_dtype = d->q_dtype; u.out = d->out;
     u.batch = d->batch; u.hq = d->hq; u.hkv = d->hkv;
     u.qscale = d->scale * 1.4426950408889634f;
-    u.rot16 = kc->rotation_parts; u.rotT = vc->rotation_parts + 2 * 128 * 128;
-    for (int i = 0; i < 16; ++i) u.kcent[i] = kc->host_centroids[i];
+    u.rot16 = kc->rotation_parts; u.vrot = vc->rotation;
+    for (int i = 0; i < 16; ++i) {
+      const float x = kc->host_centroids[i];
+      const _Float16 xh = (_Float16)x;
+      u.khl[i] = (uint32_t)__builtin_bit_cast(uint16_t, xh) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(x - (float)xh)) << 16);
+    }
     for (int i = 0; i < 4; ++i) u.vtab[i] = vc->value_table[i];
     u.vscale = vc->value_scale;
     u.part = part;

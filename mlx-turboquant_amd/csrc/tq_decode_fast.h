@@ -80,8 +80,8 @@ int launch_partial_merge(float* part, int nwg, int G, int hq, int hkv, int batch
 // Arguments of the K4/V2 kernels for uniform batches (tq_decode_uniform.hip):
 // grid (nwg, hkv, batch), workgroup c of (b, g) takes the compressed blocks
 // [c bpw, (c + 1) bpw) and the fp16 tokens [c fpw, (c + 1) fpw) of the
-// [sink | ring] list; partials in original space (FAST_PART_FLOATS per query
-// head, nwg per (b, g)).
+// [sink | ring] list; partials with a rotated and an original-space part
+// (PACKED_PART_FLOATS per query head, nwg per (b, g)).
 constexpr int UNI_BLOCKS_PER_WAVE = 8;  // compressed blocks per wave at most (kernels for 4 and 8)
 constexpr int UNI_FP16_PER_WG = 16;     // fp16 tokens per workgroup, staged in LDS
 constexpr int UNI_MAX_WG = 256;         // workgroups per (sequence, kv head)
@@ -94,18 +94,15 @@ struct UniformArgs {
   const void* sink_k; const void* sink_v; int64_t sink_hs;   // fp16, elements
   const void* res_k;  const void* res_v;  int64_t res_hs;    // fp16 ring
   int res_cap, res_start0;
-  const int32_t* comp_len_b;   // per-sequence lengths (NULL: the maximal ones)
-  const int32_t* sink_len_b;
-  const int32_t* res_len_b;
-  const int32_t* res_start_b;
+  const int32_t* res_start_b;  // per-sequence ring starts (NULL: res_start0); lengths are the maximal ones
   int max_comp, max_sink, max_res;
   const void* q; int q_dtype;
   float* out;
   int batch, hq, hkv;
   float qscale;          // scale * log2(e)
   const uint16_t* rot16; // (2, 128, 128) fp16 high part / remainder of R (key codec): query rotation
-  const uint16_t* rotT;  // (2, 128, 128) fp16 high part / remainder of R^T (value codec): inverse rotation
-  float kcent[16];       // key centroids (tq_codec.host_centroids)
+  const float* vrot;     // (128, 128) R float32, row-major (value codec): inverse rotation in the merge
+  uint32_t khl[16];      // key centroid i: fp16 bits of c_hi = fp16(c) | fp16(c - c_hi) << 16
   uint32_t vtab[4];      // value table: fp16 bits of entry i (tq_codec.value_table)
   float vscale;          // value centroid i = vscale * table value i
   float* part;           // per-workgroup partials (workspace)

@@ -65,12 +65,13 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef __fp16 hx2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int FD = 128;
 constexpr int FW = FAST_WAVES;            // waves per workgroup (FW * 16 == FD)
 constexpr int FT = FW * 64;               // threads
-constexpr int PS = FAST_PART_FLOATS;      // floats per (workgroup, head) partial
-constexpr int P_OUT = 4;                  // partial: [M, L, pad, pad, out[128]]
+constexpr int PPS = PACKED_PART_FLOATS;   // floats per (workgroup, head) partial
+constexpr int P_OUT = 4;                  // partial: [M, L, has_orig, pad, rotated out[128], original out[128]]
 constexpr int MAXWG = UNI_MAX_WG;         // workgroups per (sequence, kv head)
 constexpr int FROW = 272;                 // LDS row of a staged fp16 token (256 + 16 against bank conflicts)
 constexpr float M_INIT = -1e30f;          // running max before the first block
@@ -95,8 +96,6 @@ struct Layout {
   static constexpr uint32_t vlut = 0;            // 256 rows x 256 B
   static constexpr uint32_t klut = 65536;        // 256 rows x 256 B
   static constexpr uint32_t cmb = 0;             // [8 waves][8 heads][CMS] f32
-  static constexpr uint32_t aop = 34816;         // [8 heads][AOPS bytes: 128 f32] normalised rotated sum
-  static constexpr uint32_t onr = aop + 8 * 576; // [8 heads][128] f32 normalised original-space sum
   static constexpr uint32_t cml = 131072;        // [8 waves][8 heads][4] f32 max, sum, max of the orig part
   static constexpr uint32_t qop = cml + 1024;    // [8 heads][2 parts][QOPS bytes: 4][8][8] fp16 rotated-q B operands
   static constexpr uint32_t qfo = qop + 16 * 528; // [8 heads][2 parts][4][4][8] fp16 original-space q B operands
@@ -104,18 +103,14 @@ struct Layout {
   static constexpr uint32_t nst = opk + 4096;    // [8 waves][64] f32 norm staging
   static constexpr uint32_t qst = nst + 2048;    // [8 heads][128] q as given (up to 4 bytes per element)
   static constexpr uint32_t f16s = qst + 4096;   // [16 tokens][keys, values][FROW] staged fp16 tokens
-  static constexpr uint32_t hmx = f16s + UNI_FP16_PER_WG * 2 * FROW;  // [8 heads] u32 max |rotated sum| (float bits)
-  static constexpr uint32_t total = hmx + 32;
+  static constexpr uint32_t total = f16s + UNI_FP16_PER_WG * 2 * FROW;
 };
 // Row strides padded so that rows read by different lanes of one LDS
 // instruction start in different banks: the rotated-q operand rows of the 8
-// (head, part) columns, the combine rows of the G heads, the inverse-rotation
-// operand rows of the G heads.
+// (head, part) columns, the combine rows of the G heads.
 constexpr uint32_t QOPS = 528;  // bytes per (head, part) of qop (512 + 16)
 constexpr int CMS = FD + 4;     // floats per (wave, head) of cmb
-constexpr uint32_t AOPS = 576;  // bytes per head of aop (512 + 64)
-static_assert(FW * 8 * CMS * 4 <= Layout::aop && Layout::onr == Layout::aop + 8 * AOPS &&
-              Layout::onr + 8 * FD * 4 <= Layout::cml, "combine buffers fit the table region");
+static_assert(FW * 8 * CMS * 4 <= Layout::cml, "combine buffers fit the table region");
 static_assert(Layout::total <= 160 * 1024, "LDS of one workgroup");
 static_assert(UNI_FP16_PER_WG == 16, "fp16 tokens: one 16-token score tile, one staging pass");
 
@@ -167,16 +162,6 @@ __device__ inline u2 lds_u2(const uint8_t* smem, uint32_t addr) {
 }
 
 
-// Merge of the partials of (sequence b, kv head g), a second launch on the
-// same stream (the kernel boundary makes the partials visible), in float32
-// (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40). Each partial p holds its max
-// M_p, its sum L_p and its output x_p in original space, normalised by L_p:
-//   out = sum_p w_p x_p,  w_p = 2^(M_p - M) L_p / L,
-//   M = max_p M_p,  L = sum_p 2^(M_p - M) L_p.
-// One wave per (query head, half of the dims): lane p + 64k holds the
-// header of partial p + 64k, lane j sums dim 64 * half + j.
-constexpr int MB = 32;  // partials per batch of loads
-
 // max / sum over the wave: DPP rotations within each 16-lane row, then the
 // four rows
 __device__ inline float wave_max(float v) {
@@ -193,66 +178,6 @@ __device__ inline float wave_sum(float v) {
   v += row_ror<2>(v);
   v += row_ror<1>(v);
   return rows_sum(v);
-}
-
-template <int G>
-__global__ __launch_bounds__(64) void uniform_merge_kernel(UniformArgs a) {
-  __shared__ __align__(16) float wsh[MAXWG];  // w_p, written and read back by the one wave
-  const int half = blockIdx.x, hqi = blockIdx.y, b = blockIdx.z;
-  const int g = hqi / G, h = hqi % G;
-  const int lane = threadIdx.x;
-  const int np = a.nwg;
-  const int64_t pstride = (int64_t)G * PS;
-  const float* pall = a.part + (int64_t)(b * a.hkv + g) * np * pstride + h * PS;  // partial p at pall + p*pstride
-  const int dim = 64 * half + lane;
-
-  // headers (partials past np re-read the last one and are masked), then the
-  // first batch of outputs
-  static_assert(MAXWG == 256 && MB == 32, "merge register layout");
-  float2 hd[MAXWG / 64];
-#pragma unroll
-  for (int k = 0; k < MAXWG / 64; ++k)
-    hd[k] = *reinterpret_cast<const float2*>(pall + min(lane + 64 * k, np - 1) * pstride);
-  float x[MB];
-#pragma unroll
-  for (int i = 0; i < MB; ++i) x[i] = pall[min(i, np - 1) * pstride + P_OUT + dim];
-
-  float m = M_INIT;
-#pragma unroll
-  for (int k = 0; k < MAXWG / 64; ++k)
-    if (lane + 64 * k < np) m = fmaxf(m, hd[k].x);
-  m = wave_max(m);
-  float w[MAXWG / 64];
-  float l = 0.f;
-#pragma unroll
-  for (int k = 0; k < MAXWG / 64; ++k) {
-    w[k] = lane + 64 * k < np ? fexp2(hd[k].x - m) * hd[k].y : 0.f;
-    l += w[k];
-  }
-  l = wave_sum(l);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-#pragma unroll
-  for (int k = 0; k < MAXWG / 64; ++k) wsh[lane + 64 * k] = w[k];  // zero past np
-
-  float acc = 0.f;
-  for (int p0 = 0;; p0 += MB) {
-#pragma unroll
-    for (int i = 0; i < MB; i += 4) {
-      const float4 wp = *reinterpret_cast<const float4*>(wsh + p0 + i);  // one address: a broadcast
-      acc = fmaf(wp.x, x[i], acc);
-      acc = fmaf(wp.y, x[i + 1], acc);
-      acc = fmaf(wp.z, x[i + 2], acc);
-      acc = fmaf(wp.w, x[i + 3], acc);
-    }
-    if (p0 + MB >= np) break;
-#pragma unroll
-    for (int i = 0; i < MB; ++i) x[i] = pall[min(p0 + MB + i, np - 1) * pstride + P_OUT + dim];
-  }
-  a.out[((int64_t)b * a.hq + hqi) * FD + dim] = acc * inv;
-  if (a.ml && half == 0 && lane == 0) {
-    a.ml[((int64_t)b * a.hq + hqi) * 2] = m;
-    a.ml[((int64_t)b * a.hq + hqi) * 2 + 1] = l;
-  }
 }
 
 // The compressed blocks of one wave: loads issued at kernel start (lane r, q4)
@@ -289,41 +214,49 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   const bool writer = !lo_part && c8 < G;  // one column per (tile, head) writes the combine rows
 
   // All kernel arguments the set-up needs are loaded in one batch of scalar
-  // loads and waited for once (a branch on an argument would otherwise split
-  // them into dependent round trips).
+  // loads and waited for once; the set-up below has no branch on them, which
+  // would split them into dependent round trips (the compiler reloads kernel
+  // arguments inside branches).
   {
-    const void* p0 = a.comp_len_b; const void* p1 = a.sink_len_b;
-    const void* p2 = a.res_len_b; const void* p3 = a.res_start_b;
     const void* p4 = a.kc; const void* p5 = a.kn; const void* p6 = a.vc; const void* p7 = a.vn;
-    const void* p8 = a.q; const void* p9 = a.rot16; const void* p10 = a.rotT; const void* p11 = a.part;
+    const void* p8 = a.q; const void* p9 = a.rot16; const void* p10 = a.vrot; const void* p11 = a.part;
     const void* p12 = a.sink_k; const void* p13 = a.sink_v; const void* p14 = a.res_k; const void* p15 = a.res_v;
+    const void* p3 = a.res_start_b;
     const int64_t s0 = a.k_hs, s1 = a.kn_hs, s2 = a.v_hs, s3 = a.vn_hs, s4 = a.sink_hs, s5 = a.res_hs;
     const int i0 = a.max_comp, i1 = a.max_sink, i2 = a.max_res, i3 = a.res_start0, i4 = a.bpw, i5 = a.hkv,
               i6 = a.hq, i7 = a.q_dtype, i8 = a.fpw, i9 = a.res_cap;
-    asm volatile("" ::"s"(p0), "s"(p1), "s"(p2), "s"(p3), "s"(p4), "s"(p5), "s"(p6), "s"(p7), "s"(p8), "s"(p9),
-                 "s"(p10), "s"(p11), "s"(p12), "s"(p13), "s"(p14), "s"(p15), "s"(s0), "s"(s1), "s"(s2), "s"(s3),
-                 "s"(s4), "s"(s5), "s"(i0), "s"(i1), "s"(i2), "s"(i3), "s"(i4), "s"(i5), "s"(i6), "s"(i7), "s"(i8),
-                 "s"(i9));
+    asm volatile("" ::"s"(p3), "s"(p4), "s"(p5), "s"(p6), "s"(p7), "s"(p8), "s"(p9), "s"(p10), "s"(p11),
+                 "s"(p12), "s"(p13), "s"(p14), "s"(p15), "s"(s0), "s"(s1), "s"(s2), "s"(s3), "s"(s4), "s"(s5),
+                 "s"(i0), "s"(i1), "s"(i2), "s"(i3), "s"(i4), "s"(i5), "s"(i6), "s"(i7), "s"(i8), "s"(i9));
   }
   // the codebook entries this wave's table rows share (e >> 4 = 2w + k / 4,
   // (e >> 2) & 3 and e >> 6 of row e = 32w + 4k + lane / 16), at uniform
   // offsets of the kernel arguments, with the ones every lane selects from
+  typedef const __attribute__((address_space(4))) uint32_t* kptr;
   const auto* kargs = (const __attribute__((address_space(4))) uint8_t*)__builtin_amdgcn_kernarg_segment_ptr();
-  const auto* kcu = reinterpret_cast<const __attribute__((address_space(4))) float*>(kargs + offsetof(UniformArgs, kcent));
-  const auto* vtu = reinterpret_cast<const __attribute__((address_space(4))) uint32_t*>(kargs + offsetof(UniformArgs, vtab));
-  const float cbw[2] = {kcu[2 * w], kcu[2 * w + 1]};
+  const kptr khu = (kptr)(kargs + offsetof(UniformArgs, khl));
+  const kptr vtu = (kptr)(kargs + offsetof(UniformArgs, vtab));
+  const uint32_t cbw[2] = {khu[2 * w], khu[2 * w + 1]};
   const uint32_t vtw[3] = {vtu[(2 * w) & 3], vtu[(2 * w + 1) & 3], vtu[w >> 1]};
-  asm volatile("" ::"s"(cbw[0]), "s"(cbw[1]), "s"(vtw[0]), "s"(vtw[1]), "s"(vtw[2]), "s"(a.vtab[0]), "s"(a.vtab[1]),
-               "s"(a.vtab[2]), "s"(a.vtab[3]), "s"(a.kcent[0]), "s"(a.kcent[1]), "s"(a.kcent[2]), "s"(a.kcent[3]),
-               "s"(a.kcent[4]), "s"(a.kcent[5]), "s"(a.kcent[6]), "s"(a.kcent[7]), "s"(a.kcent[8]), "s"(a.kcent[9]),
-               "s"(a.kcent[10]), "s"(a.kcent[11]), "s"(a.kcent[12]), "s"(a.kcent[13]), "s"(a.kcent[14]),
-               "s"(a.kcent[15]));
-  // per-sequence values clamped to the bounds the host checked, so every read
-  // stays inside the stores, the sink and the ring
-  const int comp = a.comp_len_b ? min(max(a.comp_len_b[b], 0), a.max_comp) : a.max_comp;
-  const int sink = a.sink_len_b ? min(max(a.sink_len_b[b], 0), a.max_sink) : a.max_sink;
-  const int res = a.res_len_b ? min(max(a.res_len_b[b], 0), a.max_res) : a.max_res;
-  const int rstart = a.res_start_b ? min(max(a.res_start_b[b], 0), max(a.res_cap - 1, 0)) : a.res_start0;
+  // the ring start of the sequence: its res_start_b entry, or res_start0 (one
+  // scalar load from either address, no branch); clamped to the ring, so
+  // every read stays inside it
+  const kptr rsp = a.res_start_b ? (kptr)(a.res_start_b + b) : (kptr)(kargs + offsetof(UniformArgs, res_start0));
+  const int rs_raw = (int)*rsp;
+  // the codebooks as opaque register values (the compiler would otherwise
+  // reload them from the kernel arguments, one round trip per reload)
+  uint32_t kh[16], vt[4];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) kh[i] = a.khl[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) vt[i] = a.vtab[i];
+  asm volatile("" : "+s"(kh[0]), "+s"(kh[1]), "+s"(kh[2]), "+s"(kh[3]), "+s"(kh[4]), "+s"(kh[5]), "+s"(kh[6]),
+               "+s"(kh[7]), "+s"(kh[8]), "+s"(kh[9]), "+s"(kh[10]), "+s"(kh[11]), "+s"(kh[12]), "+s"(kh[13]),
+               "+s"(kh[14]), "+s"(kh[15]), "+s"(vt[0]), "+s"(vt[1]), "+s"(vt[2]), "+s"(vt[3])
+               : "s"(cbw[0]), "s"(cbw[1]), "s"(vtw[0]), "s"(vtw[1]), "s"(vtw[2]), "s"(rs_raw));
+  // a uniform call: every sequence at the maximal lengths
+  const int comp = a.max_comp, sink = a.max_sink, res = a.max_res;
+  const int rstart = min(max(rs_raw, 0), max(a.res_cap - 1, 0));
   const int nbc = (comp + 31) >> 5;
   const int blk0 = c * a.bpw, blk1 = min(blk0 + a.bpw, nbc);
   const int f0 = c * a.fpw, nf = max(0, min(a.fpw, sink + res - f0));  // fp16 tokens [f0, f0 + nf)
@@ -359,32 +292,27 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   // of the row
   u4 fst;
   {
-    {
-      const int e = tid;
-      const int u = f0 + min(e >> 5, max(nf - 1, 0));  // token of the [sink | residual] list
-      const bool is_v = (e >> 4) & 1;
-      const uint16_t* src;
-      if (nf == 0) {
-        src = a.rot16;  // nothing staged: a dummy read
-      } else if (u < sink) {
-        src = static_cast<const uint16_t*>(is_v ? a.sink_v : a.sink_k) + (int64_t)row * a.sink_hs + (int64_t)u * FD;
-      } else {
-        int sl = rstart + (u - sink);  // ring slot (rstart + t < 2 * res_cap)
-        sl = sl >= a.res_cap ? sl - a.res_cap : sl;
-        src = static_cast<const uint16_t*>(is_v ? a.res_v : a.res_k) + (int64_t)row * a.res_hs + (int64_t)sl * FD;
-      }
-      fst = *reinterpret_cast<const u4*>(src + 8 * (e & 15));
-    }
+    const int e = tid;
+    const int u = f0 + min(e >> 5, max(nf - 1, 0));  // token of the [sink | residual] list
+    const bool is_v = (e >> 4) & 1;
+    int sl = rstart + (u - sink);  // ring slot (rstart + t < 2 * res_cap)
+    sl = sl >= a.res_cap ? sl - a.res_cap : sl;
+    // candidate rows, selected without a branch; nothing staged: a dummy read
+    const uint16_t* ps = static_cast<const uint16_t*>(is_v ? a.sink_v : a.sink_k) + (int64_t)row * a.sink_hs + (int64_t)u * FD;
+    const uint16_t* pr = static_cast<const uint16_t*>(is_v ? a.res_v : a.res_k) + (int64_t)row * a.res_hs + (int64_t)sl * FD;
+    const uint16_t* src = nf == 0 ? a.rot16 : (u < sink ? ps : pr);
+    fst = *reinterpret_cast<const u4*>(src + 8 * (e & 15));
   }
   // ---- loads of the compressed blocks of this wave: blocks blk0 + w + 8k.
   // Buffer loads over the tokens [t0, comp) of the row: bytes past the
   // sequence read as zero (those tokens are masked), slots past the wave's
   // blocks re-read block 0 and are masked.
-  const bool has_comp = comp > 0;
-  const uint8_t* kcodes = has_comp ? a.kc + (int64_t)row * a.k_hs : nullptr;
-  const uint8_t* vcodes = has_comp ? a.vc + (int64_t)row * a.v_hs : nullptr;
-  const float* knorm = has_comp ? a.kn + (int64_t)row * a.kn_hs : nullptr;
-  const float* vnorm = has_comp ? a.vn + (int64_t)row * a.vn_hs : nullptr;
+  // (with no compressed token every buffer has zero bytes: its loads read zero
+  // and touch no memory, whatever the base)
+  const uint8_t* kcodes = a.kc + (int64_t)row * a.k_hs;
+  const uint8_t* vcodes = a.vc + (int64_t)row * a.v_hs;
+  const float* knorm = a.kn + (int64_t)row * a.kn_hs;
+  const float* vnorm = a.vn + (int64_t)row * a.vn_hs;
   auto slot_t0 = [&](int k) {
     const int blk = blk0 + w + FW * k;
     return blk < blk1 ? blk << 5 : 0;
@@ -398,7 +326,7 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   Blk B[NPW];
   auto load_slot = [&](int k) {
     const int t0 = slot_t0(k);
-    const int n = has_comp ? comp - t0 : 0;  // tokens readable from t0 on
+    const int n = comp - t0;  // tokens readable from t0 on (t0 = 0 when comp = 0)
     const __amdgpu_buffer_rsrc_t rk = rsrc(kcodes + (int64_t)t0 * 64, n * 64);
     const __amdgpu_buffer_rsrc_t rv = rsrc(vcodes + (int64_t)t0 * 32, n * 32);
     const __amdgpu_buffer_rsrc_t rkn = rsrc(knorm + t0, n * 4);
@@ -416,35 +344,36 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   load_slot(0);
   // ---- tables, from the codebooks passed by value (no memory round trip):
   // key byte e -> (c_hi[e&15], c_hi[e>>4], c_lo[e&15], c_lo[e>>4]) fp16
-  //   (c_hi = fp16(c), c_lo = fp16(c - c_hi), as in tq_codec.decode_table)
+  //   (c_hi = fp16(c), c_lo = fp16(c - c_hi), as in tq_codec.decode_table;
+  //   khl[i] holds the pair of centroid i)
   // value byte e -> (t[e&3], t[(e>>2)&3], t[(e>>4)&3], t[(e>>6)&3]) fp16
   // Store k of wave w fills rows 4s .. 4s + 3 (s = 8w + k) of a table with one
   // 16-byte store (two replicas) per lane, lane-linear and so conflict-free:
   // lane l writes entry e = 4s + (l >> 4), replicas 2(l & 15) and 2(l & 15) + 1.
   // Of e, only e & 3 = l >> 4 varies over the lanes.
   {
-    const int qg = lane >> 4;
-    auto sel4 = [&](auto x0, auto x1, auto x2, auto x3) { return qg == 0 ? x0 : qg == 1 ? x1 : qg == 2 ? x2 : x3; };
-    auto h2 = [](float x, float y) {
-      return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y) << 16);
+    // x[lane >> 4], by bit masks (a conditional form becomes divergent branches)
+    const uint32_t m1 = 0u - ((uint32_t)lane >> 4 & 1u), m2 = 0u - ((uint32_t)lane >> 5 & 1u);
+    auto sel4 = [&](uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3) {
+      const uint32_t lo = (m1 & x1) | (~m1 & x0), hi = (m1 & x3) | (~m1 & x2);
+      return (m2 & hi) | (~m2 & lo);
     };
-    const uint32_t vq = sel4(a.vtab[0], a.vtab[1], a.vtab[2], a.vtab[3]);  // t[e & 3]
+    const uint32_t vq = sel4(vt[0], vt[1], vt[2], vt[3]);  // t[e & 3]
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int sx = 8 * w + k;  // uniform
-      const float ca = sel4(a.kcent[4 * (k & 3)], a.kcent[4 * (k & 3) + 1], a.kcent[4 * (k & 3) + 2],
-                            a.kcent[4 * (k & 3) + 3]);  // c[e & 15]
-      const float cb = cbw[k >> 2];                       // c[e >> 4]
-      const float ha = (float)(_Float16)ca, hb = (float)(_Float16)cb;
-      const uint32_t k0 = h2(ca, cb), k1 = h2(ca - ha, cb - hb);
+      const uint32_t ka = sel4(kh[4 * (k & 3)], kh[4 * (k & 3) + 1], kh[4 * (k & 3) + 2],
+                               kh[4 * (k & 3) + 3]);  // centroid e & 15
+      const uint32_t kb = cbw[k >> 2];                   // centroid e >> 4
+      const uint32_t k0 = __builtin_amdgcn_perm(kb, ka, 0x05040100u);  // (c_hi[e&15], c_hi[e>>4])
+      const uint32_t k1 = __builtin_amdgcn_perm(kb, ka, 0x07060302u);  // (c_lo[e&15], c_lo[e>>4])
       *reinterpret_cast<u4*>(smem + Layout::klut + sx * 1024 + lane * 16) = u4{k0, k1, k0, k1};
-      const uint32_t v0 = vq | (a.vtab[k & 3] << 16);
+      const uint32_t v0 = vq | (vt[k & 3] << 16);
       const uint32_t v1 = vtw[k >> 2] | (vtw[2] << 16);  // t[(e >> 4) & 3], t[e >> 6]
       *reinterpret_cast<u4*>(smem + Layout::vlut + sx * 1024 + lane * 16) = u4{v0, v1, v0, v1};
     }
   }
   if (tid < qchunks) *reinterpret_cast<u4*>(smem + Layout::qst + 16 * tid) = qld;
-  if (tid < 8) reinterpret_cast<uint32_t*>(smem + Layout::hmx)[tid] = 0u;
   // staged fp16 tokens: [slot][keys | values][272-byte row]
   *reinterpret_cast<u4*>(smem + Layout::f16s + (tid >> 5) * (2 * FROW) + ((tid >> 4) & 1) * FROW + 16 * (tid & 15)) = fst;
   __syncthreads();
@@ -457,52 +386,80 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   // 32*kb + 8*q4 ..): fp16 high part and remainder of q 2^-qe, the power of
   // two 2^qe of the head keeping scale * |R q| <= scale * ||q|| below Q_LIMIT
   half8 qo_hi[4], qo_lo[4];
-  float qe_scale;  // 2^qe of this lane's column head: multiplies its scores
+  float qe_scale = 1.f;  // 2^qe of this lane's column head: multiplies its scores
+  bool q_exact = false;  // the remainders qo_lo are zero
   {
     const uint8_t* qr = smem + Layout::qst + (uint32_t)min(r, G - 1) * FD * esz;
-    float x[4][8];
+    if (a.q_dtype == TQ_F16) {
+      // fp16 queries: the operands are the inputs themselves (remainder zero)
+      // unless a head of the wave needs scaling down
+      u4 raw[4];
+      float ss = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int d = 32 * kb + 8 * q4;
-      if (a.q_dtype == TQ_F32) {
-        const float4 u0 = *reinterpret_cast<const float4*>(qr + 4 * d);
-        const float4 u1 = *reinterpret_cast<const float4*>(qr + 4 * d + 16);
-        x[kb][0] = u0.x; x[kb][1] = u0.y; x[kb][2] = u0.z; x[kb][3] = u0.w;
-        x[kb][4] = u1.x; x[kb][5] = u1.y; x[kb][6] = u1.z; x[kb][7] = u1.w;
-      } else {
-        const u4 u = *reinterpret_cast<const u4*>(qr + 2 * d);
+      for (int kb = 0; kb < 4; ++kb) {
+        raw[kb] = *reinterpret_cast<const u4*>(qr + 2 * (32 * kb + 8 * q4));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t hb = (u[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-          x[kb][i] = a.q_dtype == TQ_BF16 ? __uint_as_float(hb << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+        for (int j = 0; j < 4; ++j) {
+          const f16x2 h = __builtin_bit_cast(f16x2, raw[kb][j]);
+          ss = __builtin_amdgcn_fdot2(h, h, ss, false);
+        }
+      }
+      ss = rows_sum(ss);
+      q_exact = __builtin_amdgcn_ballot_w64(sqrtf(ss) * a.qscale > Q_LIMIT) == 0;
+      if (q_exact) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          qo_hi[kb] = as_h8(raw[kb]);
+          qo_lo[kb] = as_h8(u4{0u, 0u, 0u, 0u});
         }
       }
     }
-    float ss = 0.f;
+    if (!q_exact) {
+      // the fp16 high part / remainder of q 2^-qe
+      float x[4][8];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb) {
+        const int d = 32 * kb + 8 * q4;
+        if (a.q_dtype == TQ_F32) {
+          const float4 u0 = *reinterpret_cast<const float4*>(qr + 4 * d);
+          const float4 u1 = *reinterpret_cast<const float4*>(qr + 4 * d + 16);
+          x[kb][0] = u0.x; x[kb][1] = u0.y; x[kb][2] = u0.z; x[kb][3] = u0.w;
+          x[kb][4] = u1.x; x[kb][5] = u1.y; x[kb][6] = u1.z; x[kb][7] = u1.w;
+        } else {
+          const u4 u = *reinterpret_cast<const u4*>(qr + 2 * d);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss = fmaf(x[kb][i], x[kb][i], ss);
-    ss = rows_sum(ss);  // the 4 lanes of row r hold the 128 dims of its head
-    const float qn = sqrtf(ss) * a.qscale;
-    const int qe = qn > Q_LIMIT ? (int)ceilf(log2f(qn / Q_LIMIT)) : 0;  // lanes r: head min(r, G - 1)
-    const float qdown = __builtin_amdgcn_ldexpf(1.f, -qe);
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float xs = x[kb][i] * qdown;
-        qo_hi[kb][i] = (_Float16)xs;
-        qo_lo[kb][i] = (_Float16)(xs - (float)qo_hi[kb][i]);
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t hb = (u[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+            x[kb][i] = a.q_dtype == TQ_BF16 ? __uint_as_float(hb << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+          }
+        }
       }
-    // lane h (column h, group 0) holds the exponent of head h
-    int qeh = 0;
+      float ss = 0.f;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const int xh = __builtin_amdgcn_readlane(qe, h);
-      qeh = hd == h ? xh : qeh;
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fmaf(x[kb][i], x[kb][i], ss);
+      ss = rows_sum(ss);  // the 4 lanes of row r hold the 128 dims of its head
+      const float qn = sqrtf(ss) * a.qscale;
+      const int qe = qn > Q_LIMIT ? (int)ceilf(log2f(qn / Q_LIMIT)) : 0;  // lanes r: head min(r, G - 1)
+      const float qdown = __builtin_amdgcn_ldexpf(1.f, -qe);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float xs = x[kb][i] * qdown;
+          qo_hi[kb][i] = (_Float16)xs;
+          qo_lo[kb][i] = (_Float16)(xs - (float)qo_hi[kb][i]);
+        }
+      // lane h (column h, group 0) holds the exponent of head h
+      int qeh = 0;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const int xh = __builtin_amdgcn_readlane(qe, h);
+        qeh = hd == h ? xh : qeh;
+      }
+      qe_scale = __builtin_amdgcn_ldexpf(1.f, qeh);
     }
-    qe_scale = __builtin_amdgcn_ldexpf(1.f, qeh);
   }
   // ---- q_rot tile: D[h][n] = sum_i q[h][i] R[j0+n][i]   (B[k=i][n] = R[j0+n][i]),
   // written (times qscale) as fp16 high part / remainder straight into the
@@ -514,7 +471,7 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
     for (int kb = 0; kb < 4; ++kb) {
       dq = mfma(qo_hi[kb], as_h8(rqh[kb]), dq);
       dq = mfma(qo_hi[kb], as_h8(rql[kb]), dq);
-      dq = mfma(qo_lo[kb], as_h8(rqh[kb]), dq);
+      if (!q_exact) dq = mfma(qo_lo[kb], as_h8(rqh[kb]), dq);
     }
     const int j = j0 + r, e = j & 3;
     const uint32_t off = ((uint32_t)(j >> 5) * 8 + ((j >> 2) & 7)) * 16 + 2 * ((e & 1) + 4 * (e >> 1));
@@ -692,18 +649,6 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) acc_r[nb] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // R^T rows 16w + r as fp16 MFMA B operands of the inverse rotation (k-slot
-  // (q4, i) of step kb = rotated dim 32*kb + 8*q4 + i), high part and
-  // remainder; requested as the wave's last-but-one slot starts
-  u4 rth[4], rtl[4];
-  auto load_rt = [&]() {
-    const uint16_t* rt = a.rotT + (16 * w + r) * FD + 8 * q4;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      rth[kb] = *reinterpret_cast<const u4*>(rt + 32 * kb);
-      rtl[kb] = *reinterpret_cast<const u4*>(rt + FD * FD + 32 * kb);
-    }
-  };
   static_assert(NPW >= 2, "two blocks in flight");
 
   // ---- the compressed blocks of this wave (rotated space)
@@ -712,11 +657,9 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   for (int k = 0; k < NPW; ++k) {
     // every slot is computed (no branch between them, so the scheduler can
     // overlap one block's lookups with the previous block's softmax); a slot
-    // past the wave's blocks masks all its tokens. Block k + 2 (or, past the
-    // last block, R^T) is requested as slot k starts, so two blocks stay in
-    // flight while slot k computes.
+    // past the wave's blocks masks all its tokens. Block k + 2 is requested
+    // as slot k starts, so two blocks stay in flight while slot k computes.
     if (k + 2 < NPW) load_slot(k + 2);
-    if (k + 2 == NPW) load_rt();
     const Blk& L = B[k];
     const int t0 = slot_t0(k);
     const int tend = blk0 + w + FW * k < blk1 ? comp : 0;
@@ -834,9 +777,9 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   __syncthreads();
   // thread (head, dim): merge the 8 waves into the workgroup's rotated sum
   // (times the value scale) and original-space sum at the workgroup max M,
-  // both divided by the workgroup sum L, into LDS; each wave (half a head)
-  // raises the head's max |rotated sum|
-  float* part = a.part + ((int64_t)row * a.nwg + c) * G * PS;
+  // both divided by the workgroup sum L, straight into the partial; the
+  // merge kernel applies the inverse rotation once per query head
+  float* part = a.part + ((int64_t)row * a.nwg + c) * G * PPS;
   const bool wg_has_fp16 = nf > 0;
   {
     const float* cms = reinterpret_cast<const float*>(smem + Layout::cmb);
@@ -855,60 +798,127 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
         sr = fmaf(sc, cms[(ww * 8 + h) * CMS + j], sr);
         L = fmaf(sc, st.y, L);
       }
-      float so = 0.f;
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      part[h * PPS + P_OUT + j] = sr * inv * a.vscale;
       if (wg_has_fp16) {
         // original-space part of wave WF16, parked at its max then
         const float mo = cls[WF16 * 32 + 4 * h + 2];
-        so = mo > M_INIT ? fexp2(mo - M) * opk[h * FD + j] : 0.f;
+        const float so = mo > M_INIT ? fexp2(mo - M) * opk[h * FD + j] : 0.f;
+        part[h * PPS + P_OUT + FD + j] = so * inv;
       }
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      const float rn = sr * inv * a.vscale;
-      reinterpret_cast<float*>(smem + Layout::aop + h * AOPS)[j] = rn;
-      const float hm = wave_max(fabsf(rn));  // the wave's lanes share h (FD = 2 x 64)
-      if (lane == 0) atomicMax(reinterpret_cast<uint32_t*>(smem + Layout::hmx) + h, __float_as_uint(hm));
-      reinterpret_cast<float*>(smem + Layout::onr)[h * FD + j] = so * inv;
-      if (j == 0) *reinterpret_cast<float4*>(part + h * PS) = make_float4(M, L, 0.f, 0.f);
+      if (j == 0) *reinterpret_cast<float4*>(part + h * PPS) = make_float4(M, L, wg_has_fp16 ? 1.f : 0.f, 0.f);
     }
   }
+}
+
+// Merge of the partials of (sequence b, kv head g), a second launch on the
+// same stream (the kernel boundary makes the partials visible), in float32
+// (docs/FULL_FUSED_ATTENTION_RESULTS.md:34-40). Partial p holds its max M_p,
+// its sum L_p, its rotated output y_p and (flag f_p) its original-space
+// output x_p, both normalised by L_p:
+//   out = (sum_p w_p y_p) @ R + sum_p w_p f_p x_p,  w_p = 2^(M_p - M) L_p / L,
+//   M = max_p M_p,  L = sum_p 2^(M_p - M) L_p,
+// with R the value codec's float32 rotation (x = R^T y). One workgroup of 256
+// threads per (query head, b): thread t sums dim t & 127 of the partials of
+// parity t >> 7, and for the rotation takes output dims 4 (t & 31) .. + 3
+// over rows 16 (t >> 5) .. + 15 of R. Headers, the first MB partials of each
+// parity and the R block are requested together, headers first.
+constexpr int MB = 16;     // partials per parity per batch of loads
+constexpr int MT = 256;    // threads of the merge
+
+template <int G>
+__global__ __launch_bounds__(MT) void uniform_merge_kernel(UniformArgs a) {
+  __shared__ __align__(16) float wsh[MT / 64][MAXWG];  // per wave: w_p (0 past nwg and for empty partials)
+  __shared__ __align__(16) float hsh[MT / 64][MAXWG];  // per wave: f_p
+  __shared__ __align__(16) float ys[2][FD];   // the two parities' weighted sums, rotated
+  __shared__ __align__(16) float xs[2][FD];   // and original-space
+  __shared__ __align__(16) float red[8][FD];  // rotation: sums over the 8 row blocks
+  const int hqi = blockIdx.x, b = blockIdx.y;
+  const int g = hqi / G, h = hqi % G;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int d = tid & (FD - 1), par = tid >> 7;
+  const int np = a.nwg;
+
+  const int64_t pst = (int64_t)G * PPS;
+  const float* pp = a.part + (int64_t)(b * a.hkv + g) * np * pst + h * PPS;  // partial p at pp + p * pst
+  const int last = np - 1;
+  // every wave reads all headers (lane + 64k), so the weights need no barrier
+  static_assert(MAXWG == 256, "four headers per lane");
+  float4 hd[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) hd[k] = *reinterpret_cast<const float4*>(pp + min(lane + 64 * k, last) * pst);
+  float x[MB], xo[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    const float* pr = pp + min(2 * i + par, last) * pst + P_OUT + d;
+    x[i] = pr[0];
+    xo[i] = pr[FD];
+  }
+  const int j4 = 4 * (tid & 31), ib = tid >> 5;
+  float4 rr[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) rr[k] = *reinterpret_cast<const float4*>(a.vrot + (16 * ib + k) * FD + j4);
+
+  // the global max over the partials with a sum, then the weights
+  float m = M_INIT;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) m = lane + 64 * k < np && hd[k].y > 0.f ? fmaxf(m, hd[k].x) : m;
+  const float M = wave_max(m);
+  float ls = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const bool ok = lane + 64 * k < np && hd[k].y > 0.f;
+    const float wp = ok ? fexp2(hd[k].x - M) * hd[k].y : 0.f;
+    wsh[wv][lane + 64 * k] = wp;  // zero past np
+    hsh[wv][lane + 64 * k] = ok ? hd[k].z : 0.f;
+    ls += wp;
+  }
+  const float Ls = wave_sum(ls);
+  const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+  float acc = 0.f, acco = 0.f;
+  for (int p0 = 0;; p0 += 2 * MB) {
+    // branch-free: values of empty partials (weight 0) and of partials
+    // without an original-space part are replaced by 0 (they may hold
+    // anything, NaN included); partials past np have weight 0
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      const float w = wsh[wv][p0 + 2 * i + par], f = hsh[wv][p0 + 2 * i + par];
+      acc = fmaf(w, w != 0.f ? x[i] : 0.f, acc);
+      acco = fmaf(w, f != 0.f ? xo[i] : 0.f, acco);
+    }
+    if (p0 + 2 * MB >= np) break;
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      const float* pr = pp + min(p0 + 2 * MB + 2 * i + par, last) * pst + P_OUT + d;
+      x[i] = pr[0];
+      xo[i] = pr[FD];
+    }
+  }
+  ys[par][d] = acc;
+  xs[par][d] = acco;
   __syncthreads();
-  // ---- inverse rotation, wave w: out[h][j] = sum_i rn[h][i] R[i][j] + on[h][j]
-  // for j in [16w, 16w + 16): A = rn 2^(14 - E_h) as fp16 high part /
-  // remainder (row = head min(r, G-1); E_h the exponent of the head's max
-  // |rn|, so the operand stays below 2^15), B = R^T rows (fp16 parts)
-  {
-    const uint32_t* hmx = reinterpret_cast<const uint32_t*>(smem + Layout::hmx);
-    auto head_exp = [&](int h) {  // exponent of head h's max (0 for an all-zero head)
-      const uint32_t mb = hmx[h];
-      return mb == 0u ? 0 : max((int)((mb >> 23) & 0xFFu), 1) - 127;
-    };
-    const int hr = min(r, G - 1);
-    const float up = __builtin_amdgcn_ldexpf(1.f, 14 - head_exp(hr));
-    const float* src = reinterpret_cast<const float*>(smem + Layout::aop + (uint32_t)hr * AOPS) + 8 * q4;
-    f4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0, d2 = d0;  // three independent MFMA chains
+  // rotation: rows 16 ib .. + 15 of R times the merged rotated sum
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const float4 u0 = *reinterpret_cast<const float4*>(src + 32 * kb);
-      const float4 u1 = *reinterpret_cast<const float4*>(src + 32 * kb + 4);
-      const float xv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-      half8 ah, al;
+  for (int k = 0; k < 16; ++k) {
+    const int i = 16 * ib + k;
+    const float y = ys[0][i] + ys[1][i];  // one address per wave: a broadcast
+    o.x = fmaf(y, rr[k].x, o.x);
+    o.y = fmaf(y, rr[k].y, o.y);
+    o.z = fmaf(y, rr[k].z, o.z);
+    o.w = fmaf(y, rr[k].w, o.w);
+  }
+  *reinterpret_cast<float4*>(&red[ib][j4]) = o;
+  __syncthreads();
+  if (tid < FD) {
+    float r = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float xs = xv[i] * up;
-        ah[i] = (_Float16)xs;
-        al[i] = (_Float16)(xs - (float)ah[i]);
-      }
-      d0 = mfma(ah, as_h8(rth[kb]), d0);
-      d1 = mfma(ah, as_h8(rtl[kb]), d1);
-      d2 = mfma(al, as_h8(rth[kb]), d2);
-    }
-    const f4 d = d0 + (d1 + d2);
-    const int j = 16 * w + r;
-    const float* onr = reinterpret_cast<const float*>(smem + Layout::onr);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * q4 + i;
-      if (h < G) part[h * PS + P_OUT + j] = d[i] * __builtin_amdgcn_ldexpf(1.f, head_exp(h) - 14) + onr[h * FD + j];
-    }
+    for (int k = 0; k < 8; ++k) r += red[k][tid];
+    a.out[((int64_t)b * a.hq + hqi) * FD + tid] = (r + (xs[0][tid] + xs[1][tid])) * inv;
+  }
+  if (a.ml && tid == 0) {
+    a.ml[((int64_t)b * a.hq + hqi) * 2] = M;
+    a.ml[((int64_t)b * a.hq + hqi) * 2 + 1] = Ls;
   }
 }
 
@@ -920,7 +930,7 @@ static void launch_u(const UniformArgs& a, int merge, hipStream_t s) {
     hipLaunchKernelGGL((uk::uniform_decode_kernel<G, QB, 8>), dim3(a.nwg, a.hkv, a.batch), dim3(uk::FT), 0, s, a);
   else
     hipLaunchKernelGGL((uk::uniform_decode_kernel<G, QB, 4>), dim3(a.nwg, a.hkv, a.batch), dim3(uk::FT), 0, s, a);
-  if (merge) hipLaunchKernelGGL((uk::uniform_merge_kernel<G>), dim3(2, a.hq, a.batch), dim3(64), 0, s, a);
+  if (merge) hipLaunchKernelGGL((uk::uniform_merge_kernel<G>), dim3(a.hq, a.batch), dim3(uk::MT), 0, s, a);
 }
 
 int launch_uniform_decode(const UniformArgs& a, int G, bool qb, int merge, hipStream_t s) {

@@ -231,7 +231,9 @@ def bench_config4(dev, steps: int = 12):
     fused decode attention over every sequence in one call. With the QJL
     sketch (m = 128) the K4/V2 kernels run with the sketch's key and value
     terms around them; without it the K4/V2 kernels alone. Eager launches,
-    events around each step."""
+    events around each step (these include the host's launch overhead when
+    the GPU waits for it); then 8 attention calls back to back between two
+    events, the GPU time of one call with the host running ahead."""
     import numpy as np
     import torch
     from turboquant_amd.ragged import RaggedKVBatch
@@ -260,6 +262,15 @@ def bench_config4(dev, steps: int = 12):
             if i >= 2:
                 t_step.append(e0.elapsed_time(e2))
                 t_attn.append(e1.elapsed_time(e2))
+        rep = 8
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(rep):
+            rb.attend(q, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_b = e0.elapsed_time(e1) / rep
         per_tok = sum(c.row_hi + c.row_lo + 4 + (c.row_sign + 4 if qjl_m else 0) for c in (rb.kc, rb.vc))
         byt = 8 * (int(rb.comp_len.sum()) * per_tok + int(rb.res_len.sum()) * 512) + 16 * 32 * 128 * 6
         ms_s, ms_a = float(np.median(t_step)), float(np.median(t_attn))
@@ -267,7 +278,9 @@ def bench_config4(dev, steps: int = 12):
             "kernel": ("K4/V2 + sketch (qjl_bias_kernel, decode_partials_kernel with the key term, merge, "
                        "qjl_value_kernel, qjl_final_kernel)") if qjl_m else "K4/V2 (decode_partials_kernel + merge)",
             "layer_step_us": round(ms_s * 1e3, 1), "attend_us": round(ms_a * 1e3, 1),
-            "attend_bytes": byt, "attend_GBps": round(byt / (ms_a * 1e-3) / 1e9, 1)}
+            "attend_bytes": byt, "attend_GBps": round(byt / (ms_a * 1e-3) / 1e9, 1),
+            "attend_back_to_back_us": round(ms_b * 1e3, 1),
+            "attend_back_to_back_GBps": round(byt / (ms_b * 1e-3) / 1e9, 1)}
         del rb
     return res
 

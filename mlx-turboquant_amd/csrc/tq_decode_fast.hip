@@ -209,7 +209,20 @@ struct Plan {
 
 __device__ inline int round8(int64_t t) { return (int)((max<int64_t>(t, 1) + FW - 1) / FW * FW); }
 
-// Identical in every wave of both kernels (wave-uniform results).
+// inclusive prefix sum over the 64 lanes of the wave
+__device__ inline int wave_prefix(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    x += lane >= o ? y : 0;
+  }
+  return x;
+}
+
+// Identical in every wave of both kernels (wave-uniform results). Lane
+// b - base holds sequence b of each 64-sequence batch: one division per lane
+// and wave sums (no per-sequence loop of divisions).
 __device__ Plan make_plan(const FastArgs& a) {
   Plan p{};
   const int lane = threadIdx.x & 63;
@@ -222,7 +235,6 @@ __device__ Plan make_plan(const FastArgs& a) {
     return p;
   }
   const int64_t div = (int64_t)a.chunks * a.nwg;
-  // lane b - base holds W_b of this 64-sequence batch; sums through readlane
   int64_t U = 0;
   int w0 = 0;  // lane b's units of the first 64 sequences
   for (int base = 0; base < a.batch; base += 64) {
@@ -231,8 +243,7 @@ __device__ Plan make_plan(const FastArgs& a) {
     if (b < a.batch) s = seq_len(a, b);
     const int w = b < a.batch ? units_of(s.comp, s.sink + s.res) : 0;
     if (base == 0) w0 = w;
-    const int nb = min(64, a.batch - base);
-    for (int k = 0; k < nb; ++k) U += __builtin_amdgcn_readlane(w, k);
+    U += __builtin_amdgcn_readlane(wave_prefix(w), 63);
   }
   U *= a.hkv;
   p.T = round8((U + div - 1) / div);
@@ -245,8 +256,7 @@ __device__ Plan make_plan(const FastArgs& a) {
       if (b < a.batch) s = seq_len(a, b);
       w = b < a.batch ? units_of(s.comp, s.sink + s.res) : 0;
     }
-    const int nb = min(64, a.batch - base);
-    for (int k = 0; k < nb; ++k) V += cdiv(__builtin_amdgcn_readlane(w, k), p.T);
+    V += __builtin_amdgcn_readlane(wave_prefix(cdiv(w, p.T)), 63);
   }
   p.V = V * a.hkv;
   return p;
@@ -270,32 +280,38 @@ __device__ Loc locate(const FastArgs& a, const Plan& p, int key, bool by_seq) {
     L.s = seq_len(a, L.b);
     return L;
   }
+  // lane b - base: its sequence's chunks hkv n_b and their end (inclusive
+  // prefix) after the chunks of the sequences before the batch (carry)
   const int lane = threadIdx.x & 63;
-  int carry = 0;  // chunks of the sequences before the current one
-  bool found = false;
-  for (int base = 0; base < a.batch && !found; base += 64) {
+  int carry = 0;
+  for (int base = 0; base < a.batch; base += 64) {
     const int b = base + lane;
     SeqLen s{};
     if (b < a.batch) s = seq_len(a, b);
     const int w = b < a.batch ? units_of(s.comp, s.sink + s.res) : 0;
-    const int nb = min(64, a.batch - base);
-    for (int k = 0; k < nb; ++k) {
-      const int wk = __builtin_amdgcn_readlane(w, k);
-      const int n = a.hkv * cdiv(wk, p.T);
-      if (by_seq ? base + k == key : key < carry + n) {
-        L.b = base + k;
-        L.Nb = carry;
-        L.nb = n / a.hkv;
-        L.W = wk;
-        L.s.comp = __builtin_amdgcn_readlane(s.comp, k);
-        L.s.sink = __builtin_amdgcn_readlane(s.sink, k);
-        L.s.res = __builtin_amdgcn_readlane(s.res, k);
-        L.s.rstart = __builtin_amdgcn_readlane(s.rstart, k);
-        found = true;
-        break;
-      }
-      carry += n;
+    const int n = a.hkv * cdiv(w, p.T);
+    const int end = carry + wave_prefix(n);
+    int k = -1;
+    if (by_seq) {
+      if (key >= base && key < base + 64) k = key - base;
+    } else {
+      // the first sequence whose chunks end past the key (sequences past the
+      // batch end at the total and are never the first)
+      const uint64_t past = __builtin_amdgcn_ballot_w64(b < a.batch && end > key);
+      if (past != 0) k = (int)__builtin_ctzll(past);
     }
+    if (k >= 0) {
+      L.b = base + k;
+      L.nb = __builtin_amdgcn_readlane(n, k) / a.hkv;
+      L.Nb = __builtin_amdgcn_readlane(end, k) - __builtin_amdgcn_readlane(n, k);
+      L.W = __builtin_amdgcn_readlane(w, k);
+      L.s.comp = __builtin_amdgcn_readlane(s.comp, k);
+      L.s.sink = __builtin_amdgcn_readlane(s.sink, k);
+      L.s.res = __builtin_amdgcn_readlane(s.res, k);
+      L.s.rstart = __builtin_amdgcn_readlane(s.rstart, k);
+      break;
+    }
+    carry = __builtin_amdgcn_readlane(end, 63);
   }
   return L;
 }

@@ -597,47 +597,106 @@ static int group_heads(int G) {
 // u_h = sum_t p_t gamma_t z_t per projection (p the normalised softmax
 // weight of compressed token t) and a final kernel adds sqrt(pi/2)/d S^T u_h to
 // the output, as combine_kernel does for the general path.
-constexpr int QCH = 256;  // tokens per workgroup of the QJL kernels
+constexpr int QCH = 256;  // tokens per chunk of the QJL kernels
+constexpr int QVC = 1;    // chunks per workgroup of the value kernel (more per workgroup measured slower)
+constexpr int QBC = 8;    // chunks per workgroup of the bias kernel (one sign-pattern table for all)
 
 struct QjlArgs {
   tq_attn_desc d;
-  const float* sq;      // (batch, hq, m) S (scale q), natural units (prologue_kernel)
+  const float* sq;      // (batch, hq, m) S (scale q), natural units (qjl_sq_kernel)
   const float* proj;    // (m, 128)
   int m;
   float* bias;          // (batch*hkv*G, qb_hs) key term in base-2 score units
   const float* scores;  // (batch*hkv*G, qb_hs) final base-2 scores
   const float* ml;      // (batch, hq, 2) global max and sum of the merge
-  float* upart;         // (batch, hq, nvc, m) per-chunk value terms
+  float* upart;         // (batch, hq, nvc, m) value terms, one per value-kernel workgroup (QVC chunks)
   int64_t qb_hs;
   int nvc;
 };
 
+// S (scale q) of the G query heads of (b, g), natural units: thread i takes
+// projection i (and i + 128), S row i read in 16-byte pieces, the same
+// float32 order as prologue_kernel.
+template <int G>
+__global__ __launch_bounds__(128) void qjl_sq_kernel(QjlArgs a) {
+  __shared__ float qsm[G][128];
+  const int g = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, m = a.m;
+  for (int e = tid; e < G * 128; e += 128)
+    qsm[e >> 7][e & 127] =
+        a.d.scale * load_elem(a.d.q, ((int64_t)b * a.d.hq + g * G + (e >> 7)) * 128 + (e & 127), a.d.q_dtype);
+  __syncthreads();
+  for (int i = tid; i < m; i += 128) {
+    const float* si = a.proj + (int64_t)i * 128;
+    float acc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[h] = 0.f;
+    for (int k = 0; k < 128; k += 4) {
+      const float4 s4 = *reinterpret_cast<const float4*>(si + k);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        acc[h] = fmaf(qsm[h][k], s4.x, acc[h]);
+        acc[h] = fmaf(qsm[h][k + 1], s4.y, acc[h]);
+        acc[h] = fmaf(qsm[h][k + 2], s4.z, acc[h]);
+        acc[h] = fmaf(qsm[h][k + 3], s4.w, acc[h]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) const_cast<float*>(a.sq)[((int64_t)b * a.d.hq + g * G + h) * m + i] = acc[h];
+  }
+}
+
+// Key term of each compressed token: z_h = sum_k sign_k (S q_h)_k from a
+// table of the 16 sign patterns of each 4 consecutive projections, lut[p][n][h]
+// = sum_{j < 4} (bit j of n ? 1 : -1) (S q_h)_{4p + j} (one LDS read of G
+// floats and G adds per 4 signs).
 template <int G>
 __global__ __launch_bounds__(NT) void qjl_bias_kernel(QjlArgs a) {
   constexpr int MAXM = 256;
-  __shared__ __align__(16) float sq[G][MAXM];
+  __shared__ __align__(16) float lut[MAXM / 4][16][G];
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m;
   const int comp = seq_comp(a.d, b);
   // past the sequence's last 32-token block the bias is never read (those
   // scores are masked after it is added)
-  if (c * QCH >= ((comp + 31) & ~31)) return;
-  for (int e = tid; e < G * m; e += NT) sq[e / m][e % m] = a.sq[((int64_t)b * a.d.hq + g * G + e / m) * m + e % m];
-  __syncthreads();
-  const int t = c * QCH + tid;
-  if (t >= a.qb_hs) return;
-  float zs[G];
+  if (c * QBC * QCH >= ((comp + 31) & ~31)) return;
+  for (int e = tid; e < (m / 4) * 16 * G; e += NT) {
+    const int h = e % G, n = (e / G) & 15, p = e / (16 * G);
+    const float* sqh = a.sq + ((int64_t)b * a.d.hq + g * G + h) * m + 4 * p;
+    float v = 0.f;
 #pragma unroll
-  for (int h = 0; h < G; ++h) zs[h] = 0.f;
-  float coef = 0.f;
-  if (t < comp) {
-    const tq_store& ks = a.d.kstore;
-    const float gk = ks.gamma[(int64_t)row * ks.gamma_head_stride + t];
-    dot_signs<G, MAXM>(ks.signs + (int64_t)row * ks.sign_head_stride + (int64_t)t * (m / 8), m, sq, zs);
-    coef = 1.4426950408889634f * SQRT_HALF_PI / 128.f * gk;
+    for (int j = 0; j < 4; ++j) v += ((n >> j) & 1) ? sqh[j] : -sqh[j];
+    lut[p][n][h] = v;
   }
+  __syncthreads();
+  // tokens c QBC QCH + tid + QCH i: the bias of the tokens past comp (up to
+  // the 32-token block) is 0
+  const int tend = min((int)a.qb_hs, (comp + 31) & ~31);
+  const tq_store& ks = a.d.kstore;
+  for (int i = 0; i < QBC; ++i) {
+    const int t = (c * QBC + i) * QCH + tid;
+    if (t >= tend) break;
+    float zs[G];
 #pragma unroll
-  for (int h = 0; h < G; ++h) a.bias[((int64_t)row * G + h) * a.qb_hs + t] = coef * zs[h];
+    for (int h = 0; h < G; ++h) zs[h] = 0.f;
+    float coef = 0.f;
+    if (t < comp) {
+      const float gk = ks.gamma[(int64_t)row * ks.gamma_head_stride + t];
+      const uint32_t* sw = reinterpret_cast<const uint32_t*>(ks.signs + (int64_t)row * ks.sign_head_stride +
+                                                             (int64_t)t * (m / 8));
+      for (int wi = 0; wi < m / 32; ++wi) {
+        const uint32_t wd = sw[wi];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float* e = lut[8 * wi + k][(wd >> (4 * k)) & 15u];
+#pragma unroll
+          for (int h = 0; h < G; ++h) zs[h] += e[h];
+        }
+      }
+      coef = 1.4426950408889634f * SQRT_HALF_PI / 128.f * gk;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) a.bias[((int64_t)row * G + h) * a.qb_hs + t] = coef * zs[h];
+  }
 }
 
 typedef _Float16 qh8 __attribute__((ext_vector_type(8)));
@@ -670,110 +729,133 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   __shared__ __align__(16) uint32_t sgw[256 / 32][QCH];
   __shared__ uint32_t wmx[G];  // per head: the chunk's max weight (float bits; weights are >= 0)
   __shared__ float invl[G];    // per head: 1 / L
-  const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int cg = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq;
   const int comp = seq_comp(a.d, b);
-  const int base = c * QCH, nvalid = max(0, min(QCH, comp - base));
-  if (nvalid == 0) {  // past the sequence: a zero partial (the final kernel sums every chunk)
-    for (int e = tid; e < G * m; e += NT)
-      a.upart[(((int64_t)b * hq + g * G + e / m) * a.nvc + c) * m + e % m] = 0.f;
-    return;
-  }
   const tq_store& vs = a.d.vstore;
-  if (tid < G) wmx[tid] = 0u;
-  __syncthreads();
-  // unnormalised weights w = 2^(s - M) gamma (O(gamma), whatever the context
-  // length); 1 / L is applied in float32 to the sums
-  {
-    const int t = tid;
-    const float gv = t < nvalid ? vs.gamma[(int64_t)row * vs.gamma_head_stride + base + t] : 0.f;
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float p = 0.f;
-      if (t < nvalid) {
-        const float M = a.ml[((int64_t)b * hq + g * G + h) * 2], L = a.ml[((int64_t)b * hq + g * G + h) * 2 + 1];
-        const float sc = a.scores[((int64_t)row * G + h) * a.qb_hs + base + t];
-        p = L > 0.f ? __builtin_amdgcn_exp2f(sc - M) : 0.f;
-        if (t == 0) invl[h] = L > 0.f ? 1.f / L : 0.f;
-      }
-      const float wt = p * gv;
-      pw[h][t] = wt;
-      const float mx = wave_max_dpp(wt);
-      if ((tid & 63) == 0) atomicMax(&wmx[h], __float_as_uint(mx));
-    }
-  }
-  {
-    const uint32_t* gs = reinterpret_cast<const uint32_t*>(vs.signs + (int64_t)row * vs.sign_head_stride +
-                                                           (int64_t)base * (m / 8));
-    const int nw = m / 32;
-    for (int e = tid; e < nvalid * nw; e += NT) {
-      const int t = e / nw, k = e - t * nw;
-      sgw[k][t] = gs[e];
-    }
-  }
-  __syncthreads();
+  const int lane = tid & 63, w = tid >> 6, r = lane & 15, q4 = lane >> 4;
+  const int h = r & 7;
+  const bool lo_row = r >= 8;
   // head h's weights enter fp16 as w 2^(14 - E_h) (E_h the exponent of the
   // chunk's max weight: operands below 2^15, none subnormal but the tiny)
   auto head_exp = [&](int hh) {
     const uint32_t mb = wmx[hh];
     return mb == 0u ? 0 : max((int)((mb >> 23) & 0xFFu), 1) - 127;
   };
-  const int lane = tid & 63, w = tid >> 6, r = lane & 15, q4 = lane >> 4;
-  const int h = r & 7;
-  const bool lo_row = r >= 8;
-  const int nblk = (nvalid + 31) >> 5;
-  // A operands of the (at most 8) blocks: weights of head h, the fp16 high
-  // part (rows < 8) or remainder (rows >= 8); zero past G and past nvalid
-  qu4 aw[QCH / 32];
-  const float up_h = h < G ? __builtin_amdgcn_ldexpf(1.f, 14 - head_exp(h)) : 0.f;
+  // the wave's projection tiles ct = w + 4k (k < QT), summed over the chunks
+  // of the group in float32: rows 4 q4 + i (q4 < 2) of tile k
+  constexpr int QT = 256 / 16 / (NT / 64);
+  float tot[QT][4];
 #pragma unroll
-  for (int bk = 0; bk < QCH / 32; ++bk) {
-    const int t0 = 32 * bk + 8 * q4;  // the lane's 8 tokens (k-slots 8 q4 .. 8 q4 + 7)
+  for (int k = 0; k < QT; ++k)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float w0 = 0.f, w1 = 0.f;
-      if (h < G) {
-        w0 = pw[h][t0 + 2 * e] * up_h;
-        w1 = pw[h][t0 + 2 * e + 1] * up_h;
-      }
-      const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
-      const _Float16 l0 = (_Float16)(w0 - (float)h0), l1 = (_Float16)(w1 - (float)h1);
-      const _Float16 x0 = lo_row ? l0 : h0, x1 = lo_row ? l1 : h1;
-      aw[bk][e] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
-    }
+    for (int i = 0; i < 4; ++i) tot[k][i] = 0.f;
+  if (tid < G) {
+    const float L = a.ml[((int64_t)b * hq + g * G + tid) * 2 + 1];
+    invl[tid] = L > 0.f ? 1.f / L : 0.f;
   }
-  for (int ct = w; ct < m / 16; ct += NT / 64) {
-    qf4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int cc = 0; cc < QVC; ++cc) {
+    const int base = (cg * QVC + cc) * QCH, nvalid = max(0, min(QCH, comp - base));
+    if (nvalid == 0) break;  // past the sequence (uniform over the workgroup)
+    __syncthreads();  // the previous chunk's readers of pw / sgw / wmx are done
+    if (tid < G) wmx[tid] = 0u;
+    __syncthreads();
+    // unnormalised weights w = 2^(s - M) gamma (O(gamma), whatever the context
+    // length); 1 / L is applied in float32 to the sums
+    {
+      const int t = tid;
+      const float gv = t < nvalid ? vs.gamma[(int64_t)row * vs.gamma_head_stride + base + t] : 0.f;
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) {
+        float p = 0.f;
+        if (t < nvalid) {
+          const float M = a.ml[((int64_t)b * hq + g * G + hh) * 2], L = a.ml[((int64_t)b * hq + g * G + hh) * 2 + 1];
+          const float sc = a.scores[((int64_t)row * G + hh) * a.qb_hs + base + t];
+          p = L > 0.f ? __builtin_amdgcn_exp2f(sc - M) : 0.f;
+        }
+        const float wt = p * gv;
+        pw[hh][t] = wt;
+        const float mx = wave_max_dpp(wt);
+        if ((tid & 63) == 0) atomicMax(&wmx[hh], __float_as_uint(mx));
+      }
+    }
+    {
+      const uint32_t* gs = reinterpret_cast<const uint32_t*>(vs.signs + (int64_t)row * vs.sign_head_stride +
+                                                             (int64_t)base * (m / 8));
+      const int nw = m / 32;
+      for (int e = tid; e < nvalid * nw; e += NT) {
+        const int t = e / nw, k = e - t * nw;
+        sgw[k][t] = gs[e];
+      }
+    }
+    __syncthreads();
+    const int nblk = (nvalid + 31) >> 5;
+    // A operands of the (at most 8) blocks: weights of head h, the fp16 high
+    // part (rows < 8) or remainder (rows >= 8); zero past G and past nvalid
+    qu4 aw[QCH / 32];
+    const float up_h = h < G ? __builtin_amdgcn_ldexpf(1.f, 14 - head_exp(h)) : 0.f;
 #pragma unroll
     for (int bk = 0; bk < QCH / 32; ++bk) {
-      if (bk >= nblk) break;
-      const int t0 = 32 * bk + 8 * q4;
-      const qu4 av = aw[bk];
-      // B: +-1 of projection 16 ct + r for the lane's 8 tokens (bit set -> +1)
-      const int pj = 16 * ct + r, bit = pj & 31;
-      const qu4 x0 = *reinterpret_cast<const qu4*>(&sgw[pj >> 5][t0]);
-      const qu4 x1 = *reinterpret_cast<const qu4*>(&sgw[pj >> 5][t0 + 4]);
-      const uint32_t xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-      qu4 bv;
+      const int t0 = 32 * bk + 8 * q4;  // the lane's 8 tokens (k-slots 8 q4 .. 8 q4 + 7)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t s0 = (xs[2 * e] >> bit) & 1u;
-        const uint32_t s1 = (xs[2 * e + 1] >> bit) & 1u;
-        bv[e] = 0xBC00BC00u ^ (s0 << 15) ^ (s1 << 31);
+        float w0 = 0.f, w1 = 0.f;
+        if (h < G) {
+          w0 = pw[h][t0 + 2 * e] * up_h;
+          w1 = pw[h][t0 + 2 * e + 1] * up_h;
+        }
+        const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
+        const _Float16 l0 = (_Float16)(w0 - (float)h0), l1 = (_Float16)(w1 - (float)h1);
+        const _Float16 x0 = lo_row ? l0 : h0, x1 = lo_row ? l1 : h1;
+        aw[bk][e] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
       }
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qh8, av), __builtin_bit_cast(qh8, bv), acc, 0, 0,
-                                                   0);
     }
-    // rows 4 q4 + i: add the remainder rows (lane ^ 32 holds rows + 8)
+#pragma unroll
+    for (int k = 0; k < QT; ++k) {
+      const int ct = w + (NT / 64) * k;
+      if (ct >= m / 16) break;
+      qf4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int bk = 0; bk < QCH / 32; ++bk) {
+        if (bk >= nblk) break;
+        const int t0 = 32 * bk + 8 * q4;
+        const qu4 av = aw[bk];
+        // B: +-1 of projection 16 ct + r for the lane's 8 tokens (bit set -> +1)
+        const int pj = 16 * ct + r, bit = pj & 31;
+        const qu4 x0 = *reinterpret_cast<const qu4*>(&sgw[pj >> 5][t0]);
+        const qu4 x1 = *reinterpret_cast<const qu4*>(&sgw[pj >> 5][t0 + 4]);
+        const uint32_t xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        qu4 bv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t s0 = (xs[2 * e] >> bit) & 1u;
+          const uint32_t s1 = (xs[2 * e + 1] >> bit) & 1u;
+          bv[e] = 0xBC00BC00u ^ (s0 << 15) ^ (s1 << 31);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qh8, av), __builtin_bit_cast(qh8, bv), acc, 0,
+                                                     0, 0);
+      }
+      // rows 4 q4 + i: add the remainder rows (lane ^ 32 holds rows + 8),
+      // back to the chunk's weight scale
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
+        const float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        const int hh = min(4 * q4 + i, G - 1);
+        tot[k][i] = fmaf(v, __builtin_amdgcn_ldexpf(1.f, head_exp(hh) - 14), tot[k][i]);
+      }
+    }
+  }
+  __syncthreads();  // invl (an empty group has had no barrier)
+#pragma unroll
+  for (int k = 0; k < QT; ++k) {
+    const int ct = w + (NT / 64) * k;
+    if (ct >= m / 16) break;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
-      const float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
       const int hh = 4 * q4 + i;
-      if (q4 < 2 && hh < G) {
-        const float down = __builtin_amdgcn_ldexpf(invl[hh], head_exp(hh) - 14);
-        a.upart[(((int64_t)b * hq + g * G + hh) * a.nvc + c) * m + 16 * ct + r] = v * down;
-      }
+      if (q4 < 2 && hh < G)
+        a.upart[(((int64_t)b * hq + g * G + hh) * a.nvc + cg) * m + 16 * ct + r] = tot[k][i] * invl[hh];
     }
   }
 }
@@ -807,7 +889,7 @@ __global__ __launch_bounds__(128) void qjl_final_kernel(QjlArgs a) {
   out[j] += SQRT_HALF_PI / 128.f * ((z0 + z1) + (z2 + z3));
 }
 
-// Workspace of the QJL fast route: [fast partials | qr qs sq | bias | scores | ml | upart], 256-byte pieces.
+// Workspace of the QJL fast route: [fast partials | sq | bias | scores | ml | upart], 256-byte pieces.
 struct QjlLayout {
   size_t part, pro, bias, scores, ml, upart, total;
   int64_t qb_hs;
@@ -924,11 +1006,11 @@ static QjlLayout qjl_layout(const tq_codec* kc, const tq_attn_desc* d) {
   const int m = kc->qjl_m;
   L.qb_hs = ((int64_t)d->max_comp + 31) / 32 * 32;
   if (L.qb_hs < 32) L.qb_hs = 32;
-  L.nvc = (d->max_comp + QCH - 1) / QCH;
+  L.nvc = ((d->max_comp + QCH - 1) / QCH + QVC - 1) / QVC;  // value-kernel workgroups per (b, g)
   if (L.nvc < 1) L.nvc = 1;
   size_t off = 0;
   L.part = off; off += al256(fast_part_bytes(d));
-  L.pro = off; off += al256(heads * 128 * 4 * 2 + heads * (size_t)m * 4);
+  L.pro = off; off += al256(heads * (size_t)m * 4);  // S q
   L.bias = off; off += al256((size_t)d->batch * d->hkv * G * (size_t)L.qb_hs * 4);
   L.scores = off; off += al256((size_t)d->batch * d->hkv * G * (size_t)L.qb_hs * 4);
   L.ml = off; off += al256(heads * 2 * 4);
@@ -1005,7 +1087,7 @@ static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_des
   return launch_fast_decode(f, G, qb, merge, s);
 }
 
-// The QJL route: prologue (S q), key-term bias, K4/V2 partials with the bias
+// The QJL route: S q, key-term bias, K4/V2 partials with the bias
 // (scores stored) + merge (max and sum exported), value term, final S^T add.
 static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace,
                         size_t workspace_bytes, hipStream_t s) {
@@ -1014,21 +1096,9 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     return set_error(TQ_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, QL.total);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const int G = d->hq / d->hkv;
-  const size_t heads = (size_t)d->batch * d->hq;
-  AttnArgs pa{};
-  pa.d = *d;
-  pa.D = 128;
-  pa.rot = kc->rotation;
-  pa.proj = kc->qjl_proj;
-  pa.m = kc->qjl_m;
-  pa.qr = reinterpret_cast<float*>(ws + QL.pro);
-  pa.qs = pa.qr + heads * 128;
-  pa.sq = pa.qs + heads * 128;
-  hipLaunchKernelGGL(prologue_kernel, dim3(d->hq, d->batch), dim3(128), 128 * 4, s, pa);
-  TQ_LAUNCH_CHECK("tq_decode_attention qjl prologue");
   QjlArgs qa;
   qa.d = *d;
-  qa.sq = pa.sq;
+  qa.sq = reinterpret_cast<float*>(ws + QL.pro);
   qa.proj = kc->qjl_proj;
   qa.m = kc->qjl_m;
   qa.bias = reinterpret_cast<float*>(ws + QL.bias);
@@ -1037,7 +1107,14 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   qa.upart = reinterpret_cast<float*>(ws + QL.upart);
   qa.qb_hs = QL.qb_hs;
   qa.nvc = QL.nvc;
-  const dim3 bgrid((unsigned)((QL.qb_hs + QCH - 1) / QCH), d->hkv, d->batch);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((qjl_sq_kernel<1>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;
+    case 2: hipLaunchKernelGGL((qjl_sq_kernel<2>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;
+    case 4: hipLaunchKernelGGL((qjl_sq_kernel<4>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;
+    default: hipLaunchKernelGGL((qjl_sq_kernel<8>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;
+  }
+  TQ_LAUNCH_CHECK("tq_decode_attention qjl S q");
+  const dim3 bgrid((unsigned)((QL.qb_hs + QBC * QCH - 1) / (QBC * QCH)), d->hkv, d->batch);
   switch (G) {
     case 1: hipLaunchKernelGGL((qjl_bias_kernel<1>), bgrid, dim3(NT), 0, s, qa); break;
     case 2: hipLaunchKernelGGL((qjl_bias_kernel<2>), bgrid, dim3(NT), 0, s, qa); break;

@@ -59,13 +59,13 @@ typedef struct tq_codec {
   const float* qjl_proj;       /* (qjl_m, d) Gaussian S (qjl.py:23-36) or NULL */
   int32_t qjl_m;               /* number of projections (multiple of 32) or 0 */
   int32_t flags;               /* TQ_CODEC_* bits */
-  const uint16_t* rotation_parts; /* (4, d, d) 16-bit words, row-major, or NULL:
-                                     [0] = fp16(R), [1] = fp16(R - [0]),
-                                     [2] = fp16(R^T), [3] = fp16(R^T - [2]).
+  const uint16_t* rotation_parts; /* (2, d, d) 16-bit words, row-major, or NULL:
+                                     [0] = fp16(R), [1] = fp16(R - [0]).
                                      The K4/V2 decode kernels rotate the query
-                                     with the key codec's [0, 1] and rotate the
-                                     output back with the value codec's [2, 3];
-                                     others ignore it. */
+                                     with the key codec's planes (the output
+                                     goes back with the value codec's float32
+                                     `rotation`); others ignore it. Arrays with
+                                     more planes work: only [0, 1] are read. */
   /* Host-side tables, filled by tq_codec_prepare() from a host copy of
    * centroids_hi (codebooks of at most 16 entries; passed to kernels by value):
    * host_centroids = centroids_hi, n_host_centroids entries; and for 2-bit
@@ -74,9 +74,7 @@ typedef struct tq_codec {
    * value_table_err (relative). The K4/V2 route runs only when the key
    * codec has rotation_parts, 16 host_centroids and its decode_table, and the
    * value codec its decode_table with value_table_err <= 2e-7 (else the
-   * general kernels); a uniform batch (no per-sequence lengths) also uses
-   * the value codec's rotation_parts [2, 3] (without them the persistent
-   * kernel of ragged batches takes it). */
+   * general kernels). */
   float host_centroids[16];
   int32_t n_host_centroids;
   uint16_t value_table[4];

@@ -42,12 +42,11 @@
 // is raised with a margin, so most blocks need no rescale. The accumulator of
 // lane (column r, q4), MFMA nb, register i is rotated dim 32*q4 + 8*i + nb.
 //
-// The 8 waves of a workgroup are combined through LDS; the workgroup applies
-// the inverse rotation to its rotated sum (MFMA 16x16x32 f16 on fp16 high
-// part / remainder of both operands, the sum scaled per head by a power of
-// two into fp16 range), adds the original-space sum, and writes (max, sum,
-// output / sum) per query head. The merge kernel combines the partials of
-// each (b, g) with their softmax weights.
+// The 8 waves of a workgroup are combined through LDS into one partial per
+// query head: (max, sum, rotated sum / sum, original-space sum / sum). The
+// merge kernel combines the partials of each (b, g) with their softmax
+// weights and applies the inverse rotation (the value codec's float32 R) once
+// per query head.
 
 #include <math.h>
 #include <stddef.h>

@@ -37,14 +37,11 @@ class DeviceCodec:
             raise ValueError(f"Unsupported bit-width: {bits}. Use 1, 2, 3, or 4.")
         self.device = device
         self.rotation = get_rotation_matrix(d, seed, device)
-        # MFMA operands of the K4/V2 decode kernels: fp16 high part and
-        # remainder of R (query rotation) and of R^T (inverse rotation), as
-        # 16-bit words
-        rt = self.rotation.t().contiguous()
-        hi, hit = self.rotation.half(), rt.half()
+        # MFMA operands of the K4/V2 decode kernels' query rotation: fp16
+        # high part and remainder of R, as 16-bit words
+        hi = self.rotation.half()
         self.rotation_parts = torch.stack([
-            hi.view(torch.int16), (self.rotation - hi.float()).half().view(torch.int16),
-            hit.view(torch.int16), (rt - hit.float()).half().view(torch.int16)]).contiguous()
+            hi.view(torch.int16), (self.rotation - hi.float()).half().view(torch.int16)]).contiguous()
         self.c_hi, self.b_hi = get_codebook(d, self.bits_hi, device)
         self.c_lo, self.b_lo = get_codebook(d, self.bits_lo, device)
         self.qjl_m = qjl_m

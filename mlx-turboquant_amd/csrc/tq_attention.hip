@@ -729,13 +729,12 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   __shared__ __align__(16) uint32_t sgw[256 / 32][QCH];
   __shared__ uint32_t wmx[G];  // per head: the chunk's max weight (float bits; weights are >= 0)
   __shared__ float invl[G];    // per head: 1 / L
+  __shared__ __align__(16) qu4 awl[QCH / 32][16][4];  // MFMA A operands (weights), lane (r, q4) of block bk
   const int cg = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq;
   const int comp = seq_comp(a.d, b);
   const tq_store& vs = a.d.vstore;
   const int lane = tid & 63, w = tid >> 6, r = lane & 15, q4 = lane >> 4;
-  const int h = r & 7;
-  const bool lo_row = r >= 8;
   // head h's weights enter fp16 as w 2^(14 - E_h) (E_h the exponent of the
   // chunk's max weight: operands below 2^15, none subnormal but the tiny)
   auto head_exp = [&](int hh) {
@@ -790,26 +789,30 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
     }
     __syncthreads();
     const int nblk = (nvalid + 31) >> 5;
-    // A operands of the (at most 8) blocks: weights of head h, the fp16 high
-    // part (rows < 8) or remainder (rows >= 8); zero past G and past nvalid
-    qu4 aw[QCH / 32];
-    const float up_h = h < G ? __builtin_amdgcn_ldexpf(1.f, 14 - head_exp(h)) : 0.f;
+    // A operands of the (at most 8) blocks, built once for the four waves:
+    // entry (bk, r, q4) = the weights of head r & 7 for tokens 32 bk + 8 q4
+    // .. + 7, their fp16 high part (r < 8) or remainder (r >= 8); zero past G
+    // and past nvalid
+    for (int e = tid; e < (QCH / 32) * 16 * 4; e += NT) {
+      const int bk = e >> 6, rr = (e >> 2) & 15, qq = e & 3, hh = rr & 7;
+      const int t0 = 32 * bk + 8 * qq;
+      const float up = hh < G ? __builtin_amdgcn_ldexpf(1.f, 14 - head_exp(hh)) : 0.f;
+      qu4 v;
 #pragma unroll
-    for (int bk = 0; bk < QCH / 32; ++bk) {
-      const int t0 = 32 * bk + 8 * q4;  // the lane's 8 tokens (k-slots 8 q4 .. 8 q4 + 7)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int k = 0; k < 4; ++k) {
         float w0 = 0.f, w1 = 0.f;
-        if (h < G) {
-          w0 = pw[h][t0 + 2 * e] * up_h;
-          w1 = pw[h][t0 + 2 * e + 1] * up_h;
+        if (hh < G) {
+          w0 = pw[hh][t0 + 2 * k] * up;
+          w1 = pw[hh][t0 + 2 * k + 1] * up;
         }
         const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
         const _Float16 l0 = (_Float16)(w0 - (float)h0), l1 = (_Float16)(w1 - (float)h1);
-        const _Float16 x0 = lo_row ? l0 : h0, x1 = lo_row ? l1 : h1;
-        aw[bk][e] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
+        const _Float16 x0 = rr >= 8 ? l0 : h0, x1 = rr >= 8 ? l1 : h1;
+        v[k] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
       }
+      awl[bk][rr][qq] = v;
     }
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < QT; ++k) {
       const int ct = w + (NT / 64) * k;
@@ -819,7 +822,7 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
       for (int bk = 0; bk < QCH / 32; ++bk) {
         if (bk >= nblk) break;
         const int t0 = 32 * bk + 8 * q4;
-        const qu4 av = aw[bk];
+        const qu4 av = awl[bk][r][q4];
         // B: +-1 of projection 16 ct + r for the lane's 8 tokens (bit set -> +1)
         const int pj = 16 * ct + r, bit = pj & 31;
         const qu4 x0 = *reinterpret_cast<const qu4*>(&sgw[pj >> 5][t0]);

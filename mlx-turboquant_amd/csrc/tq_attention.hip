@@ -863,33 +863,38 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   }
 }
 
-__global__ __launch_bounds__(128) void qjl_final_kernel(QjlArgs a) {
-  __shared__ float u[256];
+// Thread t: projection i = t & 127 (and i + 128) over the value partials of
+// parity t >> 7, then output dim j = t & 127 over projection rows of parity
+// t >> 7; eight independent sums each, so the loads go out eight at a time.
+__global__ __launch_bounds__(256) void qjl_final_kernel(QjlArgs a) {
+  __shared__ float us[2][256];
+  __shared__ float os[2][128];
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, m = a.m;
+  const int lo = tid & 127, par = tid >> 7;
   const float* up = a.upart + ((int64_t)b * a.d.hq + h) * a.nvc * m;
-  for (int i = tid; i < m; i += 128) {
-    float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
-    int c = 0;
-    for (; c + 4 <= a.nvc; c += 4) {
-      v0 += up[(int64_t)c * m + i];
-      v1 += up[(int64_t)(c + 1) * m + i];
-      v2 += up[(int64_t)(c + 2) * m + i];
-      v3 += up[(int64_t)(c + 3) * m + i];
+  for (int i = lo; i < m; i += 128) {
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int c = par;
+    for (; c + 14 < a.nvc; c += 16) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] += up[(int64_t)(c + 2 * k) * m + i];
     }
-    for (; c < a.nvc; ++c) v0 += up[(int64_t)c * m + i];
-    u[i] = (v0 + v1) + (v2 + v3);
+    for (; c < a.nvc; c += 2) v[0] += up[(int64_t)c * m + i];
+    us[par][i] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
   }
   __syncthreads();
-  float* out = a.d.out + ((int64_t)b * a.d.hq + h) * 128;
-  const int j = tid;
-  float z0 = 0.f, z1 = 0.f, z2 = 0.f, z3 = 0.f;
-  for (int i = 0; i < m; i += 4) {
-    z0 = fmaf(u[i], a.proj[(int64_t)i * 128 + j], z0);
-    z1 = fmaf(u[i + 1], a.proj[(int64_t)(i + 1) * 128 + j], z1);
-    z2 = fmaf(u[i + 2], a.proj[(int64_t)(i + 2) * 128 + j], z2);
-    z3 = fmaf(u[i + 3], a.proj[(int64_t)(i + 3) * 128 + j], z3);
+  for (int i = tid; i < m; i += 256) us[0][i] += us[1][i];
+  __syncthreads();
+  const int j = lo;
+  float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int i = 8 * par;  // rows i .. i + 7 of every 16
+  for (; i + 7 < m; i += 16) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) z[k] = fmaf(us[0][i + k], a.proj[(int64_t)(i + k) * 128 + j], z[k]);
   }
-  out[j] += SQRT_HALF_PI / 128.f * ((z0 + z1) + (z2 + z3));
+  os[par][j] = ((z[0] + z[1]) + (z[2] + z[3])) + ((z[4] + z[5]) + (z[6] + z[7]));
+  __syncthreads();
+  if (tid < 128) a.d.out[((int64_t)b * a.d.hq + h) * 128 + j] += SQRT_HALF_PI / 128.f * (os[0][j] + os[1][j]);
 }
 
 // Workspace of the QJL fast route: [fast partials | sq | bias | scores | ml | upart], 256-byte pieces.
@@ -1136,7 +1141,7 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     default: hipLaunchKernelGGL((qjl_value_kernel<8>), vgrid, dim3(NT), 0, s, qa); break;
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl value");
-  hipLaunchKernelGGL(qjl_final_kernel, dim3(d->hq, d->batch), dim3(128), 0, s, qa);
+  hipLaunchKernelGGL(qjl_final_kernel, dim3(d->hq, d->batch), dim3(256), 0, s, qa);
   TQ_LAUNCH_CHECK("tq_decode_attention qjl final");
   return TQ_OK;
 }

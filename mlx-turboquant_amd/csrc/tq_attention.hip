@@ -597,19 +597,19 @@ static int group_heads(int G) {
 // u_h = sum_t p_t gamma_t z_t per projection (p the normalised softmax
 // weight of compressed token t) and a final kernel adds sqrt(pi/2)/d S^T u_h to
 // the output, as combine_kernel does for the general path.
-constexpr int QCH = 256;  // tokens per chunk of the QJL kernels
-constexpr int QVC = 1;    // chunks per workgroup of the value kernel (more per workgroup measured slower)
-constexpr int QBC = 8;    // chunks per workgroup of the bias kernel (one sign-pattern table for all)
+constexpr int QCH = 256;  // tokens per chunk of the QJL kernels (one chunk per value-kernel workgroup)
+constexpr int QBC = 4;    // chunks per workgroup of the bias kernel (one sign-pattern table for all)
 
 struct QjlArgs {
   tq_attn_desc d;
   const float* sq;      // (batch, hq, m) S (scale q), natural units (qjl_sq_kernel)
   const float* proj;    // (m, 128)
   int m;
+  int ksign16, vsign16; // key / value sign rows 16-byte aligned with m a multiple of 128 (16-byte loads)
   float* bias;          // (batch*hkv*G, qb_hs) key term in base-2 score units
   const float* scores;  // (batch*hkv*G, qb_hs) final base-2 scores
   const float* ml;      // (batch, hq, 2) global max and sum of the merge
-  float* upart;         // (batch, hq, nvc, m) value terms, one per value-kernel workgroup (QVC chunks)
+  float* upart;         // (batch, hq, nvc, m) value terms, one per value-kernel workgroup
   int64_t qb_hs;
   int nvc;
 };
@@ -645,69 +645,100 @@ __global__ __launch_bounds__(128) void qjl_sq_kernel(QjlArgs a) {
   }
 }
 
+typedef _Float16 qh8 __attribute__((ext_vector_type(8)));
+typedef float qf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t qu4 __attribute__((ext_vector_type(4)));
+
+// The nw = m / 32 sign words of token row `p` (m / 8 bytes): 16-byte loads
+// when the rows allow them (v16), else one word per load. NW4: words held,
+// in groups of 4 (nw <= 4 NW4).
+template <int NW4>
+__device__ inline void load_sign_row(const uint8_t* p, int nw, bool v16, uint32_t (&sw)[4 * NW4]) {
+  const uint32_t* wp = reinterpret_cast<const uint32_t*>(p);
+  if (v16) {
+#pragma unroll
+    for (int q = 0; q < NW4; ++q) {
+      const qu4 x = reinterpret_cast<const qu4*>(p)[q];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sw[4 * q + k] = x[k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4 * NW4; ++k) sw[k] = k < nw ? wp[k] : 0u;
+  }
+}
+
 // Key term of each compressed token: z_h = sum_k sign_k (S q_h)_k from a
 // table of the 16 sign patterns of each 4 consecutive projections, lut[p][n][h]
 // = sum_{j < 4} (bit j of n ? 1 : -1) (S q_h)_{4p + j} (one LDS read of G
-// floats and G adds per 4 signs).
-template <int G>
+// floats and G adds per 4 signs). Thread tid takes tokens (c QBC + i) QCH +
+// tid, i < QBC: S q and all of its tokens' sign rows and gammas are requested
+// up front, so the workgroup waits for one memory round trip.
+template <int G, int NW4>
 __global__ __launch_bounds__(NT) void qjl_bias_kernel(QjlArgs a) {
-  constexpr int MAXM = 256;
+  constexpr int MAXM = 128 * NW4;
   __shared__ __align__(16) float lut[MAXM / 4][16][G];
+  __shared__ float sqs[G][MAXM];
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
-  const int row = b * a.d.hkv + g, m = a.m;
+  const int row = b * a.d.hkv + g, m = a.m, nw = m / 32;
   const int comp = seq_comp(a.d, b);
   // past the sequence's last 32-token block the bias is never read (those
   // scores are masked after it is added)
-  if (c * QBC * QCH >= ((comp + 31) & ~31)) return;
+  const int tend = min((int)a.qb_hs, (comp + 31) & ~31);
+  if (c * QBC * QCH >= tend) return;
+  constexpr int NSQ = (G * MAXM + NT - 1) / NT;
+  float sqv[NSQ];
+  {
+    const float* sqp = a.sq + ((int64_t)b * a.d.hq + g * G) * m;  // the G rows are contiguous
+#pragma unroll
+    for (int i = 0; i < NSQ; ++i) sqv[i] = tid + NT * i < G * m ? sqp[tid + NT * i] : 0.f;
+  }
+  const tq_store& ks = a.d.kstore;
+  uint32_t sw[QBC][4 * NW4];
+  float gk[QBC];
+#pragma unroll
+  for (int i = 0; i < QBC; ++i) {
+    const int tc = min((c * QBC + i) * QCH + tid, comp - 1);  // comp >= 1 here
+    gk[i] = ks.gamma[(int64_t)row * ks.gamma_head_stride + tc];
+    load_sign_row<NW4>(ks.signs + (int64_t)row * ks.sign_head_stride + (int64_t)tc * (m / 8), nw, a.ksign16 != 0, sw[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < NSQ; ++i)
+    if (tid + NT * i < G * m) sqs[(tid + NT * i) / m][(tid + NT * i) % m] = sqv[i];
+  __syncthreads();
   for (int e = tid; e < (m / 4) * 16 * G; e += NT) {
     const int h = e % G, n = (e / G) & 15, p = e / (16 * G);
-    const float* sqh = a.sq + ((int64_t)b * a.d.hq + g * G + h) * m + 4 * p;
     float v = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v += ((n >> j) & 1) ? sqh[j] : -sqh[j];
+    for (int j = 0; j < 4; ++j) v += ((n >> j) & 1) ? sqs[h][4 * p + j] : -sqs[h][4 * p + j];
     lut[p][n][h] = v;
   }
   __syncthreads();
-  // tokens c QBC QCH + tid + QCH i: the bias of the tokens past comp (up to
-  // the 32-token block) is 0
-  const int tend = min((int)a.qb_hs, (comp + 31) & ~31);
-  const tq_store& ks = a.d.kstore;
+#pragma unroll
   for (int i = 0; i < QBC; ++i) {
     const int t = (c * QBC + i) * QCH + tid;
     if (t >= tend) break;
     float zs[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) zs[h] = 0.f;
-    float coef = 0.f;
-    if (t < comp) {
-      const float gk = ks.gamma[(int64_t)row * ks.gamma_head_stride + t];
-      const uint32_t* sw = reinterpret_cast<const uint32_t*>(ks.signs + (int64_t)row * ks.sign_head_stride +
-                                                             (int64_t)t * (m / 8));
-      for (int wi = 0; wi < m / 32; ++wi) {
-        const uint32_t wd = sw[wi];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float* e = lut[8 * wi + k][(wd >> (4 * k)) & 15u];
+    for (int wi = 0; wi < 4 * NW4; ++wi) {
+      if (wi >= nw) break;
+      const uint32_t wd = sw[i][wi];
 #pragma unroll
-          for (int h = 0; h < G; ++h) zs[h] += e[h];
-        }
+      for (int k = 0; k < 8; ++k) {
+        const float* e = lut[8 * wi + k][(wd >> (4 * k)) & 15u];
+#pragma unroll
+        for (int h = 0; h < G; ++h) zs[h] += e[h];
       }
-      coef = 1.4426950408889634f * SQRT_HALF_PI / 128.f * gk;
     }
+    // the bias of the tokens past comp (up to the 32-token block) is 0
+    const float coef = t < comp ? 1.4426950408889634f * SQRT_HALF_PI / 128.f * gk[i] : 0.f;
 #pragma unroll
     for (int h = 0; h < G; ++h) a.bias[((int64_t)row * G + h) * a.qb_hs + t] = coef * zs[h];
   }
 }
 
-typedef _Float16 qh8 __attribute__((ext_vector_type(8)));
-typedef float qf4 __attribute__((ext_vector_type(4)));
-typedef uint32_t qu4 __attribute__((ext_vector_type(4)));
-
-// u = sum_t w_t z_t (w_t = p_t gamma_t per head) by MFMA 16x16x32 f16:
-// A = W (row h: the fp16 high part of head h's weights, row h + 8 the
-// remainder; k = 32 tokens of a block), B = Z (k = the same tokens, columns =
-// 16 projections, exact +-1 built from the staged sign rows), so output rows h
-// and h + 8 added give head h. Wave w takes the projection tiles w, w + 4, ...
 // max over the 64 lanes of a wave in VALU cross-lane moves: DPP rotations
 // within each 16-lane row, then the four rows (every lane gets the result)
 __device__ inline float wave_max_dpp(float v) {
@@ -721,165 +752,193 @@ __device__ inline float wave_max_dpp(float v) {
   return fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
 }
 
-template <int G>
+// max over the 64 lanes of a wave of non-negative floats, compared as their
+// bit patterns (unsigned integers order them alike)
+__device__ inline uint32_t wave_max_nonneg(float f) {
+  uint32_t v = __float_as_uint(f);
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x122, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x121, 0xF, 0xF, true));
+  const auto x = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(x[0], x[1]);
+  const auto y = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(y[0], y[1]);
+}
+
+// the value of lane ^ 1 (DPP quad permutation 1, 0, 3, 2)
+__device__ inline uint32_t lane_xor1(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true);
+}
+
+// u_h = sum_t w_t z_t (w_t = 2^(s_t - M) gamma_t for head h, z_t the +-1
+// sign row of token t) by MFMA 16x16x32 f16, one 256-token chunk per
+// workgroup, thread t = token t of the chunk:
+//   A = W: row h the fp16 high part of head h's weights times 2^(14 - E_h)
+//       (E_h the exponent of the chunk's max weight of head h: none is
+//       subnormal in fp16 but the tiny), row h + 8 the remainder; k = the 32
+//       tokens of a block;
+//   B = Z: k = the same tokens, column = one of 16 projections, built from a
+//       word holding the 16 projection bits of two tokens in its halves: the
+//       lane's bit shifted to bit 15 / 31 and or-ed into 0x3C00 gives 1 for a
+//       clear bit and -1 for a set one, i.e. -z (the sums are negated back).
+// Output rows h and h + 8 (lanes q4 and q4 + 2) added give head h. Wave w
+// takes the projection tiles w, w + 4, ... The weights stay unnormalised
+// (O(gamma), whatever the context length); 2^(E_h - 14) / L_h is applied in
+// float32 to the sums.
+template <int G, int NW4>
 __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
-  __shared__ __align__(16) float pw[G][QCH];
-  // sign words transposed: sgw[k][t] = projections 32k .. 32k + 31 of token
-  // t, so a lane reads its 8 consecutive tokens' words in two 16-byte loads
-  __shared__ __align__(16) uint32_t sgw[256 / 32][QCH];
-  __shared__ uint32_t wmx[G];  // per head: the chunk's max weight (float bits; weights are >= 0)
-  __shared__ float invl[G];    // per head: 1 / L
-  __shared__ __align__(16) qu4 awl[QCH / 32][16][4];  // MFMA A operands (weights), lane (r, q4) of block bk
+  static_assert(NT == QCH, "thread t = token t of the chunk");
+  constexpr int MAXM = 128 * NW4;
+  constexpr int YS = QCH / 2 + 32;  // row of ysm (+32 words: the rows the even and odd threads write sit 32 banks apart)
+  // A operands, word (bk, q4, row, pair) at bk ASB + q4 ASQ + 4 row + pair:
+  // the 16 rows of a (bk, q4) group contiguous (a lane's 16-byte read, 16
+  // lanes over all banks); groups padded so that the words one wave writes
+  // (two blocks x 4 groups x 4 pairs x 2 row halves) fall in 64 banks
+  constexpr int ASQ = 68, ASB = 4 * ASQ;
+  // ysm[c][p]: projections 16c .. 16c + 15 of token 2p (low half) and 2p + 1 (high half)
+  __shared__ __align__(16) uint32_t ysm[MAXM / 16][YS];
+  __shared__ __align__(16) uint32_t aw[QCH / 32 * ASB];
+  __shared__ uint32_t wm[NT / 64][G];  // per wave and head: the max weight (float bits)
   const int cg = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
-  const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq;
+  const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq, nw = m / 32;
   const int comp = seq_comp(a.d, b);
+  const int base = cg * QCH, nvalid = min(QCH, comp - base);
+  if (nvalid <= 0) return;  // past the sequence: qjl_final_kernel reads no partial of it
   const tq_store& vs = a.d.vstore;
   const int lane = tid & 63, w = tid >> 6, r = lane & 15, q4 = lane >> 4;
-  // head h's weights enter fp16 as w 2^(14 - E_h) (E_h the exponent of the
-  // chunk's max weight: operands below 2^15, none subnormal but the tiny)
-  auto head_exp = [&](int hh) {
-    const uint32_t mb = wmx[hh];
-    return mb == 0u ? 0 : max((int)((mb >> 23) & 0xFFu), 1) - 127;
-  };
-  // the wave's projection tiles ct = w + 4k (k < QT), summed over the chunks
-  // of the group in float32: rows 4 q4 + i (q4 < 2) of tile k
-  constexpr int QT = 256 / 16 / (NT / 64);
-  float tot[QT][4];
+  const int t = tid, tc = min(t, nvalid - 1);
+  // ---- the token's sign row, gamma and scores; the heads' max and sum
+  uint32_t sw[4 * NW4];
+  load_sign_row<NW4>(vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base * (m / 8) + tc * (m / 8), nw,
+                     a.vsign16 != 0, sw);
+  const float gv = vs.gamma[(int64_t)row * vs.gamma_head_stride + base + tc];
+  float sc[G], Mh[G], Lh[G];
+  {
+    const float* sp = a.scores + (int64_t)row * G * a.qb_hs + base + tc;
+    const float* mlp = a.ml + ((int64_t)b * hq + g * G) * 2;
 #pragma unroll
-  for (int k = 0; k < QT; ++k)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) tot[k][i] = 0.f;
-  if (tid < G) {
-    const float L = a.ml[((int64_t)b * hq + g * G + tid) * 2 + 1];
-    invl[tid] = L > 0.f ? 1.f / L : 0.f;
-  }
-  for (int cc = 0; cc < QVC; ++cc) {
-    const int base = (cg * QVC + cc) * QCH, nvalid = max(0, min(QCH, comp - base));
-    if (nvalid == 0) break;  // past the sequence (uniform over the workgroup)
-    __syncthreads();  // the previous chunk's readers of pw / sgw / wmx are done
-    if (tid < G) wmx[tid] = 0u;
-    __syncthreads();
-    // unnormalised weights w = 2^(s - M) gamma (O(gamma), whatever the context
-    // length); 1 / L is applied in float32 to the sums
-    {
-      const int t = tid;
-      const float gv = t < nvalid ? vs.gamma[(int64_t)row * vs.gamma_head_stride + base + t] : 0.f;
-#pragma unroll
-      for (int hh = 0; hh < G; ++hh) {
-        float p = 0.f;
-        if (t < nvalid) {
-          const float M = a.ml[((int64_t)b * hq + g * G + hh) * 2], L = a.ml[((int64_t)b * hq + g * G + hh) * 2 + 1];
-          const float sc = a.scores[((int64_t)row * G + hh) * a.qb_hs + base + t];
-          p = L > 0.f ? __builtin_amdgcn_exp2f(sc - M) : 0.f;
-        }
-        const float wt = p * gv;
-        pw[hh][t] = wt;
-        const float mx = wave_max_dpp(wt);
-        if ((tid & 63) == 0) atomicMax(&wmx[hh], __float_as_uint(mx));
-      }
-    }
-    {
-      const uint32_t* gs = reinterpret_cast<const uint32_t*>(vs.signs + (int64_t)row * vs.sign_head_stride +
-                                                             (int64_t)base * (m / 8));
-      const int nw = m / 32;
-      for (int e = tid; e < nvalid * nw; e += NT) {
-        const int t = e / nw, k = e - t * nw;
-        sgw[k][t] = gs[e];
-      }
-    }
-    __syncthreads();
-    const int nblk = (nvalid + 31) >> 5;
-    // A operands of the (at most 8) blocks, built once for the four waves:
-    // entry (bk, r, q4) = the weights of head r & 7 for tokens 32 bk + 8 q4
-    // .. + 7, their fp16 high part (r < 8) or remainder (r >= 8); zero past G
-    // and past nvalid
-    for (int e = tid; e < (QCH / 32) * 16 * 4; e += NT) {
-      const int bk = e >> 6, rr = (e >> 2) & 15, qq = e & 3, hh = rr & 7;
-      const int t0 = 32 * bk + 8 * qq;
-      const float up = hh < G ? __builtin_amdgcn_ldexpf(1.f, 14 - head_exp(hh)) : 0.f;
-      qu4 v;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        float w0 = 0.f, w1 = 0.f;
-        if (hh < G) {
-          w0 = pw[hh][t0 + 2 * k] * up;
-          w1 = pw[hh][t0 + 2 * k + 1] * up;
-        }
-        const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
-        const _Float16 l0 = (_Float16)(w0 - (float)h0), l1 = (_Float16)(w1 - (float)h1);
-        const _Float16 x0 = rr >= 8 ? l0 : h0, x1 = rr >= 8 ? l1 : h1;
-        v[k] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
-      }
-      awl[bk][rr][qq] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < QT; ++k) {
-      const int ct = w + (NT / 64) * k;
-      if (ct >= m / 16) break;
-      qf4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int bk = 0; bk < QCH / 32; ++bk) {
-        if (bk >= nblk) break;
-        const int t0 = 32 * bk + 8 * q4;
-        const qu4 av = awl[bk][r][q4];
-        // B: +-1 of projection 16 ct + r for the lane's 8 tokens (bit set -> +1)
-        const int pj = 16 * ct + r, bit = pj & 31;
-        const qu4 x0 = *reinterpret_cast<const qu4*>(&sgw[pj >> 5][t0]);
-        const qu4 x1 = *reinterpret_cast<const qu4*>(&sgw[pj >> 5][t0 + 4]);
-        const uint32_t xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        qu4 bv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t s0 = (xs[2 * e] >> bit) & 1u;
-          const uint32_t s1 = (xs[2 * e + 1] >> bit) & 1u;
-          bv[e] = 0xBC00BC00u ^ (s0 << 15) ^ (s1 << 31);
-        }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qh8, av), __builtin_bit_cast(qh8, bv), acc, 0,
-                                                     0, 0);
-      }
-      // rows 4 q4 + i: add the remainder rows (lane ^ 32 holds rows + 8),
-      // back to the chunk's weight scale
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
-        const float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-        const int hh = min(4 * q4 + i, G - 1);
-        tot[k][i] = fmaf(v, __builtin_amdgcn_ldexpf(1.f, head_exp(hh) - 14), tot[k][i]);
-      }
+    for (int h = 0; h < G; ++h) {
+      sc[h] = sp[h * a.qb_hs];
+      Mh[h] = mlp[2 * h];
+      Lh[h] = mlp[2 * h + 1];
     }
   }
-  __syncthreads();  // invl (an empty group has had no barrier)
+  // ---- sign pairs: token 2p's word and token 2p + 1's word of projections
+  // 32k .. 32k + 31 give ysm[2k][p] (low halves, by the even thread) and
+  // ysm[2k + 1][p] (high halves, by the odd thread)
+  const bool odd = (t & 1) != 0;
+#pragma unroll
+  for (int k = 0; k < 4 * NW4; ++k) {
+    if (k >= nw) break;
+    const uint32_t nb = lane_xor1(sw[k]);
+    ysm[2 * k + (odd ? 1 : 0)][t >> 1] =
+        odd ? __builtin_amdgcn_perm(sw[k], nb, 0x07060302u) : __builtin_amdgcn_perm(nb, sw[k], 0x05040100u);
+  }
+  // ---- unnormalised weights and their per-wave max per head
+  float wt[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float p = t < nvalid && Lh[h] > 0.f ? __builtin_amdgcn_exp2f(sc[h] - Mh[h]) : 0.f;
+    wt[h] = p * gv;
+    const uint32_t mx = wave_max_nonneg(wt[h]);
+    if (lane == 0) wm[w][h] = mx;
+  }
+  __syncthreads();
+  // E_h: the exponent of the chunk's max weight (weights are >= 0)
+  int eh[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    uint32_t mb = wm[0][h];
+#pragma unroll
+    for (int ww = 1; ww < NT / 64; ++ww) mb = max(mb, wm[ww][h]);
+    eh[h] = mb == 0u ? 0 : max((int)((mb >> 23) & 0xFFu), 1) - 127;
+  }
+  // ---- A operands: thread t of block bk = t >> 5, q4 group (t >> 3) & 3,
+  // token pair (t >> 1) & 3; the even thread writes the high-part pair of row
+  // h, the odd one the remainder pair of row h + 8; rows of absent heads zero
+  {
+    const int bk = t >> 5, qq = (t >> 3) & 3, j = (t >> 1) & 3;
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      uint32_t val = 0u;
+      if (h < G) {
+        const float x = wt[h] * __builtin_amdgcn_ldexpf(1.f, 14 - eh[h]);
+        const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
+        const uint32_t own = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+        const uint32_t nb = lane_xor1(own);
+        val = odd ? __builtin_amdgcn_perm(own, nb, 0x07060302u) : __builtin_amdgcn_perm(nb, own, 0x05040100u);
+      }
+      aw[bk * ASB + qq * ASQ + 4 * (h + (odd ? 8 : 0)) + j] = val;
+    }
+  }
+  __syncthreads();
+  // ---- the MFMAs of the wave's projection tiles over the chunk's blocks
+  const int nblk = (nvalid + 31) >> 5;
+  qu4 av[QCH / 32];
+#pragma unroll
+  for (int bk = 0; bk < QCH / 32; ++bk) av[bk] = *reinterpret_cast<const qu4*>(&aw[bk * ASB + q4 * ASQ + 4 * r]);
+  // lane (column r, q4) ends with rows 4 q4 + i: head 4 q4 + i for q4 < 2;
+  // its scale -2^(E_h - 14) / L_h (the B operands hold -z)
+  float hsc[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) hsc[h] = Lh[h] > 0.f ? -__builtin_amdgcn_ldexpf(1.f, eh[h] - 14) / Lh[h] : 0.f;
+  float osc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) osc[i] = q4 == 0 ? hsc[min(i, G - 1)] : hsc[min(4 + i, G - 1)];
+  float* uo = a.upart + (((int64_t)b * hq + g * G + 4 * q4) * a.nvc + cg) * m + r;  // row 4 q4 of the lane
+  const int64_t ust = (int64_t)a.nvc * m;                                            // next head
+  const uint32_t shl = 15u - (uint32_t)r;
+  // the sign-bit mask and the halves 1.0 in registers, so that each operand
+  // word is one shift and one bit-field insert
+  uint32_t bmask = 0x80008000u, bone = 0x3C003C00u;
+  asm volatile("" : "+v"(bmask), "+s"(bone));
+  constexpr int QT = MAXM / 16 / (NT / 64);
 #pragma unroll
   for (int k = 0; k < QT; ++k) {
     const int ct = w + (NT / 64) * k;
     if (ct >= m / 16) break;
+    qf4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int bk = 0; bk < QCH / 32; ++bk) {
+      if (bk >= nblk) break;
+      const qu4 y = *reinterpret_cast<const qu4*>(&ysm[ct][16 * bk + 4 * q4]);
+      qu4 bv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[e] = ((y[e] << shl) & bmask) | (bone & ~bmask);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qh8, av[bk]), __builtin_bit_cast(qh8, bv), acc, 0,
+                                                   0, 0);
+    }
+    // rows 4 q4 + i: add the remainder rows (lane ^ 32 holds rows + 8)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
+      const float v = __uint_as_float(sw2[0]) + __uint_as_float(sw2[1]);
       const int hh = 4 * q4 + i;
-      if (q4 < 2 && hh < G)
-        a.upart[(((int64_t)b * hq + g * G + hh) * a.nvc + cg) * m + 16 * ct + r] = tot[k][i] * invl[hh];
+      if (q4 < 2 && hh < G) uo[i * ust + 16 * ct] = v * osc[i];
     }
   }
 }
 
 // Thread t: projection i = t & 127 (and i + 128) over the value partials of
-// parity t >> 7, then output dim j = t & 127 over projection rows of parity
-// t >> 7; eight independent sums each, so the loads go out eight at a time.
+// parity t >> 7 (the chunks holding compressed tokens of the sequence), then
+// output dim j = t & 127 over projection rows of parity t >> 7; eight
+// independent sums each, so the loads go out eight at a time.
 __global__ __launch_bounds__(256) void qjl_final_kernel(QjlArgs a) {
   __shared__ float us[2][256];
   __shared__ float os[2][128];
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, m = a.m;
   const int lo = tid & 127, par = tid >> 7;
   const float* up = a.upart + ((int64_t)b * a.d.hq + h) * a.nvc * m;
+  const int nvb = min(a.nvc, (seq_comp(a.d, b) + QCH - 1) / QCH);  // chunks the value kernel wrote
   for (int i = lo; i < m; i += 128) {
     float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     int c = par;
-    for (; c + 14 < a.nvc; c += 16) {
+    for (; c + 14 < nvb; c += 16) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] += up[(int64_t)(c + 2 * k) * m + i];
     }
-    for (; c < a.nvc; c += 2) v[0] += up[(int64_t)c * m + i];
+    for (; c < nvb; c += 2) v[0] += up[(int64_t)c * m + i];
     us[par][i] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
   }
   __syncthreads();
@@ -1014,7 +1073,7 @@ static QjlLayout qjl_layout(const tq_codec* kc, const tq_attn_desc* d) {
   const int m = kc->qjl_m;
   L.qb_hs = ((int64_t)d->max_comp + 31) / 32 * 32;
   if (L.qb_hs < 32) L.qb_hs = 32;
-  L.nvc = ((d->max_comp + QCH - 1) / QCH + QVC - 1) / QVC;  // value-kernel workgroups per (b, g)
+  L.nvc = (d->max_comp + QCH - 1) / QCH;  // value-kernel workgroups per (b, g)
   if (L.nvc < 1) L.nvc = 1;
   size_t off = 0;
   L.part = off; off += al256(fast_part_bytes(d));
@@ -1109,6 +1168,13 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   qa.sq = reinterpret_cast<float*>(ws + QL.pro);
   qa.proj = kc->qjl_proj;
   qa.m = kc->qjl_m;
+  // 16-byte loads of the sign rows: rows of a multiple of 16 bytes at 16-byte alignment
+  auto sign16 = [&](const tq_store& st) {
+    return kc->qjl_m % 128 == 0 && aligned16(st.signs) && st.sign_head_stride % 16 == 0 ? 1 : 0;
+  };
+  qa.ksign16 = sign16(d->kstore);
+  qa.vsign16 = sign16(d->vstore);
+  const bool w8 = kc->qjl_m > 128;  // more than 4 sign words per token
   qa.bias = reinterpret_cast<float*>(ws + QL.bias);
   qa.scores = reinterpret_cast<float*>(ws + QL.scores);
   qa.ml = reinterpret_cast<float*>(ws + QL.ml);
@@ -1123,22 +1189,30 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl S q");
   const dim3 bgrid((unsigned)((QL.qb_hs + QBC * QCH - 1) / (QBC * QCH)), d->hkv, d->batch);
-  switch (G) {
-    case 1: hipLaunchKernelGGL((qjl_bias_kernel<1>), bgrid, dim3(NT), 0, s, qa); break;
-    case 2: hipLaunchKernelGGL((qjl_bias_kernel<2>), bgrid, dim3(NT), 0, s, qa); break;
-    case 4: hipLaunchKernelGGL((qjl_bias_kernel<4>), bgrid, dim3(NT), 0, s, qa); break;
-    default: hipLaunchKernelGGL((qjl_bias_kernel<8>), bgrid, dim3(NT), 0, s, qa); break;
+  switch (G * 2 + (w8 ? 1 : 0)) {
+    case 2: hipLaunchKernelGGL((qjl_bias_kernel<1, 1>), bgrid, dim3(NT), 0, s, qa); break;
+    case 3: hipLaunchKernelGGL((qjl_bias_kernel<1, 2>), bgrid, dim3(NT), 0, s, qa); break;
+    case 4: hipLaunchKernelGGL((qjl_bias_kernel<2, 1>), bgrid, dim3(NT), 0, s, qa); break;
+    case 5: hipLaunchKernelGGL((qjl_bias_kernel<2, 2>), bgrid, dim3(NT), 0, s, qa); break;
+    case 8: hipLaunchKernelGGL((qjl_bias_kernel<4, 1>), bgrid, dim3(NT), 0, s, qa); break;
+    case 9: hipLaunchKernelGGL((qjl_bias_kernel<4, 2>), bgrid, dim3(NT), 0, s, qa); break;
+    case 16: hipLaunchKernelGGL((qjl_bias_kernel<8, 1>), bgrid, dim3(NT), 0, s, qa); break;
+    default: hipLaunchKernelGGL((qjl_bias_kernel<8, 2>), bgrid, dim3(NT), 0, s, qa); break;
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl bias");
   if (launch_k4v2(kc, vc, d, reinterpret_cast<float*>(ws + QL.part), true, qa.bias, const_cast<float*>(qa.scores),
                   QL.qb_hs, const_cast<float*>(qa.ml), 1, s) != 0)
     TQ_LAUNCH_CHECK("tq_decode_attention qjl fast");
   const dim3 vgrid((unsigned)QL.nvc, d->hkv, d->batch);
-  switch (G) {
-    case 1: hipLaunchKernelGGL((qjl_value_kernel<1>), vgrid, dim3(NT), 0, s, qa); break;
-    case 2: hipLaunchKernelGGL((qjl_value_kernel<2>), vgrid, dim3(NT), 0, s, qa); break;
-    case 4: hipLaunchKernelGGL((qjl_value_kernel<4>), vgrid, dim3(NT), 0, s, qa); break;
-    default: hipLaunchKernelGGL((qjl_value_kernel<8>), vgrid, dim3(NT), 0, s, qa); break;
+  switch (G * 2 + (w8 ? 1 : 0)) {
+    case 2: hipLaunchKernelGGL((qjl_value_kernel<1, 1>), vgrid, dim3(NT), 0, s, qa); break;
+    case 3: hipLaunchKernelGGL((qjl_value_kernel<1, 2>), vgrid, dim3(NT), 0, s, qa); break;
+    case 4: hipLaunchKernelGGL((qjl_value_kernel<2, 1>), vgrid, dim3(NT), 0, s, qa); break;
+    case 5: hipLaunchKernelGGL((qjl_value_kernel<2, 2>), vgrid, dim3(NT), 0, s, qa); break;
+    case 8: hipLaunchKernelGGL((qjl_value_kernel<4, 1>), vgrid, dim3(NT), 0, s, qa); break;
+    case 9: hipLaunchKernelGGL((qjl_value_kernel<4, 2>), vgrid, dim3(NT), 0, s, qa); break;
+    case 16: hipLaunchKernelGGL((qjl_value_kernel<8, 1>), vgrid, dim3(NT), 0, s, qa); break;
+    default: hipLaunchKernelGGL((qjl_value_kernel<8, 2>), vgrid, dim3(NT), 0, s, qa); break;
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl value");
   hipLaunchKernelGGL(qjl_final_kernel, dim3(d->hq, d->batch), dim3(256), 0, s, qa);

@@ -1029,7 +1029,8 @@ static bool uniform_route(const tq_codec* vc, const tq_attn_desc* d, int& nwg, i
 static size_t fast_part_bytes(const tq_attn_desc* d) {
   const int G = d->hkv > 0 ? d->hq / d->hkv : 1;
   int nwg, bpw, fpw;
-  size_t b = (size_t)fast_plan(d).vmax * G * PACKED_PART_FLOATS * 4;
+  // the partial slots, then the ragged plan's per-sequence table
+  size_t b = al256((size_t)fast_plan(d).vmax * G * PACKED_PART_FLOATS * 4) + (size_t)d->batch * 8;
   if (uniform_geometry(d, nwg, bpw, fpw)) {
     const size_t u = (size_t)d->batch * d->hkv * nwg * G * PACKED_PART_FLOATS * 4;
     if (u > b) b = u;
@@ -1109,6 +1110,8 @@ static void fill_fast(FastArgs& f, const tq_codec* kc, const tq_codec* vc, const
   f.part = part;
   const FastPlan p = fast_plan(d);
   f.nwg = p.nwg; f.chunks = p.chunks; f.vmax = p.vmax;
+  f.plan_tab = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(part) +
+                                          al256((size_t)p.vmax * (d->hq / d->hkv) * PACKED_PART_FLOATS * 4));
   f.uni = !d->comp_len && !d->sink_len && !d->res_len;
   if (f.uni) fast_uniform_plan(d->batch, d->hkv, d->max_comp, d->max_sink, d->max_res, f.nwg, f.chunks, f.plan_T,
                                f.plan_nu, f.plan_V);

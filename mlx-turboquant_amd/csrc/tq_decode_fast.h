@@ -59,6 +59,8 @@ struct FastArgs {
   float* scores;         // final base-2 scores of the compressed tokens (written)
   int64_t qb_hs;
   float* ml;             // merge output: (batch, hq, 2) global max and sum, or NULL
+  int32_t* plan_tab;     // (batch, 2): first partial slot N_b and chunks n_b per kv head of each sequence,
+                         // written by the partials kernel when uni == 0 (workspace, after the partials)
 };
 
 // Host-side sizing of the K4/V2 path for a call: workgroups, chunks per

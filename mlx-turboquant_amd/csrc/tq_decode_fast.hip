@@ -75,7 +75,6 @@ constexpr float PV_LIMIT = 32768.f;
 // |scale * (R q)_j| <= scale * ||q|| must stay below this for the fp16 query
 // operands; larger queries are scaled by a power of two per head.
 constexpr float Q_LIMIT = 16384.f;
-constexpr int MERGE_SLOTS = 2112;    // partial slots of one (b, g) the merge kernel holds weights for (a multiple of 32)
 
 // LDS layout. Lookup tables: key entry of code byte e (two 4-bit codes) and
 // value entry of byte e (four 2-bit codes), NCP replicas of 8 bytes each in
@@ -324,6 +323,26 @@ struct Seg {
   int comp, sink, nf, rstart;
 };
 
+// Per sequence b: (N_b, n_b) of the plan into tab[2b], tab[2b + 1], for the
+// merge kernel (one wave; the lanes take 64 sequences at a time).
+__device__ void write_plan_table(const FastArgs& a, const Plan& p, int32_t* tab) {
+  const int lane = threadIdx.x & 63;
+  int carry = 0;
+  for (int base = 0; base < a.batch; base += 64) {
+    const int b = base + lane;
+    SeqLen s{};
+    if (b < a.batch) s = seq_len(a, b);
+    const int w = b < a.batch ? units_of(s.comp, s.sink + s.res) : 0;
+    const int n = a.hkv * cdiv(w, p.T);
+    const int end = carry + wave_prefix(n);
+    if (b < a.batch) {
+      tab[2 * b] = end - n;
+      tab[2 * b + 1] = n / a.hkv;
+    }
+    carry = __builtin_amdgcn_readlane(end, 63);
+  }
+}
+
 __device__ inline Seg segment(const FastArgs& a, const Plan& P, int v, int v1) {
   const Loc L = locate(a, P, v, false);
   Seg S;
@@ -432,6 +451,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
     ve[k] = a.vlut[e];
   }
   const Plan P = make_plan(a);
+  if (!P.uni && blockIdx.x == 0 && w == 0) write_plan_table(a, P, a.plan_tab);
   const int v0 = (int)((int64_t)blockIdx.x * P.V / a.nwg);
   const int v1 = (int)((int64_t)(blockIdx.x + 1) * P.V / a.nwg);
 
@@ -964,130 +984,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
 }
 
 // ---------------------------------------------------------------- merge kernel
-// Query head hqi of sequence b, output dims [32 sl, 32 sl + 32): the partials
-// of (b, g) combined with w_p = 2^(M_p - M) L_p / L (M = max_p M_p, L = sum_p
-// 2^(M_p - M) L_p), then out = (sum_p w_p rot_p) @ R + sum_p w_p orig_p
-// (float32, R of the value codec). Thread t holds rotated dim t and, for
-// t < 32, original-space dim 32 sl + t; the loads of the first MB partials
-// are issued together with the headers and the R column slice.
-constexpr int MB = 32;  // partials per batch of loads
-
-__device__ inline float block_max128(float v, float* sh) {
-  v = fmaxf(v, row_ror<8>(v));
-  v = fmaxf(v, row_ror<4>(v));
-  v = fmaxf(v, row_ror<2>(v));
-  v = fmaxf(v, row_ror<1>(v));
-  v = rows_max(v);
-  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return fmaxf(sh[0], sh[1]);
-}
-
-__device__ inline float block_sum128(float v, float* sh) {
-  v += row_ror<8>(v);
-  v += row_ror<4>(v);
-  v += row_ror<2>(v);
-  v += row_ror<1>(v);
-  v = rows_sum(v);
-  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return sh[0] + sh[1];
-}
-
-template <int G>
-__global__ __launch_bounds__(128) void decode_merge_kernel(FastArgs a) {
-  __shared__ float wsh[MERGE_SLOTS];  // w_p (0 for empty partials)
-  __shared__ float hsh[MERGE_SLOTS];  // has_orig_p
-  __shared__ float rs[FD];
-  __shared__ float red[4][32];
-  __shared__ float rm[2], rl[2];
-  const int sl = blockIdx.x, hqi = blockIdx.y, b = blockIdx.z;
-  const int g = hqi / G, h = hqi % G;
-  const int tid = threadIdx.x;
-  const int jj = tid & 31, qq = tid >> 5;
-
-  // R[i][32 sl + jj] for the 32 rows i of this thread's quarter
-  float rv[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) rv[i] = a.vrot[(32 * qq + i) * FD + 32 * sl + jj];
-
-  const Plan P = make_plan(a);
-  const Loc L = locate(a, P, b, true);
-  const int s0 = L.Nb + g * L.nb, cnt = L.nb;
-  const float* pp = a.part + ((int64_t)s0 * G + h) * PPS;  // partial p at pp + p * G * PPS
-  const int64_t pst = (int64_t)G * PPS;
-  const int last = max(cnt - 1, 0);
-  float x[MB], xo[MB];
-#pragma unroll
-  for (int i = 0; i < MB; ++i) {
-    x[i] = pp[min(i, last) * pst + P_OUT + tid];
-    xo[i] = pp[min(i, last) * pst + P_OUT + FD + 32 * sl + jj];
-  }
-  float4 hd0 = make_float4(M_INIT, 0.f, 0.f, 0.f);
-  if (tid < cnt) hd0 = *reinterpret_cast<const float4*>(pp + tid * pst);
-
-  // the global max over the partials with a sum (headers past 128 in a loop)
-  float m = hd0.y > 0.f ? hd0.x : M_INIT;
-  for (int p = tid + 128; p < cnt; p += 128) {
-    const float2 hh = *reinterpret_cast<const float2*>(pp + p * pst);
-    if (hh.y > 0.f) m = fmaxf(m, hh.x);
-  }
-  const float M = block_max128(m, rm);
-  float ls = 0.f;
-  const int cpad = (cnt + MB - 1) / MB * MB;  // weights past cnt are zero
-  for (int p = tid; p < cpad; p += 128) {
-    float4 hh = make_float4(M_INIT, 0.f, 0.f, 0.f);
-    if (p < cnt) hh = p == tid ? hd0 : *reinterpret_cast<const float4*>(pp + p * pst);
-    const float wp = hh.y > 0.f ? fexp2(hh.x - M) * hh.y : 0.f;
-    wsh[p] = wp;
-    hsh[p] = hh.y > 0.f ? hh.z : 0.f;
-    ls += wp;
-  }
-  const float Ls = block_sum128(ls, rl);  // its barrier also publishes wsh / hsh
-  const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
-  float acc = 0.f, acco = 0.f;
-  for (int p0 = 0; p0 < cnt; p0 += MB) {
-    if (p0 > 0) {
-#pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        x[i] = pp[min(p0 + i, last) * pst + P_OUT + tid];
-        xo[i] = pp[min(p0 + i, last) * pst + P_OUT + FD + 32 * sl + jj];
-      }
-    }
-    // branch-free: values of empty partials (weight 0) and of partials
-    // without an original-space part are replaced by 0 (they may hold
-    // anything, NaN included)
-#pragma unroll
-    for (int i = 0; i < MB; i += 4) {
-      const float4 w4 = *reinterpret_cast<const float4*>(wsh + p0 + i);
-      const float4 h4 = *reinterpret_cast<const float4*>(hsh + p0 + i);
-      const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, hv[4] = {h4.x, h4.y, h4.z, h4.w};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        acc = fmaf(wv[u], wv[u] != 0.f ? x[i + u] : 0.f, acc);
-        acco = fmaf(wv[u], hv[u] != 0.f ? xo[i + u] : 0.f, acco);
-      }
-    }
-  }
-  rs[tid] = acc * inv;
-  __syncthreads();
-  float o = 0.f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) o = fmaf(rs[32 * qq + i], rv[i], o);
-  red[qq][jj] = o;
-  __syncthreads();
-  if (tid < 32)
-    a.out[((int64_t)b * a.hq + hqi) * FD + 32 * sl + tid] =
-        (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]) + acco * inv;
-  if (a.ml && sl == 0 && tid == 0) {
-    a.ml[((int64_t)b * a.hq + hqi) * 2] = M;
-    a.ml[((int64_t)b * a.hq + hqi) * 2 + 1] = Ls;
-  }
-}
-
-// ------------------------------------------------ merge of original-space partials
-// (the dense kernel's): one wave per (query head, half of the dims); lane p +
-// 64k holds the header of partial p + 64k, lane j sums dim 64 * half + j.
+// max / sum over the 64 lanes of a wave (every lane gets the result)
 __device__ inline float wave_max(float v) {
   v = fmaxf(v, row_ror<8>(v));
   v = fmaxf(v, row_ror<4>(v));
@@ -1104,6 +1001,137 @@ __device__ inline float wave_sum(float v) {
   return rows_sum(v);
 }
 
+// Query head hqi of sequence b: the partials of (b, g) combined with w_p =
+// 2^(M_p - M) L_p / L (M = max_p M_p, L = sum_p 2^(M_p - M) L_p), then out =
+// (sum_p w_p rot_p) @ R + sum_p w_p f_p orig_p (float32, R the value codec's
+// rotation). One workgroup of 256 threads per (query head, sequence): every
+// wave reads all headers for M and L (no barrier), thread t sums dim t & 127
+// of the partials of parity t >> 7 with the weights recomputed from the
+// headers (uniform over the wave: scalar loads), and for the rotation takes
+// output dims 4 (t & 31) .. + 3 over rows 16 (t >> 5) .. + 15 of R. The first
+// MB partials of each parity and the R block are requested with the headers.
+constexpr int MB = 32;   // partials per batch of loads (orig_merge_kernel)
+constexpr int RMB = 16;  // partials per parity per batch of loads (decode_merge_kernel)
+constexpr int RMT = 256; // threads of decode_merge_kernel
+
+template <int G>
+__global__ __launch_bounds__(RMT) void decode_merge_kernel(FastArgs a) {
+  __shared__ __align__(16) float ys[2][FD];   // the two parities' weighted sums, rotated
+  __shared__ __align__(16) float xs[2][FD];   // and original-space
+  __shared__ __align__(16) float red[8][FD];  // rotation: sums over the 8 row blocks
+  const int hqi = blockIdx.x, b = blockIdx.y;
+  const int g = hqi / G, h = hqi % G;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int d = tid & (FD - 1), par = tid >> 7;
+
+  // R[16 ib + k][j4 .. j4 + 3]: independent of the plan, requested first
+  const int j4 = 4 * (tid & 31), ib = tid >> 5;
+  float4 rr[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) rr[k] = *reinterpret_cast<const float4*>(a.vrot + (16 * ib + k) * FD + j4);
+
+  // the partials of (b, g): slots N_b + g n_b .. + n_b - 1 (the uniform plan
+  // from the host's figures, else the partials kernel's table)
+  int Nb, nb;
+  if (a.uni) {
+    nb = a.plan_nu;
+    Nb = b * a.hkv * nb;
+  } else {
+    const int2 e = *reinterpret_cast<const int2*>(a.plan_tab + 2 * b);
+    Nb = e.x;
+    nb = e.y;
+  }
+  const int s0 = Nb + g * nb, cnt = nb;
+  const int64_t pst = (int64_t)G * PPS;
+  const float* pp = a.part + ((int64_t)s0 * G + h) * PPS;  // partial p at pp + p * pst
+  const int last = max(cnt - 1, 0);
+  const int upar = __builtin_amdgcn_readfirstlane(par);  // wave-uniform
+  // one round of loads: the first RMB partials of the parity (values and,
+  // uniform over the wave, headers) and the headers lane + 64 k
+  float x[RMB], xo[RMB];
+  float4 hu[RMB];
+#pragma unroll
+  for (int i = 0; i < RMB; ++i) {
+    const float* pr = pp + min(2 * i + upar, last) * pst;
+    hu[i] = *reinterpret_cast<const float4*>(pr);
+    x[i] = pr[P_OUT + d];
+    xo[i] = pr[P_OUT + FD + d];
+  }
+  constexpr int HK = 4;  // headers per lane held in registers (cnt <= 256)
+  float2 hl[HK];
+#pragma unroll
+  for (int k = 0; k < HK; ++k) hl[k] = *reinterpret_cast<const float2*>(pp + min(lane + 64 * k, last) * pst);
+  // the global max and sum, every wave over all headers
+  float m = M_INIT;
+#pragma unroll
+  for (int k = 0; k < HK; ++k)
+    if (lane + 64 * k < cnt && hl[k].y > 0.f) m = fmaxf(m, hl[k].x);
+  for (int p = lane + 64 * HK; p < cnt; p += 64) {
+    const float2 hh = *reinterpret_cast<const float2*>(pp + p * pst);
+    if (hh.y > 0.f) m = fmaxf(m, hh.x);
+  }
+  const float M = wave_max(m);
+  float ls = 0.f;
+#pragma unroll
+  for (int k = 0; k < HK; ++k) ls += lane + 64 * k < cnt && hl[k].y > 0.f ? fexp2(hl[k].x - M) * hl[k].y : 0.f;
+  for (int p = lane + 64 * HK; p < cnt; p += 64) {
+    const float2 hh = *reinterpret_cast<const float2*>(pp + p * pst);
+    ls += hh.y > 0.f ? fexp2(hh.x - M) * hh.y : 0.f;
+  }
+  const float Ls = wave_sum(ls);
+  const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+  float acc = 0.f, acco = 0.f;
+  for (int p0 = 0;; p0 += 2 * RMB) {
+    // branch-free: values of empty partials (weight 0) and of partials
+    // without an original-space part are replaced by 0 (they may hold
+    // anything, NaN included); partials past cnt have weight 0
+#pragma unroll
+    for (int i = 0; i < RMB; ++i) {
+      const int p = p0 + 2 * i + upar;
+      const float w = p < cnt && hu[i].y > 0.f ? fexp2(hu[i].x - M) * hu[i].y : 0.f;
+      acc = fmaf(w, w != 0.f ? x[i] : 0.f, acc);
+      acco = fmaf(w, w != 0.f && hu[i].z != 0.f ? xo[i] : 0.f, acco);
+    }
+    if (p0 + 2 * RMB >= cnt) break;
+#pragma unroll
+    for (int i = 0; i < RMB; ++i) {
+      const float* pr = pp + min(p0 + 2 * RMB + 2 * i + upar, last) * pst;
+      hu[i] = *reinterpret_cast<const float4*>(pr);
+      x[i] = pr[P_OUT + d];
+      xo[i] = pr[P_OUT + FD + d];
+    }
+  }
+  ys[par][d] = acc;
+  xs[par][d] = acco;
+  __syncthreads();
+  // rotation: rows 16 ib .. + 15 of R times the merged rotated sum
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int i = 16 * ib + k;
+    const float y = ys[0][i] + ys[1][i];  // one address per wave: a broadcast
+    o.x = fmaf(y, rr[k].x, o.x);
+    o.y = fmaf(y, rr[k].y, o.y);
+    o.z = fmaf(y, rr[k].z, o.z);
+    o.w = fmaf(y, rr[k].w, o.w);
+  }
+  *reinterpret_cast<float4*>(&red[ib][j4]) = o;
+  __syncthreads();
+  if (tid < FD) {
+    float r = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) r += red[k][tid];
+    a.out[((int64_t)b * a.hq + hqi) * FD + tid] = (r + (xs[0][tid] + xs[1][tid])) * inv;
+  }
+  if (a.ml && tid == 0) {
+    a.ml[((int64_t)b * a.hq + hqi) * 2] = M;
+    a.ml[((int64_t)b * a.hq + hqi) * 2 + 1] = Ls;
+  }
+}
+
+// ------------------------------------------------ merge of original-space partials
+// (the dense kernel's): one wave per (query head, half of the dims); lane p +
+// 64k holds the header of partial p + 64k, lane j sums dim 64 * half + j.
 struct OrigMergeArgs {
   const float* part;
   float* out;
@@ -1194,11 +1222,10 @@ void fast_uniform_plan(int batch, int hkv, int max_comp, int max_sink, int max_r
 template <int G, bool QB>
 static void launch_g(const FastArgs& a, int merge, hipStream_t s) {
   hipLaunchKernelGGL((decode_partials_kernel<G, QB>), dim3(a.nwg), dim3(FT), 0, s, a);
-  if (merge) hipLaunchKernelGGL((decode_merge_kernel<G>), dim3(4, a.hq, a.batch), dim3(128), 0, s, a);
+  if (merge) hipLaunchKernelGGL((decode_merge_kernel<G>), dim3(a.hq, a.batch), dim3(RMT), 0, s, a);
 }
 
 int launch_fast_decode(const FastArgs& a, int G, bool qb, int merge, hipStream_t s) {
-  if (a.chunks * a.nwg + 1 > MERGE_SLOTS) return -1;
   switch (G * 2 + (qb ? 1 : 0)) {
     case 2: launch_g<1, false>(a, merge, s); break;
     case 3: launch_g<1, true>(a, merge, s); break;

@@ -162,6 +162,26 @@ def test_ragged_short_sequences_fill_sink_and_ring(qjl_m):
     assert rel_err(a, b) < 1e-4
 
 
+@pytest.mark.parametrize("qjl_m", [0, 128], ids=["k4v2", "k4v2_qjl"])
+def test_ragged_many_partials_per_sequence(qjl_m):
+    """One kv head and one ~100,000-token sequence beside a short one: the
+    ragged plan cuts the long sequence into more than 256 chunks, so the merge
+    reads more headers than its registers hold (its loop past them); batched
+    vs single-sequence calls and float64 attention over the stored codes."""
+    lens = [100000, 3000]
+    rb = make_batch(lens, H=1, qjl_m=qjl_m, sink=16, window=64, seed=21)
+    # the plan of the partials kernel (tq_decode_fast.hip: fast_plan_host,
+    # make_plan): chunks of T units (32-token blocks), T a multiple of 8
+    W = [(int(c) + 31) // 32 for c in rb.comp_len]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    nwg = min(cus, (sum(W) + 7) // 8)
+    T = max(1, -(-sum(W) // (8 * nwg)))
+    T = (T + 7) // 8 * 8
+    assert -(-W[0] // T) > 256, (W, nwg, T)
+    q = torch.randn(rb.B, HQ_PER_KV, D, generator=rb.g, device=DEV).half()
+    check_batch(rb, q, oracle_rows=range(rb.B), label=f"many partials m={qjl_m}")
+
+
 def test_ragged_errors():
     from turboquant_amd.ragged import RaggedKVBatch
     rb = RaggedKVBatch(2, 2, D, residual_window=8, device=DEV)

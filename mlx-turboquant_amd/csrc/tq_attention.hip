@@ -611,7 +611,8 @@ struct QjlArgs {
   const float* ml;      // (batch, hq, 2) global max and sum of the merge
   float* upart;         // (batch, hq, nvc, m) value terms, one per value-kernel workgroup
   int64_t qb_hs;
-  int nvc;
+  int nvc;              // value-kernel workgroups per (b, g), one partial each
+  int qvc;              // chunks of QCH tokens per value-kernel workgroup
 };
 
 // S (scale q) of the G query heads of (b, g), natural units: thread i takes
@@ -771,11 +772,17 @@ __device__ inline uint32_t lane_xor1(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true);
 }
 
+// Chunks of QCH tokens per workgroup of the value kernel (the sign words of
+// all of them are held in registers: fewer for the longer sketches).
+template <int NW4>
+constexpr int qjl_value_chunks() { return NW4 == 1 ? 4 : 2; }
+static int qjl_value_chunks_host(int m) { return m > 128 ? qjl_value_chunks<2>() : qjl_value_chunks<1>(); }
+
 // u_h = sum_t w_t z_t (w_t = 2^(s_t - M) gamma_t for head h, z_t the +-1
-// sign row of token t) by MFMA 16x16x32 f16, one 256-token chunk per
-// workgroup, thread t = token t of the chunk:
+// sign row of token t) by MFMA 16x16x32 f16 over QV chunks of 256 tokens per
+// workgroup, thread t = token t of each chunk:
 //   A = W: row h the fp16 high part of head h's weights times 2^(14 - E_h)
-//       (E_h the exponent of the chunk's max weight of head h: none is
+//       (E_h the exponent of the workgroup's max weight of head h: none is
 //       subnormal in fp16 but the tiny), row h + 8 the remainder; k = the 32
 //       tokens of a block;
 //   B = Z: k = the same tokens, column = one of 16 projections, built from a
@@ -783,12 +790,14 @@ __device__ inline uint32_t lane_xor1(uint32_t v) {
 //       lane's bit shifted to bit 15 / 31 and or-ed into 0x3C00 gives 1 for a
 //       clear bit and -1 for a set one, i.e. -z (the sums are negated back).
 // Output rows h and h + 8 (lanes q4 and q4 + 2) added give head h. Wave w
-// takes the projection tiles w, w + 4, ... The weights stay unnormalised
-// (O(gamma), whatever the context length); 2^(E_h - 14) / L_h is applied in
-// float32 to the sums.
+// takes the projection tiles w, w + 4, ... Every chunk's loads are issued up
+// front; one accumulator per tile runs over the chunks. The weights stay
+// unnormalised (O(gamma), whatever the context length); -2^(E_h - 14) / L_h is
+// applied in float32 to the sums.
 template <int G, int NW4>
 __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   static_assert(NT == QCH, "thread t = token t of the chunk");
+  constexpr int QV = qjl_value_chunks<NW4>();
   constexpr int MAXM = 128 * NW4;
   constexpr int YS = QCH / 2 + 32;  // row of ysm (+32 words: the rows the even and odd threads write sit 32 banks apart)
   // A operands, word (bk, q4, row, pair) at bk ASB + q4 ASQ + 4 row + pair:
@@ -803,49 +812,49 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   const int cg = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq, nw = m / 32;
   const int comp = seq_comp(a.d, b);
-  const int base = cg * QCH, nvalid = min(QCH, comp - base);
-  if (nvalid <= 0) return;  // past the sequence: qjl_final_kernel reads no partial of it
+  const int base0 = cg * QV * QCH, ntok = min(QV * QCH, comp - base0);
+  if (ntok <= 0) return;  // past the sequence: qjl_final_kernel reads no partial of it
   const tq_store& vs = a.d.vstore;
   const int lane = tid & 63, w = tid >> 6, r = lane & 15, q4 = lane >> 4;
-  const int t = tid, tc = min(t, nvalid - 1);
-  // ---- the token's sign row, gamma and scores; the heads' max and sum
-  uint32_t sw[4 * NW4];
-  load_sign_row<NW4>(vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base * (m / 8) + tc * (m / 8), nw,
-                     a.vsign16 != 0, sw);
-  const float gv = vs.gamma[(int64_t)row * vs.gamma_head_stride + base + tc];
-  float sc[G], Mh[G], Lh[G];
+  const int t = tid;
+  // ---- every chunk's sign row, gamma and scores of token t; the heads' max and sum
+  uint32_t sw[QV][4 * NW4];
+  float gv[QV], sc[QV][G], Mh[G], Lh[G];
   {
-    const float* sp = a.scores + (int64_t)row * G * a.qb_hs + base + tc;
     const float* mlp = a.ml + ((int64_t)b * hq + g * G) * 2;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      sc[h] = sp[h * a.qb_hs];
       Mh[h] = mlp[2 * h];
       Lh[h] = mlp[2 * h + 1];
     }
-  }
-  // ---- sign pairs: token 2p's word and token 2p + 1's word of projections
-  // 32k .. 32k + 31 give ysm[2k][p] (low halves, by the even thread) and
-  // ysm[2k + 1][p] (high halves, by the odd thread)
-  const bool odd = (t & 1) != 0;
+    const uint8_t* srow = vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base0 * (m / 8);
+    const float* grow = vs.gamma + (int64_t)row * vs.gamma_head_stride + base0;
+    const float* sp = a.scores + (int64_t)row * G * a.qb_hs + base0;
 #pragma unroll
-  for (int k = 0; k < 4 * NW4; ++k) {
-    if (k >= nw) break;
-    const uint32_t nb = lane_xor1(sw[k]);
-    ysm[2 * k + (odd ? 1 : 0)][t >> 1] =
-        odd ? __builtin_amdgcn_perm(sw[k], nb, 0x07060302u) : __builtin_amdgcn_perm(nb, sw[k], 0x05040100u);
+    for (int c = 0; c < QV; ++c) {
+      const int tc = min(c * QCH + t, ntok - 1);  // tokens past the sequence re-read its last one (weight 0)
+      load_sign_row<NW4>(srow + tc * (m / 8), nw, a.vsign16 != 0, sw[c]);
+      gv[c] = grow[tc];
+#pragma unroll
+      for (int h = 0; h < G; ++h) sc[c][h] = sp[h * a.qb_hs + tc];
+    }
   }
-  // ---- unnormalised weights and their per-wave max per head
-  float wt[G];
+  // ---- unnormalised weights and their per-wave max per head over the chunks
+  float wt[QV][G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const float p = t < nvalid && Lh[h] > 0.f ? __builtin_amdgcn_exp2f(sc[h] - Mh[h]) : 0.f;
-    wt[h] = p * gv;
-    const uint32_t mx = wave_max_nonneg(wt[h]);
-    if (lane == 0) wm[w][h] = mx;
+    float mx = 0.f;
+#pragma unroll
+    for (int c = 0; c < QV; ++c) {
+      const float p = c * QCH + t < ntok && Lh[h] > 0.f ? __builtin_amdgcn_exp2f(sc[c][h] - Mh[h]) : 0.f;
+      wt[c][h] = p * gv[c];
+      mx = fmaxf(mx, wt[c][h]);
+    }
+    const uint32_t wmx = wave_max_nonneg(mx);
+    if (lane == 0) wm[w][h] = wmx;
   }
   __syncthreads();
-  // E_h: the exponent of the chunk's max weight (weights are >= 0)
+  // E_h: the exponent of the workgroup's max weight (weights are >= 0)
   int eh[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
@@ -854,30 +863,72 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
     for (int ww = 1; ww < NT / 64; ++ww) mb = max(mb, wm[ww][h]);
     eh[h] = mb == 0u ? 0 : max((int)((mb >> 23) & 0xFFu), 1) - 127;
   }
-  // ---- A operands: thread t of block bk = t >> 5, q4 group (t >> 3) & 3,
-  // token pair (t >> 1) & 3; the even thread writes the high-part pair of row
-  // h, the odd one the remainder pair of row h + 8; rows of absent heads zero
-  {
-    const int bk = t >> 5, qq = (t >> 3) & 3, j = (t >> 1) & 3;
+  const bool odd = (t & 1) != 0;
+  const uint32_t shl = 15u - (uint32_t)r;
+  // the sign-bit mask and the halves 1.0 in registers, so that each operand
+  // word is one shift and one bit-field insert
+  uint32_t bmask = 0x80008000u, bone = 0x3C003C00u;
+  asm volatile("" : "+v"(bmask), "+s"(bone));
+  constexpr int QT = MAXM / 16 / (NT / 64);
+  qf4 acc[QT];
 #pragma unroll
-    for (int h = 0; h < 8; ++h) {
-      uint32_t val = 0u;
-      if (h < G) {
-        const float x = wt[h] * __builtin_amdgcn_ldexpf(1.f, 14 - eh[h]);
-        const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
-        const uint32_t own = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
-        const uint32_t nb = lane_xor1(own);
-        val = odd ? __builtin_amdgcn_perm(own, nb, 0x07060302u) : __builtin_amdgcn_perm(nb, own, 0x05040100u);
+  for (int k = 0; k < QT; ++k) acc[k] = qf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < QV; ++c) {
+    const int nvalid = ntok - c * QCH;  // uniform
+    if (nvalid <= 0) break;
+    if (c > 0) __syncthreads();  // the previous chunk's operand reads are done
+    // ---- sign pairs: token 2p's word and token 2p + 1's word of projections
+    // 32k .. 32k + 31 give ysm[2k][p] (low halves, by the even thread) and
+    // ysm[2k + 1][p] (high halves, by the odd thread)
+#pragma unroll
+    for (int k = 0; k < 4 * NW4; ++k) {
+      if (k >= nw) break;
+      const uint32_t nb = lane_xor1(sw[c][k]);
+      ysm[2 * k + (odd ? 1 : 0)][t >> 1] =
+          odd ? __builtin_amdgcn_perm(sw[c][k], nb, 0x07060302u) : __builtin_amdgcn_perm(nb, sw[c][k], 0x05040100u);
+    }
+    // ---- A operands: thread t of block bk = t >> 5, q4 group (t >> 3) & 3,
+    // token pair (t >> 1) & 3; the even thread writes the high-part pair of
+    // row h, the odd one the remainder pair of row h + 8; rows of absent heads zero
+    {
+      const int bk = t >> 5, qq = (t >> 3) & 3, j = (t >> 1) & 3;
+#pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        uint32_t val = 0u;
+        if (h < G) {
+          const float x = wt[c][h] * __builtin_amdgcn_ldexpf(1.f, 14 - eh[h]);
+          const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
+          const uint32_t own =
+              (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+          const uint32_t nb = lane_xor1(own);
+          val = odd ? __builtin_amdgcn_perm(own, nb, 0x07060302u) : __builtin_amdgcn_perm(nb, own, 0x05040100u);
+        }
+        aw[bk * ASB + qq * ASQ + 4 * (h + (odd ? 8 : 0)) + j] = val;
       }
-      aw[bk * ASB + qq * ASQ + 4 * (h + (odd ? 8 : 0)) + j] = val;
+    }
+    __syncthreads();
+    // ---- the MFMAs of the wave's projection tiles over the chunk's blocks
+    const int nblk = (min(nvalid, QCH) + 31) >> 5;
+    qu4 av[QCH / 32];
+#pragma unroll
+    for (int bk = 0; bk < QCH / 32; ++bk) av[bk] = *reinterpret_cast<const qu4*>(&aw[bk * ASB + q4 * ASQ + 4 * r]);
+#pragma unroll
+    for (int k = 0; k < QT; ++k) {
+      const int ct = w + (NT / 64) * k;
+      if (ct >= m / 16) break;
+#pragma unroll
+      for (int bk = 0; bk < QCH / 32; ++bk) {
+        if (bk >= nblk) break;
+        const qu4 y = *reinterpret_cast<const qu4*>(&ysm[ct][16 * bk + 4 * q4]);
+        qu4 bv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = ((y[e] << shl) & bmask) | (bone & ~bmask);
+        acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qh8, av[bk]), __builtin_bit_cast(qh8, bv),
+                                                        acc[k], 0, 0, 0);
+      }
     }
   }
-  __syncthreads();
-  // ---- the MFMAs of the wave's projection tiles over the chunk's blocks
-  const int nblk = (nvalid + 31) >> 5;
-  qu4 av[QCH / 32];
-#pragma unroll
-  for (int bk = 0; bk < QCH / 32; ++bk) av[bk] = *reinterpret_cast<const qu4*>(&aw[bk * ASB + q4 * ASQ + 4 * r]);
   // lane (column r, q4) ends with rows 4 q4 + i: head 4 q4 + i for q4 < 2;
   // its scale -2^(E_h - 14) / L_h (the B operands hold -z)
   float hsc[G];
@@ -888,31 +939,15 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   for (int i = 0; i < 4; ++i) osc[i] = q4 == 0 ? hsc[min(i, G - 1)] : hsc[min(4 + i, G - 1)];
   float* uo = a.upart + (((int64_t)b * hq + g * G + 4 * q4) * a.nvc + cg) * m + r;  // row 4 q4 of the lane
   const int64_t ust = (int64_t)a.nvc * m;                                            // next head
-  const uint32_t shl = 15u - (uint32_t)r;
-  // the sign-bit mask and the halves 1.0 in registers, so that each operand
-  // word is one shift and one bit-field insert
-  uint32_t bmask = 0x80008000u, bone = 0x3C003C00u;
-  asm volatile("" : "+v"(bmask), "+s"(bone));
-  constexpr int QT = MAXM / 16 / (NT / 64);
 #pragma unroll
   for (int k = 0; k < QT; ++k) {
     const int ct = w + (NT / 64) * k;
     if (ct >= m / 16) break;
-    qf4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int bk = 0; bk < QCH / 32; ++bk) {
-      if (bk >= nblk) break;
-      const qu4 y = *reinterpret_cast<const qu4*>(&ysm[ct][16 * bk + 4 * q4]);
-      qu4 bv;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bv[e] = ((y[e] << shl) & bmask) | (bone & ~bmask);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qh8, av[bk]), __builtin_bit_cast(qh8, bv), acc, 0,
-                                                   0, 0);
-    }
     // rows 4 q4 + i: add the remainder rows (lane ^ 32 holds rows + 8)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
+      const auto sw2 =
+          __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[k][i]), __float_as_uint(acc[k][i]), false, false);
       const float v = __uint_as_float(sw2[0]) + __uint_as_float(sw2[1]);
       const int hh = 4 * q4 + i;
       if (q4 < 2 && hh < G) uo[i * ust + 16 * ct] = v * osc[i];
@@ -930,7 +965,7 @@ __global__ __launch_bounds__(256) void qjl_final_kernel(QjlArgs a) {
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, m = a.m;
   const int lo = tid & 127, par = tid >> 7;
   const float* up = a.upart + ((int64_t)b * a.d.hq + h) * a.nvc * m;
-  const int nvb = min(a.nvc, (seq_comp(a.d, b) + QCH - 1) / QCH);  // chunks the value kernel wrote
+  const int nvb = min(a.nvc, ((seq_comp(a.d, b) + QCH - 1) / QCH + a.qvc - 1) / a.qvc);  // partials written
   for (int i = lo; i < m; i += 128) {
     float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     int c = par;
@@ -1074,7 +1109,8 @@ static QjlLayout qjl_layout(const tq_codec* kc, const tq_attn_desc* d) {
   const int m = kc->qjl_m;
   L.qb_hs = ((int64_t)d->max_comp + 31) / 32 * 32;
   if (L.qb_hs < 32) L.qb_hs = 32;
-  L.nvc = (d->max_comp + QCH - 1) / QCH;  // value-kernel workgroups per (b, g)
+  const int qv = qjl_value_chunks_host(kc->qjl_m);
+  L.nvc = ((d->max_comp + QCH - 1) / QCH + qv - 1) / qv;  // value-kernel workgroups per (b, g)
   if (L.nvc < 1) L.nvc = 1;
   size_t off = 0;
   L.part = off; off += al256(fast_part_bytes(d));
@@ -1184,6 +1220,7 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   qa.upart = reinterpret_cast<float*>(ws + QL.upart);
   qa.qb_hs = QL.qb_hs;
   qa.nvc = QL.nvc;
+  qa.qvc = qjl_value_chunks_host(kc->qjl_m);
   switch (G) {
     case 1: hipLaunchKernelGGL((qjl_sq_kernel<1>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;
     case 2: hipLaunchKernelGGL((qjl_sq_kernel<2>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;

@@ -615,32 +615,43 @@ struct QjlArgs {
   int qvc;              // chunks of QCH tokens per value-kernel workgroup
 };
 
-// S (scale q) of the G query heads of (b, g), natural units: thread i takes
-// projection i (and i + 128), S row i read in 16-byte pieces, the same
-// float32 order as prologue_kernel.
+// S (scale q) of the G query heads of (b, g), natural units: 64 projections
+// per workgroup, four threads per projection (thread t: projection 64 x + t /
+// 4, dims 32 (t & 3) .. + 31 in float32 order, the four quarters added in a
+// fixed order). The projection rows are requested before the queries arrive.
 template <int G>
-__global__ __launch_bounds__(128) void qjl_sq_kernel(QjlArgs a) {
+__global__ __launch_bounds__(256) void qjl_sq_kernel(QjlArgs a) {
   __shared__ float qsm[G][128];
-  const int g = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, m = a.m;
-  for (int e = tid; e < G * 128; e += 128)
+  const int g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, m = a.m;
+  const int i = 64 * blockIdx.x + (tid >> 2), kq = tid & 3;
+  float4 s4[8];
+  {
+    const float* si = a.proj + (int64_t)min(i, m - 1) * 128 + 32 * kq;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s4[k] = *reinterpret_cast<const float4*>(si + 4 * k);
+  }
+  for (int e = tid; e < G * 128; e += 256)
     qsm[e >> 7][e & 127] =
         a.d.scale * load_elem(a.d.q, ((int64_t)b * a.d.hq + g * G + (e >> 7)) * 128 + (e & 127), a.d.q_dtype);
   __syncthreads();
-  for (int i = tid; i < m; i += 128) {
-    const float* si = a.proj + (int64_t)i * 128;
-    float acc[G];
+  float acc[G];
 #pragma unroll
-    for (int h = 0; h < G; ++h) acc[h] = 0.f;
-    for (int k = 0; k < 128; k += 4) {
-      const float4 s4 = *reinterpret_cast<const float4*>(si + k);
+  for (int h = 0; h < G; ++h) {
+    const float* qh = &qsm[h][32 * kq];
+    float x = 0.f;
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        acc[h] = fmaf(qsm[h][k], s4.x, acc[h]);
-        acc[h] = fmaf(qsm[h][k + 1], s4.y, acc[h]);
-        acc[h] = fmaf(qsm[h][k + 2], s4.z, acc[h]);
-        acc[h] = fmaf(qsm[h][k + 3], s4.w, acc[h]);
-      }
+    for (int k = 0; k < 8; ++k) {
+      x = fmaf(qh[4 * k], s4[k].x, x);
+      x = fmaf(qh[4 * k + 1], s4[k].y, x);
+      x = fmaf(qh[4 * k + 2], s4[k].z, x);
+      x = fmaf(qh[4 * k + 3], s4[k].w, x);
     }
+    // (q0 + q1) + (q2 + q3) over the four threads of the projection
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));  // lane ^ 1
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));  // lane ^ 2
+    acc[h] = x;
+  }
+  if (kq == 0 && i < m) {
 #pragma unroll
     for (int h = 0; h < G; ++h) const_cast<float*>(a.sq)[((int64_t)b * a.d.hq + g * G + h) * m + i] = acc[h];
   }
@@ -1221,11 +1232,12 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   qa.qb_hs = QL.qb_hs;
   qa.nvc = QL.nvc;
   qa.qvc = qjl_value_chunks_host(kc->qjl_m);
+  const dim3 sgrid((unsigned)((kc->qjl_m + 63) / 64), d->hkv, d->batch);
   switch (G) {
-    case 1: hipLaunchKernelGGL((qjl_sq_kernel<1>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;
-    case 2: hipLaunchKernelGGL((qjl_sq_kernel<2>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;
-    case 4: hipLaunchKernelGGL((qjl_sq_kernel<4>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;
-    default: hipLaunchKernelGGL((qjl_sq_kernel<8>), dim3(d->hkv, d->batch), dim3(128), 0, s, qa); break;
+    case 1: hipLaunchKernelGGL((qjl_sq_kernel<1>), sgrid, dim3(256), 0, s, qa); break;
+    case 2: hipLaunchKernelGGL((qjl_sq_kernel<2>), sgrid, dim3(256), 0, s, qa); break;
+    case 4: hipLaunchKernelGGL((qjl_sq_kernel<4>), sgrid, dim3(256), 0, s, qa); break;
+    default: hipLaunchKernelGGL((qjl_sq_kernel<8>), sgrid, dim3(256), 0, s, qa); break;
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl S q");
   const dim3 bgrid((unsigned)((QL.qb_hs + QBC * QCH - 1) / (QBC * QCH)), d->hkv, d->batch);

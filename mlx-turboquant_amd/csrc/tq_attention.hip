@@ -1168,33 +1168,53 @@ static void fill_fast(FastArgs& f, const tq_codec* kc, const tq_codec* vc, const
 // uniform-batch kernels when the call is uniform and fits their grid, else
 // the persistent kernel. qb: the QJL key term is added (qjl_bias) and the
 // scores stored; ml receives the merge's global max and sum when not NULL.
+// fp16 high part | remainder << 16 of each host centroid (the first n)
+static void centroid_pairs(const tq_codec* c, int n, uint32_t* out) {
+  for (int i = 0; i < 16; ++i) {
+    const float x = i < n ? c->host_centroids[i] : 0.f;
+    const _Float16 xh = (_Float16)x;
+    out[i] = (uint32_t)__builtin_bit_cast(uint16_t, xh) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(x - (float)xh)) << 16);
+  }
+}
+
+// Arguments of the uniform-batch kernels for a uniform call (false when the
+// call is ragged or too long for their grid): key centroids as fp16 pairs;
+// 2-bit values through the codec's exact fp16 table and scale, 3- / 4-bit
+// values as fp16 pairs of the centroids (scale 1).
+static bool fill_uniform(UniformArgs& u, const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part) {
+  u = UniformArgs{};
+  if (!uniform_route(vc, d, u.nwg, u.bpw, u.fpw)) return false;
+  u.kc = d->kstore.codes_hi; u.k_hs = d->kstore.hi_head_stride;
+  u.kn = d->kstore.norms; u.kn_hs = d->kstore.norm_head_stride;
+  u.vc = d->vstore.codes_hi; u.v_hs = d->vstore.hi_head_stride;
+  u.vn = d->vstore.norms; u.vn_hs = d->vstore.norm_head_stride;
+  u.sink_k = d->sink_k; u.sink_v = d->sink_v; u.sink_hs = d->sink_head_stride;
+  u.res_k = d->res_k; u.res_v = d->res_v; u.res_hs = d->res_head_stride;
+  u.res_cap = d->res_cap; u.res_start0 = d->res_start0;
+  u.res_start_b = d->res_start;  // the lengths are the maximal ones
+  u.max_comp = d->max_comp; u.max_sink = d->max_sink; u.max_res = d->max_res;
+  u.q = d->q; u.q_dtype = d->q_dtype; u.out = d->out;
+  u.batch = d->batch; u.hq = d->hq; u.hkv = d->hkv;
+  u.qscale = d->scale * 1.4426950408889634f;
+  u.rot16 = kc->rotation_parts; u.vrot = vc->rotation;
+  centroid_pairs(kc, 1 << kc->bits_hi, u.khl);
+  if (vc->bits_hi == 2) {
+    for (int i = 0; i < 4; ++i) u.vtab[i] = vc->value_table[i];
+    u.vscale = vc->value_scale;
+  } else {
+    centroid_pairs(vc, 1 << vc->bits_hi, u.vhl);
+    u.vscale = 1.f;
+  }
+  u.part = part;
+  return true;
+}
+
 static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part, bool qb,
                        float* qjl_bias, float* scores, int64_t qb_hs, float* ml, int merge, hipStream_t s) {
   const int G = d->hq / d->hkv;
-  UniformArgs u{};
-  if (uniform_route(vc, d, u.nwg, u.bpw, u.fpw)) {
-    u.kc = d->kstore.codes_hi; u.k_hs = d->kstore.hi_head_stride;
-    u.kn = d->kstore.norms; u.kn_hs = d->kstore.norm_head_stride;
-    u.vc = d->vstore.codes_hi; u.v_hs = d->vstore.hi_head_stride;
-    u.vn = d->vstore.norms; u.vn_hs = d->vstore.norm_head_stride;
-    u.sink_k = d->sink_k; u.sink_v = d->sink_v; u.sink_hs = d->sink_head_stride;
-    u.res_k = d->res_k; u.res_v = d->res_v; u.res_hs = d->res_head_stride;
-    u.res_cap = d->res_cap; u.res_start0 = d->res_start0;
-    u.res_start_b = d->res_start;  // the lengths are the maximal ones
-    u.max_comp = d->max_comp; u.max_sink = d->max_sink; u.max_res = d->max_res;
-    u.q = d->q; u.q_dtype = d->q_dtype; u.out = d->out;
-    u.batch = d->batch; u.hq = d->hq; u.hkv = d->hkv;
-    u.qscale = d->scale * 1.4426950408889634f;
-    u.rot16 = kc->rotation_parts; u.vrot = vc->rotation;
-    for (int i = 0; i < 16; ++i) {
-      const float x = kc->host_centroids[i];
-      const _Float16 xh = (_Float16)x;
-      u.khl[i] = (uint32_t)__builtin_bit_cast(uint16_t, xh) |
-                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(x - (float)xh)) << 16);
-    }
-    for (int i = 0; i < 4; ++i) u.vtab[i] = vc->value_table[i];
-    u.vscale = vc->value_scale;
-    u.part = part;
+  UniformArgs u;
+  if (fill_uniform(u, kc, vc, d, part)) {
     u.qjl_bias = qjl_bias; u.scores = scores; u.qb_hs = qb_hs; u.ml = ml;
     return launch_uniform_decode(u, G, qb, merge, s);
   }
@@ -1202,6 +1222,36 @@ static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_des
   fill_fast(f, kc, vc, d, part);
   f.qjl_bias = qjl_bias; f.scores = scores; f.qb_hs = qb_hs; f.ml = ml;
   return launch_fast_decode(f, G, qb, merge, s);
+}
+
+// The uniform-batch MFMA kernels for the other integer widths (key and value
+// bits 2..4 with one codebook each, K4/V2 excepted): d = 128, fp16 K/V, one
+// query token, no sketch, G in {1, 2, 4, 8}; 2-bit values need the exact
+// fp16 table; the rows every load touches aligned as the loads need (key
+// codes 16-byte, value codes 4-byte, 2-byte for 2-bit values). The call must
+// be uniform (fill_uniform); ragged batches take the general kernel.
+static bool widths_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
+  const int G = d->hq / d->hkv, kb = kc->bits_hi, vb = vc->bits_hi;
+  if (d->n_q > 1 || d->qjl) return false;
+  if (!(kc->d == 128 && vc->d == 128 && kc->split == 128 && vc->split == 128 && kb >= 2 && kb <= 4 && vb >= 2 &&
+        vb <= 4 && !(kb == 4 && vb == 2)))
+    return false;
+  if (!(kc->rotation_parts && vc->rotation && kc->n_host_centroids == (1 << kb) &&
+        vc->n_host_centroids == (1 << vb)))
+    return false;
+  if (vb == 2 && !(vc->value_table_err <= 2e-7f)) return false;
+  if (d->kv_dtype != TQ_F16 || !(G == 1 || G == 2 || G == 4 || G == 8)) return false;
+  if (!aligned16(d->q)) return false;
+  const uintptr_t va = vb == 2 ? 1 : 3;
+  if (d->max_comp > 0 &&
+      !(aligned16(d->kstore.codes_hi) && d->kstore.hi_head_stride % 16 == 0 && aligned16(d->kstore.norms) &&
+        d->kstore.norm_head_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(d->vstore.codes_hi) & va) == 0 &&
+        d->vstore.hi_head_stride % (int64_t)(va + 1) == 0 && aligned16(d->vstore.norms) &&
+        d->vstore.norm_head_stride % 4 == 0))
+    return false;
+  if (d->max_sink > 0 && !(aligned16(d->sink_k) && aligned16(d->sink_v) && d->sink_head_stride % 8 == 0)) return false;
+  if (d->max_res > 0 && !(aligned16(d->res_k) && aligned16(d->res_v) && d->res_head_stride % 8 == 0)) return false;
+  return true;
 }
 
 // The QJL route: S q, key-term bias, K4/V2 partials with the bias
@@ -1445,6 +1495,14 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
       TQ_LAUNCH_CHECK("tq_decode_attention (fast)");
     return TQ_OK;
   }
+  if (widths_eligible(kc, vc, d) && !(d->flags & TQ_ATTN_GENERAL)) {
+    UniformArgs u;
+    if (fill_uniform(u, kc, vc, d, static_cast<float*>(workspace))) {
+      if (launch_uniform_widths(u, d->hq / d->hkv, kc->bits_hi, vc->bits_hi, 1, s) != 0)
+        TQ_LAUNCH_CHECK("tq_decode_attention (widths)");
+      return TQ_OK;
+    }
+  }
 
   AttnArgs a;
   a.d = *d;
@@ -1506,13 +1564,36 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
 // not written), so its launches can be timed with events on their stream.
 int tq_measure_decode_partials(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace,
                                size_t workspace_bytes, void* stream) {
-  if (!kc || !vc || !d || d->hkv <= 0 || d->hq % d->hkv || !fast_eligible(kc, vc, d) || d->qjl)
-    return set_error(TQ_ERR_UNSUPPORTED, "measurement: not a K4/V2 call");
+  if (!kc || !vc || !d || d->hkv <= 0 || d->hq % d->hkv || d->qjl)
+    return set_error(TQ_ERR_UNSUPPORTED, "measurement: not a packed uniform or K4/V2 call");
   if (!workspace || workspace_bytes < fast_part_bytes(d)) return set_error(TQ_ERR_WORKSPACE, "workspace too small");
-  if (launch_k4v2(kc, vc, d, static_cast<float*>(workspace), false, nullptr, nullptr, 0, nullptr, 0,
-                  static_cast<hipStream_t>(stream)) != 0)
-    TQ_LAUNCH_CHECK("measurement partials");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fast_eligible(kc, vc, d)) {
+    if (launch_k4v2(kc, vc, d, static_cast<float*>(workspace), false, nullptr, nullptr, 0, nullptr, 0, s) != 0)
+      TQ_LAUNCH_CHECK("measurement partials");
+    return TQ_OK;
+  }
+  UniformArgs u;
+  if (!widths_eligible(kc, vc, d) || !fill_uniform(u, kc, vc, d, static_cast<float*>(workspace)))
+    return set_error(TQ_ERR_UNSUPPORTED, "measurement: not a packed uniform or K4/V2 call");
+  if (launch_uniform_widths(u, d->hq / d->hkv, kc->bits_hi, vc->bits_hi, 0, s) != 0)
+    TQ_LAUNCH_CHECK("measurement partials (widths)");
   return TQ_OK;
+}
+
+// Test hook, not part of the ABI: the route tq_decode_attention takes for a
+// valid call, without launching anything: 0 the general kernel, 1 the dense
+// kernel, 2 the K4/V2 kernels, 3 the K4/V2 kernels with the QJL terms, 4 the
+// uniform-batch kernels of the other integer widths.
+int tq_debug_decode_route(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
+  if (!kc || !vc || !d || d->hkv <= 0 || d->hq % d->hkv) return -1;
+  if (d->flags & TQ_ATTN_GENERAL) return 0;
+  if (d->max_comp == 0 && (d->max_sink > 0 || d->max_res > 0) && dense_check(d, kc->d, false) == TQ_OK) return 1;
+  if (d->qjl && d->max_comp > 0 && fast_eligible(kc, vc, d, true)) return 3;
+  if (fast_eligible(kc, vc, d)) return 2;
+  int nwg, bpw, fpw;
+  if (widths_eligible(kc, vc, d) && uniform_route(vc, d, nwg, bpw, fpw)) return 4;
+  return 0;
 }
 
 size_t tq_decode_noalloc_scratch_bytes(void) { return TQ_NOALLOC_SCRATCH_BYTES; }

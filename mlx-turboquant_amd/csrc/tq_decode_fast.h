@@ -113,10 +113,14 @@ struct UniformArgs {
   float* scores;         // final base-2 scores of the compressed tokens (written with QB)
   int64_t qb_hs;
   float* ml;             // merge output: (batch, hq, 2) global max and sum, or NULL
+  uint32_t vhl[16];      // value centroid i (3- / 4-bit values): fp16 bits of c_hi | c_lo << 16
 };
 // Launches the uniform-batch partials kernel (qb: with the QJL key bias,
 // scores stored) and, when merge != 0, its merge kernel. G in {1, 2, 4, 8}.
 int launch_uniform_decode(const UniformArgs& a, int G, bool qb, int merge, hipStream_t s);
+// The same kernels for the other integer widths (key bits kb, value bits vb
+// in 2..4, (kb, vb) != (4, 2)), without the QJL term (tq_decode_widths.hip).
+int launch_uniform_widths(const UniformArgs& a, int G, int kb, int vb, int merge, hipStream_t s);
 
 // Arguments of the dense (fp16 / bf16 K/V) decode-attention kernel: the
 // fp16 segments of tq_attn_desc, head_dim 128.

@@ -299,6 +299,65 @@ def test_fast_kernel_matches_general_and_oracle(G, T, sink, window, chunk):
     assert e_g < REL_TOL
 
 
+def decode_route(c, q):
+    """The route the library takes for c.attend(q): tq_debug_decode_route, a
+    test hook of the library (0 general kernel, 2 K4/V2 kernels, 4 the
+    uniform-batch kernels of the other integer widths)."""
+    import ctypes
+    from turboquant_amd import _lib
+    fn = _lib.load().tq_debug_decode_route
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_void_p] * 3
+    qq = q[:, :, 0].contiguous()
+    out = torch.empty(qq.shape, dtype=torch.float32, device=qq.device)
+    desc = c.attention_descriptor(qq, out, q.shape[-1] ** -0.5)
+    return fn(ctypes.addressof(c._kc.struct), ctypes.addressof(c._vc.struct), ctypes.addressof(desc))
+
+
+WIDTHS = [(2, 2), (2, 3), (2, 4), (3, 2), (3, 3), (3, 4), (4, 3), (4, 4)]
+
+
+@pytest.mark.parametrize("G,T,sink,window", [
+    (4, 3000, 128, 128),    # one block per wave, a workgroup's fp16 tokens
+    (1, 700, 16, 64),       # partial last block
+    (8, 40000, 0, 128),     # 8 blocks per wave (the NPW = 8 kernels)
+])
+@pytest.mark.parametrize("kb,vb", WIDTHS, ids=[f"K{k}V{v}" for k, v in WIDTHS])
+def test_uniform_widths_match_oracle(kb, vb, G, T, sink, window):
+    """The uniform-batch MFMA kernels for the integer widths other than K4/V2
+    (key tables of 2-dim fp16 high part / remainder pairs keyed by 2 KB-bit
+    fields; the exact 2-bit value table, or 3- / 4-bit value pairs with a
+    second PV MFMA for the remainders): the route is taken, and the output
+    agrees with float64 attention over the stored codes at the K4/V2 kernels'
+    bound and with the general kernel."""
+    k, v = _kv(1, 2, T, 128, seed=T + 10 * kb + vb)
+    c, o = build(dict(head_dim=128, num_kv_heads=2, key_bits=kb, value_bits=vb, residual_window=window,
+                      fp16_sink_size=sink), k, v)
+    q = np.random.RandomState(kb * 8 + vb).randn(1, 2 * G, 1, 128).astype(np.float16)
+    qd = to_dev(q)
+    assert decode_route(c, qd) == 4
+    fast = c.attend(qd).cpu().numpy()
+    gen = c.attend(qd, general_kernel=True).cpu().numpy()
+    kk, vv = dense_from_gpu_codes(c, o)
+    ref = O.attention(q, kk, vv)
+    e_f = rel_err(fast, ref)
+    print(f"K{kb}/V{vb} G={G} T={T}: rel {e_f:.3e} vs general {rel_err(fast, gen):.3e}")
+    assert e_f < FAST_REL_TOL and min_cos(fast, ref) >= COS_TOL
+    assert rel_err(fast, gen) < 1e-4
+
+
+def test_uniform_widths_route_limits():
+    """K4/V2 keeps its own kernels; ragged batches, QJL sketches and
+    fractional widths of the other widths take the general kernel."""
+    k, v = _kv(1, 2, 900, 128, seed=5)
+    q = to_dev(np.random.RandomState(6).randn(1, 8, 1, 128).astype(np.float16))
+    for kw, route in ((dict(key_bits=4, value_bits=2), 2), (dict(key_bits=3, value_bits=3), 4),
+                      (dict(key_bits=3, value_bits=3, qjl_correction=True, qjl_n_proj=64), 0),
+                      (dict(key_bits=3.5, value_bits=2), 0)):
+        c, _ = build(dict(head_dim=128, num_kv_heads=2, residual_window=64, fp16_sink_size=16, **kw), k, v)
+        assert decode_route(c, q) == route, kw
+
+
 def test_fast_kernel_large_value_norms():
     """Values of norm ~6e5 (fp16 entries near 5e4): p * n_v passes the fp16
     range, so the kernels scale the P^T operand of such columns by a power of

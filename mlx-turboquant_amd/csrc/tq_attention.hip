@@ -1043,9 +1043,9 @@ static FastPlan fast_plan(const tq_attn_desc* d) {
 // UNI_FP16_PER_WG fp16 tokens per workgroup. False when the call is not
 // uniform (per-sequence lengths given) or needs more than UNI_MAX_WG
 // workgroups: the persistent kernel takes it.
-static bool uniform_geometry(const tq_attn_desc* d, int& nwg, int& bpw, int& fpw) {
+static bool uniform_geometry(const tq_attn_desc* d, int& nwg, int& bpw, int& fpw, bool ragged_ok = false) {
   nwg = bpw = fpw = 0;
-  if (d->comp_len || d->sink_len || d->res_len) return false;
+  if (!ragged_ok && (d->comp_len || d->sink_len || d->res_len)) return false;
   const int nbc = (d->max_comp + 31) / 32;
   const int n16 = d->max_sink + d->max_res;
   const int groups = d->batch * d->hkv > 0 ? d->batch * d->hkv : 1;
@@ -1065,8 +1065,9 @@ static bool uniform_geometry(const tq_attn_desc* d, int& nwg, int& bpw, int& fpw
 
 // The uniform-batch kernels take a uniform call (their merge applies the
 // value codec's float32 rotation).
-static bool uniform_route(const tq_codec* vc, const tq_attn_desc* d, int& nwg, int& bpw, int& fpw) {
-  return vc->rotation != nullptr && uniform_geometry(d, nwg, bpw, fpw);
+static bool uniform_route(const tq_codec* vc, const tq_attn_desc* d, int& nwg, int& bpw, int& fpw,
+                          bool ragged_ok = false) {
+  return vc->rotation != nullptr && uniform_geometry(d, nwg, bpw, fpw, ragged_ok);
 }
 
 // Partials workspace of the K4/V2 routes of a call: the larger of the uniform
@@ -1077,7 +1078,8 @@ static size_t fast_part_bytes(const tq_attn_desc* d) {
   int nwg, bpw, fpw;
   // the partial slots, then the ragged plan's per-sequence table
   size_t b = al256((size_t)fast_plan(d).vmax * G * PACKED_PART_FLOATS * 4) + (size_t)d->batch * 8;
-  if (uniform_geometry(d, nwg, bpw, fpw)) {
+  // (a grid over the maximal lengths: the other widths' kernels take ragged calls too)
+  if (uniform_geometry(d, nwg, bpw, fpw, true)) {
     const size_t u = (size_t)d->batch * d->hkv * nwg * G * PACKED_PART_FLOATS * 4;
     if (u > b) b = u;
   }
@@ -1178,13 +1180,17 @@ static void centroid_pairs(const tq_codec* c, int n, uint32_t* out) {
   }
 }
 
-// Arguments of the uniform-batch kernels for a uniform call (false when the
-// call is ragged or too long for their grid): key centroids as fp16 pairs;
+// Arguments of the uniform-batch kernels (false when the call is ragged and
+// ragged_ok is not set, or too long for their grid; a ragged call gets the
+// grid of its maximal lengths and the per-sequence arrays, which only the
+// other widths' kernels read): key centroids as fp16 pairs;
 // 2-bit values through the codec's exact fp16 table and scale, 3- / 4-bit
 // values as fp16 pairs of the centroids (scale 1).
-static bool fill_uniform(UniformArgs& u, const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part) {
+static bool fill_uniform(UniformArgs& u, const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part,
+                         bool ragged_ok = false) {
   u = UniformArgs{};
-  if (!uniform_route(vc, d, u.nwg, u.bpw, u.fpw)) return false;
+  if (!uniform_route(vc, d, u.nwg, u.bpw, u.fpw, ragged_ok)) return false;
+  u.comp_len_b = d->comp_len; u.sink_len_b = d->sink_len; u.res_len_b = d->res_len;
   u.kc = d->kstore.codes_hi; u.k_hs = d->kstore.hi_head_stride;
   u.kn = d->kstore.norms; u.kn_hs = d->kstore.norm_head_stride;
   u.vc = d->vstore.codes_hi; u.v_hs = d->vstore.hi_head_stride;
@@ -1228,8 +1234,9 @@ static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_des
 // bits 2..4 with one codebook each, K4/V2 excepted): d = 128, fp16 K/V, one
 // query token, no sketch, G in {1, 2, 4, 8}; 2-bit values need the exact
 // fp16 table; the rows every load touches aligned as the loads need (key
-// codes 16-byte, value codes 4-byte, 2-byte for 2-bit values). The call must
-// be uniform (fill_uniform); ragged batches take the general kernel.
+// codes 16-byte, value codes 4-byte, 2-byte for 2-bit values). Uniform and
+// ragged calls (a grid over the maximal lengths; workgroups past a shorter
+// sequence write empty partials).
 static bool widths_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
   const int G = d->hq / d->hkv, kb = kc->bits_hi, vb = vc->bits_hi;
   if (d->n_q > 1 || d->qjl) return false;
@@ -1497,7 +1504,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   }
   if (widths_eligible(kc, vc, d) && !(d->flags & TQ_ATTN_GENERAL)) {
     UniformArgs u;
-    if (fill_uniform(u, kc, vc, d, static_cast<float*>(workspace))) {
+    if (fill_uniform(u, kc, vc, d, static_cast<float*>(workspace), true)) {
       if (launch_uniform_widths(u, d->hq / d->hkv, kc->bits_hi, vc->bits_hi, 1, s) != 0)
         TQ_LAUNCH_CHECK("tq_decode_attention (widths)");
       return TQ_OK;
@@ -1574,7 +1581,7 @@ int tq_measure_decode_partials(const tq_codec* kc, const tq_codec* vc, const tq_
     return TQ_OK;
   }
   UniformArgs u;
-  if (!widths_eligible(kc, vc, d) || !fill_uniform(u, kc, vc, d, static_cast<float*>(workspace)))
+  if (!widths_eligible(kc, vc, d) || !fill_uniform(u, kc, vc, d, static_cast<float*>(workspace), true))
     return set_error(TQ_ERR_UNSUPPORTED, "measurement: not a packed uniform or K4/V2 call");
   if (launch_uniform_widths(u, d->hq / d->hkv, kc->bits_hi, vc->bits_hi, 0, s) != 0)
     TQ_LAUNCH_CHECK("measurement partials (widths)");
@@ -1592,7 +1599,7 @@ int tq_debug_decode_route(const tq_codec* kc, const tq_codec* vc, const tq_attn_
   if (d->qjl && d->max_comp > 0 && fast_eligible(kc, vc, d, true)) return 3;
   if (fast_eligible(kc, vc, d)) return 2;
   int nwg, bpw, fpw;
-  if (widths_eligible(kc, vc, d) && uniform_route(vc, d, nwg, bpw, fpw)) return 4;
+  if (widths_eligible(kc, vc, d) && uniform_route(vc, d, nwg, bpw, fpw, true)) return 4;
   return 0;
 }
 

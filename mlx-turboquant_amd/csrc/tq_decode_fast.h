@@ -114,6 +114,11 @@ struct UniformArgs {
   int64_t qb_hs;
   float* ml;             // merge output: (batch, hq, 2) global max and sum, or NULL
   uint32_t vhl[16];      // value centroid i (3- / 4-bit values): fp16 bits of c_hi | c_lo << 16
+  // per-sequence lengths (NULL: the maximal ones); read by the kernels of the
+  // other widths only (the K4/V2 instantiation serves uniform calls)
+  const int32_t* comp_len_b;
+  const int32_t* sink_len_b;
+  const int32_t* res_len_b;
 };
 // Launches the uniform-batch partials kernel (qb: with the QJL key bias,
 // scores stored) and, when merge != 0, its merge kernel. G in {1, 2, 4, 8}.

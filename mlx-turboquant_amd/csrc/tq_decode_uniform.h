@@ -317,8 +317,20 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
     for (int i = 0; i < (VB == 2 ? 4 : 16); ++i) asm volatile("" : "+s"(vt[i]));
     asm volatile("" ::"s"(cbw[0]), "s"(cbw[1]), "s"(vtw[0]), "s"(vtw[1]), "s"(vtw[2]), "s"(rs_raw));
   }
-  // a uniform call: every sequence at the maximal lengths
-  const int comp = a.max_comp, sink = a.max_sink, res = a.max_res;
+  // K4/V2: a uniform call, every sequence at the maximal lengths; the other
+  // widths also serve ragged calls: the sequence's lengths (one scalar load
+  // each, from its array entry or the maximum), clamped to the maxima
+  auto seq_len = [&](const int32_t* arr, size_t max_off, int mx) {
+    if constexpr (K4V2) {
+      return mx;
+    } else {
+      const kptr p = arr ? (kptr)(arr + b) : (kptr)(kargs + max_off);
+      return min(max((int)*p, 0), mx);
+    }
+  };
+  const int comp = seq_len(a.comp_len_b, offsetof(UniformArgs, max_comp), a.max_comp);
+  const int sink = seq_len(a.sink_len_b, offsetof(UniformArgs, max_sink), a.max_sink);
+  const int res = seq_len(a.res_len_b, offsetof(UniformArgs, max_res), a.max_res);
   const int rstart = min(max(rs_raw, 0), max(a.res_cap - 1, 0));
   const int nbc = (comp + 31) >> 5;
   const int blk0 = c * a.bpw, blk1 = min(blk0 + a.bpw, nbc);

@@ -182,6 +182,38 @@ def test_ragged_many_partials_per_sequence(qjl_m):
     check_batch(rb, q, oracle_rows=range(rb.B), label=f"many partials m={qjl_m}")
 
 
+def batch_route(rb, q):
+    """tq_debug_decode_route (a test hook of the library) for rb.attend(q):
+    0 the general kernel, 2 the K4/V2 kernels, 4 the other widths' kernels."""
+    from turboquant_amd import _lib
+    fn = _lib.load().tq_debug_decode_route
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_void_p] * 3
+    out = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+    d, _ = rb.descriptor(q.contiguous(), out, D ** -0.5)
+    return fn(rb.kc.ref(), rb.vc.ref(), ctypes.addressof(d))
+
+
+@pytest.mark.parametrize("kb,vb", [(3, 2), (4, 4), (2, 3)], ids=["K3V2", "K4V4", "K2V3"])
+def test_ragged_other_widths(kb, vb):
+    """Ragged batches at integer widths other than K4/V2 run the uniform-batch
+    MFMA kernels of those widths over the maximal lengths' grid, each
+    workgroup reading its sequence's lengths (workgroups past a shorter
+    sequence write empty partials): batched vs single-sequence calls, float64
+    over the stored codes, the general kernel; then with wrapped rings."""
+    lens = [300, 5000, 164, 2000, 700]
+    rb = make_batch(lens, H=2, kb=kb, vb=vb, sink=16, window=32, seed=7 + kb + vb)
+    q = torch.randn(rb.B, 2 * HQ_PER_KV, D, generator=rb.g, device=DEV).half()
+    assert batch_route(rb, q) == 4
+    check_batch(rb, q, oracle_rows=range(rb.B), label=f"K{kb}/V{vb} ragged")
+    a = rb.attend(q).cpu().numpy()
+    b = rb.attend(q, general=True).cpu().numpy()
+    assert rel_err(a, b) < 1e-4
+    for _ in range(40):
+        step(rb)
+    check_batch(rb, q, oracle_rows=range(rb.B), label=f"K{kb}/V{vb} ragged +40")
+
+
 def test_ragged_errors():
     from turboquant_amd.ragged import RaggedKVBatch
     rb = RaggedKVBatch(2, 2, D, residual_window=8, device=DEV)

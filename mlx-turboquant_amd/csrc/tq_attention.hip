@@ -1098,8 +1098,12 @@ static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_
         kc->n_host_centroids == 16 && vc->n_host_centroids == 4 && vc->d == 128 && kc->d == 128 &&
         kc->bits_hi == 4 && kc->split == 128 &&
         vc->bits_hi == 2 && vc->split == 128 && vc->value_table_err <= 2e-7f && (!d->qjl || qjl_ok) &&
-        d->kv_dtype == TQ_F16 && (G == 1 || G == 2 || G == 4 || G == 8)))
+        (d->kv_dtype == TQ_F16 || d->kv_dtype == TQ_BF16) && (G == 1 || G == 2 || G == 4 || G == 8)))
     return false;
+  // bf16 sink / ring tokens: the uniform-batch kernels only (the persistent
+  // kernel of ragged batches reads fp16)
+  int nwg, bpw, fpw;
+  if (d->kv_dtype == TQ_BF16 && !uniform_route(vc, d, nwg, bpw, fpw)) return false;
   if (d->qjl && d->max_comp > 0 &&
       !((reinterpret_cast<uintptr_t>(d->kstore.signs) & 3) == 0 && d->kstore.sign_head_stride % 4 == 0 &&
         (reinterpret_cast<uintptr_t>(d->vstore.signs) & 3) == 0 && d->vstore.sign_head_stride % 4 == 0))
@@ -1222,7 +1226,7 @@ static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_des
   UniformArgs u;
   if (fill_uniform(u, kc, vc, d, part)) {
     u.qjl_bias = qjl_bias; u.scores = scores; u.qb_hs = qb_hs; u.ml = ml;
-    return launch_uniform_decode(u, G, qb, merge, s);
+    return launch_uniform_decode(u, G, qb, merge, s, d->kv_dtype == TQ_BF16);
   }
   FastArgs f;
   fill_fast(f, kc, vc, d, part);

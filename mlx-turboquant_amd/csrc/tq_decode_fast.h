@@ -121,8 +121,9 @@ struct UniformArgs {
   const int32_t* res_len_b;
 };
 // Launches the uniform-batch partials kernel (qb: with the QJL key bias,
-// scores stored) and, when merge != 0, its merge kernel. G in {1, 2, 4, 8}.
-int launch_uniform_decode(const UniformArgs& a, int G, bool qb, int merge, hipStream_t s);
+// scores stored) and, when merge != 0, its merge kernel. G in {1, 2, 4, 8};
+// bf16_kv: the sink / ring tokens are bf16 (else fp16).
+int launch_uniform_decode(const UniformArgs& a, int G, bool qb, int merge, hipStream_t s, bool bf16_kv = false);
 // The same kernels for the other integer widths (key bits kb, value bits vb
 // in 2..4, (kb, vb) != (4, 2)), without the QJL term (tq_decode_widths.hip).
 int launch_uniform_widths(const UniformArgs& a, int G, int kb, int vb, int merge, hipStream_t s);
@@ -147,6 +148,19 @@ struct DenseArgs {
 };
 
 constexpr int DENSE_WAVES = 4;  // waves per workgroup of the dense kernel
+
+// Power of two 2^qe of one query head for the fp16 query operands of the
+// K4/V2 and uniform-batch kernels (s = qscale, the scores' scale): a head
+// with s ||q|| above `hi` is scaled down to at most `hi`; a head with
+// s ||q|| below `lo` (the fp16 remainders of its rotated coordinates s (R q)_j
+// would go subnormal) is scaled up with both 2^-qe ||q|| and 2^-qe s ||q||
+// at most `hi`; otherwise 0. The scores of the head are multiplied by 2^qe.
+__device__ inline int query_exponent(float qnorm, float qscale, float hi, float lo) {
+  const float qn = qnorm * qscale;
+  if (qn > hi) return (int)ceilf(log2f(qn / hi));
+  if (qn < lo && qnorm > 0.f) return max(min((int)ceilf(log2f(qnorm * fmaxf(qscale, 1.f) / hi)), 0), -100);
+  return 0;
+}
 
 void dense_geometry(int batch, int hkv, int max_sink, int max_res, int cus, int& nwg, int& bpw);
 // bf: bf16 K/V (else fp16); merge 0 skips the merge launch (measurement)

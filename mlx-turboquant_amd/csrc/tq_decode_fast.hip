@@ -72,9 +72,17 @@ constexpr float RESCALE_MARGIN = 3.f;
 // p * n_v above this is scaled down by a power of two (fp16 operand range);
 // the column's exponent is applied at the combine.
 constexpr float PV_LIMIT = 32768.f;
+// the first non-empty compressed block of a column sets its exponent so that
+// its largest p * n_v lands in (PV_SET / 2, PV_SET], up or down: small value
+// norms keep fp16 remainders normal, and later blocks (p up to 8x the first
+// block's, the rescale margin) stay below PV_LIMIT unless their norms grow
+constexpr float PV_SET = 2048.f;
 // |scale * (R q)_j| <= scale * ||q|| must stay below this for the fp16 query
 // operands; larger queries are scaled by a power of two per head.
 constexpr float Q_LIMIT = 16384.f;
+// scale * ||q|| below this: the head is scaled up by a power of two (keeps
+// the fp16 remainders of the rotated query normal)
+constexpr float Q_LOW = 0.25f;
 
 // LDS layout. Lookup tables: key entry of code byte e (two 4-bit codes) and
 // value entry of byte e (four 2-bit codes), NCP replicas of 8 bytes each in
@@ -580,9 +588,10 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
   // B0..B3 of the block, column r); returns the P^T operand (p * nv, high
   // part or remainder by column, zero in the k-slots of the other tile) and
   // rescales `acc` when a block's max exceeds the running max, or when p *
-  // nv would leave the fp16 range (the column exponent vx then grows).
+  // nv would leave the fp16 range (the column exponent vx then grows); with
+  // `setx` (compressed blocks) the first non-empty block sets vx (`vset`).
   auto softmax_pv = [&](float (&s)[NS], const float (&nv)[NS], f4 (&acc)[8], float& m_run, float& l_run,
-                        int& vx) {
+                        int& vx, bool& vset, bool setx) {
     float bm = s[0];
 #pragma unroll
     for (int i = 1; i < NS; ++i) bm = fmaxf(bm, s[i]);
@@ -604,9 +613,17 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
       pv[i] = p * nv[i];
       pm = fmaxf(pm, pv[i]);
     }
-    if (__builtin_amdgcn_ballot_w64(pm * __builtin_amdgcn_ldexpf(1.f, -vx) > PV_LIMIT) != 0) {
-      const float cm = rows_max(pm * __builtin_amdgcn_ldexpf(1.f, -vx));
-      const int d = cm > PV_LIMIT ? (int)ceilf(log2f(cm / PV_LIMIT)) : 0;
+    const float pmx = pm * __builtin_amdgcn_ldexpf(1.f, -vx);
+    const bool first = setx && !vset;  // wave-uniform
+    if (__builtin_amdgcn_ballot_w64(pmx > PV_LIMIT || (first && pmx > 0.f)) != 0) {
+      const float cm = rows_max(pmx);
+      int d;
+      if (first) {
+        d = cm > 0.f ? max((int)ceilf(log2f(cm / PV_SET)), -110) : 0;
+        vset = true;
+      } else {
+        d = cm > PV_LIMIT ? (int)ceilf(log2f(cm / PV_LIMIT)) : 0;
+      }
       const float f = __builtin_amdgcn_ldexpf(1.f, -d);
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) acc[nb] *= f;
@@ -717,8 +734,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
       // rotated coordinate: the power of two that keeps the operands in fp16
       // range
       ss = rows_sum(ss);
-      const float qn = sqrtf(ss) * a.qscale;
-      const int qe = qn > Q_LIMIT ? (int)ceilf(log2f(qn / Q_LIMIT)) : 0;  // lanes r: head r
+      const int qe = query_exponent(sqrtf(ss), a.qscale, Q_LIMIT, Q_LOW);  // lanes r: head r
       const float qdown = __builtin_amdgcn_ldexpf(1.f, -qe);
       half8 qo_hi[4], qo_lo[4];
 #pragma unroll
@@ -792,6 +808,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
       for (int nb = 0; nb < 8; ++nb) acc_o[nb] = f4{0.f, 0.f, 0.f, 0.f};
       float m_o = M_INIT, l_o = 0.f;
       int vx_o = 0;
+      bool vset_o = true;  // p * 1 <= 1: the fp16 tiles keep vx_o = 0
       const float sf = a.qscale * qe_scale;
       for (int t = S.t0; t < S.t1; ++t) {
         if (t != S.t0) load_tile(t);
@@ -809,7 +826,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < NS; ++i) ones[i] = 1.f;
-        const half8 pb = softmax_pv(sc, ones, acc_o, m_o, l_o, vx_o);
+        const half8 pb = softmax_pv(sc, ones, acc_o, m_o, l_o, vx_o, vset_o, false);
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) {
           const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
@@ -840,6 +857,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
     for (int nb = 0; nb < 8; ++nb) acc[nb] = f4{0.f, 0.f, 0.f, 0.f};
     float m_run = M_INIT, l_run = 0.f;
     int vx = 0;
+    bool vset = false;
 
     // The norms go to the wave's staging row first, for every slot (also the
     // skipped ones): the wait for a slot's loads then sits before the branch
@@ -918,7 +936,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
                 make_float4(sc[4 * t], sc[4 * t + 1], sc[4 * t + 2], sc[4 * t + 3]);
         }
       }
-      const half8 pb = softmax_pv(sc, nv, acc, m_run, l_run, vx);
+      const half8 pb = softmax_pv(sc, nv, acc, m_run, l_run, vx, vset, true);
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) acc[nb] = mfma(as_h8(va[nb]), pb, acc[nb]);
     };

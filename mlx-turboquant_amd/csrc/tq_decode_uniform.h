@@ -98,9 +98,17 @@ constexpr float RESCALE_MARGIN = 3.f;
 // p * n_v above this is scaled down by a power of two (fp16 operand range);
 // the column's exponent is applied at the combine.
 constexpr float PV_LIMIT = 32768.f;
+// the first non-empty compressed block of a column sets its exponent so that
+// its largest p * n_v lands in (PV_SET / 2, PV_SET], up or down: small value
+// norms keep fp16 remainders normal, and later blocks (p up to 8x the first
+// block's, the rescale margin) stay below PV_LIMIT unless their norms grow
+constexpr float PV_SET = 2048.f;
 // |scale * (R q)_j| <= scale * ||q|| must stay below this for the fp16 query
 // operands; larger queries are scaled by a power of two per head.
 constexpr float Q_LIMIT = 16384.f;
+// scale * ||q|| below this: the head is scaled up by a power of two (keeps
+// the fp16 remainders of the rotated query normal)
+constexpr float Q_LOW = 0.25f;
 
 struct Layout {
   // Lookup tables: value entry e (four 2-bit codes) and key entry e (two
@@ -203,6 +211,30 @@ struct Blk {
   float nk, nv;   // key / value norm of token t0 + (lane & 31)
 };
 
+// max over the 64 lanes of a wave (unsigned), every lane gets it
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x122, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x121, 0xF, 0xF, true));
+  const auto x = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(x[0], x[1]);
+  const auto y = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(y[0], y[1]);
+}
+
+// 8 bf16 values (bits) -> 8 fp16 values of x * s (s a power of two that keeps
+// them in the fp16 range: exact for every scaled value in fp16's normal range)
+__device__ inline u4 bf16_to_f16(u4 x, float s) {
+  u4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float lo = __uint_as_float(x[j] << 16) * s, hi = __uint_as_float(x[j] & 0xFFFF0000u) * s;
+    o[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+  }
+  return o;
+}
+
 // The 4-row stores of a pair table by wave w (B-bit codes: entry e of 2B bits
 // -> (c_hi[e & M], c_hi[e >> B], c_lo[e & M], c_lo[e >> B]) fp16, M = 2^B - 1,
 // c[i] = fp16 bits of c_hi[i] | c_lo[i] << 16, rows of 32 replicas): store sx
@@ -236,7 +268,7 @@ __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
 
 // NPW: compressed blocks per wave (4, or 8 for long contexts and large
 // batches, where fewer workgroups pay the set-up and combine)
-template <int G, bool QB, int NPW, int KB = 4, int VB = 2>
+template <int G, bool QB, int NPW, int KB = 4, int VB = 2, bool BF = false>
 __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   static_assert(KB >= 2 && KB <= 4 && VB >= 2 && VB <= 4, "integer widths 2-4");
   static_assert(!QB || (KB == 4 && VB == 2), "the QJL key term runs with K4/V2");
@@ -497,6 +529,24 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
       }
     }
   }
+  if constexpr (BF) {
+    // bf16 sink / ring tokens: the largest |x| of the staged keys and of the
+    // staged values (bf16 bits, sign cleared), per wave into the combine
+    // header region (free until the combine), for the fp16 scale of the tile
+    uint32_t mx = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t x = fst[j] & 0x7FFF7FFFu;
+      mx = max(mx, max(x & 0xFFFFu, x >> 16));
+    }
+    const bool isv = (tid >> 4) & 1;
+    const uint32_t mk = wave_max_u32(isv ? 0u : mx), mv = wave_max_u32(isv ? mx : 0u);
+    if (lane == 0) {
+      uint32_t* bm = reinterpret_cast<uint32_t*>(smem + Layout::cml);
+      bm[2 * w] = mk;
+      bm[2 * w + 1] = mv;
+    }
+  }
   if (tid < qchunks) *reinterpret_cast<u4*>(smem + Layout::qst + 16 * tid) = qld;
   // staged fp16 tokens: [slot][keys | values][272-byte row]
   *reinterpret_cast<u4*>(smem + Layout::f16s + (tid >> 5) * (2 * FROW) + ((tid >> 4) & 1) * FROW + 16 * (tid & 15)) = fst;
@@ -509,6 +559,7 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   // q rows as MFMA A operands (row r = query head min(r, G-1), k-slots = dims
   // 32*kb + 8*q4 ..): fp16 high part and remainder of q 2^-qe, the power of
   // two 2^qe of the head keeping scale * |R q| <= scale * ||q|| below Q_LIMIT
+  // and, for small queries, the rotated remainders normal
   half8 qo_hi[4], qo_lo[4];
   float qe_scale = 1.f;  // 2^qe of this lane's column head: multiplies its scores
   bool q_exact = false;  // the remainders qo_lo are zero
@@ -529,7 +580,10 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
         }
       }
       ss = rows_sum(ss);
-      q_exact = __builtin_amdgcn_ballot_w64(sqrtf(ss) * a.qscale > Q_LIMIT) == 0;
+      // scale * ||q|| in [Q_LOW, Q_LIMIT] (query_exponent 0) for every head:
+      // one unsigned range test of the float bits
+      q_exact = __builtin_amdgcn_ballot_w64(__float_as_uint(sqrtf(ss) * a.qscale) - __float_as_uint(Q_LOW) >
+                                            __float_as_uint(Q_LIMIT) - __float_as_uint(Q_LOW)) == 0;
       if (q_exact) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
@@ -564,8 +618,7 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) ss = fmaf(x[kb][i], x[kb][i], ss);
       ss = rows_sum(ss);  // the 4 lanes of row r hold the 128 dims of its head
-      const float qn = sqrtf(ss) * a.qscale;
-      const int qe = qn > Q_LIMIT ? (int)ceilf(log2f(qn / Q_LIMIT)) : 0;  // lanes r: head min(r, G - 1)
+      const int qe = query_exponent(sqrtf(ss), a.qscale, Q_LIMIT, Q_LOW);  // lanes r: head min(r, G - 1)
       const float qdown = __builtin_amdgcn_ldexpf(1.f, -qe);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -630,6 +683,7 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   // ---- per-lane online softmax state of column r (head hd)
   float m_run = M_INIT, l_run = 0.f;
   int vx = 0;             // exponent of the column: acc_r holds the sums times 2^-vx
+  bool vset = false;      // vx set by the wave's first non-empty compressed block (wave-uniform)
   float m_orig = M_INIT;  // running max the parked original-space partial refers to
   f4 acc_r[8];            // rotated-space output accumulators
 
@@ -647,8 +701,9 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
   // B0..B3 of the block, column r), returns the P^T operand (p * nv 2^-vx,
   // high part or remainder by column, zero in the k-slots of the other tile)
   // and rescales `acc` when a block's max exceeds the running max, or when
-  // p * nv would leave the fp16 range (the column exponent vx then grows).
-  auto softmax_pv = [&](float (&s)[NS], const float (&nv)[NS], f4 (&acc)[8]) {
+  // p * nv would leave the fp16 range (the column exponent vx then grows);
+  // with `setx` (compressed blocks) the first non-empty block sets vx.
+  auto softmax_pv = [&](float (&s)[NS], const float (&nv)[NS], f4 (&acc)[8], bool setx) {
     float bm = s[0];
 #pragma unroll
     for (int i = 1; i < NS; ++i) bm = fmaxf(bm, s[i]);
@@ -670,9 +725,17 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
       pv[i] = p * nv[i];
       pm = fmaxf(pm, fabsf(pv[i]));
     }
-    if (__builtin_amdgcn_ballot_w64(pm * __builtin_amdgcn_ldexpf(1.f, -vx) > PV_LIMIT) != 0) {
-      const float cm = rows_max(pm * __builtin_amdgcn_ldexpf(1.f, -vx));  // max of the column
-      const int dx = cm > PV_LIMIT ? (int)ceilf(log2f(cm / PV_LIMIT)) : 0;
+    const float pmx = pm * __builtin_amdgcn_ldexpf(1.f, -vx);
+    const bool first = setx && !vset;  // wave-uniform
+    if (__builtin_amdgcn_ballot_w64(pmx > PV_LIMIT || (first && pmx > 0.f)) != 0) {
+      const float cm = rows_max(pmx);  // max of the column
+      int dx;
+      if (first) {
+        dx = cm > 0.f ? max((int)ceilf(log2f(cm / PV_SET)), -110) : 0;
+        vset = true;
+      } else {
+        dx = cm > PV_LIMIT ? (int)ceilf(log2f(cm / PV_LIMIT)) : 0;
+      }
       const float f = __builtin_amdgcn_ldexpf(1.f, -dx);
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) acc[nb] *= f;
@@ -714,28 +777,52 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc_o[nb] = f4{0.f, 0.f, 0.f, 0.f};
     const uint8_t* fs = smem + Layout::f16s;
+    // bf16 tokens: keys and values scaled by powers of two 2^-ek, 2^-ev that
+    // bring the tile's largest |x| into [2^14, 2^15): exact in fp16 down to
+    // 2^-38 of it (fp16 subnormals below); the scores and the parked sums are
+    // scaled back
+    float ks = 1.f, vs = 1.f, kback = 1.f, vback = 1.f;
+    if constexpr (BF) {
+      const uint32_t* bm = reinterpret_cast<const uint32_t*>(smem + Layout::cml);
+      uint32_t mk = 0, mv = 0;
+#pragma unroll
+      for (int ww = 0; ww < FW; ++ww) {
+        mk = max(mk, bm[2 * ww]);
+        mv = max(mv, bm[2 * ww + 1]);
+      }
+      // bf16 exponent field (bits 14..7) of the tile maxima; zero tiles keep 1
+      const int ek = mk == 0u ? 0 : max(-100, (int)(mk >> 7) - 127 - 14);
+      const int ev = mv == 0u ? 0 : max(-100, (int)(mv >> 7) - 127 - 14);
+      ks = __builtin_amdgcn_ldexpf(1.f, -ek);
+      vs = __builtin_amdgcn_ldexpf(1.f, -ev);
+      kback = __builtin_amdgcn_ldexpf(1.f, ek);
+      vback = __builtin_amdgcn_ldexpf(1.f, ev);
+    }
     // one 16-token score tile (tokens r); the k-slots of tokens 16.. of the
     // P^T operand stay empty
     f4 sA = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const u4 kA = *reinterpret_cast<const u4*>(fs + r * (2 * FROW) + 64 * q4 + 16 * kb);
+      u4 kA = *reinterpret_cast<const u4*>(fs + r * (2 * FROW) + 64 * q4 + 16 * kb);
+      if constexpr (BF) kA = bf16_to_f16(kA, ks);
       sA = mfma(as_h8(kA), qf[kb], sA);
     }
     float sc[NS], ones[NS];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float full = (sA[i] + partner<G>(sA[i])) * (a.qscale * qe_scale);
+      const float full = (sA[i] + partner<G>(sA[i])) * (a.qscale * qe_scale * kback);
       sc[i] = tile == 0 && 4 * q4 + i < nf ? full : -INFINITY;  // the tile-1 columns see no fp16 token
       if constexpr (NS == 8) sc[4 + i] = -INFINITY;
     }
 #pragma unroll
     for (int i = 0; i < NS; ++i) ones[i] = 1.f;
-    const half8 pb = softmax_pv(sc, ones, acc_o);
+    const half8 pb = softmax_pv(sc, ones, acc_o, false);
     u4 vv[8];  // values: dims 8r .. 8r+7 of tokens A0..A3 (k-slots of B0..B3 zero)
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 8; ++i) {
       vv[i] = i < 4 ? *reinterpret_cast<const u4*>(fs + (4 * q4 + i) * (2 * FROW) + FROW + 16 * r) : u4{0u, 0u, 0u, 0u};
+      if constexpr (BF) vv[i] = bf16_to_f16(vv[i], vs);
+    }
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
       const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
@@ -750,7 +837,7 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
     for (int i = 0; i < 4; ++i) {
       float vo[8];
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) vo[nb] = acc_o[nb][i] + partner<G>(acc_o[nb][i]);
+      for (int nb = 0; nb < 8; ++nb) vo[nb] = (acc_o[nb][i] + partner<G>(acc_o[nb][i])) * vback;
       if (writer && tile == 0) {
         float* d = reinterpret_cast<float*>(smem + Layout::opk) + hd * FD + 32 * q4 + 8 * i;
         *reinterpret_cast<float4*>(d) = make_float4(vo[0], vo[1], vo[2], vo[3]);
@@ -872,7 +959,7 @@ __global__ __launch_bounds__(FT) void uniform_decode_kernel(UniformArgs a) {
           *reinterpret_cast<float4*>(so + 16 * (t + tile)) = make_float4(sc[4 * t], sc[4 * t + 1], sc[4 * t + 2], sc[4 * t + 3]);
       }
     }
-    const half8 pb = softmax_pv(sc, nv, acc_r);
+    const half8 pb = softmax_pv(sc, nv, acc_r, true);
     u4 vl[8];  // the remainders (value pair tables)
     if constexpr (VB != 2) {
       // built after the scores: fewer registers live across the score MFMAs

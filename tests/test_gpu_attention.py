@@ -359,6 +359,62 @@ def test_uniform_widths_route_limits():
         assert decode_route(c, q) == route, kw
 
 
+@pytest.mark.parametrize("G,T,sink,window,kmul,vmul", [
+    (4, 3000, 128, 128, 1.0, 1.0),
+    (8, 700, 16, 64, 1.0, 1.0),
+    (2, 5000, 64, 128, 300.0, 3e4),  # bf16 sink / ring entries past the fp16 range
+    (1, 3000, 32, 64, 1e-3, 1e-7),  # entries below fp16's normal range
+])
+def test_fast_kernel_bf16_kv(G, T, sink, window, kmul, vmul):
+    """bf16 K/V: the sink and residual tokens stay bf16 and run on the K4/V2
+    uniform-batch kernels, scaled into the fp16 range by a power of two per
+    staged tile (keys and values apart) and back; against float64 over the
+    stored codes and the bf16 tokens at the fp16 route's bound."""
+    from turboquant_amd import TurboQuantKVCache
+    k, v = _kv(1, 2, T, 128, seed=T + G)
+    kt = (torch.from_numpy(k.astype(np.float32)) * kmul).to(torch.bfloat16)
+    vt = (torch.from_numpy(v.astype(np.float32)) * vmul).to(torch.bfloat16)
+    kw = dict(head_dim=128, num_kv_heads=2, key_bits=4, value_bits=2, residual_window=window, fp16_sink_size=sink)
+    c = TurboQuantKVCache(**kw)
+    c.update(kt.cuda(), vt.cuda())
+    o = O.CacheOracle(**kw)
+    o.update(kt.float().numpy(), vt.float().numpy())
+    q = np.random.RandomState(G).randn(1, 2 * G, 1, 128).astype(np.float16) / np.float16(kmul)
+    qd = to_dev(q)
+    assert decode_route(c, qd) == 2
+    fast = c.attend(qd).cpu().numpy()
+    kk, vv = dense_from_gpu_codes(c, o)
+    ref = O.attention(q, kk, vv)
+    assert np.isfinite(fast).all()
+    assert rel_err(fast, ref) < FAST_REL_TOL and min_cos(fast, ref) >= COS_TOL, rel_err(fast, ref)
+    gen = c.attend(qd, general_kernel=True).cpu().numpy()
+    assert rel_err(fast, gen) < 1e-4
+
+
+@pytest.mark.parametrize("qdt,qmul", [("f16", 1 / 300), ("f16", 1e-5), ("f32", 1e-9), ("bf16", 3e-3)],
+                         ids=["f16_div300", "f16_1e-5", "f32_1e-9", "bf16_3e-3"])
+def test_fast_kernel_small_queries(qdt, qmul):
+    """Queries far below unit norm: the fp16 remainders of their rotated
+    coordinates would go subnormal, so the K4/V2 kernels scale such heads up by
+    a power of two (the scores back down). Against float64 at the fast bound
+    and the general kernel at 1e-5."""
+    k, v = _kv(1, 2, 3000, 128, seed=71)
+    c, o = build(dict(head_dim=128, num_kv_heads=2, key_bits=4, value_bits=2, residual_window=64,
+                      fp16_sink_size=32), k, v)
+    dt = {"f16": torch.float16, "f32": torch.float32, "bf16": torch.bfloat16}[qdt]
+    qt = (torch.from_numpy(np.random.RandomState(72).randn(1, 8, 1, 128)) * qmul).to(dt)
+    qd = qt.cuda()
+    assert decode_route(c, qd) == 2
+    fast = c.attend(qd).cpu().numpy()
+    kk, vv = dense_from_gpu_codes(c, o)
+    ref = O.attention(qt.double().numpy(), kk, vv)
+    gen = c.attend(qd, general_kernel=True).cpu().numpy()
+    print(f"{qdt} x{qmul:g}: fast {rel_err(fast, ref):.2e} general {rel_err(gen, ref):.2e}")
+    assert np.isfinite(fast).all()
+    assert rel_err(fast, ref) < FAST_REL_TOL and min_cos(fast, ref) >= COS_TOL, rel_err(fast, ref)
+    assert rel_err(fast, gen) < 1e-5
+
+
 def test_fast_kernel_large_value_norms():
     """Values of norm ~6e5 (fp16 entries near 5e4): p * n_v passes the fp16
     range, so the kernels scale the P^T operand of such columns by a power of

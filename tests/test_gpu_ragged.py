@@ -32,15 +32,16 @@ COS_TOL = 0.9999
 DEV = torch.device("cuda", 0)
 
 
-def make_batch(lens, H=8, kb=4, vb=2, qjl_m=0, sink=128, window=128, seed=0):
-    """RaggedKVBatch with sequence b loaded from lens[b] seeded N(0,1) tokens."""
+def make_batch(lens, H=8, kb=4, vb=2, qjl_m=0, sink=128, window=128, seed=0, vmul=1.0):
+    """RaggedKVBatch with sequence b loaded from lens[b] seeded N(0,1) tokens
+    (values times vmul)."""
     from turboquant_amd.ragged import RaggedKVBatch
     rb = RaggedKVBatch(len(lens), H, D, kb, vb, residual_window=window, fp16_sink_size=sink, qjl_n_proj=qjl_m,
                        device=DEV)
     g = torch.Generator(device=DEV).manual_seed(seed)
     for b, T in enumerate(lens):
         k = torch.randn(H, int(T), D, generator=g, device=DEV).half()
-        v = torch.randn(H, int(T), D, generator=g, device=DEV).half()
+        v = (torch.randn(H, int(T), D, generator=g, device=DEV) * vmul).half()
         rb.load(b, k, v)
     rb.g = g
     return rb
@@ -180,6 +181,22 @@ def test_ragged_many_partials_per_sequence(qjl_m):
     assert -(-W[0] // T) > 256, (W, nwg, T)
     q = torch.randn(rb.B, HQ_PER_KV, D, generator=rb.g, device=DEV).half()
     check_batch(rb, q, oracle_rows=range(rb.B), label=f"many partials m={qjl_m}")
+
+
+def test_ragged_small_queries_and_values():
+    """Queries of norm ~0.01 and values of scale 1e-3 on a ragged batch (the
+    K4/V2 partials kernel): each query head is scaled up by a power of two
+    into the range where the fp16 remainders of the rotated query stay normal,
+    and the first compressed block of a column sets the power of two of its
+    p * n_v operands; against the general kernel (float32 operands) at 1e-5."""
+    rb = make_batch([5000, 1200, 2600], H=2, sink=32, window=64, seed=31, vmul=1e-3)
+    assert batch_route(rb, torch.zeros(rb.B, 2 * HQ_PER_KV, D, device=DEV).half()) == 2
+    q = (torch.randn(rb.B, 2 * HQ_PER_KV, D, generator=rb.g, device=DEV) * 1e-3).half()
+    fast = check_batch(rb, q, label="small queries").cpu().numpy()
+    gen = rb.attend(q, general=True).cpu().numpy()
+    e = rel_err(fast, gen)
+    print(f"small queries: partials kernel vs general {e:.3e}")
+    assert e < 1e-5
 
 
 def batch_route(rb, q):

@@ -30,10 +30,11 @@ from .rotation import DEFAULT_SEED
 _workspaces: dict[tuple[str, int], torch.Tensor] = {}
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def _workspace(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
     """Per (device, stream) attention workspace: scratch for the partials of
-    one call, reused by every later call ordered on the same stream."""
-    key = (str(device), _lib.stream_ptr(device))
+    one call, reused by every later call ordered on the same stream (the
+    current stream unless its handle is given)."""
+    key = (str(device), _lib.stream_ptr(device) if stream is None else stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)

@@ -37,34 +37,55 @@ class _IntStage:
 
     def __init__(self, n: int, dev: torch.device):
         self.host = [torch.empty(n, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self.host_np = [h.numpy() for h in self.host]
         self.dev = [torch.empty(n, dtype=torch.int32, device=dev) for _ in range(2)]
-        self.done = [None, None]
+        self.events = [torch.cuda.Event(), torch.cuda.Event()]
+        self.used = [False, False]
         self.k = 0
 
-    def put(self, *arrays) -> list[torch.Tensor]:
+    def _stage(self, arrays) -> torch.Tensor:
         k = self.k
         self.k ^= 1
-        if self.done[k] is not None:
-            self.done[k].synchronize()
-        h = self.host[k].numpy()
+        if self.used[k]:
+            self.events[k].synchronize()
+        h = self.host_np[k]
         n = 0
         for x in arrays:
             h[n:n + len(x)] = x
             n += len(x)
         d = self.dev[k]
-        d[:n].copy_(self.host[k][:n], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        self.done[k] = ev
+        if n == len(h):
+            d.copy_(self.host[k], non_blocking=True)
+        else:
+            d[:n].copy_(self.host[k][:n], non_blocking=True)
+        self.events[k].record()
+        self.used[k] = True
+        return d
+
+    def put(self, *arrays) -> list[torch.Tensor]:
+        """Device views of the staged arrays (valid until the call after next)."""
+        d = self._stage(arrays)
         views, n = [], 0
         for x in arrays:
             views.append(d[n:n + len(x)])
             n += len(x)
         return views
 
+    def put_ptrs(self, *arrays) -> tuple[torch.Tensor, list[int]]:
+        """The staging tensor and the device address of each staged array."""
+        d = self._stage(arrays)
+        base, ptrs, n = d.data_ptr(), [], 0
+        for x in arrays:
+            ptrs.append(base + 4 * n)
+            n += len(x)
+        return d, ptrs
+
 
 class RaggedKVBatch:
-    """``batch`` sequences of one layer, ``num_kv_heads`` kv heads each."""
+    """``batch`` sequences of one layer, ``num_kv_heads`` kv heads each. The
+    per-sequence length arrays (sink_len, comp_len, res_len, res_start,
+    offset) belong to the batch: load() and step() update them (and the
+    device copy the next attention call reads); other code reads them only."""
 
     def __init__(self, batch: int, num_kv_heads: int, head_dim: int = 128, key_bits: float = 4,
                  value_bits: float = 2, residual_window: int = 128, fp16_sink_size: int = 0,
@@ -88,9 +109,16 @@ class RaggedKVBatch:
         self.ring_v = torch.zeros_like(self.ring_k)
         z = lambda: np.zeros(batch, dtype=np.int64)
         self.sink_len, self.comp_len, self.res_len, self.res_start, self.offset = z(), z(), z(), z(), z()
-        self._step_ints = _IntStage(4 * batch, dev)   # ring slots / drain arrays of a step
+        self._step_ints = _IntStage(8 * batch, dev)   # ring slots / drain arrays / post-step lengths of a step
         self._attn_ints = _IntStage(4 * batch, dev)   # per-sequence lengths of an attention call
         self._rows = torch.arange(batch, device=dev)
+        self._desc = None        # the attention descriptor, refreshed per call
+        self._structs = None     # (store capacities, tq_store of kstore, of vstore)
+        # the lengths change only in load() and step(): a step stages the
+        # post-step lengths with its own arrays, and the next attention call
+        # uses them while the version still matches
+        self._lens_ver = 0
+        self._lens_staged = None  # (version, device addresses, staging tensor)
 
     # ------------------------------------------------------------------ fill
     def load(self, b: int, keys: torch.Tensor, values: torch.Tensor) -> None:
@@ -118,6 +146,7 @@ class RaggedKVBatch:
         self.ring_v[b, :, :r] = v[:, s + c:]
         self.sink_len[b], self.comp_len[b], self.res_len[b], self.res_start[b] = s, c, r, 0
         self.offset[b] = T
+        self._lens_ver += 1
 
     @staticmethod
     def _row_view(store: _codec.PackedStore, b: int) -> _codec.PackedStore:
@@ -151,8 +180,14 @@ class RaggedKVBatch:
             self.sink_k[bt, :, pt] = keys[bt]
             self.sink_v[bt, :, pt] = values[bt]
             self.sink_len[bi] += 1
-        # one staged copy: ring slots, then the drain arrays (count, ring start, store position)
-        slot_t, n_b, src_b, dst_b = self._step_ints.put(ring_slot, drain, self.res_start, self.comp_len)
+        # one staged copy: ring slots, the drain arrays (count, ring start, store
+        # position), then the lengths after this step for the next attention call
+        comp_after = self.comp_len + drain
+        start_after = np.where(drain, (self.res_start + 1) % self.cap, self.res_start)
+        staged, ptrs = self._step_ints.put_ptrs(ring_slot, drain, self.res_start, self.comp_len,
+                                                comp_after, self.sink_len, res_after - drain, start_after)
+        slot_t = staged[:B]
+        n_b, src_b, dst_b = ptrs[1:4]
         if (~to_sink).all():
             self.ring_k[self._rows, :, slot_t] = keys
             self.ring_v[self._rows, :, slot_t] = values
@@ -167,35 +202,54 @@ class RaggedKVBatch:
             need = int((self.comp_len + drain).max())
             self.kstore.reserve(need, int(self.comp_len.max()))
             self.vstore.reserve(need, int(self.comp_len.max()))
-            span = _lib.Span(rows=B * H, heads=H, n_tok=1, reserved=0, n_tok_b=n_b.data_ptr(),
-                             src_tok0_b=src_b.data_ptr(), dst_tok0_b=dst_b.data_ptr())
+            span = _lib.Span(rows=B * H, heads=H, n_tok=1, reserved=0, n_tok_b=n_b, src_tok0_b=src_b, dst_tok0_b=dst_b)
             lib = _lib.load()
-            for codec, ring, store in ((self.kc, self.ring_k, self.kstore), (self.vc, self.ring_v, self.vstore)):
-                st = store.struct(0)
+            for codec, ring, st in zip((self.kc, self.vc), (self.ring_k, self.ring_v), self._store_structs()):
                 _lib.check(lib.tq_compress(codec.ref(), ring.data_ptr(), _lib.dtype_code(ring.dtype), self.cap * D,
                                            ctypes.byref(span), ctypes.byref(st), _lib.stream_ptr(dev)), "tq_compress")
-            self.comp_len += drain
-            self.res_start = np.where(drain, (self.res_start + 1) % self.cap, self.res_start)
+            self.comp_len = comp_after
+            self.res_start = start_after
             self.res_len -= drain
         self.offset += 1
+        self._lens_ver += 1
+        self._lens_staged = (self._lens_ver, ptrs[4:8], staged)
 
     # ------------------------------------------------------------- attention
+    def _store_structs(self) -> tuple[_lib.Store, _lib.Store]:
+        """``tq_store`` of the key and value stores, rebuilt only when a
+        reserve has reallocated them (their capacities then grow)."""
+        caps = (self.kstore.cap, self.vstore.cap)
+        if self._structs is None or self._structs[0] != caps:
+            self._structs = (caps, self.kstore.struct(0), self.vstore.struct(0))
+        return self._structs[1], self._structs[2]
+
     def descriptor(self, q: torch.Tensor, out: torch.Tensor, scale: float, general: bool = False):
         """``tq_attn_desc`` of a (B, Hq, D) query against every sequence; the
-        per-sequence arrays are device views valid until the call after next."""
-        comp, sink, res, start = self._attn_ints.put(self.comp_len, self.sink_len, self.res_len, self.res_start)
-        arrays = [comp, sink, res, start]
-        d = _lib.AttnDesc(
-            batch=self.B, hq=q.shape[1], hkv=self.H, qjl=1 if self.qjl else 0, scale=scale,
-            max_comp=int(self.comp_len.max()), max_sink=int(self.sink_len.max()), max_res=int(self.res_len.max()),
-            q_dtype=_lib.dtype_code(q.dtype), kv_dtype=_lib.dtype_code(self.sink_k.dtype),
-            q=q.data_ptr(), out=out.data_ptr(), kstore=self.kstore.struct(0), vstore=self.vstore.struct(0),
-            comp_len=comp.data_ptr(), sink_k=self.sink_k.data_ptr(), sink_v=self.sink_v.data_ptr(),
-            sink_head_stride=self.sink_k.shape[2] * self.D, sink_len=sink.data_ptr(),
-            res_k=self.ring_k.data_ptr(), res_v=self.ring_v.data_ptr(), res_head_stride=self.cap * self.D,
-            res_cap=self.cap, res_start0=0, res_start=start.data_ptr(), res_len=res.data_ptr(),
-            flags=_lib.TQ_ATTN_GENERAL if general else 0)
-        return d, arrays
+        per-sequence arrays are device arrays valid until the call after next.
+        One descriptor object is kept and refreshed per call (the fields that
+        never change are set once): the host path of a decode step stays
+        short, since the GPU waits for it in a step-by-step loop."""
+        ls = self._lens_staged
+        if ls is not None and ls[0] == self._lens_ver:
+            (comp, sink, res, start), staged = ls[1], ls[2]
+        else:
+            staged, (comp, sink, res, start) = self._attn_ints.put_ptrs(
+                self.comp_len, self.sink_len, self.res_len, self.res_start)
+        d = self._desc
+        if d is None:
+            d = self._desc = _lib.AttnDesc(
+                batch=self.B, hkv=self.H, qjl=1 if self.qjl else 0, kv_dtype=_lib.dtype_code(self.sink_k.dtype),
+                sink_k=self.sink_k.data_ptr(), sink_v=self.sink_v.data_ptr(),
+                sink_head_stride=self.sink_k.shape[2] * self.D,
+                res_k=self.ring_k.data_ptr(), res_v=self.ring_v.data_ptr(), res_head_stride=self.cap * self.D,
+                res_cap=self.cap, res_start0=0, n_q=0)
+        d.kstore, d.vstore = self._store_structs()
+        d.hq, d.scale, d.q_dtype = q.shape[1], scale, _lib.dtype_code(q.dtype)
+        d.max_comp, d.max_sink, d.max_res = int(self.comp_len.max()), int(self.sink_len.max()), int(self.res_len.max())
+        d.q, d.out = q.data_ptr(), out.data_ptr()
+        d.comp_len, d.sink_len, d.res_len, d.res_start = comp, sink, res, start
+        d.flags = _lib.TQ_ATTN_GENERAL if general else 0
+        return d, [staged]
 
     def attend(self, q: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
                general: bool = False) -> torch.Tensor:
@@ -211,8 +265,9 @@ class RaggedKVBatch:
             out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
         d, arrays = self.descriptor(q, out, scale if scale is not None else self.D ** -0.5, general)
         lib = _lib.load()
-        ws = _workspace(q.device, lib.tq_decode_workspace_bytes(self.kc.ref(), ctypes.byref(d)))
+        stream = _lib.stream_ptr(q.device)
+        ws = _workspace(q.device, lib.tq_decode_workspace_bytes(self.kc.ref(), ctypes.byref(d)), stream)
         _lib.check(lib.tq_decode_attention(self.kc.ref(), self.vc.ref(), ctypes.byref(d), ws.data_ptr(), ws.numel(),
-                                           _lib.stream_ptr(q.device)), "tq_decode_attention")
+                                           stream), "tq_decode_attention")
         self._attn_keep = arrays
         return out

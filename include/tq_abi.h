@@ -259,6 +259,19 @@ size_t tq_dense_decode_workspace_bytes(const tq_attn_desc* desc, int32_t head_di
 int tq_dense_decode_attention(const tq_attn_desc* desc, int32_t head_dim, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* Append one token per (sequence, kv head) to residual rings of keys and
+ * values: rows (batch*heads, ring_cap, d) of `dtype` (TQ_F16 / TQ_BF16) with
+ * head stride ring_head_stride elements; token (b, h) of k and v (batch,
+ * heads, d), contiguous, goes to slot slot_b[b] (device int32 array) of row
+ * b*heads + h. Sequences with slot_b[b] outside [0, ring_cap) are skipped.
+ * d and ring_head_stride multiples of 8, pointers 16-byte aligned. No
+ * counterpart in the reference, whose fp16 tail grows by concatenation in
+ * update_and_fetch (cache.py:620-706); the fixed ring of this library takes
+ * its place, and one launch writes both sides of a decode step. */
+int tq_ring_append(const void* k, const void* v, int32_t dtype, void* ring_k, void* ring_v,
+                   int64_t ring_head_stride, int32_t ring_cap, int32_t batch, int32_t heads, int32_t d,
+                   const int32_t* slot_b, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -681,7 +681,51 @@ int tq_codec_prepare(tq_codec* c, const float* cen, int32_t n) {
   return TQ_OK;
 }
 
+namespace tq {
+// Ring append: workgroup (b*heads + h), thread t < d/8 copies 16 bytes of the
+// key, thread d/8 + t the same bytes of the value, into slot slot_b[b].
+__global__ __launch_bounds__(256) void ring_append_kernel(const uint4* k, const uint4* v, uint4* rk, uint4* rv,
+                                                           int64_t rhs16, int cap, int heads, int d16,
+                                                           const int32_t* slot_b) {
+  const int row = blockIdx.x, b = row / heads, t = threadIdx.x;
+  const int slot = slot_b[b];
+  if (slot < 0 || slot >= cap || t >= 2 * d16) return;
+  const bool val = t >= d16;
+  const int j = val ? t - d16 : t;
+  const int64_t dst = (int64_t)row * rhs16 + (int64_t)slot * d16 + j;
+  const int64_t src = (int64_t)row * d16 + j;
+  if (val)
+    rv[dst] = v[src];
+  else
+    rk[dst] = k[src];
+}
+}  // namespace tq
+
 const char* tq_last_error(void) { return tq::g_err; }
+
+int tq_ring_append(const void* k, const void* v, int32_t dtype, void* ring_k, void* ring_v, int64_t ring_head_stride,
+                   int32_t ring_cap, int32_t batch, int32_t heads, int32_t d, const int32_t* slot_b, void* stream) {
+  using namespace tq;
+  if (dtype != TQ_F16 && dtype != TQ_BF16) return set_error(TQ_ERR_UNSUPPORTED, "ring_append: dtype %d", dtype);
+  if (!k || !v || !ring_k || !ring_v || !slot_b) return set_error(TQ_ERR_INVALID, "ring_append: NULL pointer");
+  if (batch < 0 || heads <= 0 || d <= 0 || d % 8 || d > 1024 || ring_cap <= 0 || ring_head_stride % 8 ||
+      ring_head_stride < (int64_t)ring_cap * d)
+    return set_error(TQ_ERR_INVALID, "ring_append: bad shape (batch %d heads %d d %d cap %d stride %lld)", batch, heads,
+                     d, ring_cap, (long long)ring_head_stride);
+  const auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (!a16(k) || !a16(v) || !a16(ring_k) || !a16(ring_v))
+    return set_error(TQ_ERR_INVALID, "ring_append: pointers must be 16-byte aligned");
+  if (batch == 0) return TQ_OK;
+  const int64_t rows = (int64_t)batch * heads;
+  if (rows >= ((int64_t)1 << 31)) return set_error(TQ_ERR_INVALID, "ring_append: too many rows");
+  const int d16 = d / 8;
+  hipLaunchKernelGGL(ring_append_kernel, dim3((unsigned)rows), dim3(((2 * d16 + 63) / 64) * 64), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint4*>(k), static_cast<const uint4*>(v),
+                     static_cast<uint4*>(ring_k), static_cast<uint4*>(ring_v), ring_head_stride / 8, (int)ring_cap,
+                     (int)heads, d16, slot_b);
+  TQ_LAUNCH_CHECK("tq_ring_append");
+  return TQ_OK;
+}
 
 int tq_device_supported(void) {
   int dev = 0;

@@ -1220,7 +1220,7 @@ void fast_plan_host(int batch, int hkv, int max_comp, int max_sink, int max_res,
   if (n < 1) n = 1;
   if (n > cus) n = cus;
   nwg = (int)n;
-  chunks = uniform ? 1 : 8;
+  chunks = uniform ? 1 : 16;
   vmax = chunks * nwg + batch * hkv;
 }
 

@@ -83,6 +83,7 @@ SIGNATURES = {
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_device_supported": (_i32, []),
     "tq_compress": (_i32, [_PC, _p, _i32, _i64, _PSp, _PS, _p]),
+    "tq_ring_append": (_i32, [_p, _p, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p]),
     "tq_codec_prepare": (_i32, [_PC, _p, _i32]),
     "tq_codec_decode_table": (_i32, [_PC, _p]),
     "tq_dequantize": (_i32, [_PC, _PS, _PSp, _p, _i64, _i32, _p]),

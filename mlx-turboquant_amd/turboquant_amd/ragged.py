@@ -111,7 +111,6 @@ class RaggedKVBatch:
         self.sink_len, self.comp_len, self.res_len, self.res_start, self.offset = z(), z(), z(), z(), z()
         self._step_ints = _IntStage(8 * batch, dev)   # ring slots / drain arrays / post-step lengths of a step
         self._attn_ints = _IntStage(4 * batch, dev)   # per-sequence lengths of an attention call
-        self._rows = torch.arange(batch, device=dev)
         self._desc = None        # the attention descriptor, refreshed per call
         self._structs = None     # (store capacities, tq_store of kstore, of vstore)
         # the lengths change only in load() and step(): a step stages the
@@ -184,29 +183,27 @@ class RaggedKVBatch:
         # position), then the lengths after this step for the next attention call
         comp_after = self.comp_len + drain
         start_after = np.where(drain, (self.res_start + 1) % self.cap, self.res_start)
-        staged, ptrs = self._step_ints.put_ptrs(ring_slot, drain, self.res_start, self.comp_len,
-                                                comp_after, self.sink_len, res_after - drain, start_after)
-        slot_t = staged[:B]
+        # (ring slot -1: the token went to the sink)
+        staged, ptrs = self._step_ints.put_ptrs(np.where(to_sink, -1, ring_slot), drain, self.res_start,
+                                                self.comp_len, comp_after, self.sink_len, res_after - drain,
+                                                start_after)
         n_b, src_b, dst_b = ptrs[1:4]
-        if (~to_sink).all():
-            self.ring_k[self._rows, :, slot_t] = keys
-            self.ring_v[self._rows, :, slot_t] = values
-        elif (~to_sink).any():
-            bi = np.nonzero(~to_sink)[0]
-            bt = torch.as_tensor(bi, device=dev)
-            st = slot_t[bt]
-            self.ring_k[bt, :, st] = keys[bt]
-            self.ring_v[bt, :, st] = values[bt]
+        lib = _lib.load()
+        stream = _lib.stream_ptr(dev)
+        if not to_sink.all():
+            keys, values = keys.contiguous(), values.contiguous()
+            _lib.check(lib.tq_ring_append(keys.data_ptr(), values.data_ptr(), _lib.TQ_F16, self.ring_k.data_ptr(),
+                                          self.ring_v.data_ptr(), self.cap * D, self.cap, B, H, D, ptrs[0], stream),
+                       "tq_ring_append")
         self.res_len = res_after
         if drain.any():
             need = int((self.comp_len + drain).max())
             self.kstore.reserve(need, int(self.comp_len.max()))
             self.vstore.reserve(need, int(self.comp_len.max()))
             span = _lib.Span(rows=B * H, heads=H, n_tok=1, reserved=0, n_tok_b=n_b, src_tok0_b=src_b, dst_tok0_b=dst_b)
-            lib = _lib.load()
             for codec, ring, st in zip((self.kc, self.vc), (self.ring_k, self.ring_v), self._store_structs()):
-                _lib.check(lib.tq_compress(codec.ref(), ring.data_ptr(), _lib.dtype_code(ring.dtype), self.cap * D,
-                                           ctypes.byref(span), ctypes.byref(st), _lib.stream_ptr(dev)), "tq_compress")
+                _lib.check(lib.tq_compress(codec.ref(), ring.data_ptr(), _lib.TQ_F16, self.cap * D,
+                                           ctypes.byref(span), ctypes.byref(st), stream), "tq_compress")
             self.comp_len = comp_after
             self.res_start = start_after
             self.res_len -= drain

@@ -92,6 +92,15 @@ def test_host_side_validation_errors():
     assert lib.tq_dense_decode_attention(ctypes.byref(d), 128, None, 0, None) == _lib.TQ_ERR_UNSUPPORTED
     d.hq, d.sink_k = 8, 18  # rows not 16-byte aligned
     assert lib.tq_dense_decode_attention(ctypes.byref(d), 128, None, 0, None) == _lib.TQ_ERR_UNSUPPORTED
+    # ring append: dtype, NULL pointers, shapes, alignment (fake non-NULL addresses: nothing is launched)
+    ra = lib.tq_ring_append
+    assert ra(16, 16, _lib.TQ_F32, 16, 16, 1024, 8, 1, 1, 128, 16, None) == _lib.TQ_ERR_UNSUPPORTED
+    assert ra(None, 16, _lib.TQ_F16, 16, 16, 1024, 8, 1, 1, 128, 16, None) == _lib.TQ_ERR_INVALID
+    assert ra(16, 16, _lib.TQ_F16, 16, 16, 1024, 8, 1, 1, 100, 16, None) == _lib.TQ_ERR_INVALID  # d % 8
+    assert ra(16, 16, _lib.TQ_F16, 16, 16, 512, 8, 1, 1, 128, 16, None) == _lib.TQ_ERR_INVALID  # stride < cap * d
+    assert b"bad shape" in lib.tq_last_error()
+    assert ra(16, 24, _lib.TQ_F16, 16, 16, 1024, 8, 1, 1, 128, 16, None) == _lib.TQ_ERR_INVALID  # alignment
+    assert ra(16, 16, _lib.TQ_BF16, 16, 16, 1024, 8, 0, 1, 128, 16, None) == _lib.TQ_OK  # empty batch: no-op
 
 
 def test_value_table_is_an_exact_fp16_copy_of_the_2bit_codebook():

@@ -199,6 +199,30 @@ def test_ragged_small_queries_and_values():
     assert e < 1e-5
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_ring_append(dtype):
+    """tq_ring_append against torch indexing: token (b, h) to slot slot_b[b]
+    of both rings, sequences with a slot outside [0, cap) left untouched,
+    rings with spare row capacity (head stride > cap * d); bit-exact."""
+    from turboquant_amd import _lib
+    B, H, cap, d, cap_alloc = 5, 3, 7, 64, 9
+    g = torch.Generator(device=DEV).manual_seed(3)
+    rk = torch.randn(B, H, cap_alloc, d, generator=g, device=DEV).to(dtype)
+    rv = torch.randn(B, H, cap_alloc, d, generator=g, device=DEV).to(dtype)
+    k = torch.randn(B, H, d, generator=g, device=DEV).to(dtype)
+    v = torch.randn(B, H, d, generator=g, device=DEV).to(dtype)
+    slots = torch.tensor([2, -1, 6, 0, 7], dtype=torch.int32, device=DEV)  # -1 and 7 (= cap): skipped
+    ek, ev = rk.clone(), rv.clone()
+    for b, sl in enumerate(slots.tolist()):
+        if 0 <= sl < cap:
+            ek[b, :, sl], ev[b, :, sl] = k[b], v[b]
+    lib = _lib.load()
+    _lib.check(lib.tq_ring_append(k.data_ptr(), v.data_ptr(), _lib.dtype_code(dtype), rk.data_ptr(), rv.data_ptr(),
+                                  cap_alloc * d, cap, B, H, d, slots.data_ptr(), _lib.stream_ptr(DEV)), "ring append")
+    torch.cuda.synchronize()
+    assert torch.equal(rk, ek) and torch.equal(rv, ev)
+
+
 def batch_route(rb, q):
     """tq_debug_decode_route (a test hook of the library) for rb.attend(q):
     0 the general kernel, 2 the K4/V2 kernels, 4 the other widths' kernels."""

@@ -138,20 +138,22 @@ def bench_layer_batched(dev, layers: int, ctx: int, reps: int, warmup: int):
             "kernel": "uniform_decode_kernel<4> + uniform_merge_kernel<4>, batch = layers"}
 
 
-def bench_widths(dev, widths=((3, 2), (2, 2), (3, 3), (4, 3), (4, 4)), layers: int = 12, reps: int = 20,
+def bench_widths(dev, widths=((3, 2), (2, 2), (3, 3), (4, 3), (4, 4), (3.5, 3.5)), layers: int = 12, reps: int = 20,
                  warmup: int = 5):
     """configs[1]'s layer shape (T = 32768: sink 128, 32512 packed, window
-    128; Hq = 32, Hkv = 8) at the other integer widths, on the uniform-batch
-    MFMA kernels of those widths: a graph of `layers` attend calls (whole
-    call per layer) and of the partials kernel alone (HIP events); 12 layers,
-    so the graph's bytes (300-450 MB) exceed the 256 MB last-level cache.""" 
+    128; Hq = 32, Hkv = 8) at the other widths: the integer ones on the
+    uniform-batch MFMA kernels of those widths, a graph of `layers` attend
+    calls (whole call per layer) and of the partials kernel alone (HIP
+    events); the fractional K3.5/V3.5 on the general kernels (whole call
+    only). 12 layers, so the graph's bytes (300-450 MB) exceed the 256 MB
+    last-level cache."""
     import torch
     from turboquant_amd import TurboQuantKVCache
     res = []
     for kb, vb in widths:
         caches, qs = [], []
         for l in range(layers):
-            g = torch.Generator(device=dev).manual_seed(2000 + 10 * kb + vb + 100 * l)
+            g = torch.Generator(device=dev).manual_seed(int(2000 + 10 * kb + vb + 100 * l))
             scale = torch.exp(torch.randn(128, generator=g, device=dev) * 0.5)
             k = (torch.randn(1, 8, 32768, 128, generator=g, device=dev) * scale).half()
             v = torch.randn(1, 8, 32768, 128, generator=g, device=dev).half()
@@ -167,13 +169,17 @@ def bench_widths(dev, widths=((3, 2), (2, 2), (3, 3), (4, 3), (4, 4)), layers: i
             for c, q, o in zip(caches, qs, outs):
                 c.attend(q, out=o)
 
-        ms, _, _ = time_graph(step, reps, warmup)
-        ms_k = time_partials_kernel(caches, qs, outs, reps, warmup)
+        mfma = float(kb).is_integer() and float(vb).is_integer()
+        ms, _, _ = time_graph(step, reps if mfma else 5, warmup if mfma else 2)
         byt = decode_bytes_per_layer(caches[0], 32)
-        res.append({"key_bits": kb, "value_bits": vb, "bytes_per_layer": byt,
-                    "whole_call_us": round(ms * 1e3 / layers, 3), "GBps": round(byt / (ms / layers * 1e-3) / 1e9, 1),
-                    "partials_us": round(ms_k * 1e3, 3), "partials_GBps": round(byt / (ms_k * 1e-3) / 1e9, 1),
-                    "partials_frac": round(byt / (ms_k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        r = {"key_bits": kb, "value_bits": vb, "route": "uniform_decode_kernel" if mfma else "general (chunk_kernel)",
+             "bytes_per_layer": byt, "whole_call_us": round(ms * 1e3 / layers, 3),
+             "GBps": round(byt / (ms / layers * 1e-3) / 1e9, 1)}
+        if mfma:
+            ms_k = time_partials_kernel(caches, qs, outs, reps, warmup)
+            r.update({"partials_us": round(ms_k * 1e3, 3), "partials_GBps": round(byt / (ms_k * 1e-3) / 1e9, 1),
+                      "partials_frac": round(byt / (ms_k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        res.append(r)
         del caches, qs, outs
         torch.cuda.empty_cache()
     return res

@@ -113,17 +113,39 @@ __device__ inline uint32_t code_at(const uint8_t* row, int j, int bits) {
 __device__ inline void stage_rows(uint8_t* dst, int stride, int col, const uint8_t* src, int row_bytes, int n) {
   if (row_bytes <= 0 || n <= 0) return;
   const int tid = threadIdx.x;
+  // SB loads per thread are issued before the first LDS store: one memory
+  // round trip per SB * NT elements (a load-store loop waits once per element)
+  constexpr int SB = 8;
   if ((row_bytes & 3) == 0 && (col & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 3) == 0) {
-    const int rw = row_bytes >> 2;
+    const int rw = row_bytes >> 2, total = n * rw;
     const uint32_t* sw = reinterpret_cast<const uint32_t*>(src);
-    for (int e = tid; e < n * rw; e += NT) {
-      const int t = e / rw, k = e - t * rw;
-      *reinterpret_cast<uint32_t*>(dst + t * stride + col + 4 * k) = sw[e];
+    for (int e0 = tid; e0 < total; e0 += SB * NT) {
+      uint32_t v[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) v[u] = e0 + u * NT < total ? sw[e0 + u * NT] : 0u;
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int e = e0 + u * NT;
+        if (e < total) {
+          const int t = e / rw, k = e - t * rw;
+          *reinterpret_cast<uint32_t*>(dst + t * stride + col + 4 * k) = v[u];
+        }
+      }
     }
   } else {
-    for (int e = tid; e < n * row_bytes; e += NT) {
-      const int t = e / row_bytes, k = e - t * row_bytes;
-      dst[t * stride + col + k] = src[e];
+    const int total = n * row_bytes;
+    for (int e0 = tid; e0 < total; e0 += SB * NT) {
+      uint8_t v[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) v[u] = e0 + u * NT < total ? src[e0 + u * NT] : (uint8_t)0;
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int e = e0 + u * NT;
+        if (e < total) {
+          const int t = e / row_bytes, k = e - t * row_bytes;
+          dst[t * stride + col + k] = v[u];
+        }
+      }
     }
   }
 }
@@ -329,10 +351,47 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
         kp = a.d.res_k;
         ko = (int64_t)row * a.d.res_head_stride + (int64_t)pos * D;
       }
-      for (int j = 0; j < D; ++j) {
-        const float kv = load_elem(kp, ko + j, a.d.kv_dtype);
+      const int esz = a.d.kv_dtype == TQ_F32 ? 4 : 2;
+      const uint8_t* kb = static_cast<const uint8_t*>(kp) + ko * esz;
+      if ((reinterpret_cast<uintptr_t>(kb) & 15) == 0) {
+        // the token's row in 16-byte pieces, KB of them requested at once
+        constexpr int KB = 8;
+        const int npc = D * esz / 16;  // pieces per row
+        for (int c0 = 0; c0 < npc; c0 += KB) {
+          uint4 raw[KB];
 #pragma unroll
-        for (int h = 0; h < G; ++h) s[h] = fmaf(qv[h][j], kv, s[h]);
+          for (int u = 0; u < KB; ++u) raw[u] = *reinterpret_cast<const uint4*>(kb + 16 * min(c0 + u, npc - 1));
+#pragma unroll
+          for (int u = 0; u < KB; ++u) {
+            if (c0 + u >= npc) break;
+            const uint32_t wd[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+            if (esz == 4) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int j = 4 * (c0 + u) + e;
+                const float kv = __uint_as_float(wd[e]);
+#pragma unroll
+                for (int h = 0; h < G; ++h) s[h] = fmaf(qv[h][j], kv, s[h]);
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const int j = 8 * (c0 + u) + e;
+                const uint32_t hb = (wd[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                const float kv = a.d.kv_dtype == TQ_BF16 ? __uint_as_float(hb << 16)
+                                                         : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+#pragma unroll
+                for (int h = 0; h < G; ++h) s[h] = fmaf(qv[h][j], kv, s[h]);
+              }
+            }
+          }
+        }
+      } else {
+        for (int j = 0; j < D; ++j) {
+          const float kv = load_elem(kp, ko + j, a.d.kv_dtype);
+#pragma unroll
+          for (int h = 0; h < G; ++h) s[h] = fmaf(qv[h][j], kv, s[h]);
+        }
       }
     }
   }
@@ -416,21 +475,28 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
           }
         }
       } else {
-        for (int tt = t_lo; tt < min(t_hi, nvalid); ++tt) {
-          int64_t vo;
-          const void* vp;
-          if (seg == 1) {
-            vp = a.d.sink_v;
-            vo = (int64_t)row * a.d.sink_head_stride + (int64_t)(base + tt) * D;
-          } else {
-            const int st = seq_ring_start(a.d, b);
-            const int pos = (st + base + tt) % a.d.res_cap;
-            vp = a.d.res_v;
-            vo = (int64_t)row * a.d.res_head_stride + (int64_t)pos * D;
-          }
-          const float vv = load_elem(vp, vo + j, a.d.kv_dtype);
+        // fp16 / bf16 / f32 tokens: VB tokens' values requested before any is
+        // used (a load-use loop waits one memory round trip per token)
+        constexpr int VB = 16;
+        const void* vp = seg == 1 ? a.d.sink_v : a.d.res_v;
+        const int st = seg == 1 ? 0 : seq_ring_start(a.d, b);
+        const int tend = min(t_hi, nvalid);
+        for (int tt0 = t_lo; tt0 < tend; tt0 += VB) {
+          float vv[VB];
 #pragma unroll
-          for (int h = 0; h < G; ++h) acc[h] = fmaf(w[h][tt], vv, acc[h]);
+          for (int u = 0; u < VB; ++u) {
+            const int tt = min(tt0 + u, tend - 1);
+            const int64_t vo = seg == 1 ? (int64_t)row * a.d.sink_head_stride + (int64_t)(base + tt) * D
+                                        : (int64_t)row * a.d.res_head_stride + (int64_t)((st + base + tt) % a.d.res_cap) * D;
+            vv[u] = load_elem(vp, vo + j, a.d.kv_dtype);
+          }
+#pragma unroll
+          for (int u = 0; u < VB; ++u) {
+            if (tt0 + u < tend) {
+#pragma unroll
+              for (int h = 0; h < G; ++h) acc[h] = fmaf(w[h][tt0 + u], vv[u], acc[h]);
+            }
+          }
         }
       }
     }
@@ -521,42 +587,55 @@ __global__ __launch_bounds__(128) void combine_kernel(AttnArgs a) {
   if ((tid & 63) == 0) rsum[tid >> 6] = L;
   __syncthreads();
   L = rsum[0] + rsum[1];
-  // sum over chunks [c0, c1) of wc[c] * pp[c * ps + col]
+  // sum over chunks [c0, c1) of wc[c] * pp[c * ps + col]; CU loads are
+  // requested before they are used (one memory round trip per CU chunks)
+  constexpr int CU = 16;
   auto wsum = [&](int c0, int c1, int col) {
-    float r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+    float r[CU];
+#pragma unroll
+    for (int u = 0; u < CU; ++u) r[u] = 0.f;
     int c = c0;
-    for (; c + 4 <= c1; c += 4) {
-      r0 = fmaf(wc[c], pp[c * ps + col], r0);
-      r1 = fmaf(wc[c + 1], pp[(c + 1) * ps + col], r1);
-      r2 = fmaf(wc[c + 2], pp[(c + 2) * ps + col], r2);
-      r3 = fmaf(wc[c + 3], pp[(c + 3) * ps + col], r3);
+    for (; c + CU <= c1; c += CU) {
+      float x[CU];
+#pragma unroll
+      for (int u = 0; u < CU; ++u) x[u] = pp[(c + u) * ps + col];
+#pragma unroll
+      for (int u = 0; u < CU; ++u) r[u] = fmaf(wc[c + u], x[u], r[u]);
     }
-    for (; c < c1; ++c) r0 = fmaf(wc[c], pp[c * ps + col], r0);
-    return (r0 + r1) + (r2 + r3);
+    for (; c < c1; ++c) r[0] = fmaf(wc[c], pp[c * ps + col], r[0]);
+#pragma unroll
+    for (int w = CU / 2; w > 0; w >>= 1)
+#pragma unroll
+      for (int u = 0; u < w; ++u) r[u] += r[u + w];
+    return r[0];
+  };
+  // sum over rows i < n (a multiple of 4) of v[i] * mat[i * D + j], CU rows per batch
+  auto matvec = [&](const float* v, const float* mat, int n, int j) {
+    float r[CU];
+#pragma unroll
+    for (int u = 0; u < CU; ++u) r[u] = 0.f;
+    int i = 0;
+    for (; i + CU <= n; i += CU) {
+      float x[CU];
+#pragma unroll
+      for (int u = 0; u < CU; ++u) x[u] = mat[(int64_t)(i + u) * D + j];
+#pragma unroll
+      for (int u = 0; u < CU; ++u) r[u] = fmaf(v[i + u], x[u], r[u]);
+    }
+    for (; i < n; ++i) r[0] = fmaf(v[i], mat[(int64_t)i * D + j], r[0]);
+#pragma unroll
+    for (int w = CU / 2; w > 0; w >>= 1)
+#pragma unroll
+      for (int u = 0; u < w; ++u) r[u] += r[u + w];
+    return r[0];
   };
   for (int j = tid; j < D; j += 128) accr[j] = wsum(0, a.nc, 2 + j);
   for (int i = tid; i < a.m; i += 128) azs[i] = wsum(0, a.nc, 2 + D + i);
   __syncthreads();
   float* out = a.d.out + (((int64_t)b * hq + h) * nq + qi) * D;
   for (int j = tid; j < D; j += 128) {
-    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-    for (int i = 0; i < D; i += 4) {
-      o0 = fmaf(accr[i], a.vrot[(int64_t)i * D + j], o0);
-      o1 = fmaf(accr[i + 1], a.vrot[(int64_t)(i + 1) * D + j], o1);
-      o2 = fmaf(accr[i + 2], a.vrot[(int64_t)(i + 2) * D + j], o2);
-      o3 = fmaf(accr[i + 3], a.vrot[(int64_t)(i + 3) * D + j], o3);
-    }
-    float o = (o0 + o1) + (o2 + o3) + wsum(a.nc, nch, 2 + j);
-    if (a.m > 0) {
-      float z0 = 0.f, z1 = 0.f, z2 = 0.f, z3 = 0.f;
-      for (int i = 0; i < a.m; i += 4) {
-        z0 = fmaf(azs[i], a.proj[(int64_t)i * D + j], z0);
-        z1 = fmaf(azs[i + 1], a.proj[(int64_t)(i + 1) * D + j], z1);
-        z2 = fmaf(azs[i + 2], a.proj[(int64_t)(i + 2) * D + j], z2);
-        z3 = fmaf(azs[i + 3], a.proj[(int64_t)(i + 3) * D + j], z3);
-      }
-      o = fmaf(SQRT_HALF_PI / (float)D, (z0 + z1) + (z2 + z3), o);
-    }
+    float o = matvec(accr, a.vrot, D, j) + wsum(a.nc, nch, 2 + j);
+    if (a.m > 0) o = fmaf(SQRT_HALF_PI / (float)D, matvec(azs, a.proj, a.m, j), o);
     out[j] = (L > 0.f) ? o / L : 0.f;
   }
 }

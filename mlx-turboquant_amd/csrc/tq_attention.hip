@@ -188,6 +188,59 @@ __device__ inline void dot_codes(const uint8_t* row, int nd, const float* lut, c
   }
 }
 
+// Up to four row sets staged together (dword path: every source, row size
+// and column 4-byte aligned): each pass requests SB dwords of every source
+// before any LDS store, so the four sets cost one memory round trip per pass.
+struct StageSrc {
+  uint8_t* dst;
+  int col;
+  const uint8_t* src;
+  int row_bytes;
+};
+__device__ inline bool stage_aligned(const StageSrc& q) {
+  return q.row_bytes <= 0 || ((q.row_bytes & 3) == 0 && (q.col & 3) == 0 && (reinterpret_cast<uintptr_t>(q.src) & 3) == 0);
+}
+__device__ inline void stage_rows_multi(const StageSrc (&S)[4], int stride, int n) {
+  if (n <= 0) return;
+  bool ok = true;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) ok = ok && stage_aligned(S[q]);
+  if (!ok) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) stage_rows(S[q].dst, stride, S[q].col, S[q].src, S[q].row_bytes, n);
+    return;
+  }
+  constexpr int SB = 8;
+  const int tid = threadIdx.x;
+  int tot[4], rw[4], mx = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    rw[q] = S[q].row_bytes > 0 ? S[q].row_bytes >> 2 : 0;
+    tot[q] = n * rw[q];
+    mx = max(mx, tot[q]);
+  }
+  for (int e0 = tid; e0 < mx; e0 += SB * NT) {
+    uint32_t v[4][SB];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int e = e0 + u * NT;
+        v[q][u] = e < tot[q] ? reinterpret_cast<const uint32_t*>(S[q].src)[e] : 0u;
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int e = e0 + u * NT;
+        if (e < tot[q]) {
+          const int t = e / rw[q], k = e - t * rw[q];
+          *reinterpret_cast<uint32_t*>(S[q].dst + t * stride + S[q].col + 4 * k) = v[q][u];
+        }
+      }
+  }
+}
+
 template <int D, int G>
 __device__ inline void dot_codes_bits(int bits, const uint8_t* row, int nd, const float* lut, const float (*q)[D],
                                       int j0, float (&s)[G]) {
@@ -295,21 +348,31 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   if (packed) {
     const tq_store& ks = a.d.kstore;
     const tq_store& vs = a.d.vstore;
-    stage_rows(ktile, KR, 0, ks.codes_hi + (int64_t)row * ks.hi_head_stride + (int64_t)base * a.k_row_hi, a.k_row_hi,
-               nvalid);
-    if (a.k_row_lo)
-      stage_rows(ktile, KR, a.k_row_hi, ks.codes_lo + (int64_t)row * ks.lo_head_stride + (int64_t)base * a.k_row_lo,
-                 a.k_row_lo, nvalid);
-    stage_rows(vtile, KR, 0, vs.codes_hi + (int64_t)row * vs.hi_head_stride + (int64_t)base * a.v_row_hi, a.v_row_hi,
-               nvalid);
-    if (a.v_row_lo)
-      stage_rows(vtile, KR, a.v_row_hi, vs.codes_lo + (int64_t)row * vs.lo_head_stride + (int64_t)base * a.v_row_lo,
-                 a.v_row_lo, nvalid);
+    const StageSrc S[4] = {
+        {ktile, 0, ks.codes_hi + (int64_t)row * ks.hi_head_stride + (int64_t)base * a.k_row_hi, a.k_row_hi},
+        {ktile, a.k_row_hi,
+         a.k_row_lo ? ks.codes_lo + (int64_t)row * ks.lo_head_stride + (int64_t)base * a.k_row_lo : nullptr,
+         a.k_row_lo},
+        {vtile, 0, vs.codes_hi + (int64_t)row * vs.hi_head_stride + (int64_t)base * a.v_row_hi, a.v_row_hi},
+        {vtile, a.v_row_hi,
+         a.v_row_lo ? vs.codes_lo + (int64_t)row * vs.lo_head_stride + (int64_t)base * a.v_row_lo : nullptr,
+         a.v_row_lo}};
+    stage_rows_multi(S, KR, nvalid);
     if (qjl) {
       stage_rows(ksg, SR, 0, ks.signs + (int64_t)row * ks.sign_head_stride + (int64_t)base * a.row_sign, a.row_sign,
                  nvalid);
       stage_rows(vsg, SR, 0, vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base * a.row_sign, a.row_sign,
                  nvalid);
+    }
+  }
+  // the token's norms (and gammas) requested with the staging loads
+  float nk_t = 0.f, nv_t = 1.f, gk_t = 0.f, gv_t = 0.f;
+  if (packed && tid < nvalid) {
+    nk_t = a.d.kstore.norms[(int64_t)row * a.d.kstore.norm_head_stride + base + tid];
+    nv_t = a.d.vstore.norms[(int64_t)row * a.d.vstore.norm_head_stride + base + tid];
+    if (qjl) {
+      gk_t = a.d.kstore.gamma[(int64_t)row * a.d.kstore.gamma_head_stride + base + tid];
+      gv_t = a.d.vstore.gamma[(int64_t)row * a.d.vstore.gamma_head_stride + base + tid];
     }
   }
   __syncthreads();
@@ -326,11 +389,11 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
       const uint8_t* kr = ktile + t * KR;
       dot_codes_bits<D, G>(a.kb_hi, kr, a.ks, klut[0], qv, 0, s);
       if (a.ks < D) dot_codes_bits<D, G>(a.kb_lo, kr + a.k_row_hi, D - a.ks, klut[1], qv, a.ks, s);
-      const float nk = a.d.kstore.norms[(int64_t)row * a.d.kstore.norm_head_stride + base + t];
+      const float nk = nk_t;
 #pragma unroll
       for (int h = 0; h < G; ++h) s[h] *= nk;
       if (qjl) {
-        const float gk = a.d.kstore.gamma[(int64_t)row * a.d.kstore.gamma_head_stride + base + t];
+        const float gk = gk_t;
         float zs[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) zs[h] = 0.f;
@@ -418,8 +481,8 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   {
     float nv = 1.f, gv = 0.f;
     if (packed && t < nvalid) {
-      nv = a.d.vstore.norms[(int64_t)row * a.d.vstore.norm_head_stride + base + t];
-      if (qjl) gv = a.d.vstore.gamma[(int64_t)row * a.d.vstore.gamma_head_stride + base + t];
+      nv = nv_t;
+      if (qjl) gv = gv_t;
     }
 #pragma unroll
     for (int h = 0; h < G; ++h) {

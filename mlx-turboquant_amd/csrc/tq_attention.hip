@@ -293,16 +293,20 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   constexpr int SR = MAXM / 8 + 4;
   __shared__ __align__(16) float qv[G][D];   // rotated (compressed) or plain (fp16) scaled query
   __shared__ __align__(16) float w[G][CHUNK];   // p * n_v (or p) per token
-  __shared__ __align__(16) float pg[G][CHUNK];  // p * gamma_v (QJL)
   __shared__ float red[G][NT / 64];
   __shared__ float mx[G], lsum[G];
   __shared__ float klut[2][16], vlut[2][16];
-  __shared__ __align__(16) float sqv[G][MAXM];
   __shared__ __align__(16) uint8_t ktile[CHUNK * KR];  // key code rows: hi bytes, then lo bytes
   __shared__ __align__(16) uint8_t vtile[CHUNK * KR];  // value code rows
-  __shared__ __align__(16) uint8_t ksg[CHUNK * SR];    // key sign rows (QJL)
-  __shared__ __align__(16) uint8_t vsg[CHUNK * SR];    // value sign rows (QJL)
   __shared__ float slice[G][NT];                       // per-thread partial sums of the PV / QJL phases
+  // QJL only, in the dynamic LDS of the launch (chunk_qjl_lds bytes when the
+  // codecs carry a sketch, none otherwise, so that three workgroups fit a CU):
+  // p * gamma_v per token, S q per head, key and value sign rows
+  extern __shared__ __align__(16) float sm[];
+  float (*pg)[CHUNK] = reinterpret_cast<float (*)[CHUNK]>(sm);
+  float (*sqv)[MAXM] = reinterpret_cast<float (*)[MAXM]>(sm + G * CHUNK);
+  uint8_t* ksg = reinterpret_cast<uint8_t*>(sm + G * CHUNK + G * MAXM);
+  uint8_t* vsg = ksg + CHUNK * SR;
   // group g: query heads [g G, g G + G) of kv head g / gsub; query token qi
   // of sequence b (row vb of the workspace)
   const int c = blockIdx.x + a.c0, g = blockIdx.y, vb = blockIdx.z;
@@ -487,7 +491,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       w[h][t] = p[h] * nv;
-      pg[h][t] = p[h] * gv;
+      if (qjl) pg[h][t] = p[h] * gv;
     }
   }
   __syncthreads();
@@ -712,15 +716,17 @@ static void chunk_counts(const tq_attn_desc* d, int& nc, int& ns, int& nr) {
 // G: query heads per launch group (1 .. 8)
 template <int D>
 static void launch_chunks(const AttnArgs& a, int G, dim3 grid, hipStream_t s) {
+  // dynamic LDS of chunk_kernel: the QJL arrays, when the call has a sketch
+  const size_t dl = a.m > 0 ? (size_t)G * (CHUNK + 256) * 4 + 2 * (size_t)CHUNK * (256 / 8 + 4) : 0;
   switch (G) {
-    case 1: hipLaunchKernelGGL((chunk_kernel<D, 1>), grid, dim3(NT), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((chunk_kernel<D, 2>), grid, dim3(NT), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((chunk_kernel<D, 3>), grid, dim3(NT), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((chunk_kernel<D, 4>), grid, dim3(NT), 0, s, a); break;
-    case 5: hipLaunchKernelGGL((chunk_kernel<D, 5>), grid, dim3(NT), 0, s, a); break;
-    case 6: hipLaunchKernelGGL((chunk_kernel<D, 6>), grid, dim3(NT), 0, s, a); break;
-    case 7: hipLaunchKernelGGL((chunk_kernel<D, 7>), grid, dim3(NT), 0, s, a); break;
-    default: hipLaunchKernelGGL((chunk_kernel<D, 8>), grid, dim3(NT), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((chunk_kernel<D, 1>), grid, dim3(NT), dl, s, a); break;
+    case 2: hipLaunchKernelGGL((chunk_kernel<D, 2>), grid, dim3(NT), dl, s, a); break;
+    case 3: hipLaunchKernelGGL((chunk_kernel<D, 3>), grid, dim3(NT), dl, s, a); break;
+    case 4: hipLaunchKernelGGL((chunk_kernel<D, 4>), grid, dim3(NT), dl, s, a); break;
+    case 5: hipLaunchKernelGGL((chunk_kernel<D, 5>), grid, dim3(NT), dl, s, a); break;
+    case 6: hipLaunchKernelGGL((chunk_kernel<D, 6>), grid, dim3(NT), dl, s, a); break;
+    case 7: hipLaunchKernelGGL((chunk_kernel<D, 7>), grid, dim3(NT), dl, s, a); break;
+    default: hipLaunchKernelGGL((chunk_kernel<D, 8>), grid, dim3(NT), dl, s, a); break;
   }
 }
 

@@ -133,6 +133,18 @@ def test_attention_qjl():
     check(c, o, q, "qjl")
 
 
+def test_attention_qjl_general_largest_workgroup():
+    """The general kernel's largest workgroup: head_dim 256, 8 query heads per
+    kv head and a 256-projection sketch (static plus the sketch's dynamic LDS,
+    about 126 KB); K3/V3, so the general route runs. float64 over the stored
+    codes and sketch at the attention bar."""
+    k, v = _kv(1, 1, 700, 256, seed=97)
+    c, o = build(dict(head_dim=256, num_kv_heads=1, key_bits=3, value_bits=3, residual_window=64,
+                      fp16_sink_size=16, qjl_correction=True, qjl_n_proj=256), k, v)
+    q = np.random.RandomState(98).randn(1, 8, 1, 256).astype(np.float16)
+    check(c, o, q, "qjl d256 G=8 m=256 general")
+
+
 @pytest.mark.parametrize("G,m", [(1, 32), (2, 96), (4, 64), (8, 256)])
 def test_attention_qjl_k4v2_route(G, m):
     """K4/V2 with a sketch runs the K4/V2 kernels with the sketch's key and

@@ -62,6 +62,14 @@ struct AttnArgs {
   int gsub;  // launch groups per kv head: a chunk_kernel<D, G> group holds G = (hq / hkv) / gsub query heads
 };
 
+// LDS row stride of chunk_kernel's staged code rows: the longer of a key and a
+// value row (hi bytes, then lo bytes), in dwords rounded up to an odd count so
+// that the rows of neighbouring tokens start in different banks.
+__host__ __device__ inline int tile_stride(const AttnArgs& a) {
+  const int b = max(a.k_row_hi + a.k_row_lo, a.v_row_hi + a.v_row_lo);
+  return 4 * (((b + 3) / 4) | 1);
+}
+
 __host__ __device__ inline int part_stride(int D, int m) { return ((2 + D + m) + 3) & ~3; }
 
 // Query row (b, h, query token qi) of the call: q is (batch, hq, n_q, d).
@@ -289,23 +297,26 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   // LDS row strides of staged code rows (at most 4 bits per dim) and sign
   // rows, padded by one dword so that the rows of neighbouring tokens start
   // in different banks
-  constexpr int KR = D / 2 + 4;
+  const int KR = tile_stride(a);
   constexpr int SR = MAXM / 8 + 4;
   __shared__ __align__(16) float qv[G][D];   // rotated (compressed) or plain (fp16) scaled query
   __shared__ __align__(16) float w[G][CHUNK];   // p * n_v (or p) per token
   __shared__ float red[G][NT / 64];
   __shared__ float mx[G], lsum[G];
   __shared__ float klut[2][16], vlut[2][16];
-  __shared__ __align__(16) uint8_t ktile[CHUNK * KR];  // key code rows: hi bytes, then lo bytes
-  __shared__ __align__(16) uint8_t vtile[CHUNK * KR];  // value code rows
-  __shared__ float slice[G][NT];                       // per-thread partial sums of the PV / QJL phases
-  // QJL only, in the dynamic LDS of the launch (chunk_qjl_lds bytes when the
-  // codecs carry a sketch, none otherwise, so that three workgroups fit a CU):
-  // p * gamma_v per token, S q per head, key and value sign rows
+  // per-thread partial sums of the PV / QJL phases, over w once the PV loop is done
+  static_assert(NT == CHUNK, "slice aliases w");
+  float (*slice)[NT] = reinterpret_cast<float (*)[NT]>(&w[0][0]);
+  // dynamic LDS sized per launch: the key and value code rows at the codecs'
+  // row size, then (with a sketch only) p * gamma_v per token, S q per head and
+  // the key and value sign rows; four workgroups of K3.5/V3.5 fit a CU
   extern __shared__ __align__(16) float sm[];
-  float (*pg)[CHUNK] = reinterpret_cast<float (*)[CHUNK]>(sm);
-  float (*sqv)[MAXM] = reinterpret_cast<float (*)[MAXM]>(sm + G * CHUNK);
-  uint8_t* ksg = reinterpret_cast<uint8_t*>(sm + G * CHUNK + G * MAXM);
+  uint8_t* ktile = reinterpret_cast<uint8_t*>(sm);  // key code rows: hi bytes, then lo bytes
+  uint8_t* vtile = ktile + CHUNK * KR;              // value code rows
+  float* qj = reinterpret_cast<float*>(vtile + CHUNK * KR);
+  float (*pg)[CHUNK] = reinterpret_cast<float (*)[CHUNK]>(qj);
+  float (*sqv)[MAXM] = reinterpret_cast<float (*)[MAXM]>(qj + G * CHUNK);
+  uint8_t* ksg = reinterpret_cast<uint8_t*>(qj + G * CHUNK + G * MAXM);
   uint8_t* vsg = ksg + CHUNK * SR;
   // group g: query heads [g G, g G + G) of kv head g / gsub; query token qi
   // of sequence b (row vb of the workspace)
@@ -567,6 +578,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
         }
       }
     }
+    __syncthreads();  // every thread is past its reads of w (slice aliases it)
 #pragma unroll
     for (int h = 0; h < G; ++h) slice[h][tid] = acc[h];
   }
@@ -716,8 +728,9 @@ static void chunk_counts(const tq_attn_desc* d, int& nc, int& ns, int& nr) {
 // G: query heads per launch group (1 .. 8)
 template <int D>
 static void launch_chunks(const AttnArgs& a, int G, dim3 grid, hipStream_t s) {
-  // dynamic LDS of chunk_kernel: the QJL arrays, when the call has a sketch
-  const size_t dl = a.m > 0 ? (size_t)G * (CHUNK + 256) * 4 + 2 * (size_t)CHUNK * (256 / 8 + 4) : 0;
+  // dynamic LDS of chunk_kernel: the code rows, and the QJL arrays when the call has a sketch
+  const size_t dl = 2 * (size_t)CHUNK * tile_stride(a) +
+                    (a.m > 0 ? (size_t)G * (CHUNK + 256) * 4 + 2 * (size_t)CHUNK * (256 / 8 + 4) : 0);
   switch (G) {
     case 1: hipLaunchKernelGGL((chunk_kernel<D, 1>), grid, dim3(NT), dl, s, a); break;
     case 2: hipLaunchKernelGGL((chunk_kernel<D, 2>), grid, dim3(NT), dl, s, a); break;

@@ -361,14 +361,74 @@ def cpu_baseline(caches, qs, budget_s: float = 12.0):
         threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
     except Exception:
         threads = len(os.sched_getaffinity(0))
-    # compress sample: 65536 fp16 vectors at 3 bits (configs[2] keys)
+    # compress sample: 65536 fp16 vectors at 3 bits (configs[2] keys), the
+    # median of 5 timed runs after a warm-up
     x = np.random.RandomState(0).randn(65536, 128).astype(np.float16)
     R = O.rotation_matrix(128)
     O.compress_f32(x[:1024], R, 3)
-    t0 = time.perf_counter()
-    O.compress_f32(x, R, 3)
-    t_c = time.perf_counter() - t0
-    return per_layer, threads, len(times), 65536 / t_c
+    t_c = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        O.compress_f32(x, R, 3)
+        t_c.append(time.perf_counter() - t0)
+    return per_layer, threads, len(times), 65536 / float(np.median(t_c)), len(t_c)
+
+
+def hbm_reference(dev, bytes_layer: int, layers: int = 32, reps: int = 20):
+    """The box's achievable HBM bandwidth, the reference for the decode
+    figures: (a) a 268,435,456-byte device-to-device copy (torch copy_, read +
+    write bytes counted), median of `reps` timed copies; (b) the library's
+    streaming read kernel (tq_measure_read) over one decode layer's worth of
+    bytes (bytes_layer), one launch per layer buffer, `layers` distinct buffers
+    in one graph (so the bytes come from HBM, not the 256 MB last-level
+    cache), HIP events around the replays; (c) the same kernel over one
+    268,435,456-byte buffer."""
+    import ctypes
+    import numpy as np
+    import torch
+    from turboquant_amd import _lib
+    lib = _lib.load()
+    fn = lib.tq_measure_read  # measurement hook of the library (not in include/tq_abi.h)
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    t = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        t.append(e0.elapsed_time(e1))
+    ms_copy = float(np.median(t))
+    del dst
+    nwg = 4096
+    sink = torch.empty(nwg, dtype=torch.float32, device=dev)
+    nb = (bytes_layer + 15) // 16 * 16
+    bufs = [torch.ones(nb // 4, dtype=torch.float32, device=dev) for _ in range(layers)]
+
+    def reads():
+        for b in bufs:
+            _lib.check(fn(b.data_ptr(), nb, sink.data_ptr(), nwg, _lib.stream_ptr(dev)), "tq_measure_read")
+
+    ms_layers, _, _ = time_graph(reads, reps, 5)
+    ms_one, _, _ = time_graph(lambda: _lib.check(fn(src.data_ptr(), n, sink.data_ptr(), nwg, _lib.stream_ptr(dev)),
+                                                 "tq_measure_read"), reps, 5)
+    del bufs, src
+    torch.cuda.empty_cache()
+    us_layer = ms_layers * 1e3 / layers
+    return {"copy_bytes": n, "copy_us": round(ms_copy * 1e3, 2),
+            "copy_GBps": round(2 * n / (ms_copy * 1e-3) / 1e9, 1),
+            "read_bytes_per_launch": nb, "read_us_per_launch": round(us_layer, 3),
+            "read_GBps": round(nb / (us_layer * 1e-6) / 1e9, 1),
+            "read_256MB_us": round(ms_one * 1e3, 2), "read_256MB_GBps": round(n / (ms_one * 1e-3) / 1e9, 1),
+            "method": "copy: torch copy_ of 256 MiB, median of events, read + write bytes; read: tq_measure_read "
+                      "(4096 workgroups x 256 threads, 16-byte nontemporal loads) over one decode layer's bytes, "
+                      f"{layers} distinct buffers in one graph, and over one 256 MiB buffer"}
 
 
 def call_partials_only(c, q, out):
@@ -546,6 +606,8 @@ def main():
                      "bytes_per_launch": bytes_layer[0], "avg_launch_us": round(ms_kernel * 1e3, 3),
                      "whole_call_us": round(ms_step * 1e3 / len(caches), 3)},
     }
+    log("measuring the box's HBM reference bandwidth")
+    result["hbm_reference"] = hbm_reference(dev, bytes_layer[0], args.layers, args.steps)
     if not args.no_extra:
         log("timing the layer-batched launch")
         result["layer_batched"] = bench_layer_batched(dev, args.layers, args.ctx, args.steps, args.warmup)
@@ -566,14 +628,18 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_cpu:
         log("timing CPU baseline")
-        per_layer, threads, n, cpu_vps = cpu_baseline(caches, qs)
+        per_layer, threads, n, cpu_vps, n_c = cpu_baseline(caches, qs)
         cpu_step = per_layer * args.layers
         result["cpu_baseline"] = {
             "value": round(bytes_step / cpu_step / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"float32 numpy restatement of the reference decode step (concat [sink|dequantised|residual] "
                       f"+ SDPA) for layer 0, median of {n} runs x {args.layers} layers; "
-                      f"compress: 65536 vectors K3 f32 norm+GEMM+quantize+pack",
-            "ms_per_step": round(cpu_step * 1e3, 3), "compress_vectors_per_s": round(cpu_vps, 1)}
+                      f"compress: 65536 vectors K3 f32 norm+GEMM+quantize+pack, median of {n_c} runs",
+            "ms_per_step": round(cpu_step * 1e3, 3), "compress_vectors_per_s": round(cpu_vps, 1),
+            "cores_note": "cores = OpenBLAS threads the numpy GEMMs ran with (threadpoolctl)",
+            "affinity_cores": len(os.sched_getaffinity(0)),
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS"),
+            "OPENBLAS_NUM_THREADS": os.environ.get("OPENBLAS_NUM_THREADS")}
     print(json.dumps(result), flush=True)
 
 

@@ -62,11 +62,23 @@ struct AttnArgs {
   int gsub;  // launch groups per kv head: a chunk_kernel<D, G> group holds G = (hq / hkv) / gsub query heads
 };
 
+// Column of the low-width segment in a staged code row: the hi bytes rounded
+// up to a dword, so dot_codes reads both segments as aligned dwords (head_dim
+// 96 at 2.5 bits has an 18-byte hi segment).
+__host__ __device__ inline int lo_col(int row_hi) { return (row_hi + 3) & ~3; }
+
+// Bytes dot_codes reads for a segment of n codes: whole 32-code groups of
+// 4 * bits bytes (a trailing 16-code half group reads a full group).
+__host__ __device__ inline int seg_span(int n, int bits) { return n > 0 ? (n + 31) / 32 * 4 * bits : 0; }
+
 // LDS row stride of chunk_kernel's staged code rows: the longer of a key and a
-// value row (hi bytes, then lo bytes), in dwords rounded up to an odd count so
-// that the rows of neighbouring tokens start in different banks.
+// value row (hi bytes, then lo bytes at lo_col), covering every dword the key
+// dot products read, in dwords rounded up to an odd count so that the rows of
+// neighbouring tokens start in different banks.
 __host__ __device__ inline int tile_stride(const AttnArgs& a) {
-  const int b = max(a.k_row_hi + a.k_row_lo, a.v_row_hi + a.v_row_lo);
+  const int kspan = max(seg_span(a.ks, a.kb_hi), a.k_row_lo ? lo_col(a.k_row_hi) + seg_span(a.D - a.ks, a.kb_lo) : 0);
+  const int vspan = a.v_row_lo ? lo_col(a.v_row_hi) + a.v_row_lo : a.v_row_hi;
+  const int b = max(max(kspan, a.k_row_hi), vspan);
   return 4 * (((b + 3) / 4) | 1);
 }
 
@@ -163,7 +175,8 @@ __device__ inline void stage_rows(uint8_t* dst, int stride, int col, const uint8
 // 32 dims are BITS dwords, read once; shifts are compile-time constants. A
 // trailing group of 16 codes (head_dim 96 split in halves of 48) reads the
 // BITS dwords of a full group, of which it uses the first 2 BITS bytes (the
-// row stride leaves room for the rest).
+// row stride, tile_stride, covers every dword read; bits read past a
+// segment's codes are discarded).
 template <int BITS, int D, int G>
 __device__ inline void dot_codes(const uint8_t* row, int nd, const float* lut, const float (*q)[D], int j0,
                                  float (&s)[G]) {
@@ -365,11 +378,11 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
     const tq_store& vs = a.d.vstore;
     const StageSrc S[4] = {
         {ktile, 0, ks.codes_hi + (int64_t)row * ks.hi_head_stride + (int64_t)base * a.k_row_hi, a.k_row_hi},
-        {ktile, a.k_row_hi,
+        {ktile, lo_col(a.k_row_hi),
          a.k_row_lo ? ks.codes_lo + (int64_t)row * ks.lo_head_stride + (int64_t)base * a.k_row_lo : nullptr,
          a.k_row_lo},
         {vtile, 0, vs.codes_hi + (int64_t)row * vs.hi_head_stride + (int64_t)base * a.v_row_hi, a.v_row_hi},
-        {vtile, a.v_row_hi,
+        {vtile, lo_col(a.v_row_hi),
          a.v_row_lo ? vs.codes_lo + (int64_t)row * vs.lo_head_stride + (int64_t)base * a.v_row_lo : nullptr,
          a.v_row_lo}};
     stage_rows_multi(S, KR, nvalid);
@@ -403,7 +416,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
     if (packed) {
       const uint8_t* kr = ktile + t * KR;
       dot_codes_bits<D, G>(a.kb_hi, kr, a.ks, klut[0], qv, 0, s);
-      if (a.ks < D) dot_codes_bits<D, G>(a.kb_lo, kr + a.k_row_hi, D - a.ks, klut[1], qv, a.ks, s);
+      if (a.ks < D) dot_codes_bits<D, G>(a.kb_lo, kr + lo_col(a.k_row_hi), D - a.ks, klut[1], qv, a.ks, s);
       const float nk = nk_t;
 #pragma unroll
       for (int h = 0; h < G; ++h) s[h] *= nk;
@@ -537,7 +550,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
         const bool hi = j < a.vs;
         const int bits = hi ? a.vb_hi : a.vb_lo;
         const int jl = hi ? j : j - a.vs;
-        const int off = hi ? 0 : a.v_row_hi;
+        const int off = hi ? 0 : lo_col(a.v_row_hi);
         const float* lut = vlut[hi ? 0 : 1];
         for (int tt = t_lo; tt < t_hi; tt += 4) {
           float cv[4];
@@ -1587,33 +1600,10 @@ static int noalloc_scratch(void** out) {
 
 using namespace tq;
 
-extern "C" {
-
-size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) {
-  if (!kcodec || !d) return 0;
-  int nc, ns, nr;
-  chunk_counts(d, nc, ns, nr);
-  const int D = kcodec->d;
-  const int m = d->qjl ? kcodec->qjl_m : 0;
-  const size_t nch = (size_t)(nc + ns + nr);
-  const size_t heads = (size_t)d->batch * d->hq * (d->n_q > 1 ? d->n_q : 1);  // query rows
-  size_t general = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
-  const size_t fast = d->hkv > 0 && d->hq % d->hkv == 0 ? fast_part_bytes(d) : 0;
-  size_t bytes = general > fast ? general : fast;
-  if (d->qjl && kcodec->d == 128 && kcodec->qjl_m > 0 && kcodec->qjl_m <= 256 && d->max_comp > 0 && d->hkv > 0 &&
-      d->hq % d->hkv == 0) {
-    const size_t qf = qjl_layout(kcodec, d).total;
-    if (qf > bytes) bytes = qf;
-  }
-  if (d->max_comp == 0 && kcodec->d == 128) {
-    const size_t dense = dense_workspace(d);
-    if (dense > bytes) bytes = dense;
-  }
-  return (bytes + 255) & ~(size_t)255;
-}
-
-int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+// The checks every decode-attention entry point runs before it sizes or
+// touches any workspace: codecs, descriptor, head counts, grid limits,
+// segment lengths, pointers, dtypes and the QJL arrays.
+static int check_attention_call(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
   int rc = check_codec(kc);
   if (rc) return rc;
   if ((rc = check_codec(vc))) return rc;
@@ -1651,6 +1641,40 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     if (d->max_comp > 0 && (!d->kstore.signs || !d->kstore.gamma || !d->vstore.signs || !d->vstore.gamma))
       return set_error(TQ_ERR_INVALID, "QJL attention needs stored signs and gamma");
   }
+  return TQ_OK;
+}
+
+extern "C" {
+
+size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) {
+  if (!kcodec || !d) return 0;
+  int nc, ns, nr;
+  chunk_counts(d, nc, ns, nr);
+  const int D = kcodec->d;
+  const int m = d->qjl ? kcodec->qjl_m : 0;
+  const size_t nch = (size_t)(nc + ns + nr);
+  const size_t heads = (size_t)d->batch * d->hq * (d->n_q > 1 ? d->n_q : 1);  // query rows
+  size_t general = heads * D * 4 * 2 + heads * (size_t)m * 4 + heads * nch * part_stride(D, m) * 4;
+  const size_t fast = d->hkv > 0 && d->hq % d->hkv == 0 ? fast_part_bytes(d) : 0;
+  size_t bytes = general > fast ? general : fast;
+  if (d->qjl && kcodec->d == 128 && kcodec->qjl_m > 0 && kcodec->qjl_m <= 256 && d->max_comp > 0 && d->hkv > 0 &&
+      d->hq % d->hkv == 0) {
+    const size_t qf = qjl_layout(kcodec, d).total;
+    if (qf > bytes) bytes = qf;
+  }
+  if (d->max_comp == 0 && kcodec->d == 128) {
+    const size_t dense = dense_workspace(d);
+    if (dense > bytes) bytes = dense;
+  }
+  return (bytes + 255) & ~(size_t)255;
+}
+
+int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  const int rc = check_attention_call(kc, vc, d);
+  if (rc) return rc;
+  const int G = d->hq / d->hkv;
+  const bool qjl = d->qjl != 0;
   const size_t need = tq_decode_workspace_bytes(kc, d);
   if (!workspace || workspace_bytes < need)
     return set_error(TQ_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, need);
@@ -1768,10 +1792,29 @@ int tq_debug_decode_route(const tq_codec* kc, const tq_codec* vc, const tq_attn_
   return 0;
 }
 
+// Test hook, not part of the ABI: the grid of the uniform-batch kernels for a
+// call, without launching anything: out[0..3] = workgroups per (sequence, kv
+// head), compressed 32-token blocks per workgroup, fp16 tokens per workgroup
+// and the blocks-per-wave instantiation (4 or 8) the launch selects. Returns
+// -1 when the uniform-batch grid does not take the call.
+int tq_debug_uniform_geometry(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, int32_t* out) {
+  if (!kc || !vc || !d || !out || d->hkv <= 0 || d->hq % d->hkv) return -1;
+  int nwg, bpw, fpw;
+  if (!uniform_route(vc, d, nwg, bpw, fpw, true)) return -1;
+  out[0] = nwg;
+  out[1] = bpw;
+  out[2] = fpw;
+  out[3] = bpw > FAST_WAVES * 4 ? 8 : 4;  // the selection of launch_u / launch_w
+  return 0;
+}
+
 size_t tq_decode_noalloc_scratch_bytes(void) { return TQ_NOALLOC_SCRATCH_BYTES; }
 
 int tq_decode_attention_noalloc(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* stream) {
-  if (!kc || !d) return set_error(TQ_ERR_INVALID, "codec / attention descriptor is NULL");
+  // the call is validated before its scratch size is computed: a malformed
+  // descriptor gets TQ_ERR_INVALID, not a size error
+  const int vrc = check_attention_call(kc, vc, d);
+  if (vrc) return vrc;
   const size_t need = tq_decode_workspace_bytes(kc, d);
   if (need > TQ_NOALLOC_SCRATCH_BYTES)
     return set_error(TQ_ERR_WORKSPACE, "call needs %zu bytes of scratch; the no-allocation entry point holds %zu",

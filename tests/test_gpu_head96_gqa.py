@@ -94,8 +94,10 @@ def _check(kw, k, v, G, seed, label):
     return c, q, out
 
 
-@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (2, 2), (3.5, 2.5), (4, 4)])
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (2, 2), (3.5, 2.5), (4, 4), (2.5, 2), (2.5, 3.5)])
 def test_d96_attention(kb, vb):
+    """head_dim 96 on the general kernels; K2.5 keys have an 18-byte 3-bit hi
+    segment, so their 2-bit lo segment is staged at the next dword column."""
     k, v = _kv(2, 2, 900, 96, seed=int(kb * 7 + vb))
     kw = dict(head_dim=96, num_kv_heads=2, key_bits=kb, value_bits=vb, residual_window=64, fp16_sink_size=16)
     _check(kw, k, v, 4, 3, f"d96 K{kb}/V{vb}")

@@ -75,6 +75,13 @@ def test_prefill_qjl_d96_gqa3_batch2():
     _prefill(kw, 600, 8, 3, seed=31, B=2)
 
 
+def test_prefill_d96_k25():
+    """head_dim 96 at K2.5 (an 18-byte 3-bit hi segment, the 2-bit lo segment
+    staged at the next dword column) with several query tokens."""
+    kw = dict(head_dim=96, num_kv_heads=2, key_bits=2.5, value_bits=2.5, residual_window=32, fp16_sink_size=8)
+    _prefill(kw, 900, 16, 3, seed=51)
+
+
 def test_prefill_whole_residual_window():
     """Every query in the fp16 residual window and the sink: nothing of the
     chunk is compressed yet (T_kv below the window)."""

@@ -142,11 +142,10 @@ def bench_widths(dev, widths=((3, 2), (2, 2), (3, 3), (4, 3), (4, 4), (3.5, 3.5)
                  warmup: int = 5):
     """configs[1]'s layer shape (T = 32768: sink 128, 32512 packed, window
     128; Hq = 32, Hkv = 8) at the other widths: the integer ones on the
-    uniform-batch MFMA kernels of those widths, a graph of `layers` attend
-    calls (whole call per layer) and of the partials kernel alone (HIP
-    events); the fractional K3.5/V3.5 on the general kernels (whole call
-    only). 12 layers, so the graph's bytes (300-450 MB) exceed the 256 MB
-    last-level cache."""
+    uniform-batch MFMA kernels of those widths, the fractional K3.5/V3.5 on
+    the split-codebook MFMA kernel; a graph of `layers` attend calls (whole
+    call per layer) and of the partials kernel alone (HIP events). 12 layers,
+    so the graph's bytes (300-450 MB) exceed the 256 MB last-level cache."""
     import torch
     from turboquant_amd import TurboQuantKVCache
     res = []
@@ -169,10 +168,11 @@ def bench_widths(dev, widths=((3, 2), (2, 2), (3, 3), (4, 3), (4, 4), (3.5, 3.5)
             for c, q, o in zip(caches, qs, outs):
                 c.attend(q, out=o)
 
-        mfma = float(kb).is_integer() and float(vb).is_integer()
+        frac = not (float(kb).is_integer() and float(vb).is_integer())
+        mfma = True  # every width of the list has a uniform-batch MFMA kernel
         ms, _, _ = time_graph(step, reps if mfma else 5, warmup if mfma else 2)
         byt = decode_bytes_per_layer(caches[0], 32)
-        r = {"key_bits": kb, "value_bits": vb, "route": "uniform_decode_kernel" if mfma else "general (chunk_kernel)",
+        r = {"key_bits": kb, "value_bits": vb, "route": "split_decode_kernel" if frac else "uniform_decode_kernel",
              "bytes_per_layer": byt, "whole_call_us": round(ms * 1e3 / layers, 3),
              "GBps": round(byt / (ms / layers * 1e-3) / 1e9, 1)}
         if mfma:

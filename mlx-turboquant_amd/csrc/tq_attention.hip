@@ -1439,6 +1439,47 @@ static bool widths_eligible(const tq_codec* kc, const tq_codec* vc, const tq_att
   return true;
 }
 
+// The uniform-batch MFMA kernels for fractional widths on both sides
+// (tq_decode_split.h): head_dim 128, both codecs split at dim 64 into
+// ceil(bits) / floor(bits) = 4 / 3 or 3 / 2, fp16 K/V, one query token, no
+// sketch, G in {1, 2, 4, 8}; key code rows read as dword pairs (4-byte
+// aligned), value code rows in 16-byte pieces per 32-token block (16-byte
+// aligned bases and head strides).
+static bool split_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
+  const int G = d->hq / d->hkv;
+  if (d->n_q > 1 || d->qjl) return false;
+  for (const tq_codec* c : {kc, vc})
+    if (!(c->d == 128 && c->split == 64 && (c->bits_hi == 4 || c->bits_hi == 3) && c->bits_lo == c->bits_hi - 1 &&
+          c->centroids_hi && c->centroids_lo))
+      return false;
+  if (!(kc->rotation_parts && vc->rotation)) return false;
+  if (d->kv_dtype != TQ_F16 || !(G == 1 || G == 2 || G == 4 || G == 8)) return false;
+  if (!aligned16(d->q)) return false;
+  auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
+  if (d->max_comp > 0 &&
+      !(al4(d->kstore.codes_hi) && d->kstore.hi_head_stride % 4 == 0 && al4(d->kstore.codes_lo) &&
+        d->kstore.lo_head_stride % 4 == 0 && aligned16(d->vstore.codes_hi) && d->vstore.hi_head_stride % 16 == 0 &&
+        aligned16(d->vstore.codes_lo) && d->vstore.lo_head_stride % 16 == 0 && al4(d->kstore.norms) &&
+        al4(d->vstore.norms)))
+    return false;
+  if (d->max_sink > 0 && !(aligned16(d->sink_k) && aligned16(d->sink_v) && d->sink_head_stride % 8 == 0)) return false;
+  if (d->max_res > 0 && !(aligned16(d->res_k) && aligned16(d->res_v) && d->res_head_stride % 8 == 0)) return false;
+  return true;
+}
+
+// Arguments of the fractional-width kernels: the uniform-batch arguments plus
+// the low-width code rows and the four device codebooks (false when the call
+// is ragged or too long for the uniform grid).
+static bool fill_split(UniformArgs& u, const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part) {
+  if (!fill_uniform(u, kc, vc, d, part)) return false;
+  u.kcl = d->kstore.codes_lo; u.kl_hs = d->kstore.lo_head_stride;
+  u.vcl = d->vstore.codes_lo; u.vl_hs = d->vstore.lo_head_stride;
+  u.kcen_hi = kc->centroids_hi; u.kcen_lo = kc->centroids_lo;
+  u.vcen_hi = vc->centroids_hi; u.vcen_lo = vc->centroids_lo;
+  u.vscale = 1.f;
+  return true;
+}
+
 // The QJL route: S q, key-term bias, K4/V2 partials with the bias
 // (scores stored) + merge (max and sum exported), value term, final S^T add.
 static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace,
@@ -1699,6 +1740,14 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
       return TQ_OK;
     }
   }
+  if (split_eligible(kc, vc, d) && !(d->flags & TQ_ATTN_GENERAL)) {
+    UniformArgs u;
+    if (fill_split(u, kc, vc, d, static_cast<float*>(workspace))) {
+      if (launch_uniform_split(u, d->hq / d->hkv, kc->bits_hi, vc->bits_hi, 1, s) != 0)
+        TQ_LAUNCH_CHECK("tq_decode_attention (fractional widths)");
+      return TQ_OK;
+    }
+  }
 
   AttnArgs a;
   a.d = *d;
@@ -1770,6 +1819,11 @@ int tq_measure_decode_partials(const tq_codec* kc, const tq_codec* vc, const tq_
     return TQ_OK;
   }
   UniformArgs u;
+  if (split_eligible(kc, vc, d) && fill_split(u, kc, vc, d, static_cast<float*>(workspace))) {
+    if (launch_uniform_split(u, d->hq / d->hkv, kc->bits_hi, vc->bits_hi, 0, s) != 0)
+      TQ_LAUNCH_CHECK("measurement partials (fractional widths)");
+    return TQ_OK;
+  }
   if (!widths_eligible(kc, vc, d) || !fill_uniform(u, kc, vc, d, static_cast<float*>(workspace), true))
     return set_error(TQ_ERR_UNSUPPORTED, "measurement: not a packed uniform or K4/V2 call");
   if (launch_uniform_widths(u, d->hq / d->hkv, kc->bits_hi, vc->bits_hi, 0, s) != 0)
@@ -1780,7 +1834,8 @@ int tq_measure_decode_partials(const tq_codec* kc, const tq_codec* vc, const tq_
 // Test hook, not part of the ABI: the route tq_decode_attention takes for a
 // valid call, without launching anything: 0 the general kernel, 1 the dense
 // kernel, 2 the K4/V2 kernels, 3 the K4/V2 kernels with the QJL terms, 4 the
-// uniform-batch kernels of the other integer widths.
+// uniform-batch kernels of the other integer widths, 5 those of the
+// fractional widths.
 int tq_debug_decode_route(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
   if (!kc || !vc || !d || d->hkv <= 0 || d->hq % d->hkv) return -1;
   if (d->flags & TQ_ATTN_GENERAL) return 0;
@@ -1789,6 +1844,7 @@ int tq_debug_decode_route(const tq_codec* kc, const tq_codec* vc, const tq_attn_
   if (fast_eligible(kc, vc, d)) return 2;
   int nwg, bpw, fpw;
   if (widths_eligible(kc, vc, d) && uniform_route(vc, d, nwg, bpw, fpw, true)) return 4;
+  if (split_eligible(kc, vc, d) && uniform_route(vc, d, nwg, bpw, fpw)) return 5;
   return 0;
 }
 

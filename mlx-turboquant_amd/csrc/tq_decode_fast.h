@@ -119,6 +119,12 @@ struct UniformArgs {
   const int32_t* comp_len_b;
   const int32_t* sink_len_b;
   const int32_t* res_len_b;
+  // fractional widths (split codebooks, tq_decode_split.h): the low-width
+  // code rows of keys and values and the four codebooks in device memory
+  const uint8_t* kcl; int64_t kl_hs;
+  const uint8_t* vcl; int64_t vl_hs;
+  const float* kcen_hi; const float* kcen_lo;
+  const float* vcen_hi; const float* vcen_lo;
 };
 // Launches the uniform-batch partials kernel (qb: with the QJL key bias,
 // scores stored) and, when merge != 0, its merge kernel. G in {1, 2, 4, 8};
@@ -127,6 +133,10 @@ int launch_uniform_decode(const UniformArgs& a, int G, bool qb, int merge, hipSt
 // The same kernels for the other integer widths (key bits kb, value bits vb
 // in 2..4, (kb, vb) != (4, 2)), without the QJL term (tq_decode_widths.hip).
 int launch_uniform_widths(const UniformArgs& a, int G, int kb, int vb, int merge, hipStream_t s);
+// The same kernels for fractional widths on both sides (key bits kh / kl and
+// value bits vh / vl: 4 / 3 or 3 / 2, split at dim 64), no QJL term
+// (tq_decode_split.hip).
+int launch_uniform_split(const UniformArgs& a, int G, int kh, int vh, int merge, hipStream_t s);
 
 // Arguments of the dense (fp16 / bf16 K/V) decode-attention kernel: the
 // fp16 segments of tq_attn_desc, head_dim 128.

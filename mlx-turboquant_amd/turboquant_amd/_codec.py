@@ -16,7 +16,7 @@ import torch
 
 from . import _lib
 from .codebook import get_codebook
-from .qjl import get_projection_matrix
+from .qjl import DEFAULT_SEED as QJL_SEED, get_projection_matrix, padded_count
 from .rotation import get_rotation_matrix
 
 
@@ -29,7 +29,7 @@ def split_bits(bits: float, d: int) -> tuple[int, int, int]:
 
 
 class DeviceCodec:
-    def __init__(self, d: int, bits: float, seed: int, qjl_m: int, device: torch.device):
+    def __init__(self, d: int, bits: float, seed: int, qjl_m: int, device: torch.device, qjl_seed: int = QJL_SEED):
         self.d = d
         self.bits = bits
         self.bits_hi, self.bits_lo, self.split = split_bits(bits, d)
@@ -44,18 +44,21 @@ class DeviceCodec:
             hi.view(torch.int16), (self.rotation - hi.float()).half().view(torch.int16)]).contiguous()
         self.c_hi, self.b_hi = get_codebook(d, self.bits_hi, device)
         self.c_lo, self.b_lo = get_codebook(d, self.bits_lo, device)
+        # the sketch's m projections, held as qjl_mp rows (zero rows past m)
         self.qjl_m = qjl_m
-        self.proj = get_projection_matrix(d, qjl_m, device=device) if qjl_m else None
+        self.qjl_mp = padded_count(qjl_m) if qjl_m else 0
+        self.qjl_seed = qjl_seed
+        self.proj = get_projection_matrix(d, qjl_m, qjl_seed, device=device, padded=True) if qjl_m else None
         self.row_hi = self.split * self.bits_hi // 8
         self.row_lo = (d - self.split) * self.bits_lo // 8
-        self.row_sign = qjl_m // 8
+        self.row_sign = self.qjl_mp // 8
         self.struct = _lib.Codec(
             d=d, bits_hi=self.bits_hi, bits_lo=self.bits_lo, split=self.split,
             rotation=self.rotation.data_ptr(), centroids_hi=self.c_hi.data_ptr(),
             boundaries_hi=self.b_hi.data_ptr(), centroids_lo=self.c_lo.data_ptr(),
             boundaries_lo=self.b_lo.data_ptr(),
             qjl_proj=self.proj.data_ptr() if self.proj is not None else None,
-            qjl_m=qjl_m, flags=0, rotation_parts=self.rotation_parts.data_ptr())
+            qjl_m=self.qjl_mp, flags=0, rotation_parts=self.rotation_parts.data_ptr())
         # host-side tables: the codebook by value and, for 2-bit codebooks,
         # its exact fp16 copy (the K4/V2 decode kernels' value table)
         cen = self.c_hi.detach().cpu().numpy().astype("float32")
@@ -102,14 +105,14 @@ def _require_gfx950(dev: torch.device) -> None:
         raise RuntimeError(f"turboquant_amd: {dev} is not a gfx950 (MI355X) device")
 
 
-def get_codec(d: int, bits: float, seed: int, qjl_m: int, device) -> DeviceCodec:
+def get_codec(d: int, bits: float, seed: int, qjl_m: int, device, qjl_seed: int = QJL_SEED) -> DeviceCodec:
     dev = torch.device(device)
     if dev.type == "cuda" and dev.index is None:
         dev = torch.device("cuda", torch.cuda.current_device())
-    key = (d, float(bits), seed, qjl_m, str(dev))
+    key = (d, float(bits), seed, qjl_m, qjl_seed if qjl_m else None, str(dev))
     if key not in _codecs:
         _require_gfx950(dev)
-        _codecs[key] = DeviceCodec(d, bits, seed, qjl_m, dev)
+        _codecs[key] = DeviceCodec(d, bits, seed, qjl_m, dev, qjl_seed)
     return _codecs[key]
 
 

@@ -25,6 +25,7 @@ import numpy as np
 import torch
 
 from . import _codec, _lib
+from .qjl import check_count as check_qjl_count
 from .rotation import DEFAULT_SEED
 
 _workspaces: dict[tuple[str, int], torch.Tensor] = {}
@@ -115,8 +116,8 @@ class TurboQuantKVCache:
         self.chunk_size = chunk_size
         self.qjl_correction = qjl_correction
         self.qjl_n_proj = qjl_n_proj
-        if qjl_correction and (qjl_n_proj % 32 or not 32 <= qjl_n_proj <= 256):
-            raise ValueError(f"qjl_n_proj {qjl_n_proj} must be a multiple of 32 in [32, 256]")
+        if qjl_correction:
+            check_qjl_count(qjl_n_proj)
         _codec.split_bits(key_bits, head_dim)
         _codec.split_bits(value_bits, head_dim)
         self._k_fractional = key_bits != int(key_bits)

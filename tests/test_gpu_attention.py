@@ -50,7 +50,10 @@ def dense_from_gpu_codes(c, o):
             x = O.dequantize(hi.cpu().numpy(), lo, n.cpu().numpy(), o.R, bits, c.head_dim)
             sk = c.sketch(side)
             if sk is not None:
+                # the first m bits: sketches of m projections are held as
+                # whole 32-projection words (zero projection rows past m)
                 signs = np.unpackbits(sk[0].cpu().numpy(), axis=-1, bitorder="little").astype(bool)
+                signs = signs[..., :o.S.shape[0]]
                 x = x + O.qjl_correction(signs, sk[1].cpu().numpy(), o.S, c.head_dim)
             acc.append(x)
     if o.fp16_len:
@@ -159,6 +162,28 @@ def test_attention_qjl_k4v2_route(G, m):
     a = c.attend(to_dev(q)).cpu().numpy()
     b = c.attend(to_dev(q), general_kernel=True).cpu().numpy()
     assert rel_err(a, b) < 1e-4, f"K4/V2 sketch route vs general kernel: {rel_err(a, b):.3e}"
+
+
+@pytest.mark.parametrize("kb,vb,m", [(4, 2, 48), (4, 2, 100), (3, 3, 48), (3.5, 2, 100), (4, 4, 1)])
+def test_attention_qjl_any_projection_count(kb, vb, m):
+    """Sketches of any projection count (the reference takes any qjl_n_proj,
+    cache.py:39, 55; qjl.py:23-36): the codec holds S padded with zero rows to
+    whole 32-projection words, which leaves every correction term unchanged.
+    K4/V2 (the sketch terms around the K4/V2 kernels) and the general kernel,
+    against float64 over the stored codes and the first m sign bits with the
+    reference's (m, d) projection."""
+    k, v = _kv(1, 2, 800, 128, seed=m + int(10 * kb))
+    c, o = build(dict(head_dim=128, num_kv_heads=2, key_bits=kb, value_bits=vb, residual_window=64,
+                      fp16_sink_size=16, qjl_correction=True, qjl_n_proj=m), k, v)
+    assert o.S.shape == (m, 128)
+    q = np.random.RandomState(m).randn(1, 8, 1, 128).astype(np.float16)
+    check(c, o, q, f"qjl K{kb}/V{vb} m={m}")
+    a = c.attend(to_dev(q)).cpu().numpy()
+    b = c.attend(to_dev(q), general_kernel=True).cpu().numpy()
+    assert rel_err(a, b) < 1e-4
+    kd, vd = c.fetch()  # the dequantised cache with the correction (kernels' own path)
+    kk, vv = dense_from_gpu_codes(c, o)
+    assert rel_err(kd.cpu().numpy(), kk) < 1e-5 and rel_err(vd.cpu().numpy(), vv) < 1e-5
 
 
 def test_attention_float32_inputs_and_scale():

@@ -98,11 +98,13 @@ def test_mse_identical_and_batch_vs_single():
         assert torch.equal(tq.dequantize(qs), xb[i])
 
 
-@pytest.mark.parametrize("bits,m", [(4, 128), (3, 64), (2, 128), (4, 256)])
-def test_prod_parity(bits, m):
+@pytest.mark.parametrize("bits,m,seed", [(4, 128, 12345), (3, 64, 12345), (2, 128, 12345), (4, 256, 12345),
+                                         (4, 48, 12345), (3, 100, 12345), (4, 128, 7), (2, 17, 2024)])
+def test_prod_parity(bits, m, seed):
+    """Any qjl_dim in [1, 256] and any qjl_seed (quantizer.py:122-139)."""
     from turboquant_amd import TurboQuantProd
     x = np.random.RandomState(bits + m).randn(6, 40, 128).astype(np.float32)
-    tq = TurboQuantProd(128, bits=bits, qjl_dim=m)
+    tq = TurboQuantProd(128, bits=bits, qjl_dim=m, qjl_seed=seed)
     qt = tq.quantize(to_dev(x))
     assert qt.qjl_signs.shape == (6, 40, m) and qt.qjl_norms.shape == (6, 40)
     n = 240
@@ -110,7 +112,7 @@ def test_prod_parity(bits, m):
     nrm = qt.norms.reshape(n).cpu().numpy()
     _, outside, _, _, norms_eq, _ = code_parity(x.reshape(n, 128), bits - 1, gpu=(ch, None, nrm, None, None))
     assert norms_eq and outside == 0
-    S = O.projection_matrix(128, m)
+    S = O.projection_matrix(128, m, seed)
     deq = O.dequantize(ch, None, nrm, _R(), bits - 1, 128)
     r = x.reshape(n, 128).astype(np.float64) - deq
     s_ref, g_ref, proj = O.qjl_sketch(r, S)

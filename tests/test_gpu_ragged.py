@@ -97,7 +97,7 @@ def dense64(rb, b):
             x = O.dequantize(hi, lo, store.norms[b:b + 1, :, :C].cpu().numpy(), R, codec.bits, D)
             if rb.qjl:
                 signs = np.unpackbits(store.signs[b:b + 1, :, :C].cpu().numpy(), axis=-1,
-                                      bitorder="little").astype(bool)
+                                      bitorder="little").astype(bool)[..., :S.shape[0]]
                 x = x + O.qjl_correction(signs, store.gamma[b:b + 1, :, :C].cpu().numpy(), S, D)
             segs.append(x)
         segs.append(ring[b:b + 1][:, :, slots].cpu().numpy().astype(np.float64))

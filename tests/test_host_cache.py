@@ -176,3 +176,28 @@ def test_state_shapes_and_errors():
     for n in (5, 7, 9, 11):
         with pytest.raises(ValueError):
             c.state = (None,) * n
+
+
+def test_qjl_projection_any_count_and_seed():
+    """Any projection count in [1, 256] and any seed: the codec's S is the
+    reference's RandomState(seed).randn(m, d) (qjl.py:23-36) padded with zero
+    rows to whole 32-projection words; a zero row contributes nothing to the
+    correction (its sign is +1 but it multiplies a zero row) nor to S q."""
+    from turboquant_amd import TurboQuantKVCache, qjl
+    rng = np.random.RandomState(3)
+    for m, seed in ((1, 12345), (17, 7), (32, 12345), (48, 12345), (100, 2024), (256, 12345)):
+        S = qjl.get_projection_matrix(128, m, seed, device="cpu", padded=True).numpy()
+        mp = qjl.padded_count(m)
+        assert S.shape == (mp, 128) and mp % 32 == 0 and mp - m < 32
+        assert np.array_equal(S[:m], O.projection_matrix(128, m, seed))
+        assert not S[m:].any()
+        r = rng.randn(5, 128)
+        s_pad, g_pad, _ = O.qjl_sketch(r, S)
+        s_ref, g_ref, _ = O.qjl_sketch(r, S[:m])
+        assert np.array_equal(s_pad[:, :m], s_ref) and s_pad[:, m:].all() and np.array_equal(g_pad, g_ref)
+        assert np.allclose(O.qjl_correction(s_pad, g_pad, S, 128), O.qjl_correction(s_ref, g_ref, S[:m], 128),
+                           rtol=0, atol=1e-12)
+        TurboQuantKVCache(head_dim=128, qjl_correction=True, qjl_n_proj=m)  # accepted
+    for bad in (0, 257, -3, 2.5):
+        with pytest.raises(ValueError):
+            TurboQuantKVCache(head_dim=128, qjl_correction=True, qjl_n_proj=bad)

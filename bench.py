@@ -138,7 +138,8 @@ def bench_layer_batched(dev, layers: int, ctx: int, reps: int, warmup: int):
             "kernel": "uniform_decode_kernel<4> + uniform_merge_kernel<4>, batch = layers"}
 
 
-def bench_widths(dev, widths=((3, 2), (2, 2), (3, 3), (4, 3), (4, 4), (3.5, 3.5)), layers: int = 12, reps: int = 20,
+def bench_widths(dev, widths=((3, 2), (2, 2), (3, 3), (4, 3), (4, 4), (3.5, 3.5), (3.5, 2), (2.5, 2.5)), layers: int = 12,
+                 reps: int = 20,
                  warmup: int = 5):
     """configs[1]'s layer shape (T = 32768: sink 128, 32512 packed, window
     128; Hq = 32, Hkv = 8) at the other widths: the integer ones on the

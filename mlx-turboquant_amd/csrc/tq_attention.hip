@@ -1439,27 +1439,38 @@ static bool widths_eligible(const tq_codec* kc, const tq_codec* vc, const tq_att
   return true;
 }
 
-// The uniform-batch MFMA kernels for fractional widths on both sides
-// (tq_decode_split.h): head_dim 128, both codecs split at dim 64 into
-// ceil(bits) / floor(bits) = 4 / 3 or 3 / 2, fp16 K/V, one query token, no
-// sketch, G in {1, 2, 4, 8}; key code rows read as dword pairs (4-byte
-// aligned), value code rows in 16-byte pieces per 32-token block (16-byte
-// aligned bases and head strides).
+// Width kind of a codec for the split-codebook kernels: bits_hi + bits_lo of a
+// fractional codec split at dim 64 (7 = 3.5 bits, 5 = 2.5), the bits of an
+// integer one (2 to 4), or 0 when the kernels do not take it.
+static int split_kind(const tq_codec* c) {
+  if (c->d != 128 || !c->centroids_hi || !c->centroids_lo) return 0;
+  if (c->split == 64 && (c->bits_hi == 4 || c->bits_hi == 3) && c->bits_lo == c->bits_hi - 1)
+    return c->bits_hi + c->bits_lo;
+  if (c->split == 128 && c->bits_hi >= 2 && c->bits_hi <= 4) return c->bits_hi;
+  return 0;
+}
+
+// The uniform-batch MFMA kernels for fractional widths (tq_decode_split.h):
+// head_dim 128, a codec split at dim 64 into ceil(bits) / floor(bits) = 4 / 3
+// or 3 / 2 on at least one side (the other fractional or integer 2-4 bits),
+// fp16 K/V, one query token, no sketch, G in {1, 2, 4, 8}; key code rows read
+// as dword pairs (4-byte aligned), value code rows in 16-byte pieces per
+// 32-token block (16-byte aligned bases and head strides).
 static bool split_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
   const int G = d->hq / d->hkv;
   if (d->n_q > 1 || d->qjl) return false;
-  for (const tq_codec* c : {kc, vc})
-    if (!(c->d == 128 && c->split == 64 && (c->bits_hi == 4 || c->bits_hi == 3) && c->bits_lo == c->bits_hi - 1 &&
-          c->centroids_hi && c->centroids_lo))
-      return false;
+  const int kk = split_kind(kc), vk = split_kind(vc);
+  if (!kk || !vk || (kk <= 4 && vk <= 4)) return false;  // both integer: the widths kernels
   if (!(kc->rotation_parts && vc->rotation)) return false;
   if (d->kv_dtype != TQ_F16 || !(G == 1 || G == 2 || G == 4 || G == 8)) return false;
   if (!aligned16(d->q)) return false;
   auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
+  const bool kf = kk > 4, vf = vk > 4;  // fractional sides have a lo code row
   if (d->max_comp > 0 &&
-      !(al4(d->kstore.codes_hi) && d->kstore.hi_head_stride % 4 == 0 && al4(d->kstore.codes_lo) &&
-        d->kstore.lo_head_stride % 4 == 0 && aligned16(d->vstore.codes_hi) && d->vstore.hi_head_stride % 16 == 0 &&
-        aligned16(d->vstore.codes_lo) && d->vstore.lo_head_stride % 16 == 0 && al4(d->kstore.norms) &&
+      !(al4(d->kstore.codes_hi) && d->kstore.hi_head_stride % 4 == 0 &&
+        (!kf || (al4(d->kstore.codes_lo) && d->kstore.lo_head_stride % 4 == 0)) && aligned16(d->vstore.codes_hi) &&
+        d->vstore.hi_head_stride % 16 == 0 &&
+        (!vf || (aligned16(d->vstore.codes_lo) && d->vstore.lo_head_stride % 16 == 0)) && al4(d->kstore.norms) &&
         al4(d->vstore.norms)))
     return false;
   if (d->max_sink > 0 && !(aligned16(d->sink_k) && aligned16(d->sink_v) && d->sink_head_stride % 8 == 0)) return false;
@@ -1743,7 +1754,7 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   if (split_eligible(kc, vc, d) && !(d->flags & TQ_ATTN_GENERAL)) {
     UniformArgs u;
     if (fill_split(u, kc, vc, d, static_cast<float*>(workspace))) {
-      if (launch_uniform_split(u, d->hq / d->hkv, kc->bits_hi, vc->bits_hi, 1, s) != 0)
+      if (launch_uniform_split(u, d->hq / d->hkv, split_kind(kc), split_kind(vc), 1, s) != 0)
         TQ_LAUNCH_CHECK("tq_decode_attention (fractional widths)");
       return TQ_OK;
     }
@@ -1820,7 +1831,7 @@ int tq_measure_decode_partials(const tq_codec* kc, const tq_codec* vc, const tq_
   }
   UniformArgs u;
   if (split_eligible(kc, vc, d) && fill_split(u, kc, vc, d, static_cast<float*>(workspace))) {
-    if (launch_uniform_split(u, d->hq / d->hkv, kc->bits_hi, vc->bits_hi, 0, s) != 0)
+    if (launch_uniform_split(u, d->hq / d->hkv, split_kind(kc), split_kind(vc), 0, s) != 0)
       TQ_LAUNCH_CHECK("measurement partials (fractional widths)");
     return TQ_OK;
   }

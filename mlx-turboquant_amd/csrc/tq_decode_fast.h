@@ -133,10 +133,11 @@ int launch_uniform_decode(const UniformArgs& a, int G, bool qb, int merge, hipSt
 // The same kernels for the other integer widths (key bits kb, value bits vb
 // in 2..4, (kb, vb) != (4, 2)), without the QJL term (tq_decode_widths.hip).
 int launch_uniform_widths(const UniformArgs& a, int G, int kb, int vb, int merge, hipStream_t s);
-// The same kernels for fractional widths on both sides (key bits kh / kl and
-// value bits vh / vl: 4 / 3 or 3 / 2, split at dim 64), no QJL term
-// (tq_decode_split.hip).
-int launch_uniform_split(const UniformArgs& a, int G, int kh, int vh, int merge, hipStream_t s);
+// The split-codebook kernels (tq_decode_split.h): fractional widths (3.5 =
+// 4 / 3 bits, 2.5 = 3 / 2, split at dim 64) on at least one side, the other
+// side fractional or integer; no QJL term. A width kind is bits_hi + bits_lo
+// of a fractional codec (7 or 5) or the bits of an integer one (2 to 4).
+int launch_uniform_split(const UniformArgs& a, int G, int kkind, int vkind, int merge, hipStream_t s);
 
 // Arguments of the dense (fp16 / bf16 K/V) decode-attention kernel: the
 // fp16 segments of tq_attn_desc, head_dim 128.

@@ -25,6 +25,9 @@
 //    (128-byte rows; 80 KB at K3.5 / V3.5) and are built from the codecs'
 //    float32 centroids in device memory (fp16 high part / remainder split in
 //    the kernel, one lane per centroid, rows assembled with ds_bpermute).
+// A side may also be integer (KI / VI: one codebook, the code row of 16 W
+// bytes holds both segments, the lo one from byte 8 W), so that a
+// fractional width on one side pairs with an integer width on the other.
 // Partials are in the uniform kernel's format; uniform_merge_kernel merges
 // them (value scale 1).
 #pragma once
@@ -37,17 +40,22 @@ namespace uk {
 // LDS of the split kernel below the combine headers (Layout::cml): the pair
 // tables (16 replicas of 8 bytes per row) and each wave's value-code staging
 // (a block's hi rows, then its lo rows)
-template <int KH, int KL, int VH, int VL>
+template <int KH, int KL, int VH, int VL, bool KI, bool VI>
 struct SplitLds {
   static constexpr uint32_t RB = 128;  // bytes per table row
   static constexpr uint32_t vht = 0;
-  static constexpr uint32_t vlt = vht + (RB << (2 * VH));
-  static constexpr uint32_t kht = vlt + (RB << (2 * VL));
-  static constexpr uint32_t klt = kht + (RB << (2 * KH));
+  static constexpr uint32_t vlt = VI ? vht : vht + (RB << (2 * VH));  // an integer side has one table
+  static constexpr uint32_t kht = vlt + (VI ? (RB << (2 * VH)) : (RB << (2 * VL)));
+  static constexpr uint32_t klt = KI ? kht : kht + (RB << (2 * KH));
   static constexpr uint32_t vst = klt + (RB << (2 * KL));
-  static constexpr uint32_t VHB = 32 * 8 * VH;  // a block's hi value rows (32 tokens x 8 VH bytes)
-  static constexpr uint32_t VLB = 32 * 8 * VL;
+  // a block's value rows in the wave's staging area: hi rows (32 tokens x 8 VH
+  // bytes) then lo rows, or (integer) the 32 rows of 16 VH bytes as they are
+  static constexpr uint32_t VHB = VI ? 32 * 16 * VH : 32 * 8 * VH;
+  static constexpr uint32_t VLB = VI ? 0 : 32 * 8 * VL;
   static constexpr uint32_t VSTW = VHB + VLB;   // per wave
+  // staged row stride and the offset of the lo segment of token t's codes
+  static constexpr uint32_t VRH = VI ? 16 * VH : 8 * VH, VRL = VI ? 16 * VH : 8 * VL;
+  static constexpr uint32_t VLO = VI ? 8 * VH : VHB;
   static constexpr uint32_t end = vst + FW * VSTW;
   static_assert(end <= Layout::cml, "tables and staging below the combine headers");
   static_assert(FW * 8 * CMS * 4 <= Layout::cml, "combine buffers alias the table region");
@@ -87,11 +95,11 @@ struct SBlk {
   float nk, nv;     // key / value norm of token t0 + (lane & 31)
 };
 
-template <int G, int NPW, int KH, int KL, int VH, int VL>
+template <int G, int NPW, int KH, int KL, int VH, int VL, bool KI, bool VI>
 __global__ __launch_bounds__(FT) void split_decode_kernel(UniformArgs a) {
   static_assert(KH >= 2 && KH <= 4 && KL >= 2 && KL <= 4 && VH >= 2 && VH <= 4 && VL >= 2 && VL <= 4, "widths 2-4");
-  static_assert(KL <= 3 && VL <= 3, "the low-width codebooks fit 8 lanes");
-  using SL = SplitLds<KH, KL, VH, VL>;
+  static_assert((!KI || KH == KL) && (!VI || VH == VL), "an integer side has one width");
+  using SL = SplitLds<KH, KL, VH, VL, KI, VI>;
   __shared__ __align__(16) uint8_t smem[Layout::total];
 
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
@@ -110,8 +118,8 @@ __global__ __launch_bounds__(FT) void split_decode_kernel(UniformArgs a) {
   const bool writer = !lo_part && c8 < G;
 
   // the codebooks first, one centroid per lane (keys hi: lanes 0-15, keys lo:
-  // 16-23, values hi: 32-47, values lo: 48-55), so they are the first loads
-  // to return
+  // 16-31, values hi: 32-47, values lo: 48-63; an integer side's lo codebook is
+  // its hi one), so they are the first loads to return
   float cen;
   {
     const int i = lane & 15, grp = lane >> 4;
@@ -166,8 +174,9 @@ __global__ __launch_bounds__(FT) void split_decode_kernel(UniformArgs a) {
   // ---- block loads: buffers over the tokens [t0, comp) of the row (bytes
   // past the sequence read as zero; slots past the wave's blocks re-read
   // block 0 and are masked)
+  // an integer side reads its lo segment from the same row, 8 W bytes in
   const uint8_t* kch = a.kc + (int64_t)row * a.k_hs;
-  const uint8_t* kcl = a.kcl + (int64_t)row * a.kl_hs;
+  const uint8_t* kcl = KI ? kch + 8 * KH : a.kcl + (int64_t)row * a.kl_hs;
   const uint8_t* vch = a.vc + (int64_t)row * a.v_hs;
   const uint8_t* vcl = a.vcl + (int64_t)row * a.vl_hs;
   const float* knorm = a.kn + (int64_t)row * a.kn_hs;
@@ -176,32 +185,34 @@ __global__ __launch_bounds__(FT) void split_decode_kernel(UniformArgs a) {
     const int blk = blk0 + w + FW * k;
     return blk < blk1 ? blk << 5 : 0;
   };
-  // key segment of width W of token `tok`: 16 W bits at bit 16 W q4 of a
-  // row of 8 W bytes, loaded as two dwords from a dword-aligned offset
-  // (3 bits: the segment starts 16 bits into the first dword for odd q4)
-  constexpr int RKH = 8 * KH, RKL = 8 * KL;
-  auto koff = [&](int W, int tok) { return tok * 8 * W + (W == 3 ? 4 * ((6 * q4) >> 2) : 2 * W * q4); };
+  // key segment of width W of token `tok`: 16 W bits at bit 16 W q4 of the
+  // segment (rows of RK bytes), loaded as two dwords from a dword-aligned
+  // offset (3 bits: the segment starts 16 bits into the first dword for odd q4)
+  constexpr int RKH = KI ? 16 * KH : 8 * KH, RKL = KI ? 16 * KH : 8 * KL;
+  auto koff = [&](int W, int RK, int tok) { return tok * RK + (W == 3 ? 4 * ((6 * q4) >> 2) : 2 * W * q4); };
   const int no = (lane & 31) * 4;
   SBlk B[NPW];
-  auto kload = [&](__amdgpu_buffer_rsrc_t rk, int W, int tok) -> u2 {
-    if (W == 2) return u2{__builtin_amdgcn_raw_buffer_load_b32(rk, koff(W, tok), 0, 0), 0u};
-    return __builtin_amdgcn_raw_buffer_load_b64(rk, koff(W, tok), 0, 0);
+  auto kload = [&](__amdgpu_buffer_rsrc_t rk, int W, int RK, int tok) -> u2 {
+    if (W == 2) return u2{__builtin_amdgcn_raw_buffer_load_b32(rk, koff(W, RK, tok), 0, 0), 0u};
+    return __builtin_amdgcn_raw_buffer_load_b64(rk, koff(W, RK, tok), 0, 0);
   };
   auto load_slot = [&](int k) {
     const int t0 = slot_t0(k);
     const int n = comp - t0;
     const __amdgpu_buffer_rsrc_t rkh = rsrc(kch + (int64_t)t0 * RKH, n * RKH);
     const __amdgpu_buffer_rsrc_t rkl = rsrc(kcl + (int64_t)t0 * RKL, n * RKL);
-    const __amdgpu_buffer_rsrc_t rvh = rsrc(vch + (int64_t)t0 * (8 * VH), n * 8 * VH);
-    const __amdgpu_buffer_rsrc_t rvl = rsrc(vcl + (int64_t)t0 * (8 * VL), n * 8 * VL);
+    const __amdgpu_buffer_rsrc_t rvh = rsrc(vch + (int64_t)t0 * SL::VRH, n * SL::VRH);
+    const __amdgpu_buffer_rsrc_t rvl = VI ? rvh : rsrc(vcl + (int64_t)t0 * (8 * VL), n * 8 * VL);
     const __amdgpu_buffer_rsrc_t rkn = rsrc(knorm + t0, n * 4);
     const __amdgpu_buffer_rsrc_t rvn = rsrc(vnorm + t0, n * 4);
-    B[k].kh[0] = kload(rkh, KH, r);
-    B[k].kh[1] = kload(rkh, KH, 16 + r);
-    B[k].kl[0] = kload(rkl, KL, r);
-    B[k].kl[1] = kload(rkl, KL, 16 + r);
+    B[k].kh[0] = kload(rkh, KH, RKH, r);
+    B[k].kh[1] = kload(rkh, KH, RKH, 16 + r);
+    B[k].kl[0] = kload(rkl, KL, RKL, r);
+    B[k].kl[1] = kload(rkl, KL, RKL, 16 + r);
+    // the block's value bytes: [16 lane, + 16) of the hi rows and of the lo
+    // rows, or (integer) [16 lane, + 16) and [1024 + 16 lane, + 16) of its rows
     B[k].vh = __builtin_amdgcn_raw_buffer_load_b128(rvh, 16 * lane, 0, 0);
-    B[k].vl = __builtin_amdgcn_raw_buffer_load_b128(rvl, 16 * lane, 0, 0);
+    if constexpr (!VI || SL::VHB > 1024) B[k].vl = __builtin_amdgcn_raw_buffer_load_b128(rvl, (VI ? 1024 : 0) + 16 * lane, 0, 0);
     B[k].nk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rkn, no, 0, 0));
     B[k].nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvn, no, 0, 0));
   };
@@ -214,9 +225,9 @@ __global__ __launch_bounds__(FT) void split_decode_kernel(UniformArgs a) {
     const uint32_t cw = (uint32_t)__builtin_bit_cast(uint16_t, h) |
                         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(cen - (float)h)) << 16);
     pair_table16<KH>(smem + SL::kht, tid, cw, 0);
-    pair_table16<KL>(smem + SL::klt, tid, cw, 16);
+    if constexpr (!KI) pair_table16<KL>(smem + SL::klt, tid, cw, 16);
     pair_table16<VH>(smem + SL::vht, tid, cw, 32);
-    pair_table16<VL>(smem + SL::vlt, tid, cw, 48);
+    if constexpr (!VI) pair_table16<VL>(smem + SL::vlt, tid, cw, 48);
   }
   if (tid < qchunks) *reinterpret_cast<u4*>(smem + Layout::qst + 16 * tid) = qld;
   *reinterpret_cast<u4*>(smem + Layout::f16s + (tid >> 5) * (2 * FROW) + ((tid >> 4) & 1) * FROW + 16 * (tid & 15)) = fst;
@@ -477,9 +488,9 @@ __global__ __launch_bounds__(FT) void split_decode_kernel(UniformArgs a) {
   // table address of a field value x (2 W bits) of table T
   auto taddr = [&](uint32_t T, uint32_t x) { return T + ((x << 7) | cp); };
   // the lane's 4 W value bits of token tt from the staged rows of width W
-  // (row bytes 8 W) at `base`: dims 4 r .. 4 r + 3 of the segment
-  auto vcode = [&](const uint8_t* base, int W, int tt) -> uint32_t {
-    const uint8_t* p = base + tt * 8 * W;
+  // (row stride RV) at `base`: dims 4 r .. 4 r + 3 of the segment
+  auto vcode = [&](const uint8_t* base, int W, int RV, int tt) -> uint32_t {
+    const uint8_t* p = base + tt * RV;
     if (W == 4) return *reinterpret_cast<const uint16_t*>(p + 2 * r);
     if (W == 2) return p[r];
     const uint32_t* dw = reinterpret_cast<const uint32_t*>(p) + ((12 * r) >> 5);  // 3 bits: 12 r .. 12 r + 11
@@ -493,9 +504,15 @@ __global__ __launch_bounds__(FT) void split_decode_kernel(UniformArgs a) {
     const int t0 = slot_t0(k);
     const int tend = blk0 + w + FW * k < blk1 ? comp : 0;
     *reinterpret_cast<float*>(nst + 4 * lane) = lane < 32 ? L.nk : L.nv;
-    // the block's value rows: hi rows then lo rows (lanes past each part store nothing)
-    if (16 * lane < (int)SL::VHB) *reinterpret_cast<u4*>(vst + 16 * lane) = L.vh;
-    if (16 * lane < (int)SL::VLB) *reinterpret_cast<u4*>(vst + SL::VHB + 16 * lane) = L.vl;
+    // the block's value rows: hi rows then lo rows, or the integer rows (lanes
+    // past each part store nothing)
+    if constexpr (VI) {
+      if (16 * lane < (int)SL::VHB) *reinterpret_cast<u4*>(vst + 16 * lane) = L.vh;
+      if (1024 + 16 * lane < (int)SL::VHB) *reinterpret_cast<u4*>(vst + 1024 + 16 * lane) = L.vl;
+    } else {
+      if (16 * lane < (int)SL::VHB) *reinterpret_cast<u4*>(vst + 16 * lane) = L.vh;
+      if (16 * lane < (int)SL::VLB) *reinterpret_cast<u4*>(vst + SL::VHB + 16 * lane) = L.vl;
+    }
     float nk[NS], nv[NS];
 #pragma unroll
     for (int t = 0; t < 2 / TS; ++t) {
@@ -568,8 +585,8 @@ __global__ __launch_bounds__(FT) void split_decode_kernel(UniformArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int tx = j < 2 ? 4 * q4 + 2 * j : 16 + 4 * q4 + 2 * (j - 2);
-      const uint32_t hx = vcode(vst, VH, tx), hy = vcode(vst, VH, tx + 1);
-      const uint32_t lx = vcode(vst + SL::VHB, VL, tx), ly = vcode(vst + SL::VHB, VL, tx + 1);
+      const uint32_t hx = vcode(vst, VH, SL::VRH, tx), hy = vcode(vst, VH, SL::VRH, tx + 1);
+      const uint32_t lx = vcode(vst + SL::VLO, VL, SL::VRL, tx), ly = vcode(vst + SL::VLO, VL, SL::VRL, tx + 1);
       u2 ex[4], ey[4];
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
@@ -658,4 +675,57 @@ __global__ __launch_bounds__(FT) void split_decode_kernel(UniformArgs a) {
 }
 
 }  // namespace uk
+}  // namespace tq
+
+namespace tq {
+
+// Host side: launch the split kernel (+ merge) for one (key, value) width
+// pair; a side is (H, L, I): hi / lo bits and whether it is integer.
+template <int G, int KH, int KL, bool KI, int VH, int VL, bool VI>
+inline void launch_split_g(const UniformArgs& a, int merge, hipStream_t s) {
+  if (a.bpw > FAST_WAVES * 4)
+    hipLaunchKernelGGL((uk::split_decode_kernel<G, 8, KH, KL, VH, VL, KI, VI>), dim3(a.nwg, a.hkv, a.batch),
+                       dim3(uk::FT), 0, s, a);
+  else
+    hipLaunchKernelGGL((uk::split_decode_kernel<G, 4, KH, KL, VH, VL, KI, VI>), dim3(a.nwg, a.hkv, a.batch),
+                       dim3(uk::FT), 0, s, a);
+  if (merge) hipLaunchKernelGGL((uk::uniform_merge_kernel<G>), dim3(a.hq, a.batch), dim3(uk::MT), 0, s, a);
+}
+
+template <int KH, int KL, bool KI, int VH, int VL, bool VI>
+inline int launch_split_kv(const UniformArgs& a, int G, int merge, hipStream_t s) {
+  switch (G) {
+    case 1: launch_split_g<1, KH, KL, KI, VH, VL, VI>(a, merge, s); break;
+    case 2: launch_split_g<2, KH, KL, KI, VH, VL, VI>(a, merge, s); break;
+    case 4: launch_split_g<4, KH, KL, KI, VH, VL, VI>(a, merge, s); break;
+    case 8: launch_split_g<8, KH, KL, KI, VH, VL, VI>(a, merge, s); break;
+    default: return -1;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// width kinds of one side: 7 = 3.5 bits (4 / 3), 5 = 2.5 (3 / 2), 2 / 3 / 4 integer
+template <int KH, int KL, bool KI>
+inline int launch_split_v(const UniformArgs& a, int G, int vkind, int merge, hipStream_t s) {
+  switch (vkind) {
+    case 7: return launch_split_kv<KH, KL, KI, 4, 3, false>(a, G, merge, s);
+    case 5: return launch_split_kv<KH, KL, KI, 3, 2, false>(a, G, merge, s);
+    default: break;
+  }
+  if constexpr (!KI) {  // integer values with fractional keys only
+    switch (vkind) {
+      case 2: return launch_split_kv<KH, KL, KI, 2, 2, true>(a, G, merge, s);
+      case 3: return launch_split_kv<KH, KL, KI, 3, 3, true>(a, G, merge, s);
+      case 4: return launch_split_kv<KH, KL, KI, 4, 4, true>(a, G, merge, s);
+      default: break;
+    }
+  }
+  return -1;
+}
+
+// one per key kind, each in its own translation unit (tq_decode_split*.hip)
+int launch_split_k7(const UniformArgs& a, int G, int vkind, int merge, hipStream_t s);
+int launch_split_k5(const UniformArgs& a, int G, int vkind, int merge, hipStream_t s);
+int launch_split_ki(const UniformArgs& a, int G, int kkind, int vkind, int merge, hipStream_t s);
+
 }  // namespace tq

@@ -384,14 +384,15 @@ def test_uniform_widths_match_oracle(kb, vb, G, T, sink, window):
 
 
 def test_uniform_widths_route_limits():
-    """K4/V2 keeps its own kernels; QJL sketches and fractional widths of
-    the other widths take the general kernel (ragged batches of the other
-    widths: test_gpu_ragged.py::test_ragged_other_widths)."""
+    """K4/V2 keeps its own kernels; QJL sketches of the other widths take the
+    general kernel; a fractional width takes the split-codebook kernels
+    (test_gpu_split.py; ragged batches of the other widths:
+    test_gpu_ragged.py::test_ragged_other_widths)."""
     k, v = _kv(1, 2, 900, 128, seed=5)
     q = to_dev(np.random.RandomState(6).randn(1, 8, 1, 128).astype(np.float16))
     for kw, route in ((dict(key_bits=4, value_bits=2), 2), (dict(key_bits=3, value_bits=3), 4),
                       (dict(key_bits=3, value_bits=3, qjl_correction=True, qjl_n_proj=64), 0),
-                      (dict(key_bits=3.5, value_bits=2), 0)):
+                      (dict(key_bits=3.5, value_bits=2), 5)):
         c, _ = build(dict(head_dim=128, num_kv_heads=2, residual_window=64, fp16_sink_size=16, **kw), k, v)
         assert decode_route(c, q) == route, kw
 

@@ -89,13 +89,29 @@ def test_split_large_values_and_small_queries():
     assert rel_err(fast, O.attention(q, kk, vv)) < FAST_REL_TOL
 
 
+MIXED = [(3.5, 2), (3.5, 3), (3.5, 4), (2.5, 2), (2.5, 4), (4, 3.5), (3, 3.5), (2, 3.5), (4, 2.5), (2, 2.5)]
+
+
+@pytest.mark.parametrize("kb,vb", MIXED, ids=[f"K{k}V{v}" for k, v in MIXED])
+@pytest.mark.parametrize("G,T", [(4, 3000), (1, 700), (8, 1500)])
+def test_split_mixed_integer_side(kb, vb, G, T):
+    """A fractional width on one side, an integer width (one codebook, one
+    row per token, the lo segment from byte 8 W) on the other."""
+    k, v = _kv(1, 2, T, 128, seed=int(T + 10 * kb + vb + G))
+    c, o = build(dict(head_dim=128, num_kv_heads=2, key_bits=kb, value_bits=vb, residual_window=64,
+                      fp16_sink_size=16), k, v)
+    q = np.random.RandomState(int(kb * 8 + vb + G)).randn(1, 2 * G, 1, 128).astype(np.float16)
+    _check(c, o, q, f"K{kb}/V{vb} G={G} T={T}")
+
+
 def test_split_route_limits():
-    """Integer widths keep their kernels; a sketch or a fractional width on
-    one side only takes the general kernel."""
+    """Integer widths on both sides keep their kernels; a sketch takes the
+    general kernel."""
     k, v = _kv(1, 2, 900, 128, seed=5)
     q = to_dev(np.random.RandomState(6).randn(1, 8, 1, 128).astype(np.float16))
     for kw, route in ((dict(key_bits=3.5, value_bits=3.5), 5), (dict(key_bits=3, value_bits=3), 4),
-                      (dict(key_bits=3.5, value_bits=2), 0), (dict(key_bits=4, value_bits=2.5), 0),
+                      (dict(key_bits=3.5, value_bits=2), 5), (dict(key_bits=4, value_bits=2.5), 5),
+                      (dict(key_bits=4, value_bits=2), 2),
                       (dict(key_bits=3.5, value_bits=3.5, qjl_correction=True, qjl_n_proj=64), 0)):
         c, _ = build(dict(head_dim=128, num_kv_heads=2, residual_window=64, fp16_sink_size=16, **kw), k, v)
         assert decode_route(c, q) == route, kw

@@ -43,6 +43,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "mlx-turboquant_amd")]
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA peak of one MI355X (no sparsity)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "uniform_decode_kernel_k4v2_32k_traffic.md")
 METRIC = "fused decode-attn GB/s over packed KV (% HBM peak) + compress vectors/s"
 
@@ -183,6 +184,56 @@ def bench_widths(dev, widths=((3, 2), (2, 2), (3, 3), (4, 3), (4, 4), (3.5, 3.5)
         res.append(r)
         del caches, qs, outs
         torch.cuda.empty_cache()
+    return res
+
+
+def bench_prefill(dev, ctx: int = 32768, n_qs=(128, 1024), reps: int = 10, warmup: int = 3):
+    """Prefill attention at configs[1]'s layer shape (K4/V2, Hq 32, Hkv 8,
+    D 128, sink 128, window 128): the cache's last n_q tokens attend causally
+    over all ctx tokens (cache.py:722-724), on the query-tiled MFMA kernels
+    (preparation + partials + merge, one attend call, in a graph). FLOPs are
+    the algorithmic 4 * D per visible (query head, key) pair (QK^T and PV);
+    the fraction is against the dense fp16 MFMA peak. One call of the general
+    kernel (the route before the query-tiled kernels) is timed beside it."""
+    import torch
+    from turboquant_amd import TurboQuantKVCache
+    g = torch.Generator(device=dev).manual_seed(4000)
+    scale = torch.exp(torch.randn(128, generator=g, device=dev) * 0.5)
+    c = TurboQuantKVCache(head_dim=128, num_kv_heads=8, key_bits=4, value_bits=2, residual_window=128,
+                          fp16_sink_size=128)
+    k = (torch.randn(1, 8, ctx, 128, generator=g, device=dev) * scale).half()
+    v = torch.randn(1, 8, ctx, 128, generator=g, device=dev).half()
+    c.update(k, v)
+    del k, v
+    res = []
+    for nq in n_qs:
+        q = torch.randn(1, 32, nq, 128, generator=g, device=dev).half()
+        out = torch.empty(1, 32, nq, 128, dtype=torch.float32, device=dev)
+        ms, _, _ = time_graph(lambda: c.attend(q, out=out), reps, warmup)
+        pairs = 32 * sum(ctx - nq + i + 1 for i in range(nq))
+        flops = 4 * 128 * pairs
+        tf = flops / (ms * 1e-3) / 1e12
+        byt = decode_bytes_per_layer(c, 32) - 32 * 128 * 6 + 32 * nq * 128 * 6
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gen = torch.empty_like(out)
+        c.attend(q, out=gen, general_kernel=True)
+        torch.cuda.synchronize()
+        st.record()
+        c.attend(q, out=gen, general_kernel=True)
+        en.record()
+        torch.cuda.synchronize()
+        ms_gen = st.elapsed_time(en)
+        rel = float((out - gen).norm() / gen.norm())
+        res.append({"n_q": nq, "ctx": ctx, "route": "prefill_kernel<4,2> (+ prep, merge)",
+                    "ms_per_call": round(ms, 4), "query_tokens_per_s": round(nq / (ms * 1e-3), 1),
+                    "algorithmic_TFLOPs": round(tf, 2), "mfma_peak_TFLOPs": MFMA_F16_PEAK_TFLOPS,
+                    "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "bytes": byt,
+                    "GBps": round(byt / (ms * 1e-3) / 1e9, 1),
+                    "general_kernel_ms": round(ms_gen, 3), "speedup_vs_general": round(ms_gen / ms, 1),
+                    "rel_diff_vs_general": rel})
+        del q, out, gen
+    del c
+    torch.cuda.empty_cache()
     return res
 
 
@@ -615,6 +666,9 @@ def main():
     if not args.no_extra:
         log("timing the other integer widths")
         result["widths"] = bench_widths(dev)
+    if not args.no_extra:
+        log("timing prefill attention")
+        result["prefill"] = bench_prefill(dev)
     if not args.no_compress:
         log("timing compress")
         del outs

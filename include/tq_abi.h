@@ -210,8 +210,10 @@ typedef struct tq_attn_desc {
   int32_t flags;                        /* TQ_ATTN_* bits */
   int32_t n_q;                          /* query tokens per sequence: 0 / 1 decode; > 1 the last n_q
                                            tokens of each sequence attend causally (query i sees
-                                           positions <= total - n_q + i), q and out (batch, hq, n_q, d),
-                                           general kernel (cache.py:722-724 "causal" prefill mask) */
+                                           positions <= total - n_q + i), q and out (batch, hq, n_q, d)
+                                           (cache.py:722-724 "causal" prefill mask): query-tiled MFMA
+                                           kernels for integer widths 2-4 at d = 128 without a sketch,
+                                           the general kernel otherwise */
 } tq_attn_desc;
 
 /* tq_attn_desc.flags: force the general kernel (every width / QJL) even where
@@ -220,8 +222,13 @@ typedef struct tq_attn_desc {
 
 /* Workspace: scratch for the per-workgroup partials of one call (no state is
  * kept between calls, no initial contents are needed). Calls sharing a
- * workspace must be ordered on one stream or must not overlap. */
+ * workspace must be ordered on one stream or must not overlap.
+ * tq_decode_workspace_bytes is an upper bound over every route the key codec
+ * and descriptor allow; tq_attention_workspace_bytes is the need of the route
+ * tq_decode_attention takes for (kcodec, vcodec, desc) (for prefill calls on
+ * the query-tiled kernels far less than the general kernel's partials). */
 size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* desc);
+size_t tq_attention_workspace_bytes(const tq_codec* kcodec, const tq_codec* vcodec, const tq_attn_desc* desc);
 int tq_decode_attention(const tq_codec* kcodec, const tq_codec* vcodec,
                         const tq_attn_desc* desc, void* workspace,
                         size_t workspace_bytes, void* stream);
@@ -233,7 +240,7 @@ int tq_decode_attention(const tq_codec* kcodec, const tq_codec* vcodec,
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). It calls no hipMalloc / hipFree; the
  * caller still passes q, out and the cache buffers through `desc`.
- * Calls whose tq_decode_workspace_bytes exceeds TQ_NOALLOC_SCRATCH_BYTES
+ * Calls whose tq_attention_workspace_bytes exceeds TQ_NOALLOC_SCRATCH_BYTES
  * return TQ_ERR_WORKSPACE. Every call on one GPU shares that GPU's scratch:
  * calls that overlap on one GPU (different streams, no ordering between them)
  * race; calls ordered on one stream do not. Nothing is carried from one call

@@ -1718,7 +1718,17 @@ size_t tq_decode_workspace_bytes(const tq_codec* kcodec, const tq_attn_desc* d) 
     const size_t dense = dense_workspace(d);
     if (dense > bytes) bytes = dense;
   }
+  if (d->n_q > 1 && kcodec->d == 128) {
+    const size_t pre = prefill_workspace(d);
+    if (pre > bytes) bytes = pre;
+  }
   return (bytes + 255) & ~(size_t)255;
+}
+
+size_t tq_attention_workspace_bytes(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
+  if (!kc || !vc || !d) return 0;
+  if (prefill_eligible(kc, vc, d)) return (prefill_workspace(d) + 255) & ~(size_t)255;
+  return tq_decode_workspace_bytes(kc, d);
 }
 
 int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace,
@@ -1727,11 +1737,13 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   if (rc) return rc;
   const int G = d->hq / d->hkv;
   const bool qjl = d->qjl != 0;
-  const size_t need = tq_decode_workspace_bytes(kc, d);
+  const size_t need = tq_attention_workspace_bytes(kc, vc, d);
   if (!workspace || workspace_bytes < need)
     return set_error(TQ_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, need);
 
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // several query tokens per sequence: the query-tiled prefill kernels
+  if (prefill_eligible(kc, vc, d)) return prefill_run(kc, vc, d, workspace, s);
   // nothing compressed yet: the dense kernel over the sink and ring
   if (d->max_comp == 0 && !(d->flags & TQ_ATTN_GENERAL) && (d->max_sink > 0 || d->max_res > 0) &&
       dense_check(d, kc->d, false) == TQ_OK)
@@ -1846,10 +1858,11 @@ int tq_measure_decode_partials(const tq_codec* kc, const tq_codec* vc, const tq_
 // valid call, without launching anything: 0 the general kernel, 1 the dense
 // kernel, 2 the K4/V2 kernels, 3 the K4/V2 kernels with the QJL terms, 4 the
 // uniform-batch kernels of the other integer widths, 5 those of the
-// fractional widths.
+// fractional widths, 6 the query-tiled prefill kernels.
 int tq_debug_decode_route(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
   if (!kc || !vc || !d || d->hkv <= 0 || d->hq % d->hkv) return -1;
   if (d->flags & TQ_ATTN_GENERAL) return 0;
+  if (prefill_eligible(kc, vc, d)) return 6;
   if (d->max_comp == 0 && (d->max_sink > 0 || d->max_res > 0) && dense_check(d, kc->d, false) == TQ_OK) return 1;
   if (d->qjl && d->max_comp > 0 && fast_eligible(kc, vc, d, true)) return 3;
   if (fast_eligible(kc, vc, d)) return 2;
@@ -1882,7 +1895,7 @@ int tq_decode_attention_noalloc(const tq_codec* kc, const tq_codec* vc, const tq
   // descriptor gets TQ_ERR_INVALID, not a size error
   const int vrc = check_attention_call(kc, vc, d);
   if (vrc) return vrc;
-  const size_t need = tq_decode_workspace_bytes(kc, d);
+  const size_t need = tq_attention_workspace_bytes(kc, vc, d);
   if (need > TQ_NOALLOC_SCRATCH_BYTES)
     return set_error(TQ_ERR_WORKSPACE, "call needs %zu bytes of scratch; the no-allocation entry point holds %zu",
                      need, (size_t)TQ_NOALLOC_SCRATCH_BYTES);

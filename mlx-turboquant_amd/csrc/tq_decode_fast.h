@@ -4,7 +4,10 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
+
+#include "../../include/tq_abi.h"
 
 namespace tq {
 
@@ -176,5 +179,50 @@ __device__ inline int query_exponent(float qnorm, float qscale, float hi, float 
 void dense_geometry(int batch, int hkv, int max_sink, int max_res, int cus, int& nwg, int& bpw);
 // bf: bf16 K/V (else fp16); merge 0 skips the merge launch (measurement)
 int launch_dense_decode(const DenseArgs& a, int G, bool bf, int batch, int merge, hipStream_t s);
+
+// Prefill attention (n_q > 1, tq_prefill.h): a wave owns PREFILL_WAVE_ROWS
+// query rows (PREFILL_TILES 16-row MFMA column tiles), a workgroup
+// PREFILL_WAVES waves; partials of PREFILL_PART_FLOATS floats per (key-range
+// split, query row): max, sum, pad, pad, rotated output / sum.
+constexpr int PREFILL_TILES = 2;
+constexpr int PREFILL_WAVE_ROWS = 16 * PREFILL_TILES;
+constexpr int PREFILL_WAVES = 8;
+constexpr int PREFILL_PART_FLOATS = 132;
+constexpr int PREFILL_TARGET_WG = 256;  // workgroups a launch aims for (one per CU)
+
+struct PrefillArgs {
+  int batch, hq, hkv, G, n_q, kvrows;
+  int nrows, nrows_pad;         // query rows per kv row (n_q G) and that padded to whole waves
+  int nd_pad, nbd, nbc;         // uncompressed tokens per kv row padded to 32; their blocks; compressed blocks
+  int nsplit, bps;              // key-range splits and blocks per split
+  int max_comp, max_sink, max_res;
+  const int32_t* comp_len; const int32_t* sink_len; const int32_t* res_len; const int32_t* res_start;
+  int res_start0, res_cap;
+  const uint8_t* kc; int64_t k_hs;   // key code rows (16 KB bytes)
+  const uint8_t* vc; int64_t v_hs;   // value code rows (16 VB bytes)
+  const float* kn; int64_t kn_hs;
+  const float* vn; int64_t vn_hs;
+  const float* kcen; const float* vcen;  // codebooks (2^KB, 2^VB floats)
+  const void* sink_k; const void* sink_v; int64_t sink_hs;
+  const void* res_k; const void* res_v; int64_t res_hs;
+  int kv_dtype;
+  const void* q; int q_dtype;
+  const float* rk; const float* rv;  // key / value codec R (128 x 128, row-major)
+  float scale;
+  // workspace
+  float* qr;      // (kvrows, nrows_pad, 128) rotated queries
+  uint16_t* dk;   // (kvrows, nd_pad, 2, 128) uncompressed keys: unit vector fp16 high part, remainder
+  uint16_t* dv;   // (kvrows, nbd, 2, 128, 32) uncompressed values, transposed, PV k-slot order
+  float* dnk;     // (kvrows, nd_pad) their norms
+  float* dnv;
+  float* part;    // (nsplit, kvrows, nrows_pad, PREFILL_PART_FLOATS)
+  float* out;     // (batch, hq, n_q, 128)
+};
+
+// The prefill route: eligibility, workspace bytes of a call, and the launch
+// (preparation, partials, merge kernels) with the workspace carved as above.
+bool prefill_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d);
+size_t prefill_workspace(const tq_attn_desc* d);
+int prefill_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, void* workspace, hipStream_t s);
 
 }  // namespace tq

@@ -91,6 +91,7 @@ SIGNATURES = {
     "tq_unpack_codes": (_i32, [_p, _i64, _i32, _i32, _p, _p]),
     "tq_quantize_scalar": (_i32, [_p, _i64, _p, _i32, _p, _p]),
     "tq_decode_workspace_bytes": (ctypes.c_size_t, [_PC, _PA]),
+    "tq_attention_workspace_bytes": (ctypes.c_size_t, [_PC, _PC, _PA]),
     "tq_decode_attention": (_i32, [_PC, _PC, _PA, _p, ctypes.c_size_t, _p]),
     "tq_decode_noalloc_scratch_bytes": (ctypes.c_size_t, []),
     "tq_decode_attention_noalloc": (_i32, [_PC, _PC, _PA, _p]),

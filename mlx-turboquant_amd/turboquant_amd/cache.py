@@ -397,7 +397,7 @@ class TurboQuantKVCache:
         desc = self.attention_descriptor(q, out, scale, general_kernel)
         desc.n_q = tq
         lib = _lib.load()
-        need = lib.tq_decode_workspace_bytes(self._kc.ref(), ctypes.byref(desc))
+        need = lib.tq_attention_workspace_bytes(self._kc.ref(), self._vc.ref(), ctypes.byref(desc))
         ws = _workspace(q.device, need)
         _lib.check(lib.tq_decode_attention(self._kc.ref(), self._vc.ref(), ctypes.byref(desc), ws.data_ptr(),
                                            ws.numel(), _lib.stream_ptr(q.device)), "tq_decode_attention")

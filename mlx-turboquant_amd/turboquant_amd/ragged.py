@@ -263,7 +263,7 @@ class RaggedKVBatch:
         d, arrays = self.descriptor(q, out, scale if scale is not None else self.D ** -0.5, general)
         lib = _lib.load()
         stream = _lib.stream_ptr(q.device)
-        ws = _workspace(q.device, lib.tq_decode_workspace_bytes(self.kc.ref(), ctypes.byref(d)), stream)
+        ws = _workspace(q.device, lib.tq_attention_workspace_bytes(self.kc.ref(), self.vc.ref(), ctypes.byref(d)), stream)
         _lib.check(lib.tq_decode_attention(self.kc.ref(), self.vc.ref(), ctypes.byref(d), ws.data_ptr(), ws.numel(),
                                            stream), "tq_decode_attention")
         self._attn_keep = arrays

@@ -581,6 +581,27 @@ def pmc_compress_workload():
     print(json.dumps({"copy_bytes": n, "compress": r}), flush=True)
 
 
+def pmc_prefill_workload(n_q: int = 1024):
+    """Short program for the prefill kernel trace and counter runs: one
+    configs[1]-shaped K4/V2 layer (T = 32768), 5 attend calls of its last n_q
+    tokens (causal)."""
+    import torch
+    from turboquant_amd import TurboQuantKVCache
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(4000)
+    scale = torch.exp(torch.randn(128, generator=g, device=dev) * 0.5)
+    c = TurboQuantKVCache(head_dim=128, num_kv_heads=8, key_bits=4, value_bits=2, residual_window=128,
+                          fp16_sink_size=128)
+    c.update((torch.randn(1, 8, 32768, 128, generator=g, device=dev) * scale).half(),
+             torch.randn(1, 8, 32768, 128, generator=g, device=dev).half())
+    q = torch.randn(1, 32, n_q, 128, generator=g, device=dev).half()
+    out = torch.empty(1, 32, n_q, 128, dtype=torch.float32, device=dev)
+    for _ in range(5):
+        c.attend(q, out=out)
+    torch.cuda.synchronize()
+    print(json.dumps({"prefill_calls": 5, "n_q": n_q, "ctx": 32768}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -593,6 +614,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the configs[3] / configs[4] timings")
     ap.add_argument("--pmc-workload", action="store_true", help="short program for rocprofv3 --pmc runs")
     ap.add_argument("--pmc-compress", action="store_true", help="short compress program for rocprofv3 --pmc runs")
+    ap.add_argument("--pmc-prefill", action="store_true", help="short prefill program for rocprofv3 runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -604,6 +626,9 @@ def main():
         return
     if args.pmc_compress:
         pmc_compress_workload()
+        return
+    if args.pmc_prefill:
+        pmc_prefill_workload()
         return
 
     import torch

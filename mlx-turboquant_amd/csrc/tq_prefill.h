@@ -4,17 +4,19 @@
 // value widths KB, VB in 2..4, no QJL sketch.
 //
 // Query rows are (query token, head of the kv group) pairs: row r of kv head
-// (b, g) is token r / G of query head g G + r % G. A wave owns 64 rows (four
-// 16-row tiles, the MFMA columns) and walks a range of 32-token key blocks;
-// each block's code rows are decoded once per wave and serve all 64 rows:
+// (b, g) is token r / G of query head g G + r % G. A wave owns NT 16-row tiles
+// (the MFMA columns; NT = PREFILL_TILES) and walks a range of 32-token key
+// blocks; each block's code rows are decoded once per wave and serve all its
+// rows:
 //  - scores S^T = K q^T (MFMA 16x16x32 f16, A = 16 keys x 32 dims, B = 32
 //    dims x 16 rows): k-slot 8 q4 + e of step s is rotated dim 32 q4 + 8 s + e,
 //    so lane (key r, q4) reads the 32 contiguous codes of dims [32 q4, 32 q4 +
 //    32) of its key (4 KB bytes) and looks up 2 dims per LDS pair-table entry,
-//    (c_hi[a], c_hi[b]) | (c_lo[a], c_lo[b]) (c_hi = fp16(c), c_lo = fp16(c -
-//    c_hi)): the high parts make one A operand and the remainders another,
-//    both against the same fp16 query operand (the rotated query scaled by a
-//    per-wave power of two);
+//    (c_hi[a], c_hi[b]) and (c_lo[a], c_lo[b]) (c_hi = fp16(c), c_lo = fp16(c -
+//    c_hi)): the high parts make one A operand and the remainders another;
+//    the rotated query (scaled by a per-wave power of two) is split the same
+//    way, and three MFMAs per step add c_hi q_hi + c_lo q_hi + c_hi q_lo
+//    (fp32-class scores);
 //  - output O^T += V^T P^T: k-slot 8 q4 + e is key 4 q4 + e of tile 0 (e < 4)
 //    or of tile 1, exactly the scores lane (row j, q4) holds, so p * n_v
 //    (fp16, round to nearest) is the B operand as it stands; A row i of PV

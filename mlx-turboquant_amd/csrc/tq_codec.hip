@@ -324,19 +324,45 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
 // output per lane (lane and lane + 64) summed over i = 0..127 in order with
 // fmaf, with R and S staged in LDS (rows padded to 129 floats).
 constexpr int DRW = 8;    // waves (vectors) per workgroup
-constexpr int DRP = 129;  // padded LDS row
+constexpr int DRP = 132;  // padded LDS row: 16-byte aligned, rows of 16 lanes in distinct banks
 
 __global__ __launch_bounds__(DRW * 64) void drain_kernel(CompressArgs a) {
-  __shared__ float rt[128 * DRP];   // R[c][i] at c * DRP + i
-  __shared__ float st[128 * DRP];   // S[k][i] at k * DRP + i
-  __shared__ float vec[DRW][128];
+  __shared__ __align__(16) float rt[128 * DRP];   // R[c][i] at c * DRP + i
+  __shared__ __align__(16) float st[128 * DRP];   // S[k][i] at k * DRP + i
+  __shared__ __align__(16) float vec[DRW][128];
   __shared__ uint8_t cds[DRW][128];
   __shared__ float bnd[2][16];
   __shared__ float cen[2][16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  for (int e = tid; e < 128 * 128; e += DRW * 64) rt[(e >> 7) * DRP + (e & 127)] = a.rot[e];
-  for (int e = tid; e < a.qjl_m * 128; e += DRW * 64) st[(e >> 7) * DRP + (e & 127)] = a.proj[e];
+  // R and S in 16-byte pieces, every load of a thread requested before its
+  // first store (8 pieces of R per thread, up to 16 of S)
+  {
+    const float4* r4 = reinterpret_cast<const float4*>(a.rot);
+    float4 x[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = r4[tid + k * DRW * 64];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int e = tid + k * DRW * 64, row = e >> 5, c = 4 * (e & 31);
+      *reinterpret_cast<float4*>(rt + row * DRP + c) = x[k];
+    }
+    if (a.qjl_m > 0) {
+      const float4* s4 = reinterpret_cast<const float4*>(a.proj);
+      const int n4 = a.qjl_m * 32;  // pieces of S (qjl_m <= 128 here)
+      float4 y[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int e = tid + k * DRW * 64;
+        y[k] = e < n4 ? s4[e] : float4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int e = tid + k * DRW * 64, row = e >> 5, c = 4 * (e & 31);
+        if (e < n4) *reinterpret_cast<float4*>(st + row * DRP + c) = y[k];
+      }
+    }
+  }
   if (tid < 16) {
     const int nbh = (1 << a.bits_hi) - 1, nbl = (1 << a.bits_lo) - 1;
     bnd[0][tid] = tid < nbh ? a.bnd_hi[tid] : 0.f;
@@ -365,13 +391,15 @@ __global__ __launch_bounds__(DRW * 64) void drain_kernel(CompressArgs a) {
   if (lane == 0) a.dst.norms[(int64_t)r * a.dst.norm_head_stride + dst] = n;
   xv[lane] = x0 / fmaxf(n, 1e-10f);
   xv[64 + lane] = x1 / fmaxf(n, 1e-10f);
-  // rotate: y_c = sum_i x_n[i] * R[c][i]
+  // rotate: y_c = sum_i x_n[i] * R[c][i] (i in order; four i per LDS read)
   float y0 = 0.f, y1 = 0.f;
-#pragma unroll 8
-  for (int i = 0; i < 128; ++i) {
-    const float xi = xv[i];
-    y0 = fmaf(xi, rt[lane * DRP + i], y0);
-    y1 = fmaf(xi, rt[(lane + 64) * DRP + i], y1);
+#pragma unroll 4
+  for (int i = 0; i < 128; i += 4) {
+    const float4 xi = *reinterpret_cast<const float4*>(xv + i);
+    const float4 ra = *reinterpret_cast<const float4*>(rt + lane * DRP + i);
+    const float4 rb = *reinterpret_cast<const float4*>(rt + (lane + 64) * DRP + i);
+    y0 = fmaf(xi.w, ra.w, fmaf(xi.z, ra.z, fmaf(xi.y, ra.y, fmaf(xi.x, ra.x, y0))));
+    y1 = fmaf(xi.w, rb.w, fmaf(xi.z, rb.z, fmaf(xi.y, rb.y, fmaf(xi.x, rb.x, y1))));
   }
   const bool hi0 = lane < a.split, hi1 = lane + 64 < a.split;
   const uint32_t c0 = quantize_one(y0, bnd[hi0 ? 0 : 1], (1 << (hi0 ? a.bits_hi : a.bits_lo)) - 1);
@@ -395,30 +423,41 @@ __global__ __launch_bounds__(DRW * 64) void drain_kernel(CompressArgs a) {
   xv[lane] = cen[hi0 ? 0 : 1][c0];
   xv[64 + lane] = cen[hi1 ? 0 : 1][c1];
   float a0 = 0.f, a1 = 0.f;
-#pragma unroll 8
-  for (int i = 0; i < 128; ++i) {
-    const float ci = xv[i];
-    a0 = fmaf(ci, rt[i * DRP + lane], a0);
-    a1 = fmaf(ci, rt[i * DRP + lane + 64], a1);
+#pragma unroll 4
+  for (int i = 0; i < 128; i += 4) {
+    const float4 ci = *reinterpret_cast<const float4*>(xv + i);
+    a0 = fmaf(ci.x, rt[i * DRP + lane], a0);
+    a1 = fmaf(ci.x, rt[i * DRP + lane + 64], a1);
+    a0 = fmaf(ci.y, rt[(i + 1) * DRP + lane], a0);
+    a1 = fmaf(ci.y, rt[(i + 1) * DRP + lane + 64], a1);
+    a0 = fmaf(ci.z, rt[(i + 2) * DRP + lane], a0);
+    a1 = fmaf(ci.z, rt[(i + 2) * DRP + lane + 64], a1);
+    a0 = fmaf(ci.w, rt[(i + 3) * DRP + lane], a0);
+    a1 = fmaf(ci.w, rt[(i + 3) * DRP + lane + 64], a1);
   }
   const float r0 = x0 - n * a0;
   const float r1 = x1 - n * a1;
   xv[lane] = r0;
   xv[64 + lane] = r1;
   double s2 = 0.0;
-#pragma unroll 8
-  for (int i = 0; i < 128; ++i) {
-    const double ri = (double)xv[i];
-    s2 = fma(ri, ri, s2);
+#pragma unroll 4
+  for (int i = 0; i < 128; i += 4) {
+    const float4 r4 = *reinterpret_cast<const float4*>(xv + i);
+    s2 = fma((double)r4.x, (double)r4.x, s2);
+    s2 = fma((double)r4.y, (double)r4.y, s2);
+    s2 = fma((double)r4.z, (double)r4.z, s2);
+    s2 = fma((double)r4.w, (double)r4.w, s2);
   }
   if (lane == 0) a.dst.gamma[(int64_t)r * a.dst.gamma_head_stride + dst] = (float)sqrt(s2);
   float p0 = 0.f, p1 = 0.f;
   const int k1 = min(lane + 64, a.qjl_m - 1);
-#pragma unroll 8
-  for (int i = 0; i < 128; ++i) {
-    const float ri = xv[i];
-    p0 = fmaf(ri, st[lane * DRP + i], p0);
-    p1 = fmaf(ri, st[k1 * DRP + i], p1);
+#pragma unroll 4
+  for (int i = 0; i < 128; i += 4) {
+    const float4 ri = *reinterpret_cast<const float4*>(xv + i);
+    const float4 sa = *reinterpret_cast<const float4*>(st + lane * DRP + i);
+    const float4 sb = *reinterpret_cast<const float4*>(st + k1 * DRP + i);
+    p0 = fmaf(ri.w, sa.w, fmaf(ri.z, sa.z, fmaf(ri.y, sa.y, fmaf(ri.x, sa.x, p0))));
+    p1 = fmaf(ri.w, sb.w, fmaf(ri.z, sb.z, fmaf(ri.y, sb.y, fmaf(ri.x, sb.x, p1))));
   }
   const uint64_t s_lo = __ballot(p0 >= 0.f), s_hi = __ballot(p1 >= 0.f);
   if (lane == 0) {
@@ -775,7 +814,8 @@ int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x
   hipStream_t s = static_cast<hipStream_t>(stream);
   // small spans with the QJL sketch (one-token decode drains): one vector per
   // wave (without a sketch the MFMA kernel below is as fast on such spans)
-  if (codec->d == 128 && qjl && codec->qjl_m <= 128 && span->n_tok <= 8 && !(codec->flags & TQ_CODEC_GENERAL_COMPRESS)) {
+  if (codec->d == 128 && qjl && codec->qjl_m <= 128 && span->n_tok <= 8 && !(codec->flags & TQ_CODEC_GENERAL_COMPRESS) &&
+      !(reinterpret_cast<uintptr_t>(codec->rotation) & 15) && !(reinterpret_cast<uintptr_t>(codec->qjl_proj) & 15)) {
     const int64_t nvec = (int64_t)span->rows * span->n_tok;
     hipLaunchKernelGGL(drain_kernel, dim3((unsigned)((nvec + DRW - 1) / DRW)), dim3(DRW * 64), 0, s, a);
     TQ_LAUNCH_CHECK("tq_compress (drain)");

@@ -303,16 +303,20 @@ __device__ inline void dot_signs(const uint8_t* row, int m, const float (*sq)[MA
 // thread (dim j, token slice) accumulates the weighted values of dim j for
 // every head; with QJL the sign sketches are staged too and the value term
 // sum_t p_t gamma_t z_t is accumulated per projection.
-template <int D, int G>
+template <int DP, int G>
 __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
-  constexpr int TSL = NT / D > 0 ? NT / D : 1;  // token slices of the PV phase (threads per dim)
+  // DP: an upper bound of the head_dim D (a multiple of 16), the row stride
+  // of the query arrays
+  const int D = a.D;
+  const int TSL = NT / D > 0 ? NT / D : 1;       // token slices of the PV phase (threads per dim)
+  const int PER = ((CHUNK / TSL) + 3) & ~3;      // tokens per slice (whole float4 groups of weights)
   constexpr int MAXM = 256;
   // LDS row strides of staged code rows (at most 4 bits per dim) and sign
   // rows, padded by one dword so that the rows of neighbouring tokens start
   // in different banks
   const int KR = tile_stride(a);
   constexpr int SR = MAXM / 8 + 4;
-  __shared__ __align__(16) float qv[G][D];   // rotated (compressed) or plain (fp16) scaled query
+  __shared__ __align__(16) float qv[G][DP];  // rotated (compressed) or plain (fp16) scaled query
   __shared__ __align__(16) float w[G][CHUNK];   // p * n_v (or p) per token
   __shared__ float red[G][NT / 64];
   __shared__ float mx[G], lsum[G];
@@ -415,8 +419,8 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
     for (int h = 0; h < G; ++h) s[h] = 0.f;
     if (packed) {
       const uint8_t* kr = ktile + t * KR;
-      dot_codes_bits<D, G>(a.kb_hi, kr, a.ks, klut[0], qv, 0, s);
-      if (a.ks < D) dot_codes_bits<D, G>(a.kb_lo, kr + lo_col(a.k_row_hi), D - a.ks, klut[1], qv, a.ks, s);
+      dot_codes_bits<DP, G>(a.kb_hi, kr, a.ks, klut[0], qv, 0, s);
+      if (a.ks < D) dot_codes_bits<DP, G>(a.kb_lo, kr + lo_col(a.k_row_hi), D - a.ks, klut[1], qv, a.ks, s);
       const float nk = nk_t;
 #pragma unroll
       for (int h = 0; h < G; ++h) s[h] *= nk;
@@ -541,7 +545,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(AttnArgs a) {
   float* outp = a.part;
   {
     const int j = tid % D, sl = tid / D;
-    const int t_lo = sl * (CHUNK / TSL), t_hi = min(n4, t_lo + CHUNK / TSL);
+    const int t_lo = sl * PER, t_hi = min(n4, t_lo + PER);
     float acc[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h] = 0.f;
@@ -739,20 +743,20 @@ static void chunk_counts(const tq_attn_desc* d, int& nc, int& ns, int& nr) {
 }
 
 // G: query heads per launch group (1 .. 8)
-template <int D>
+template <int DP>
 static void launch_chunks(const AttnArgs& a, int G, dim3 grid, hipStream_t s) {
   // dynamic LDS of chunk_kernel: the code rows, and the QJL arrays when the call has a sketch
   const size_t dl = 2 * (size_t)CHUNK * tile_stride(a) +
                     (a.m > 0 ? (size_t)G * (CHUNK + 256) * 4 + 2 * (size_t)CHUNK * (256 / 8 + 4) : 0);
   switch (G) {
-    case 1: hipLaunchKernelGGL((chunk_kernel<D, 1>), grid, dim3(NT), dl, s, a); break;
-    case 2: hipLaunchKernelGGL((chunk_kernel<D, 2>), grid, dim3(NT), dl, s, a); break;
-    case 3: hipLaunchKernelGGL((chunk_kernel<D, 3>), grid, dim3(NT), dl, s, a); break;
-    case 4: hipLaunchKernelGGL((chunk_kernel<D, 4>), grid, dim3(NT), dl, s, a); break;
-    case 5: hipLaunchKernelGGL((chunk_kernel<D, 5>), grid, dim3(NT), dl, s, a); break;
-    case 6: hipLaunchKernelGGL((chunk_kernel<D, 6>), grid, dim3(NT), dl, s, a); break;
-    case 7: hipLaunchKernelGGL((chunk_kernel<D, 7>), grid, dim3(NT), dl, s, a); break;
-    default: hipLaunchKernelGGL((chunk_kernel<D, 8>), grid, dim3(NT), dl, s, a); break;
+    case 1: hipLaunchKernelGGL((chunk_kernel<DP, 1>), grid, dim3(NT), dl, s, a); break;
+    case 2: hipLaunchKernelGGL((chunk_kernel<DP, 2>), grid, dim3(NT), dl, s, a); break;
+    case 3: hipLaunchKernelGGL((chunk_kernel<DP, 3>), grid, dim3(NT), dl, s, a); break;
+    case 4: hipLaunchKernelGGL((chunk_kernel<DP, 4>), grid, dim3(NT), dl, s, a); break;
+    case 5: hipLaunchKernelGGL((chunk_kernel<DP, 5>), grid, dim3(NT), dl, s, a); break;
+    case 6: hipLaunchKernelGGL((chunk_kernel<DP, 6>), grid, dim3(NT), dl, s, a); break;
+    case 7: hipLaunchKernelGGL((chunk_kernel<DP, 7>), grid, dim3(NT), dl, s, a); break;
+    default: hipLaunchKernelGGL((chunk_kernel<DP, 8>), grid, dim3(NT), dl, s, a); break;
   }
 }
 
@@ -1813,12 +1817,11 @@ int tq_decode_attention(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   TQ_LAUNCH_CHECK("tq_decode_attention prologue");
   if (a.nch > 0) {
     dim3 grid(a.nch, d->hkv * a.gsub, d->batch * nq);
-    switch (a.D) {
-      case 64: launch_chunks<64>(a, gh, grid, s); break;
-      case 96: launch_chunks<96>(a, gh, grid, s); break;
-      case 128: launch_chunks<128>(a, gh, grid, s); break;
-      default: launch_chunks<256>(a, gh, grid, s); break;
-    }
+    // the query arrays of the kernel at the next instantiated width
+    if (a.D <= 64) launch_chunks<64>(a, gh, grid, s);
+    else if (a.D <= 96) launch_chunks<96>(a, gh, grid, s);
+    else if (a.D <= 128) launch_chunks<128>(a, gh, grid, s);
+    else launch_chunks<256>(a, gh, grid, s);
     TQ_LAUNCH_CHECK("tq_decode_attention chunks");
   }
   const size_t cmb_smem = (size_t)(((a.nch + 3) & ~3) + a.D + a.m) * 4;

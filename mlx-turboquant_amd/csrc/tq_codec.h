@@ -18,6 +18,7 @@ struct CompressArgs {
   const float* cen_hi;
   const float* cen_lo;
   const float* proj;
+  int d;  // head_dim
   int bits_hi, bits_lo, split, qjl_m;
   int row_hi, row_lo, row_sign;
 };

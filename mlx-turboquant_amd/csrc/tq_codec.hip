@@ -15,6 +15,8 @@
 #include <cstdio>
 #include <cstring>
 
+#include <type_traits>
+
 #include "tq_common.h"
 #include "tq_codec.h"
 
@@ -32,8 +34,8 @@ int set_error(int code, const char* fmt, ...) {
 
 int check_codec(const tq_codec* c) {
   if (!c) return set_error(TQ_ERR_INVALID, "codec is NULL");
-  if (c->d != 64 && c->d != 96 && c->d != 128 && c->d != 256)
-    return set_error(TQ_ERR_UNSUPPORTED, "head_dim %d not supported (64, 96, 128, 256)", c->d);
+  if (c->d < 16 || c->d > 256 || (c->d % 16) != 0)
+    return set_error(TQ_ERR_UNSUPPORTED, "head_dim %d not supported (a multiple of 16 in [16, 256])", c->d);
   if (c->bits_hi < 1 || c->bits_hi > 4 || c->bits_lo < 1 || c->bits_lo > 4)
     return set_error(TQ_ERR_UNSUPPORTED, "Unsupported bit-width: %d/%d. Use 1, 2, 3, or 4.",
                      c->bits_hi, c->bits_lo);
@@ -54,13 +56,18 @@ int check_codec(const tq_codec* c) {
 // is staged in LDS with each 32-column segment padded to 36 floats so that the
 // NSEG segments of a wave read distinct LDS banks.
 // ---------------------------------------------------------------------------
-// Thread (v, q) = (tid / NSEG, tid % NSEG); for D = 96 the last thread of the
-// 256 has no vector (v == VPW): it reads vector VPW - 1 and writes nothing.
-template <int D>
+// Thread (v, q) = (tid / NSEG, tid % NSEG); when NSEG does not divide 256
+// (D = 96, 160, 192, 224) the last threads have no vector (v == VPW): they
+// read vector VPW - 1 and write nothing. DP is the head_dim rounded up to a
+// multiple of 32 (the tile width); a head_dim that is an odd multiple of 16
+// leaves the upper half of the last segment: its columns of the vector tile
+// and the matrix tiles hold zeros, and its codes are neither stored nor read.
+template <int DP>
 struct Geo {
-  static constexpr int NSEG = D / 32;          // 32-column segments
+  static_assert(DP % 32 == 0 && DP <= 256, "padded head_dim");
+  static constexpr int NSEG = DP / 32;         // 32-column segments
   static constexpr int VPW = 256 / NSEG;       // vectors per workgroup
-  static constexpr int XS = D + 1;             // padded row of the vector tile
+  static constexpr int XS = DP + 1;            // padded row of the vector tile
   static constexpr int SEGP = 36;              // padded segment
   static constexpr int MROW = NSEG * SEGP;     // padded matrix row
   static constexpr int TI = 32;                // matrix rows per LDS tile
@@ -119,10 +126,10 @@ __device__ inline uint32_t quantize_one(float y, const float* b, int nb) {
 }
 
 // acc[c] += sum_{i in tile} xs[v][i] * M[i][32q + c] for the LDS tile M.
-template <int D>
+template <int DP>
 __device__ inline void tile_madd(const float* __restrict__ xs_row, const float* __restrict__ mt,
                                  int i0, int q, float (&acc)[32]) {
-  using G = Geo<D>;
+  using G = Geo<DP>;
 #pragma unroll 4
   for (int ii = 0; ii < G::TI; ++ii) {
     const float xv = xs_row[i0 + ii];
@@ -138,27 +145,56 @@ __device__ inline void tile_madd(const float* __restrict__ xs_row, const float* 
   }
 }
 
-// Stage rows [i0, i0+TI) of M (row-major D x D, or its transpose when
-// TRANSPOSE) into the padded LDS tile mt[ii][seg][SEGP].
-template <int D, bool TRANSPOSE>
-__device__ inline void stage_tile(const float* __restrict__ m, int i0, float* mt) {
-  using G = Geo<D>;
-  for (int e = threadIdx.x; e < G::TI * D; e += blockDim.x) {
-    const int ii = e / D, j = e % D;
-    const float val = TRANSPOSE ? m[(int64_t)j * D + (i0 + ii)] : m[(int64_t)(i0 + ii) * D + j];
+// Stage rows [i0, i0+TI) of M (row-major d x d, or its transpose when
+// TRANSPOSE) into the padded LDS tile mt[ii][seg][SEGP]; rows and columns at
+// or past d are zeros.
+template <int DP, bool TRANSPOSE>
+__device__ inline void stage_tile(const float* __restrict__ m, int d, int i0, float* mt) {
+  using G = Geo<DP>;
+  for (int e = threadIdx.x; e < G::TI * DP; e += blockDim.x) {
+    const int ii = e / DP, j = e % DP;
+    const bool ok = i0 + ii < d && j < d;
+    const float val = !ok ? 0.f : TRANSPOSE ? m[(int64_t)j * d + (i0 + ii)] : m[(int64_t)(i0 + ii) * d + j];
     mt[ii * G::MROW + (j >> 5) * G::SEGP + (j & 31)] = val;
   }
 }
 
-template <int D>
+// The codes of the thread's segment q (columns [32 q, 32 q + 32) of a
+// d-dim row, the first `split` at bits_hi into rows of row_hi bytes, the rest
+// at bits_lo into rows of row_lo bytes): one dword store / load per BITS
+// dwords when the segment is whole, of one width, and dword-aligned in its
+// row; else 16-code halves byte by byte (columns at or past d skipped).
+__device__ inline bool whole_segment(int q, int d, int split, int row_hi, int row_lo) {
+  const bool hi = 32 * q < split;
+  return (split & 31) == 0 && 32 * q + 32 <= d && ((hi ? row_hi : row_lo) & 3) == 0;
+}
+
+// f(std::integral_constant<int, DP>) with DP = d rounded up to a multiple of
+// 32 (d a multiple of 16 in [16, 256], checked by check_codec)
+template <typename F>
+static void launch_padded(int d, F f) {
+  switch ((d + 31) / 32) {
+    case 1: f(std::integral_constant<int, 32>{}); break;
+    case 2: f(std::integral_constant<int, 64>{}); break;
+    case 3: f(std::integral_constant<int, 96>{}); break;
+    case 4: f(std::integral_constant<int, 128>{}); break;
+    case 5: f(std::integral_constant<int, 160>{}); break;
+    case 6: f(std::integral_constant<int, 192>{}); break;
+    case 7: f(std::integral_constant<int, 224>{}); break;
+    default: f(std::integral_constant<int, 256>{}); break;
+  }
+}
+
+template <int DP>
 __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
-  using G = Geo<D>;
+  using G = Geo<DP>;
   __shared__ float xs[G::VPW * G::XS];
   __shared__ float mt[G::TI * G::MROW];
   __shared__ float nrm[G::VPW];
   __shared__ float bnd[2][16];
   __shared__ float cen[2][16];
 
+  const int D = a.d;
   const int r = blockIdx.y;
   const int b = r / a.span.heads;
   const int n_tok = a.span.n_tok_b ? a.span.n_tok_b[b] : a.span.n_tok;
@@ -177,53 +213,53 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
     cen[1][tid] = tid <= nbl ? a.cen_lo[tid] : 0.f;
   }
 
-  // Load the fp16 tile as float32 (exact).
+  // Load the tile as float32 (exact); columns past D are zeros.
   const int64_t xrow = (int64_t)r * a.x_hs + (int64_t)src0 * D;
-  for (int e = tid; e < G::VPW * D; e += blockDim.x) {
-    const int v = e / D, i = e % D;
-    xs[v * G::XS + i] = v < nv ? load_elem(a.x, xrow + (int64_t)v * D + i, a.x_dtype) : 0.f;
+  for (int e = tid; e < G::VPW * DP; e += blockDim.x) {
+    const int v = e / DP, i = e % DP;
+    xs[v * G::XS + i] = v < nv && i < D ? load_elem(a.x, xrow + (int64_t)v * D + i, a.x_dtype) : 0.f;
   }
   __syncthreads();
 
-  // Norm: float64 sum of squares in the library's block order, rounded square root.
+  // Norm: float64 sum of squares in the library's block order, rounded square
+  // root (the zero columns past D add nothing to the last block).
   if (tid < G::VPW) {
-    const float n = (float)sqrt(sumsq_blocks<D>(xs + tid * G::XS));
+    const float n = (float)sqrt(sumsq_blocks<DP>(xs + tid * G::XS));
     nrm[tid] = n;
     if (tid < nv) a.dst.norms[(int64_t)r * a.dst.norm_head_stride + dst0 + tid] = n;
   }
   __syncthreads();
 
   // Normalise in place.
-  for (int e = tid; e < G::VPW * D; e += blockDim.x) {
-    const int v = e / D, i = e % D;
+  for (int e = tid; e < G::VPW * DP; e += blockDim.x) {
+    const int v = e / DP, i = e % DP;
     xs[v * G::XS + i] = xs[v * G::XS + i] / fmaxf(nrm[v], 1e-10f);
   }
 
   // Rotate: y = x_n @ R^T.
   const int v = tid / G::NSEG, q = tid % G::NSEG;
-  const bool vok = v < G::VPW;            // false only for the spare thread of D = 96
+  const bool vok = v < G::VPW;            // false only for the spare threads when NSEG does not divide 256
   const int vr = vok ? v : G::VPW - 1;    // the vector row it reads
   float acc[32];
 #pragma unroll
   for (int c = 0; c < 32; ++c) acc[c] = 0.f;
   for (int i0 = 0; i0 < D; i0 += G::TI) {
     __syncthreads();
-    stage_tile<D, true>(a.rot, i0, mt);
+    stage_tile<DP, true>(a.rot, D, i0, mt);
     __syncthreads();
-    tile_madd<D>(xs + vr * G::XS, mt, i0, q, acc);
+    tile_madd<DP>(xs + vr * G::XS, mt, i0, q, acc);
   }
 
   // Quantize + pack this thread's 32 coordinates (columns 32q + c; column j
   // uses the high-width codebook when j < split).
-  const bool split16 = (a.split & 31) != 0;  // a segment holds 16 codes of each width
   uint32_t code[32];
 #pragma unroll
   for (int c = 0; c < 32; ++c) {
     const bool hc = 32 * q + c < a.split;
     code[c] = quantize_one(acc[c], bnd[hc ? 0 : 1], (1 << (hc ? a.bits_hi : a.bits_lo)) - 1);
   }
-  if (v < nv) {
-    if (!split16) {
+  if (v < nv && 32 * q < D) {
+    if (whole_segment(q, D, a.split, a.row_hi, a.row_lo)) {
       const bool hi = 32 * q < a.split;
       const int bits = hi ? a.bits_hi : a.bits_lo;
       uint8_t* dst;
@@ -238,6 +274,7 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
     } else {
       for (int hh = 0; hh < 2; ++hh) {
         const int j = 32 * q + 16 * hh;
+        if (j >= D) break;
         const bool hi = j < a.split;
         const int bits = hi ? a.bits_hi : a.bits_lo;
         uint8_t* dst = hi ? a.dst.codes_hi + (int64_t)r * a.dst.hi_head_stride + (int64_t)(dst0 + v) * a.row_hi +
@@ -252,29 +289,31 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
   if (!a.proj) return;
 
   // QJL sketch of the residual r = x - n * (c[idx] @ R) (cache.py:396-427).
-  // Reconstruct in rotated space first: xs[v][j] <- c[idx_j] (overwrites x_n).
+  // Reconstruct in rotated space first: xs[v][j] <- c[idx_j] (overwrites x_n;
+  // zeros past D).
   __syncthreads();
   if (vok) {
 #pragma unroll
-    for (int c = 0; c < 32; ++c) xs[v * G::XS + 32 * q + c] = cen[32 * q + c < a.split ? 0 : 1][code[c]];
+    for (int c = 0; c < 32; ++c)
+      xs[v * G::XS + 32 * q + c] = 32 * q + c < D ? cen[32 * q + c < a.split ? 0 : 1][code[c]] : 0.f;
   }
 #pragma unroll
   for (int c = 0; c < 32; ++c) acc[c] = 0.f;
   for (int i0 = 0; i0 < D; i0 += G::TI) {
     __syncthreads();
-    stage_tile<D, false>(a.rot, i0, mt);
+    stage_tile<DP, false>(a.rot, D, i0, mt);
     __syncthreads();
-    tile_madd<D>(xs + vr * G::XS, mt, i0, q, acc);
+    tile_madd<DP>(xs + vr * G::XS, mt, i0, q, acc);
   }
   __syncthreads();
-  // residual in xs (float32: x - n * acc)
+  // residual in xs (float32: x - n * acc; zeros past D)
   if (vok) {
     const float n = nrm[v];
 #pragma unroll
     for (int c = 0; c < 32; ++c) {
       const int i = 32 * q + c;
-      const float x = v < nv ? load_elem(a.x, xrow + (int64_t)v * D + i, a.x_dtype) : 0.f;
-      xs[v * G::XS + i] = x - n * acc[c];
+      const float x = v < nv && i < D ? load_elem(a.x, xrow + (int64_t)v * D + i, a.x_dtype) : 0.f;
+      xs[v * G::XS + i] = i < D ? x - n * acc[c] : 0.f;
     }
   }
   __syncthreads();
@@ -290,20 +329,20 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
   // proj = r @ S^T, m outputs in segments of 32 (S rows are projections).
   const int nseg_m = a.qjl_m / 32;
   for (int s0 = 0; s0 < nseg_m; s0 += G::NSEG) {
-    // Stage S^T columns [32*s0, 32*s0 + D) in tiles: reuse mt with rows i of S^T.
+    // Stage S^T columns [32*s0, 32*s0 + DP) in tiles: reuse mt with rows i of S^T.
     const int qs = s0 + q;
 #pragma unroll
     for (int c = 0; c < 32; ++c) acc[c] = 0.f;
     for (int i0 = 0; i0 < D; i0 += G::TI) {
       __syncthreads();
-      for (int e = tid; e < G::TI * D; e += blockDim.x) {
-        const int ii = e / D, j = e % D;  // j indexes projection 32*s0 + j
+      for (int e = tid; e < G::TI * DP; e += blockDim.x) {
+        const int ii = e / DP, j = e % DP;  // j indexes projection 32*s0 + j
         const int mrow = 32 * s0 + j;
         mt[ii * G::MROW + (j >> 5) * G::SEGP + (j & 31)] =
-            mrow < a.qjl_m ? a.proj[(int64_t)mrow * D + i0 + ii] : 0.f;
+            mrow < a.qjl_m && i0 + ii < D ? a.proj[(int64_t)mrow * D + i0 + ii] : 0.f;
       }
       __syncthreads();
-      tile_madd<D>(xs + vr * G::XS, mt, i0, q, acc);
+      tile_madd<DP>(xs + vr * G::XS, mt, i0, q, acc);
     }
     if (v < nv && qs < nseg_m) {
       uint32_t word = 0;
@@ -479,16 +518,18 @@ struct DequantArgs {
   const float* cen_hi;
   const float* cen_lo;
   const float* proj;
+  int d;  // head_dim
   int bits_hi, bits_lo, split, qjl_m, apply_qjl;
   int row_hi, row_lo, row_sign;
 };
 
-template <int D>
+template <int DP>
 __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
-  using G = Geo<D>;
+  using G = Geo<DP>;
   __shared__ float ys[G::VPW * G::XS];
   __shared__ float mt[G::TI * G::MROW];
   __shared__ float cen[2][16];
+  const int D = a.d;
   const int r = blockIdx.y;
   const int b = r / a.span.heads;
   const int n_tok = a.span.n_tok_b ? a.span.n_tok_b[b] : a.span.n_tok;
@@ -504,11 +545,13 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
   }
   __syncthreads();
   const int v = tid / G::NSEG, q = tid % G::NSEG;
-  const bool vok = v < G::VPW;            // false only for the spare thread of D = 96
+  const bool vok = v < G::VPW;            // false only for the spare threads when NSEG does not divide 256
   const int vr = vok ? v : G::VPW - 1;
   uint32_t code[32];
-  if (v < nv) {
-    if ((a.split & 31) == 0) {
+#pragma unroll
+  for (int c = 0; c < 32; ++c) code[c] = 0;
+  if (v < nv && 32 * q < D) {
+    if (whole_segment(q, D, a.split, a.row_hi, a.row_lo)) {
       const bool hi = 32 * q < a.split;
       const int bits = hi ? a.bits_hi : a.bits_lo;
       const uint8_t* src = hi ? a.src.codes_hi + (int64_t)r * a.src.hi_head_stride +
@@ -519,6 +562,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
     } else {  // halves of 16 codes, byte loads
       for (int hh = 0; hh < 2; ++hh) {
         const int j = 32 * q + 16 * hh;
+        if (j >= D) break;
         const bool hi = j < a.split;
         const int bits = hi ? a.bits_hi : a.bits_lo;
         const uint8_t* src = hi ? a.src.codes_hi + (int64_t)r * a.src.hi_head_stride +
@@ -528,37 +572,34 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
         load_half(bits, src, code, 16 * hh);
       }
     }
-  } else {
-#pragma unroll
-    for (int c = 0; c < 32; ++c) code[c] = 0;
   }
   if (vok) {
 #pragma unroll
-    for (int c = 0; c < 32; ++c) ys[v * G::XS + 32 * q + c] = cen[32 * q + c < a.split ? 0 : 1][code[c]];
+    for (int c = 0; c < 32; ++c)
+      ys[v * G::XS + 32 * q + c] = 32 * q + c < D ? cen[32 * q + c < a.split ? 0 : 1][code[c]] : 0.f;
   }
   float acc[32];
 #pragma unroll
   for (int c = 0; c < 32; ++c) acc[c] = 0.f;
   for (int i0 = 0; i0 < D; i0 += G::TI) {
     __syncthreads();
-    stage_tile<D, false>(a.rot, i0, mt);
+    stage_tile<DP, false>(a.rot, D, i0, mt);
     __syncthreads();
-    tile_madd<D>(ys + vr * G::XS, mt, i0, q, acc);
+    tile_madd<DP>(ys + vr * G::XS, mt, i0, q, acc);
   }
   const float n = v < nv ? a.src.norms[(int64_t)r * a.src.norm_head_stride + src0 + v] : 0.f;
 #pragma unroll
   for (int c = 0; c < 32; ++c) acc[c] *= n;
 
   if (a.apply_qjl) {
-    // + sqrt(pi/2)/D * gamma * (z @ S), z = +-1 from the stored signs.
+    // + sqrt(pi/2)/D * gamma * (z @ S), z = +-1 from the stored signs, in
+    // passes of DP projections (the segments of the tile).
     __syncthreads();
     const int nseg_m = a.qjl_m / 32;
-    // z rows into ys (m <= 256 fits the padded tile width only when m <= D;
-    // process the projections in chunks of D).
     float corr[32];
 #pragma unroll
     for (int c = 0; c < 32; ++c) corr[c] = 0.f;
-    for (int m0 = 0; m0 < a.qjl_m; m0 += D) {
+    for (int m0 = 0; m0 < a.qjl_m; m0 += DP) {
       __syncthreads();
       if (v < nv) {
         const uint32_t* sg = reinterpret_cast<const uint32_t*>(
@@ -572,12 +613,17 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
 #pragma unroll
         for (int c = 0; c < 32; ++c) ys[v * G::XS + 32 * q + c] = 0.f;
       }
-      const int mi = min(D, a.qjl_m - m0);
+      // rows m0 + i of S (i < DP), columns < D
+      const int mi = min(DP, a.qjl_m - m0);
       for (int i0 = 0; i0 < mi; i0 += G::TI) {
         __syncthreads();
-        stage_tile<D, false>(a.proj + (int64_t)m0 * D, i0, mt);
+        for (int e = tid; e < G::TI * DP; e += blockDim.x) {
+          const int ii = e / DP, j = e % DP;
+          mt[ii * G::MROW + (j >> 5) * G::SEGP + (j & 31)] =
+              i0 + ii < mi && j < D ? a.proj[(int64_t)(m0 + i0 + ii) * D + j] : 0.f;
+        }
         __syncthreads();
-        tile_madd<D>(ys + vr * G::XS, mt, i0, q, corr);
+        tile_madd<DP>(ys + vr * G::XS, mt, i0, q, corr);
       }
     }
     if (v < nv) {
@@ -587,10 +633,12 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
       for (int c = 0; c < 32; ++c) acc[c] = fmaf(sc, corr[c], acc[c]);
     }
   }
-  if (v < nv) {
+  if (v < nv && 32 * q < D) {
     float4* o = reinterpret_cast<float4*>(a.out + (int64_t)r * a.out_hs + (int64_t)(dst0 + v) * D + 32 * q);
+    const int nk = min(8, (D - 32 * q) / 4);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) o[k] = make_float4(acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]);
+    for (int k = 0; k < 8; ++k)
+      if (k < nk) o[k] = make_float4(acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]);
   }
 }
 
@@ -805,6 +853,7 @@ int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x
   a.cen_lo = codec->split < codec->d ? codec->centroids_lo : codec->centroids_hi;
   a.proj = qjl ? codec->qjl_proj : nullptr;
   a.qjl_m = qjl ? codec->qjl_m : 0;
+  a.d = codec->d;
   a.bits_hi = codec->bits_hi;
   a.bits_lo = codec->split < codec->d ? codec->bits_lo : codec->bits_hi;
   a.split = codec->split;
@@ -826,28 +875,11 @@ int tq_compress(const tq_codec* codec, const void* x, int32_t x_dtype, int64_t x
     TQ_LAUNCH_CHECK("tq_compress");
     return TQ_OK;
   }
-  switch (codec->d) {
-    case 64: {
-      dim3 g((span->n_tok + Geo<64>::VPW - 1) / Geo<64>::VPW, span->rows);
-      hipLaunchKernelGGL(compress_kernel<64>, g, dim3(256), 0, s, a);
-      break;
-    }
-    case 96: {
-      dim3 g((span->n_tok + Geo<96>::VPW - 1) / Geo<96>::VPW, span->rows);
-      hipLaunchKernelGGL(compress_kernel<96>, g, dim3(256), 0, s, a);
-      break;
-    }
-    case 128: {
-      dim3 g((span->n_tok + Geo<128>::VPW - 1) / Geo<128>::VPW, span->rows);
-      hipLaunchKernelGGL(compress_kernel<128>, g, dim3(256), 0, s, a);
-      break;
-    }
-    default: {
-      dim3 g((span->n_tok + Geo<256>::VPW - 1) / Geo<256>::VPW, span->rows);
-      hipLaunchKernelGGL(compress_kernel<256>, g, dim3(256), 0, s, a);
-      break;
-    }
-  }
+  launch_padded(codec->d, [&](auto dp) {
+    constexpr int DP = decltype(dp)::value;
+    dim3 g((span->n_tok + Geo<DP>::VPW - 1) / Geo<DP>::VPW, span->rows);
+    hipLaunchKernelGGL(compress_kernel<DP>, g, dim3(256), 0, s, a);
+  });
   TQ_LAUNCH_CHECK("tq_compress");
   return TQ_OK;
 }
@@ -877,6 +909,7 @@ int tq_dequantize(const tq_codec* codec, const tq_store* src, const tq_span* spa
   a.proj = qjl ? codec->qjl_proj : nullptr;
   a.qjl_m = qjl ? codec->qjl_m : 0;
   a.apply_qjl = qjl ? 1 : 0;
+  a.d = codec->d;
   a.bits_hi = codec->bits_hi;
   a.bits_lo = codec->split < codec->d ? codec->bits_lo : codec->bits_hi;
   a.split = codec->split;
@@ -884,28 +917,11 @@ int tq_dequantize(const tq_codec* codec, const tq_store* src, const tq_span* spa
   a.row_lo = row_bytes(codec->d - codec->split, a.bits_lo);
   a.row_sign = a.qjl_m / 8;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (codec->d) {
-    case 64: {
-      dim3 g((span->n_tok + Geo<64>::VPW - 1) / Geo<64>::VPW, span->rows);
-      hipLaunchKernelGGL(dequant_kernel<64>, g, dim3(256), 0, s, a);
-      break;
-    }
-    case 96: {
-      dim3 g((span->n_tok + Geo<96>::VPW - 1) / Geo<96>::VPW, span->rows);
-      hipLaunchKernelGGL(dequant_kernel<96>, g, dim3(256), 0, s, a);
-      break;
-    }
-    case 128: {
-      dim3 g((span->n_tok + Geo<128>::VPW - 1) / Geo<128>::VPW, span->rows);
-      hipLaunchKernelGGL(dequant_kernel<128>, g, dim3(256), 0, s, a);
-      break;
-    }
-    default: {
-      dim3 g((span->n_tok + Geo<256>::VPW - 1) / Geo<256>::VPW, span->rows);
-      hipLaunchKernelGGL(dequant_kernel<256>, g, dim3(256), 0, s, a);
-      break;
-    }
-  }
+  launch_padded(codec->d, [&](auto dp) {
+    constexpr int DP = decltype(dp)::value;
+    dim3 g((span->n_tok + Geo<DP>::VPW - 1) / Geo<DP>::VPW, span->rows);
+    hipLaunchKernelGGL(dequant_kernel<DP>, g, dim3(256), 0, s, a);
+  });
   TQ_LAUNCH_CHECK("tq_dequantize");
   return TQ_OK;
 }

@@ -100,7 +100,11 @@ class TurboQuantKVCache:
     """TurboQuant-compressed KV cache (cache.py:19-116)."""
 
     step = 256
-    ATTEND_HEAD_DIMS = (64, 96, 128, 256)  # head_dims of the codecs and the decode-attention kernels
+    @staticmethod
+    def attend_head_dim(head_dim: int) -> bool:
+        """head_dims the codecs and the attention kernels take: multiples of 16
+        in [16, 256] (the MFMA kernels at 128, the general kernels at all)."""
+        return 16 <= head_dim <= 256 and head_dim % 16 == 0
 
     def __init__(self, head_dim: int = 128, num_kv_heads: int = 1, key_bits: float = 4,
                  value_bits: float = 2, residual_window: int = 128, rotation_seed: int = DEFAULT_SEED,
@@ -118,8 +122,12 @@ class TurboQuantKVCache:
         self.qjl_n_proj = qjl_n_proj
         if qjl_correction:
             check_qjl_count(qjl_n_proj)
-        _codec.split_bits(key_bits, head_dim)
-        _codec.split_bits(value_bits, head_dim)
+        if not self.attend_head_dim(head_dim):
+            raise ValueError(f"head_dim {head_dim} not supported: a multiple of 16 in [16, 256]")
+        for bits in (key_bits, value_bits):
+            if _codec.split_bits(bits, head_dim)[2] % 16:
+                raise ValueError(f"fractional bits {bits} need head_dim a multiple of 32 (the two halves of "
+                                 f"head_dim {head_dim} must be multiples of 16)")
         self._k_fractional = key_bits != int(key_bits)
         self._v_fractional = value_bits != int(value_bits)
         self._device = torch.device(device) if device is not None else None

@@ -49,8 +49,9 @@ def lloyd_max(d: int, bits: int, num_iter: int = 500, grid_size: int = 10000) ->
 
     Density: N(0, 1/d) for d >= 32, else the Beta((d-1)/2, (d-1)/2) law on
     [-1, 1]; support +-6/sqrt(d) on a uniform grid; quantile initialisation;
-    boundaries at centroid midpoints; stop when no centroid moves by 1e-12
-    (codebook.py:55-116). Returns float32 (centroids, boundaries).
+    boundaries at centroid midpoints; stop when a step moves no centroid by 1e-12
+    (codebook.py:55-116), keeping the centroids from before the step that
+    moved none by 1e-12. Returns float32 (centroids, boundaries).
     """
     levels = 1 << bits
     sigma = 1.0 / math.sqrt(d)
@@ -70,10 +71,9 @@ def lloyd_max(d: int, bits: int, num_iter: int = 500, grid_size: int = 10000) ->
             sel = (x >= edges[i]) & upper
             wsum = pdf[sel].sum()
             new[i] = np.sum(x[sel] * pdf[sel]) / wsum if wsum > 0 else c[i]
-        done = np.max(np.abs(new - c)) < 1e-12
-        c = new
-        if done:
+        if np.max(np.abs(new - c)) < 1e-12:  # converged: the centroids before this step are kept
             break
+        c = new
     b = (c[:-1] + c[1:]) / 2.0
     return c.astype(np.float32), b.astype(np.float32)
 

@@ -71,7 +71,7 @@ def fused_supported(cache, hq: int, hkv: int, head_dim: int) -> bool:
         return False
     if isinstance(cache, FP16KVCache):
         return head_dim == 128 and hq // hkv in ATTEND_GROUPS
-    return head_dim in TurboQuantKVCache.ATTEND_HEAD_DIMS
+    return TurboQuantKVCache.attend_head_dim(head_dim)
 
 
 class TurboQuantLayer(CacheLayerMixin):

@@ -43,7 +43,7 @@ QJL_SEED = 12345        # qjl.py:20
 NORM_EPS = np.float32(1e-10)  # cache.py:237
 
 __all__ = [
-    "CODEBOOK_DIR", "rotation_matrix", "projection_matrix", "codebook",
+    "CODEBOOK_DIR", "rotation_matrix", "projection_matrix", "codebook", "lloyd_max_table",
     "quantize_scalar", "dequantize_scalar", "pack_bits", "unpack_bits",
     "sumsq_f64", "vector_norms", "normalize", "rotate_f64", "split_bits", "compress",
     "CompressResult", "dequantize", "boundary_margin", "near_boundary_mask",
@@ -79,9 +79,63 @@ def projection_matrix(d: int, m: int, seed: int = QJL_SEED) -> np.ndarray:
 # --------------------------------------------------------------------------
 # a3-a5: codebook, scalar quantizer
 # --------------------------------------------------------------------------
+_LM_CACHE: dict = {}
+
+
+def lloyd_max_table(d: int, bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """Lloyd-Max quantizer of one coordinate of a rotated unit vector, as the
+    reference computes the tables it does not ship (codebook.py:55-116): a
+    10,000-point grid over +-6/sqrt(d); the density N(0, 1/d) for d >= 32,
+    else Beta((d-1)/2, (d-1)/2) on [-1, 1] (codebook.py:35-52), normalised on
+    the grid; centroids initialised at the quantiles (i + 1/2)/L of the grid
+    CDF; each step sets the boundaries to the centroid midpoints and every
+    centroid to the grid mean of its cell (cells [b_i, b_i+1), the last one
+    closed; an empty cell keeps its centroid); the loop stops, keeping the
+    centroids from before the step, once a step moves none by 1e-12, or after
+    500 steps. float32 (centroids, boundaries)."""
+    key = (d, bits)
+    if key in _LM_CACHE:
+        return _LM_CACHE[key]
+    L = 1 << bits
+    sig = 1.0 / math.sqrt(d)
+    a, b = -6.0 * sig, 6.0 * sig
+    grid = np.linspace(a, b, 10000)
+    step = grid[1] - grid[0]
+    if d >= 32:  # the same float64 operations as the reference's gaussian_pdf (codebook.py:46-49)
+        var = 1.0 / d
+        dens = np.exp(-0.5 * grid * grid / var) / math.sqrt(2.0 * math.pi * var)
+    else:
+        from scipy.special import gammaln
+        al = 0.5 * (d - 1)
+        lc = gammaln(2 * al) - 2 * gammaln(al) - (2 * al - 1) * math.log(2.0)
+        dens = np.exp(lc + (al - 1) * np.log(np.maximum(1.0 - grid * grid, 1e-300)))
+    dens = dens / (dens.sum() * step)
+    cum = np.cumsum(dens) * step
+    cum = cum / cum[-1]
+    cen = np.interp(np.linspace(0.5 / L, 1 - 0.5 / L, L), cum, grid)
+    for _ in range(500):
+        edges = np.concatenate(([a], (cen[:-1] + cen[1:]) / 2.0, [b]))
+        upd = cen.copy()
+        for i in range(L):
+            inside = (grid >= edges[i]) & ((grid <= edges[i + 1]) if i == L - 1 else (grid < edges[i + 1]))
+            wt = dens[inside]
+            if wt.sum() > 0:
+                upd[i] = (grid[inside] * wt).sum() / wt.sum()
+        if np.abs(upd - cen).max() < 1e-12:
+            break
+        cen = upd
+    out = (cen.astype(np.float32), ((cen[:-1] + cen[1:]) / 2.0).astype(np.float32))
+    _LM_CACHE[key] = out
+    return out
+
+
 def codebook(d: int, bits: int) -> tuple[np.ndarray, np.ndarray]:
-    """Shipped Lloyd-Max table (codebook.py:146-174): (centroids, boundaries) f32."""
+    """Shipped Lloyd-Max table (codebook.py:146-174): (centroids, boundaries)
+    f32; sizes the reference does not ship are computed as it computes them
+    (``lloyd_max_table``)."""
     path = os.path.join(CODEBOOK_DIR, f"codebook_d{d}_b{bits}.npz")
+    if not os.path.exists(path):
+        return lloyd_max_table(d, bits)
     with np.load(path, allow_pickle=False) as z:
         return z["centroids"].astype(np.float32), z["boundaries"].astype(np.float32)
 

@@ -71,9 +71,13 @@ def test_host_side_validation_errors():
     assert lib.tq_pack_codes(None, 1, 128, 5, None, None) == _lib.TQ_ERR_UNSUPPORTED
     assert b"Unsupported bit-width" in lib.tq_last_error()
     assert lib.tq_unpack_codes(None, 1, 5, 3, None, None) == _lib.TQ_ERR_INVALID
-    codec = _lib.Codec(d=80, bits_hi=4, bits_lo=4, split=80)
+    codec = _lib.Codec(d=72, bits_hi=4, bits_lo=4, split=72)  # head_dims are multiples of 16 in [16, 256]
     assert lib.tq_compress(ctypes.byref(codec), None, 0, 0, None, None, None) == _lib.TQ_ERR_UNSUPPORTED
-    assert b"head_dim 80" in lib.tq_last_error()
+    assert b"head_dim 72" in lib.tq_last_error()
+    codec = _lib.Codec(d=272, bits_hi=4, bits_lo=4, split=272)
+    assert lib.tq_compress(ctypes.byref(codec), None, 0, 0, None, None, None) == _lib.TQ_ERR_UNSUPPORTED
+    codec = _lib.Codec(d=80, bits_hi=4, bits_lo=4, split=80)  # a valid shape: the NULL rotation is refused
+    assert lib.tq_compress(ctypes.byref(codec), None, 0, 0, None, None, None) == _lib.TQ_ERR_INVALID
     codec = _lib.Codec(d=96, bits_hi=4, bits_lo=3, split=40)  # halves of 16 codes at most
     assert lib.tq_compress(ctypes.byref(codec), None, 0, 0, None, None, None) == _lib.TQ_ERR_UNSUPPORTED
     codec = _lib.Codec(d=96, bits_hi=4, bits_lo=3, split=48)  # a valid shape: the NULL rotation is refused

@@ -94,6 +94,53 @@ def test_codebook_matches_runtime_lloyd_max():
         assert np.all(np.diff(c) > 0)
 
 
+def test_lloyd_max_restatement_pinned():
+    """The oracle's Lloyd-Max for unshipped sizes (codebook.py:55-116): within
+    2e-4 of every shipped table (the reference's generator differs from its
+    own shipped tables by ~1e-4), the 1-bit Gaussian closed form (centroids
+    +-sqrt(2/pi)/sqrt(d)), symmetry, and the runtime tables of the package
+    equal to it bit for bit at head_dims that ship no table."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(__file__)), "mlx-turboquant_amd"))
+    from turboquant_amd.codebook import lloyd_max
+    for d in (64, 96, 128, 256):
+        for bits in (2, 3, 4):
+            c, b = O.lloyd_max_table(d, bits)
+            path = os.path.join(O.CODEBOOK_DIR, f"codebook_d{d}_b{bits}.npz")
+            with np.load(path, allow_pickle=False) as z:
+                c0, b0 = z["centroids"], z["boundaries"]
+            assert np.allclose(c, c0, atol=2e-4) and np.allclose(b, b0, atol=2e-4), (d, bits)
+    # (the grid's fixed point can sit a grid step off the symmetric one: d = 80)
+    for d in (48, 80, 160):
+        c, b = O.lloyd_max_table(d, 1)
+        assert np.allclose(c, [-math.sqrt(2 / math.pi / d), math.sqrt(2 / math.pi / d)], rtol=2e-3)
+        assert abs(float(b[0])) < 2e-4
+    for d in (16, 48, 80, 112, 160, 224):
+        for bits in (1, 2, 3, 4):
+            c, b = O.lloyd_max_table(d, bits)
+            assert np.allclose(c, -c[::-1], atol=3e-3 * float(np.abs(c).max())) and np.all(np.diff(c) > 0)
+            c2, b2 = lloyd_max(d, bits)
+            assert np.array_equal(c, c2) and np.array_equal(b, b2), (d, bits)
+    # shipped sizes read the shipped tables; others fall back to the runtime tables
+    assert np.array_equal(O.codebook(80, 3)[0], O.lloyd_max_table(80, 3)[0])
+
+
+def test_cache_head_dim_rules():
+    """Multiples of 16 in [16, 256]; fractional widths need both halves to be
+    multiples of 16 (head_dim a multiple of 32)."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(__file__)), "mlx-turboquant_amd"))
+    from turboquant_amd import TurboQuantKVCache
+    for d in (16, 48, 80, 112, 160, 256):
+        TurboQuantKVCache(head_dim=d, key_bits=3, value_bits=2)
+    for d in (8, 72, 264):
+        with pytest.raises(ValueError):
+            TurboQuantKVCache(head_dim=d, key_bits=4, value_bits=2)
+    TurboQuantKVCache(head_dim=160, key_bits=3.5, value_bits=2.5)
+    with pytest.raises(ValueError):
+        TurboQuantKVCache(head_dim=80, key_bits=3.5, value_bits=2)
+
+
 # -------------------------------------------------------- scalar quantizer
 def test_quantize_known_answers():
     c, b = O.codebook(128, 4)

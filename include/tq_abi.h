@@ -47,10 +47,10 @@ enum {
  * [split, d) use bits_lo with split == d/2 (mlx_turboquant/cache.py:63-84).
  * Both codebooks are the d-dimensional Lloyd-Max tables (codebook.py:146-174). */
 typedef struct tq_codec {
-  int32_t d;                   /* head_dim: 64, 96, 128 or 256 */
+  int32_t d;                   /* head_dim: a multiple of 16 in [16, 256] */
   int32_t bits_hi;             /* 1..4 */
   int32_t bits_lo;             /* 1..4 */
-  int32_t split;               /* multiple of 16 */
+  int32_t split;               /* a multiple of 16 in [16, d] */
   const float* rotation;       /* (d, d) row-major orthogonal R (rotation.py:17-36) */
   const float* centroids_hi;   /* (2^bits_hi,) */
   const float* boundaries_hi;  /* (2^bits_hi - 1,) */

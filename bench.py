@@ -602,6 +602,27 @@ def pmc_prefill_workload(n_q: int = 1024):
     print(json.dumps({"prefill_calls": 5, "n_q": n_q, "ctx": 32768}), flush=True)
 
 
+def pmc_general_workload():
+    """Short program for the general kernel's counter runs: one configs[1]-
+    shaped K3.5/V3.5 layer (T = 32768) on the general route (chunk_kernel),
+    5 decode calls."""
+    import torch
+    from turboquant_amd import TurboQuantKVCache
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(4100)
+    scale = torch.exp(torch.randn(128, generator=g, device=dev) * 0.5)
+    c = TurboQuantKVCache(head_dim=128, num_kv_heads=8, key_bits=3.5, value_bits=3.5, residual_window=128,
+                          fp16_sink_size=128)
+    c.update((torch.randn(1, 8, 32768, 128, generator=g, device=dev) * scale).half(),
+             torch.randn(1, 8, 32768, 128, generator=g, device=dev).half())
+    q = torch.randn(1, 32, 1, 128, generator=g, device=dev).half()
+    out = torch.empty(1, 32, 1, 128, dtype=torch.float32, device=dev)
+    for _ in range(5):
+        c.attend(q, out=out, general_kernel=True)
+    torch.cuda.synchronize()
+    print(json.dumps({"general_calls": 5, "ctx": 32768, "bits": 3.5}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -615,6 +636,7 @@ def main():
     ap.add_argument("--pmc-workload", action="store_true", help="short program for rocprofv3 --pmc runs")
     ap.add_argument("--pmc-compress", action="store_true", help="short compress program for rocprofv3 --pmc runs")
     ap.add_argument("--pmc-prefill", action="store_true", help="short prefill program for rocprofv3 runs")
+    ap.add_argument("--pmc-general", action="store_true", help="short general-kernel program for rocprofv3 runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -629,6 +651,9 @@ def main():
         return
     if args.pmc_prefill:
         pmc_prefill_workload()
+        return
+    if args.pmc_general:
+        pmc_general_workload()
         return
 
     import torch

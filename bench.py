@@ -623,6 +623,32 @@ def pmc_general_workload():
     print(json.dumps({"general_calls": 5, "ctx": 32768, "bits": 3.5}), flush=True)
 
 
+def pmc_config4_workload(steps: int = 4, calls: int = 5):
+    """Short program for the configs[4] kernel trace and counter runs: the
+    16-sequence ragged K4/V2 batch with the 128-projection sketch (lengths
+    ~ U[4096, 32768], seeded as in bench_config4), `steps` decode steps, then
+    `calls` attention calls."""
+    import numpy as np
+    import torch
+    from turboquant_amd.ragged import RaggedKVBatch
+    dev = torch.device("cuda", 0)
+    lens = np.random.RandomState(4).randint(4096, 32769, size=16)
+    rb = RaggedKVBatch(16, 8, 128, 4, 2, residual_window=128, fp16_sink_size=0, qjl_n_proj=128, device=dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    for b, T in enumerate(lens):
+        rb.load(b, torch.randn(8, int(T), 128, generator=g, device=dev).half(),
+                torch.randn(8, int(T), 128, generator=g, device=dev).half())
+    for _ in range(steps):
+        rb.step(torch.randn(16, 8, 128, generator=g, device=dev).half(),
+                torch.randn(16, 8, 128, generator=g, device=dev).half())
+    q = torch.randn(16, 32, 128, generator=g, device=dev).half()
+    out = torch.empty(16, 32, 128, dtype=torch.float32, device=dev)
+    for _ in range(calls):
+        rb.attend(q, out=out)
+    torch.cuda.synchronize()
+    print(json.dumps({"config4_calls": calls}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -637,6 +663,7 @@ def main():
     ap.add_argument("--pmc-compress", action="store_true", help="short compress program for rocprofv3 --pmc runs")
     ap.add_argument("--pmc-prefill", action="store_true", help="short prefill program for rocprofv3 runs")
     ap.add_argument("--pmc-general", action="store_true", help="short general-kernel program for rocprofv3 runs")
+    ap.add_argument("--pmc-config4", action="store_true", help="short configs[4] program for rocprofv3 runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -654,6 +681,9 @@ def main():
         return
     if args.pmc_general:
         pmc_general_workload()
+        return
+    if args.pmc_config4:
+        pmc_config4_workload()
         return
 
     import torch

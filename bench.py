@@ -374,8 +374,9 @@ def bench_config4(dev, steps: int = 12):
         byt = 8 * (int(rb.comp_len.sum()) * per_tok + int(rb.res_len.sum()) * 512) + 16 * 32 * 128 * 6
         ms_s, ms_a = float(np.median(t_step)), float(np.median(t_attn))
         res["qjl" if qjl_m else "no_qjl"] = {
-            "kernel": ("K4/V2 + sketch (qjl_bias_kernel, decode_partials_kernel with the key term, merge, "
-                       "qjl_value_kernel, qjl_final_kernel)") if qjl_m else "K4/V2 (decode_partials_kernel + merge)",
+            "kernel": ("K4/V2 + sketch (qjl_sq_kernel, decode_partials_kernel computing the key term from the "
+                       "sketch, merge, qjl_value_kernel, qjl_final_kernel)") if qjl_m
+                      else "K4/V2 (decode_partials_kernel + merge)",
             "layer_step_us": round(ms_s * 1e3, 1), "attend_us": round(ms_a * 1e3, 1),
             "attend_bytes": byt, "attend_GBps": round(byt / (ms_a * 1e-3) / 1e9, 1),
             "attend_back_to_back_us": round(ms_b * 1e3, 1),

@@ -769,9 +769,11 @@ static int group_heads(int G) {
 }
 
 // ---- QJL sketch terms around the K4/V2 kernels (K4 keys / V2 values with a
-// 1-bit sketch, qjl.py:23-94 as in the general path): a bias kernel adds the
-// key term to each compressed token's score (base 2), the partials kernel
-// stores the final scores, and after the merge a value kernel accumulates
+// 1-bit sketch, qjl.py:23-94 as in the general path): the key term of each
+// compressed token's score (base 2) comes from a bias kernel for the
+// uniform-batch kernels and is computed inside the persistent kernel (from
+// the sketch and S q) for the others; the partials kernel stores the final
+// scores, and after the merge a value kernel accumulates
 // u_h = sum_t p_t gamma_t z_t per projection (p the normalised softmax
 // weight of compressed token t) and a final kernel adds sqrt(pi/2)/d S^T u_h to
 // the output, as combine_kernel does for the general path.
@@ -1284,7 +1286,8 @@ static bool fast_eligible(const tq_codec* kc, const tq_codec* vc, const tq_attn_
   if (d->kv_dtype == TQ_BF16 && !uniform_route(vc, d, nwg, bpw, fpw)) return false;
   if (d->qjl && d->max_comp > 0 &&
       !((reinterpret_cast<uintptr_t>(d->kstore.signs) & 3) == 0 && d->kstore.sign_head_stride % 4 == 0 &&
-        (reinterpret_cast<uintptr_t>(d->vstore.signs) & 3) == 0 && d->vstore.sign_head_stride % 4 == 0))
+        (reinterpret_cast<uintptr_t>(d->vstore.signs) & 3) == 0 && d->vstore.sign_head_stride % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(d->kstore.gamma) & 3) == 0))
     return false;
   if (!aligned16(d->q)) return false;
   if (d->max_comp > 0 &&
@@ -1399,7 +1402,8 @@ static bool fill_uniform(UniformArgs& u, const tq_codec* kc, const tq_codec* vc,
 }
 
 static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part, bool qb,
-                       float* qjl_bias, float* scores, int64_t qb_hs, float* ml, int merge, hipStream_t s) {
+                       float* qjl_bias, float* scores, int64_t qb_hs, float* ml, int merge, hipStream_t s,
+                       const float* sq = nullptr) {
   const int G = d->hq / d->hkv;
   UniformArgs u;
   if (fill_uniform(u, kc, vc, d, part)) {
@@ -1409,7 +1413,18 @@ static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_des
   FastArgs f;
   fill_fast(f, kc, vc, d, part);
   f.qjl_bias = qjl_bias; f.scores = scores; f.qb_hs = qb_hs; f.ml = ml;
-  return launch_fast_decode(f, G, qb, merge, s);
+  // the persistent kernel computes the QJL key term itself (sketch and S q)
+  f.ksg = d->kstore.signs; f.ksg_hs = d->kstore.sign_head_stride;
+  f.kgam = d->kstore.gamma; f.kgam_hs = d->kstore.gamma_head_stride;
+  f.sq = sq;
+  f.qm = kc->qjl_m;
+  return launch_fast_decode(f, G, qb ? (kc->qjl_m <= 128 ? 1 : 2) : 0, merge, s);
+}
+
+// The uniform-batch kernels take this K4/V2 call (else the persistent kernel).
+static bool k4v2_uniform(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d) {
+  UniformArgs u;
+  return fill_uniform(u, kc, vc, d, nullptr);
 }
 
 // The uniform-batch MFMA kernels for the other integer widths (key and value
@@ -1531,8 +1546,11 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     default: hipLaunchKernelGGL((qjl_sq_kernel<8>), sgrid, dim3(256), 0, s, qa); break;
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl S q");
+  // the key term: a bias kernel for the uniform-batch kernels; the persistent
+  // kernel computes it from the sketch and S q
+  const bool uniform = k4v2_uniform(kc, vc, d);
   const dim3 bgrid((unsigned)((QL.qb_hs + QBC * QCH - 1) / (QBC * QCH)), d->hkv, d->batch);
-  switch (G * 2 + (w8 ? 1 : 0)) {
+  if (uniform) switch (G * 2 + (w8 ? 1 : 0)) {
     case 2: hipLaunchKernelGGL((qjl_bias_kernel<1, 1>), bgrid, dim3(NT), 0, s, qa); break;
     case 3: hipLaunchKernelGGL((qjl_bias_kernel<1, 2>), bgrid, dim3(NT), 0, s, qa); break;
     case 4: hipLaunchKernelGGL((qjl_bias_kernel<2, 1>), bgrid, dim3(NT), 0, s, qa); break;
@@ -1544,7 +1562,7 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl bias");
   if (launch_k4v2(kc, vc, d, reinterpret_cast<float*>(ws + QL.part), true, qa.bias, const_cast<float*>(qa.scores),
-                  QL.qb_hs, const_cast<float*>(qa.ml), 1, s) != 0)
+                  QL.qb_hs, const_cast<float*>(qa.ml), 1, s, qa.sq) != 0)
     TQ_LAUNCH_CHECK("tq_decode_attention qjl fast");
   const dim3 vgrid((unsigned)QL.nvc, d->hkv, d->batch);
   switch (G * 2 + (w8 ? 1 : 0)) {

@@ -64,6 +64,13 @@ struct FastArgs {
   float* ml;             // merge output: (batch, hq, 2) global max and sum, or NULL
   int32_t* plan_tab;     // (batch, 2): first partial slot N_b and chunks n_b per kv head of each sequence,
                          // written by the partials kernel when uni == 0 (workspace, after the partials)
+  // QJL key term computed in the partials kernel (QB): the keys' 128-projection
+  // sketch (16-byte sign rows, one residual norm per token) and S (scale q)
+  // per query head, (batch, hq, 128) float32
+  const uint8_t* ksg; int64_t ksg_hs;  // key sign rows (bytes)
+  const float* kgam;  int64_t kgam_hs; // key residual norms (elements)
+  const float* sq;
+  int qm;                // projections of the sketch (a multiple of 32, at most 256): sign rows of qm / 8 bytes
 };
 
 // Host-side sizing of the K4/V2 path for a call: workgroups, chunks per
@@ -73,9 +80,11 @@ void fast_plan_host(int batch, int hkv, int max_comp, int max_sink, int max_res,
 // The uniform plan (every sequence at the maximal lengths): T, n and V.
 void fast_uniform_plan(int batch, int hkv, int max_comp, int max_sink, int max_res, int nwg, int chunks, int& T,
                        int& nu, int& V);
-// Launches the partials kernel (QB: with the QJL key bias, scores stored)
-// and, when merge != 0, the merge kernel. G in {1, 2, 4, 8}.
-int launch_fast_decode(const FastArgs& a, int G, bool qb, int merge, hipStream_t s);
+// Launches the partials kernel and, when merge != 0, the merge kernel. G in
+// {1, 2, 4, 8}; qb 1 / 2: with the QJL key term of a sketch of at most 128 /
+// 256 projections computed in the kernel (ksg, kgam, sq, qm), the final scores
+// stored.
+int launch_fast_decode(const FastArgs& a, int G, int qb, int merge, hipStream_t s);
 
 // Merge of per-workgroup partials in original space ([M, L, pad, pad,
 // out[128] / L] per query head, nwg per (sequence, kv head)) into out

@@ -90,22 +90,38 @@ constexpr float Q_LOW = 0.25f;
 // the code word (code byte as address bits 8-15). NCP = 32: two tables of
 // 64 KB; NCP = 16: one table whose row e holds the 16 key replicas, then the
 // 16 value replicas.
-template <int G>
+//
+// With the QJL key term (QB = 1 for sketches of at most 128 projections, 2
+// for at most 256), the combine region holds, while the blocks run, the table
+// of the 16 patterns of 4 sign bits (row n: the halves (bit j of n ? 1 : -1),
+// j < 4, in 32 replicas: its address is a byte permute too), the S q B
+// operands of the segment's heads (zero past the sketch's projections) and
+// their key-term factors; the norm staging also holds the key residual norms.
+template <int G, int QB = 0>
 struct Lay {
   static constexpr int NCP = G <= 4 ? 32 : 16;
   static constexpr uint32_t tabs = NCP == 32 ? 0x20000u : 0x10000u;  // bytes of the tables
   static constexpr int CMS = FD + 4;                                  // floats per combine row: 128 sums, m, l
   static constexpr uint32_t cmb = tabs;                               // [FW][G][CMS] f32
+  static constexpr uint32_t slut = cmb;                               // QB: 16 rows x 256 B sign patterns
+  static constexpr uint32_t SQS = 256 * (QB > 1 ? 2 : 1) + 16;       // QB: bytes per (head, part) of sqo
+  static constexpr uint32_t sqo = slut + 4096;                        // QB: [G][2 parts][SQS] S q B operands
+  static constexpr uint32_t kfx = sqo + G * 2 * SQS;                  // QB: [G] f32 key-term factors
+  static constexpr uint32_t CMB_BYTES = !QB || FW * G * CMS * 4 >= kfx + 64 - cmb ? FW * G * CMS * 4 : kfx + 64 - cmb;
   static constexpr uint32_t QOPS = 528;                               // bytes per (head, part) of qop (512 + 16)
-  static constexpr uint32_t qop = cmb + FW * G * CMS * 4;             // [G][2 parts][QOPS] rotated-q B operands
+  static constexpr uint32_t qop = cmb + CMB_BYTES;                    // [G][2 parts][QOPS] rotated-q B operands
   static constexpr uint32_t qfo = qop + G * 2 * QOPS;                 // [G][2 parts][4 q4][4 kb][16 B] original-space q
-  static constexpr uint32_t nst = qfo + G * 2 * 256;                  // [FW][64] f32 norm staging
-  static constexpr uint32_t pre = nst + FW * 256;                     // [G][CMS] parked fp16 tiles: sums, m, l
+  static constexpr uint32_t NSTW = QB ? 384 : 256;                    // norm staging bytes per wave
+  static constexpr uint32_t nst = qfo + G * 2 * 256;                  // [FW][NSTW / 4] f32 norm staging
+  static constexpr uint32_t pre = nst + FW * NSTW;                    // [G][CMS] parked fp16 tiles: sums, m, l
   static constexpr uint32_t total = pre + G * CMS * 4;
   static constexpr uint32_t qstage = G * FD * 4;                      // bytes of the query rows as given (own array)
 };
-static_assert(Lay<4>::total + Lay<4>::qstage <= 160 * 1024 && Lay<8>::total + Lay<8>::qstage <= 160 * 1024,
-              "LDS of one workgroup");
+static_assert(Lay<4>::total + Lay<4>::qstage <= 160 * 1024 && Lay<8>::total + Lay<8>::qstage <= 160 * 1024 &&
+              Lay<4, 2>::total + Lay<4, 2>::qstage <= 160 * 1024 &&
+              Lay<8, 2>::total + Lay<8, 2>::qstage <= 160 * 1024, "LDS of one workgroup");
+static_assert((Lay<1, 1>::slut & 0xFFFFu) == 0 && (Lay<8, 1>::slut & 0xFFFFu) == 0,
+              "sign-pattern addresses are byte permutes");
 
 __device__ inline half8 as_h8(u4 v) { return __builtin_bit_cast(half8, v); }
 
@@ -375,13 +391,33 @@ __device__ inline Seg segment(const FastArgs& a, const Plan& P, int v, int v1) {
   return S;
 }
 
+// max / sum over the 64 lanes of a wave (every lane gets the result)
+__device__ inline float wave_max(float v) {
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  v = fmaxf(v, row_ror<1>(v));
+  return rows_max(v);
+}
+
+__device__ inline float wave_sum(float v) {
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  return rows_sum(v);
+}
+
 // ------------------------------------------------------------ partials kernel
 // One packed block of a wave, loaded from HBM (lane r, q4)
 struct Blk {
   u4 k0, k1;      // key codes of tokens t0 + r and t0 + 16 + r, bytes 16*q4 ..
   uint32_t v[8];  // value code halfword r of tokens A0..A3 (t0 + 4q4 + i), B0..B3 (t0 + 16 + 4q4 + i)
   float nk, nv;   // key / value norm of token t0 + (lane & 31)
-  float4 qb[2];   // QJL key term of the lane's tokens (tile `tile`, and tile 1 for G = 8)
+  // QJL key term (QB): key sign dwords 4 c + q4 (c < QB) of tokens t0 + r
+  // and t0 + 16 + r, key residual norm of token t0 + (lane & 31)
+  uint32_t ks0[2], ks1[2];
+  float gk;
 };
 
 // One fp16 tile (16 tokens of the [sink | ring] list) of wave FW - 1 (lane r, q4)
@@ -397,9 +433,9 @@ __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
 
 constexpr int WF16 = FW - 1;  // the wave that takes the fp16 tiles (it has the fewest packed blocks)
 
-template <int G, bool QB>
+template <int G, int QB>
 __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
-  using LY = Lay<G>;
+  using LY = Lay<G, QB>;
   __shared__ __align__(16) uint8_t smem[LY::total];
   // the G query rows of the segment as given, written by direct global->LDS
   // loads (an array of its own, so those loads are not ordered with smem)
@@ -474,8 +510,9 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
   Tile16 T16;
   Blk B0, B1, B2;
   int nkw = 0;
-  const uint8_t *kcodes = nullptr, *vcodes = nullptr;
-  const float *knorm = nullptr, *vnorm = nullptr;
+  const uint8_t *kcodes = nullptr, *vcodes = nullptr, *ksgn = nullptr;
+  const float *knorm = nullptr, *vnorm = nullptr, *kgam = nullptr;
+  float sqv[QB > 1 ? 4 : 2] = {};      // QB: S q of head w, projections (QB + 1) lane ..
   auto slot_t0 = [&](int m) { return (S.k0 + w + FW * m) << 5; };
   auto load_slot = [&](Blk& B, int m) {
     const bool live = m < nkw;
@@ -494,13 +531,18 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
     B.nk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rkn, no, 0, 0));
     B.nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvn, no, 0, 0));
     if constexpr (QB) {
-      const float* qbr = a.qjl_bias + ((int64_t)S.row * G + hd) * a.qb_hs + t0;
-      const __amdgpu_buffer_rsrc_t rb = rsrc(qbr, live ? min(32, (int)(a.qb_hs - t0)) * 4 : 0);
+      // dword q4 + 4 c of the sign rows of a.qm / 8 bytes; dwords past a row
+      // read the next token's (or zero past the block): their projections
+      // have zero S q operands
+      const int rb = a.qm >> 3;
+      const __amdgpu_buffer_rsrc_t rks = rsrc(ksgn + (int64_t)t0 * rb, n * rb);
+      const __amdgpu_buffer_rsrc_t rkg = rsrc(kgam + t0, n * 4);
 #pragma unroll
-      for (int t = 0; t < 2 / TS; ++t) {
-        const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rb, (16 * (t + tile) + 4 * q4) * 4, 0, 0);
-        B.qb[t] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
+      for (int c = 0; c < QB; ++c) {
+        B.ks0[c] = __builtin_amdgcn_raw_buffer_load_b32(rks, r * rb + 4 * q4 + 16 * c, 0, 0);
+        B.ks1[c] = __builtin_amdgcn_raw_buffer_load_b32(rks, (16 + r) * rb + 4 * q4 + 16 * c, 0, 0);
       }
+      B.gk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rkg, no, 0, 0));
     }
   };
   // row of token u of the [sink | ring] list (u clamped into the list)
@@ -544,6 +586,14 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
     vcodes = a.vc + (int64_t)S.row * a.v_hs;
     knorm = a.kn + (int64_t)S.row * a.kn_hs;
     vnorm = a.vn + (int64_t)S.row * a.vn_hs;
+    if constexpr (QB) {
+      ksgn = a.ksg + (int64_t)S.row * a.ksg_hs;
+      kgam = a.kgam + (int64_t)S.row * a.kgam_hs;
+      const float* sp = a.sq + ((int64_t)S.b * a.hq + S.g * G + min(w, G - 1)) * a.qm;
+      constexpr int NQ = QB > 1 ? 4 : 2;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) sqv[i] = NQ * lane + i < a.qm ? sp[NQ * lane + i] : 0.f;
+    }
     // wave WF16 requests its packed blocks after its fp16 tiles (their
     // registers do not overlap)
     if (!(w == WF16 && S.t1 > S.t0)) {
@@ -687,7 +737,8 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
   };
 
   const float vsc = a.vscale;
-  uint8_t* nst = smem + LY::nst + w * 256;  // this wave's norm staging: [key norms 32][value norms 32]
+  // this wave's norm staging: [key norms 32][value norms 32] (QB: [key residual norms 32] after them)
+  uint8_t* nst = smem + LY::nst + w * LY::NSTW;
 
   for (int v = v0; v < v1;) {
     rederive();
@@ -791,6 +842,44 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
       }
       qe_scale = __builtin_amdgcn_ldexpf(1.f, qeh);
     }
+    if constexpr (QB) {
+      // the sign-pattern table (thread t: replica t & 31 of row t >> 5) and
+      // the S q B operands of head w: (S q) 2^-e (its largest |(S q)_j| into
+      // [2^13, 2^14)) as fp16 high part / remainder at [head][part][j], and
+      // the head's factor log2(e) sqrt(pi / 2) / 128 2^e
+      {
+        const uint32_t n = (uint32_t)tid >> 5;
+        auto hv = [&](int j) { return ((n >> j) & 1u) ? 0x3C00u : 0xBC00u; };
+        *reinterpret_cast<u2*>(smem + LY::slut + n * 256 + 8 * (tid & 31)) = u2{hv(0) | hv(1) << 16, hv(2) | hv(3) << 16};
+      }
+      if (w < G) {
+        constexpr int NQ = QB > 1 ? 4 : 2;
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) mx = fmaxf(mx, fabsf(sqv[i]));
+        mx = wave_max(mx);
+        const int eh = mx > 0.f ? max((int)((__float_as_uint(mx) >> 23) & 0xFFu) - 140, -100) : 0;
+        const float sc = __builtin_amdgcn_ldexpf(1.f, -eh);
+        uint32_t hw[NQ / 2], lw[NQ / 2];
+#pragma unroll
+        for (int i = 0; i < NQ / 2; ++i) {
+          const float y0 = sqv[2 * i] * sc, y1 = sqv[2 * i + 1] * sc;
+          const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+          const _Float16 l0 = (_Float16)(y0 - (float)h0), l1 = (_Float16)(y1 - (float)h1);
+          hw[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16;
+          lw[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | (uint32_t)__builtin_bit_cast(uint16_t, l1) << 16;
+        }
+        uint8_t* d = smem + LY::sqo + (uint32_t)(w * 2) * LY::SQS + 2 * NQ * lane;
+#pragma unroll
+        for (int i = 0; i < NQ / 2; ++i) {
+          *reinterpret_cast<uint32_t*>(d + 4 * i) = hw[i];
+          *reinterpret_cast<uint32_t*>(d + LY::SQS + 4 * i) = lw[i];
+        }
+        if (lane == 0)
+          reinterpret_cast<float*>(smem + LY::kfx)[w] =
+              __builtin_amdgcn_ldexpf(1.4426950408889634f * 1.2533141373155003f / 128.f, eh);
+      }
+    }
     __syncthreads();
 
     // ---- fp16 tiles (wave WF16, original space): parked in LDS (`pre`) as
@@ -862,7 +951,19 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
     // The norms go to the wave's staging row first, for every slot (also the
     // skipped ones): the wait for a slot's loads then sits before the branch
     // on both paths, and the counts of loads in flight stay exact.
-    auto stage = [&](const Blk& Bk) { *reinterpret_cast<float*>(nst + 4 * lane) = lane < 32 ? Bk.nk : Bk.nv * vsc; };
+    auto stage = [&](const Blk& Bk) {
+      *reinterpret_cast<float*>(nst + 4 * lane) = lane < 32 ? Bk.nk : Bk.nv * vsc;
+      if constexpr (QB) {
+        if (lane < 32) *reinterpret_cast<float*>(nst + 256 + 4 * lane) = Bk.gk;
+      }
+    };
+    // QB: sign-pattern addresses (byte `byte` of a word of nibbles, one per
+    // byte), the S q operands and the key-term factor of this lane's column
+    [[maybe_unused]] const uint32_t cs = (uint32_t)(lane & 31) * 8 | LY::slut;
+    [[maybe_unused]] const uint32_t ssrc =
+        LY::sqo + (uint32_t)(hd * 2 + (lo_part ? 1 : 0)) * LY::SQS + (uint32_t)q4 * 64;
+    [[maybe_unused]] const float kfac = QB ? reinterpret_cast<const float*>(smem + LY::kfx)[hd] : 0.f;
+    auto saddr = [&](uint32_t word, int byte) { return __builtin_amdgcn_perm(word, cs, 0x0C020000u | ((4u + byte) << 8)); };
     auto compute = [&](const Blk& Bk, int m) {
       const int t0 = slot_t0(m);
       const int tend = m < nkw ? S.comp : 0;
@@ -903,6 +1004,28 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
         sA = mfma(as_h8(u4{ea0[0], ea0[1], ea1[0], ea1[1]}), qop[s], sA);
         sB = mfma(as_h8(u4{eb0[0], eb0[1], eb1[0], eb1[1]}), qop[s], sB);
       }
+      // QJL key term (QB), transposed like the scores: A = 16 tokens x 32
+      // projections of +-1 (sign patterns of 4 bits, two lookups per
+      // operand), B = (S q) 2^-e high part / remainder along the columns;
+      // lane (r, q4) holds sign dwords 4 c + q4 of token r, so step (c, kb)
+      // covers projections 128 c + 32 q4 + 8 kb .. + 7. Scaled by the key
+      // residual norm and the head's factor, added to the lane's scores.
+      f4 zA = {0.f, 0.f, 0.f, 0.f}, zB = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (QB) {
+#pragma unroll
+        for (int c = 0; c < QB; ++c) {
+          const uint32_t la = Bk.ks0[c] & 0x0F0F0F0Fu, ha = (Bk.ks0[c] >> 4) & 0x0F0F0F0Fu;
+          const uint32_t lb = Bk.ks1[c] & 0x0F0F0F0Fu, hb = (Bk.ks1[c] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) {
+            const u2 a0 = lds_u2(smem, saddr(la, kb)), a1 = lds_u2(smem, saddr(ha, kb));
+            const u2 b0 = lds_u2(smem, saddr(lb, kb)), b1 = lds_u2(smem, saddr(hb, kb));
+            const half8 so = *reinterpret_cast<const half8*>(smem + ssrc + 256 * c + 16 * kb);
+            zA = mfma(as_h8(u4{a0[0], a0[1], a1[0], a1[1]}), so, zA);
+            zB = mfma(as_h8(u4{b0[0], b0[1], b1[0], b1[1]}), so, zB);
+          }
+        }
+      }
       float sc[NS];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -915,10 +1038,16 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
         }
       }
       if constexpr (QB) {
-        // QJL key term of the lane's tokens (tile `tile`, or both for TS == 1)
+        // the key term times the key residual norm and the head's factor
 #pragma unroll
         for (int t = 0; t < 2 / TS; ++t) {
-          sc[4 * t] += Bk.qb[t].x; sc[4 * t + 1] += Bk.qb[t].y; sc[4 * t + 2] += Bk.qb[t].z; sc[4 * t + 3] += Bk.qb[t].w;
+          const float4 g4 = *reinterpret_cast<const float4*>(nst + 256 + 64 * (t + tile) + 16 * q4);
+          const float gk[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float zv = TS == 2 ? (tile ? zB[i] : zA[i]) : (t ? zB[i] : zA[i]);
+            sc[4 * t + i] = fmaf((zv + partner<G>(zv)) * kfac, gk[i], sc[4 * t + i]);
+          }
         }
       }
       if (t0 + 32 > tend) {  // uniform: only the last block of a sequence and empty slots mask
@@ -959,6 +1088,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
     // ---- combine the waves (and the parked fp16 tiles) into the segment's
     // partial: [M, L, has_orig, 0, rotated sum / L, original-space sum / L]
     rederive();
+    if constexpr (QB) __syncthreads();  // every wave is past its blocks: the sign table and S q operands are read
     to_rows(acc, m_run, l_run, vx, reinterpret_cast<float*>(smem + LY::cmb) + w * G * LY::CMS);
     __syncthreads();
     {
@@ -1002,22 +1132,6 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
 }
 
 // ---------------------------------------------------------------- merge kernel
-// max / sum over the 64 lanes of a wave (every lane gets the result)
-__device__ inline float wave_max(float v) {
-  v = fmaxf(v, row_ror<8>(v));
-  v = fmaxf(v, row_ror<4>(v));
-  v = fmaxf(v, row_ror<2>(v));
-  v = fmaxf(v, row_ror<1>(v));
-  return rows_max(v);
-}
-
-__device__ inline float wave_sum(float v) {
-  v += row_ror<8>(v);
-  v += row_ror<4>(v);
-  v += row_ror<2>(v);
-  v += row_ror<1>(v);
-  return rows_sum(v);
-}
 
 // Query head hqi of sequence b: the partials of (b, g) combined with w_p =
 // 2^(M_p - M) L_p / L (M = max_p M_p, L = sum_p 2^(M_p - M) L_p), then out =
@@ -1237,22 +1351,26 @@ void fast_uniform_plan(int batch, int hkv, int max_comp, int max_sink, int max_r
   V = batch * hkv * nu;
 }
 
-template <int G, bool QB>
+template <int G, int QB>
 static void launch_g(const FastArgs& a, int merge, hipStream_t s) {
   hipLaunchKernelGGL((decode_partials_kernel<G, QB>), dim3(a.nwg), dim3(FT), 0, s, a);
   if (merge) hipLaunchKernelGGL((decode_merge_kernel<G>), dim3(a.hq, a.batch), dim3(RMT), 0, s, a);
 }
 
-int launch_fast_decode(const FastArgs& a, int G, bool qb, int merge, hipStream_t s) {
-  switch (G * 2 + (qb ? 1 : 0)) {
-    case 2: launch_g<1, false>(a, merge, s); break;
-    case 3: launch_g<1, true>(a, merge, s); break;
-    case 4: launch_g<2, false>(a, merge, s); break;
-    case 5: launch_g<2, true>(a, merge, s); break;
-    case 8: launch_g<4, false>(a, merge, s); break;
-    case 9: launch_g<4, true>(a, merge, s); break;
-    case 16: launch_g<8, false>(a, merge, s); break;
-    case 17: launch_g<8, true>(a, merge, s); break;
+int launch_fast_decode(const FastArgs& a, int G, int qb, int merge, hipStream_t s) {
+  switch (G * 4 + qb) {
+    case 4: launch_g<1, 0>(a, merge, s); break;
+    case 5: launch_g<1, 1>(a, merge, s); break;
+    case 6: launch_g<1, 2>(a, merge, s); break;
+    case 8: launch_g<2, 0>(a, merge, s); break;
+    case 9: launch_g<2, 1>(a, merge, s); break;
+    case 10: launch_g<2, 2>(a, merge, s); break;
+    case 16: launch_g<4, 0>(a, merge, s); break;
+    case 17: launch_g<4, 1>(a, merge, s); break;
+    case 18: launch_g<4, 2>(a, merge, s); break;
+    case 32: launch_g<8, 0>(a, merge, s); break;
+    case 33: launch_g<8, 1>(a, merge, s); break;
+    case 34: launch_g<8, 2>(a, merge, s); break;
     default: return -1;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -564,6 +564,18 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) T16.v[i] = *reinterpret_cast<const u4*>(tok(sv, rv, 16 * t + 4 * q4 + i) + 8 * r);
   };
+  // the R rows j0 + n of this wave (QB: loaded at each segment's rotation
+  // from an opaque address, so that they are neither hoisted nor held across
+  // the block loop, where the sketch's operands need the registers)
+  auto load_rrows = [&]() {
+    const uint16_t* rh = a.rot16 + (j0 + r) * FD + 8 * q4;
+    if constexpr (QB) asm volatile("" : "+v"(rh));
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      rqh[kb] = *reinterpret_cast<const u4*>(rh + 32 * kb);
+      rql[kb] = *reinterpret_cast<const u4*>(rh + FD * FD + 32 * kb);
+    }
+  };
   auto issue = [&](int v) {
     S = segment(a, P, v, v1);
     {
@@ -573,14 +585,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
       if (tid < qchunks)
         load_lds16(qp + 16 * tid, qst + 1024 * w);
     }
-    {
-      const uint16_t* rh = a.rot16 + (j0 + r) * FD + 8 * q4;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        rqh[kb] = *reinterpret_cast<const u4*>(rh + 32 * kb);
-        rql[kb] = *reinterpret_cast<const u4*>(rh + FD * FD + 32 * kb);
-      }
-    }
+    if constexpr (!QB) load_rrows();
     nkw = S.k1 - S.k0 > w ? (S.k1 - S.k0 - w + FW - 1) / FW : 0;
     kcodes = a.kc + (int64_t)S.row * a.k_hs;
     vcodes = a.vc + (int64_t)S.row * a.v_hs;
@@ -753,6 +758,7 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
     // (e & 1) + 4*(e >> 1) and + 2
     float qe_scale;  // 2^qe of this lane's column head: multiplies its scores
     {
+      if constexpr (QB) load_rrows();
       // dims 32 kb + 8 q4 .. + 8 of query head min(r, G - 1) (the A operand
       // rows), as float
       float x[4][8];
@@ -931,6 +937,9 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
       load_slot(B0, 0);
       load_slot(B1, 1);
     }
+    // QB: the tile registers carry nothing into the next segment (which
+    // loads its own), so they are not held across the block loop
+    if constexpr (QB) T16 = Tile16{};
 
     // ---- packed blocks (rotated space)
     rederive();

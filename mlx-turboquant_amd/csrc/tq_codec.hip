@@ -365,15 +365,28 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
 constexpr int DRW = 8;    // waves (vectors) per workgroup
 constexpr int DRP = 132;  // padded LDS row: 16-byte aligned, rows of 16 lanes in distinct banks
 
-__global__ __launch_bounds__(DRW * 64) void drain_kernel(CompressArgs a) {
-  __shared__ __align__(16) float rt[128 * DRP];   // R[c][i] at c * DRP + i
-  __shared__ __align__(16) float st[128 * DRP];   // S[k][i] at k * DRP + i
-  __shared__ __align__(16) float vec[DRW][128];
-  __shared__ uint8_t cds[DRW][128];
-  __shared__ float bnd[2][16];
-  __shared__ float cen[2][16];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+// LDS of a drain workgroup: R and S (rows padded to DRP floats), the waves'
+// vectors and codes, the codebooks
+struct DrainLds {
+  float rt[128 * DRP];  // R[c][i] at c * DRP + i
+  float st[128 * DRP];  // S[k][i] at k * DRP + i
+  float vec[DRW][128];
+  uint8_t cds[DRW][128];
+  float bnd[2][16];
+  float cen[2][16];
+};
+
+// The drain of vector `vid` (row vid / n_tok, token vid % n_tok) by wave w of
+// a workgroup whose LDS `L` already holds R, S and the codebooks of `a`;
+// seq(b) gives sequence b's {token count, first source token, first
+// destination token}.
+template <class Seq>
+__device__ __forceinline__ void drain_vector(const CompressArgs& a, DrainLds& L, int vid, int w, int lane, Seq seq);
+
+// R, S and the codebooks of `a` into the workgroup's LDS (before a barrier)
+__device__ __forceinline__ void drain_stage(const CompressArgs& a, DrainLds& L, int tid) {
+  float* rt = L.rt;
+  float* st = L.st;
   // R and S in 16-byte pieces, every load of a thread requested before its
   // first store (8 pieces of R per thread, up to 16 of S)
   {
@@ -404,21 +417,44 @@ __global__ __launch_bounds__(DRW * 64) void drain_kernel(CompressArgs a) {
   }
   if (tid < 16) {
     const int nbh = (1 << a.bits_hi) - 1, nbl = (1 << a.bits_lo) - 1;
-    bnd[0][tid] = tid < nbh ? a.bnd_hi[tid] : 0.f;
-    bnd[1][tid] = tid < nbl ? a.bnd_lo[tid] : 0.f;
-    cen[0][tid] = tid <= nbh ? a.cen_hi[tid] : 0.f;
-    cen[1][tid] = tid <= nbl ? a.cen_lo[tid] : 0.f;
+    L.bnd[0][tid] = tid < nbh ? a.bnd_hi[tid] : 0.f;
+    L.bnd[1][tid] = tid < nbl ? a.bnd_lo[tid] : 0.f;
+    L.cen[0][tid] = tid <= nbh ? a.cen_hi[tid] : 0.f;
+    L.cen[1][tid] = tid <= nbl ? a.cen_lo[tid] : 0.f;
   }
-  __syncthreads();  // the only barrier: waves without a vector may leave after it
+}
 
-  const int vid = blockIdx.x * DRW + w;
+struct SeqRange {
+  int n_tok, src0, dst0;
+};
+
+__global__ __launch_bounds__(DRW * 64) void drain_kernel(CompressArgs a) {
+  __shared__ __align__(16) DrainLds L;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  drain_stage(a, L, tid);
+  __syncthreads();  // the only barrier: waves without a vector may leave after it
+  drain_vector(a, L, blockIdx.x * DRW + w, w, lane, [&](int b) {
+    return SeqRange{a.span.n_tok_b ? a.span.n_tok_b[b] : a.span.n_tok, a.span.src_tok0_b ? a.span.src_tok0_b[b] : 0,
+                    a.span.dst_tok0_b ? a.span.dst_tok0_b[b] : 0};
+  });
+}
+
+template <class Seq>
+__device__ __forceinline__ void drain_vector(const CompressArgs& a, DrainLds& L, int vid, int w, int lane, Seq seq) {
+  const float* rt = L.rt;
+  const float* st = L.st;
+  auto& vec = L.vec;
+  auto& cds = L.cds;
+  auto& bnd = L.bnd;
+  auto& cen = L.cen;
   const int r = vid / a.span.n_tok, t = vid % a.span.n_tok;
   if (r >= a.span.rows) return;
   const int b = r / a.span.heads;
-  const int n_tok = a.span.n_tok_b ? a.span.n_tok_b[b] : a.span.n_tok;
-  if (t >= n_tok) return;
-  const int src = (a.span.src_tok0_b ? a.span.src_tok0_b[b] : 0) + t;
-  const int dst = (a.span.dst_tok0_b ? a.span.dst_tok0_b[b] : 0) + t;
+  const SeqRange sr = seq(b);
+  if (t >= sr.n_tok) return;
+  const int src = sr.src0 + t;
+  const int dst = sr.dst0 + t;
   float* xv = vec[w];
   const int64_t xrow = (int64_t)r * a.x_hs + (int64_t)src * 128;
   const float x0 = load_elem(a.x, xrow + lane, a.x_dtype);
@@ -786,6 +822,68 @@ __global__ __launch_bounds__(256) void ring_append_kernel(const uint4* k, const 
   else
     rk[dst] = k[src];
 }
+
+// One decode step of a ragged batch in one launch (tq_ragged_step): the
+// step's key and value vectors appended to the residual rings, and the
+// one-token drains of both sides. Workgroups [0, dwg) drain keys, [dwg, 2 dwg)
+// values (the drain workgroup of drain_kernel: the same operations, so the
+// stored codes, norms, signs and gamma are bit-identical to tq_compress's),
+// the rest append. The per-sequence ints are [slot | drain | src | dst |
+// caller's extra] (batch each); up to STEP_INL of them travel in the kernel
+// arguments and are copied to ints_dev by the first append workgroup,
+// otherwise the caller's copy in ints_dev is read.
+constexpr int STEP_INL = 512;
+
+struct StepArgs {
+  CompressArgs side[2];  // key / value drains over the rings (span arrays unused)
+  const uint4* k;
+  const uint4* v;
+  uint4* rk;
+  uint4* rv;
+  int64_t rhs16;         // ring head stride, 16-byte units
+  int cap, heads, d16, rows, batch;
+  int dwg;               // drain workgroups per side
+  int awg;               // append workgroups
+  int n_ints;
+  int inl;               // the ints are in `ints` (else only in ints_dev)
+  int32_t* ints_dev;
+  int32_t ints[STEP_INL];
+};
+static_assert(sizeof(StepArgs) <= 4096, "kernel arguments of at most 4 KB");
+
+__global__ __launch_bounds__(DRW * 64) void step_kernel(StepArgs A) {
+  __shared__ __align__(16) DrainLds L;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wg = blockIdx.x;
+  const int32_t* seqi = A.inl ? A.ints : A.ints_dev;
+  if (wg >= 2 * A.dwg) {
+    // 16-byte piece e of the keys (e < rows d16) or of the values
+    const int np = A.rows * A.d16;
+    for (int e = (wg - 2 * A.dwg) * (DRW * 64) + tid; e < 2 * np; e += A.awg * (DRW * 64)) {
+      const bool val = e >= np;
+      const int f = val ? e - np : e;
+      const int row = f / A.d16, j = f - row * A.d16;
+      const int slot = seqi[row / A.heads];
+      if (slot < 0 || slot >= A.cap) continue;
+      const int64_t dst = (int64_t)row * A.rhs16 + (int64_t)slot * A.d16 + j;
+      if (val)
+        A.rv[dst] = A.v[f];
+      else
+        A.rk[dst] = A.k[f];
+    }
+    if (wg == 2 * A.dwg && A.inl)
+      for (int i = tid; i < A.n_ints; i += DRW * 64) A.ints_dev[i] = A.ints[i];
+    return;
+  }
+  const int sd = wg >= A.dwg ? 1 : 0;
+  const CompressArgs& a = A.side[sd];
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  drain_stage(a, L, tid);
+  __syncthreads();  // the only barrier: waves without a vector may leave after it
+  const int B = A.batch;
+  drain_vector(a, L, (wg - sd * A.dwg) * DRW + w, w, lane,
+               [&](int b) { return SeqRange{seqi[B + b], seqi[2 * B + b], seqi[3 * B + b]}; });
+}
 }  // namespace tq
 
 const char* tq_last_error(void) { return tq::g_err; }
@@ -811,6 +909,99 @@ int tq_ring_append(const void* k, const void* v, int32_t dtype, void* ring_k, vo
                      static_cast<uint4*>(ring_k), static_cast<uint4*>(ring_v), ring_head_stride / 8, (int)ring_cap,
                      (int)heads, d16, slot_b);
   TQ_LAUNCH_CHECK("tq_ring_append");
+  return TQ_OK;
+}
+
+int tq_ragged_step(const tq_codec* kcodec, const tq_codec* vcodec, const void* k, const void* v, int32_t dtype,
+                   void* ring_k, void* ring_v, int64_t ring_head_stride, int32_t ring_cap, const tq_store* kstore,
+                   const tq_store* vstore, int32_t batch, int32_t heads, const int32_t* seq_ints, int32_t n_ints,
+                   int32_t* seq_ints_dev, void* stream) {
+  using namespace tq;
+  int rc = check_codec(kcodec);
+  if (rc || (rc = check_codec(vcodec))) return rc;
+  if (dtype != TQ_F16 && dtype != TQ_BF16) return set_error(TQ_ERR_UNSUPPORTED, "ragged_step: dtype %d", dtype);
+  if (!k || !v || !ring_k || !ring_v || !kstore || !vstore || !seq_ints || !seq_ints_dev)
+    return set_error(TQ_ERR_INVALID, "ragged_step: NULL pointer");
+  if (batch < 0 || heads <= 0 || ring_cap <= 0 || (ring_head_stride & 7) || ring_head_stride < (int64_t)ring_cap * 128 ||
+      n_ints < 4 * batch || (int64_t)batch * heads >= ((int64_t)1 << 24))
+    return set_error(TQ_ERR_INVALID, "ragged_step: bad shape (batch %d heads %d cap %d stride %lld ints %d)", batch, heads,
+                     ring_cap, (long long)ring_head_stride, n_ints);
+  // the one-token drain workgroup serves d = 128 with a sketch of <= 128
+  // projections (the tq_compress drain route); other codecs use
+  // tq_ring_append + tq_compress
+  const tq_codec* cs[2] = {kcodec, vcodec};
+  const tq_store* ss[2] = {kstore, vstore};
+  for (int i = 0; i < 2; ++i) {
+    const tq_codec* c = cs[i];
+    if (c->d != 128 || !c->qjl_proj || c->qjl_m > 128 || (c->flags & TQ_CODEC_GENERAL_COMPRESS) ||
+        (reinterpret_cast<uintptr_t>(c->rotation) & 15) || (reinterpret_cast<uintptr_t>(c->qjl_proj) & 15))
+      return set_error(TQ_ERR_UNSUPPORTED, "ragged_step: codec (d %d, qjl_m %d) has no one-launch step", c->d, c->qjl_m);
+    const tq_store* st = ss[i];
+    if (!st->codes_hi || !st->norms || !st->signs || !st->gamma || (c->split < c->d && !st->codes_lo))
+      return set_error(TQ_ERR_INVALID, "ragged_step: store without codes / norms / signs / gamma");
+    if (!aligned4(st->codes_hi) || (st->hi_head_stride & 3) || (st->codes_lo && (!aligned4(st->codes_lo) || (st->lo_head_stride & 3))) ||
+        !aligned4(st->signs) || (st->sign_head_stride & 3))
+      return set_error(TQ_ERR_INVALID, "ragged_step: packed outputs must be 4-byte aligned");
+  }
+  const auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (!a16(k) || !a16(v) || !a16(ring_k) || !a16(ring_v))
+    return set_error(TQ_ERR_INVALID, "ragged_step: k, v and the rings must be 16-byte aligned");
+  // a drained ring position is read while the appends write: never the same slot
+  for (int b = 0; b < batch; ++b) {
+    const int slot = seq_ints[b], dr = seq_ints[batch + b], src = seq_ints[2 * batch + b], dst = seq_ints[3 * batch + b];
+    if (dr != 0 && dr != 1) return set_error(TQ_ERR_INVALID, "ragged_step: drain count %d of sequence %d", dr, b);
+    if (dr && (src < 0 || src >= ring_cap || dst < 0 || slot == src))
+      return set_error(TQ_ERR_INVALID, "ragged_step: sequence %d drains ring slot %d to token %d (append slot %d)", b, src,
+                       dst, slot);
+  }
+  if (batch == 0) return TQ_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  StepArgs A;
+  for (int i = 0; i < 2; ++i) {
+    const tq_codec* c = cs[i];
+    CompressArgs& a = A.side[i];
+    a.x = i ? ring_v : ring_k;
+    a.x_dtype = dtype;
+    a.x_hs = ring_head_stride;
+    a.span = tq_span{batch * heads, heads, 1, 0, nullptr, nullptr, nullptr};
+    a.dst = *ss[i];
+    a.rot = c->rotation;
+    a.bnd_hi = c->boundaries_hi;
+    a.bnd_lo = c->split < c->d ? c->boundaries_lo : c->boundaries_hi;
+    a.cen_hi = c->centroids_hi;
+    a.cen_lo = c->split < c->d ? c->centroids_lo : c->centroids_hi;
+    a.proj = c->qjl_proj;
+    a.qjl_m = c->qjl_m;
+    a.d = c->d;
+    a.bits_hi = c->bits_hi;
+    a.bits_lo = c->split < c->d ? c->bits_lo : c->bits_hi;
+    a.split = c->split;
+    a.row_hi = row_bytes(c->split, c->bits_hi);
+    a.row_lo = row_bytes(c->d - c->split, a.bits_lo);
+    a.row_sign = a.qjl_m / 8;
+  }
+  A.k = static_cast<const uint4*>(k);
+  A.v = static_cast<const uint4*>(v);
+  A.rk = static_cast<uint4*>(ring_k);
+  A.rv = static_cast<uint4*>(ring_v);
+  A.rhs16 = ring_head_stride / 8;
+  A.cap = ring_cap;
+  A.heads = heads;
+  A.d16 = 16;
+  A.rows = batch * heads;
+  A.batch = batch;
+  A.dwg = (A.rows + DRW - 1) / DRW;
+  A.awg = (2 * A.rows * A.d16 + DRW * 64 - 1) / (DRW * 64);
+  A.n_ints = n_ints;
+  A.ints_dev = seq_ints_dev;
+  A.inl = n_ints <= STEP_INL;
+  if (A.inl) {
+    memcpy(A.ints, seq_ints, sizeof(int32_t) * n_ints);
+  } else if (hipMemcpyAsync(seq_ints_dev, seq_ints, sizeof(int32_t) * n_ints, hipMemcpyHostToDevice, s) != hipSuccess) {
+    return set_error(TQ_ERR_LAUNCH, "ragged_step: copy of the sequence ints: %s", hipGetErrorString(hipGetLastError()));
+  }
+  hipLaunchKernelGGL(step_kernel, dim3((unsigned)(2 * A.dwg + A.awg)), dim3(DRW * 64), 0, s, A);
+  TQ_LAUNCH_CHECK("tq_ragged_step");
   return TQ_OK;
 }
 

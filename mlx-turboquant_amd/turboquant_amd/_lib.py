@@ -84,6 +84,7 @@ SIGNATURES = {
     "tq_device_supported": (_i32, []),
     "tq_compress": (_i32, [_PC, _p, _i32, _i64, _PSp, _PS, _p]),
     "tq_ring_append": (_i32, [_p, _p, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p]),
+    "tq_ragged_step": (_i32, [_PC, _PC, _p, _p, _i32, _p, _p, _i64, _i32, _PS, _PS, _i32, _i32, _p, _i32, _p, _p]),
     "tq_codec_prepare": (_i32, [_PC, _p, _i32]),
     "tq_codec_decode_table": (_i32, [_PC, _p]),
     "tq_dequantize": (_i32, [_PC, _PS, _PSp, _p, _i64, _i32, _p]),

@@ -28,6 +28,10 @@ from . import _codec, _lib
 from .cache import _workspace
 from .rotation import DEFAULT_SEED
 
+# per-sequence ints of a tq_ragged_step call carried in its kernel arguments
+# (more travel by an asynchronous copy)
+_STEP_INLINE_INTS = 512
+
 
 class _IntStage:
     """Host int32 arrays to the device in one asynchronous copy per call,
@@ -110,6 +114,18 @@ class RaggedKVBatch:
         z = lambda: np.zeros(batch, dtype=np.int64)
         self.sink_len, self.comp_len, self.res_len, self.res_start, self.offset = z(), z(), z(), z(), z()
         self._step_ints = _IntStage(8 * batch, dev)   # ring slots / drain arrays / post-step lengths of a step
+        # tq_ragged_step (one launch per step; codecs with a sketch at head_dim
+        # 128): the per-sequence ints of a step from host arrays, two slots
+        # (pinned, and guarded by an event, when they travel by an
+        # asynchronous copy rather than in the kernel arguments)
+        self._fused = self.qjl
+        self._seq_async = 8 * batch > _STEP_INLINE_INTS
+        self._seq_host = [torch.empty(8 * batch, dtype=torch.int32, pin_memory=self._seq_async).numpy()
+                          for _ in range(2)]
+        self._seq_dev = [torch.empty(8 * batch, dtype=torch.int32, device=dev) for _ in range(2)]
+        self._seq_events = [torch.cuda.Event(), torch.cuda.Event()] if self._seq_async else None
+        self._seq_used = [False, False]
+        self._seq_k = 0
         self._attn_ints = _IntStage(4 * batch, dev)   # per-sequence lengths of an attention call
         self._desc = None        # the attention descriptor, refreshed per call
         self._structs = None     # (store capacities, tq_store of kstore, of vstore)
@@ -163,7 +179,9 @@ class RaggedKVBatch:
         """Append one token per sequence ((B, H, D) keys / values). Sequences
         still filling their sink write there; the others append to their ring,
         and a sequence whose ring then holds residual_window + 1 tokens drains
-        its oldest one into the store (one ragged launch per side)."""
+        its oldest one into the store: with QJL sketches at head_dim 128 the
+        appends and both sides' drains are one tq_ragged_step launch, else
+        tq_ring_append and one ragged tq_compress per side."""
         B, H, D, dev = self.B, self.H, self.D, self.device
         if keys.shape != (B, H, D) or values.shape != keys.shape:
             raise ValueError("keys / values must be (batch, num_kv_heads, head_dim)")
@@ -179,17 +197,26 @@ class RaggedKVBatch:
             self.sink_k[bt, :, pt] = keys[bt]
             self.sink_v[bt, :, pt] = values[bt]
             self.sink_len[bi] += 1
-        # one staged copy: ring slots, the drain arrays (count, ring start, store
-        # position), then the lengths after this step for the next attention call
         comp_after = self.comp_len + drain
         start_after = np.where(drain, (self.res_start + 1) % self.cap, self.res_start)
-        # (ring slot -1: the token went to the sink)
-        staged, ptrs = self._step_ints.put_ptrs(np.where(to_sink, -1, ring_slot), drain, self.res_start,
-                                                self.comp_len, comp_after, self.sink_len, res_after - drain,
-                                                start_after)
-        n_b, src_b, dst_b = ptrs[1:4]
+        # the step's ints: ring slots (-1: the token went to the sink), the drain
+        # arrays (count, ring start, store position), then the lengths after
+        # this step for the next attention call
+        ints = (np.where(to_sink, -1, ring_slot), drain, self.res_start, self.comp_len, comp_after, self.sink_len,
+                res_after - drain, start_after)
         lib = _lib.load()
         stream = _lib.stream_ptr(dev)
+        if drain.any():
+            need = int(comp_after.max())
+            self.kstore.reserve(need, int(self.comp_len.max()))
+            self.vstore.reserve(need, int(self.comp_len.max()))
+        if self._fused and self._step_fused(lib, keys, values, ints, stream):
+            self.comp_len, self.res_start, self.res_len = comp_after, start_after, res_after - drain
+            self.offset += 1
+            self._lens_ver += 1
+            return
+        staged, ptrs = self._step_ints.put_ptrs(*ints)
+        n_b, src_b, dst_b = ptrs[1:4]
         if not to_sink.all():
             keys, values = keys.contiguous(), values.contiguous()
             _lib.check(lib.tq_ring_append(keys.data_ptr(), values.data_ptr(), _lib.TQ_F16, self.ring_k.data_ptr(),
@@ -197,9 +224,6 @@ class RaggedKVBatch:
                        "tq_ring_append")
         self.res_len = res_after
         if drain.any():
-            need = int((self.comp_len + drain).max())
-            self.kstore.reserve(need, int(self.comp_len.max()))
-            self.vstore.reserve(need, int(self.comp_len.max()))
             span = _lib.Span(rows=B * H, heads=H, n_tok=1, reserved=0, n_tok_b=n_b, src_tok0_b=src_b, dst_tok0_b=dst_b)
             for codec, ring, st in zip((self.kc, self.vc), (self.ring_k, self.ring_v), self._store_structs()):
                 _lib.check(lib.tq_compress(codec.ref(), ring.data_ptr(), _lib.TQ_F16, self.cap * D,
@@ -210,6 +234,36 @@ class RaggedKVBatch:
         self.offset += 1
         self._lens_ver += 1
         self._lens_staged = (self._lens_ver, ptrs[4:8], staged)
+
+    def _step_fused(self, lib, keys: torch.Tensor, values: torch.Tensor, ints, stream: int) -> bool:
+        """The step's appends and drains in one tq_ragged_step launch; False
+        (and the two-call path from then on) when the codecs have no such
+        launch."""
+        B = self.B
+        k = self._seq_k
+        self._seq_k ^= 1
+        if self._seq_async and self._seq_used[k]:
+            self._seq_events[k].synchronize()  # the copy from this slot has completed
+        h = self._seq_host[k]
+        for i, x in enumerate(ints):
+            h[i * B:(i + 1) * B] = x
+        keys, values = keys.contiguous(), values.contiguous()
+        d = self._seq_dev[k]
+        kst, vst = self._store_structs()
+        rc = lib.tq_ragged_step(self.kc.ref(), self.vc.ref(), keys.data_ptr(), values.data_ptr(), _lib.TQ_F16,
+                                self.ring_k.data_ptr(), self.ring_v.data_ptr(), self.cap * self.D, self.cap,
+                                ctypes.byref(kst), ctypes.byref(vst), B, self.H, h.ctypes.data, 8 * B, d.data_ptr(),
+                                stream)
+        if rc == _lib.TQ_ERR_UNSUPPORTED:
+            self._fused = False
+            return False
+        _lib.check(rc, "tq_ragged_step")
+        if self._seq_async:
+            self._seq_events[k].record()
+            self._seq_used[k] = True
+        base = d.data_ptr()
+        self._lens_staged = (self._lens_ver + 1, [base + 4 * i * B for i in range(4, 8)], d)
+        return True
 
     # ------------------------------------------------------------- attention
     def _store_structs(self) -> tuple[_lib.Store, _lib.Store]:

@@ -105,6 +105,24 @@ def test_host_side_validation_errors():
     assert b"bad shape" in lib.tq_last_error()
     assert ra(16, 24, _lib.TQ_F16, 16, 16, 1024, 8, 1, 1, 128, 16, None) == _lib.TQ_ERR_INVALID  # alignment
     assert ra(16, 16, _lib.TQ_BF16, 16, 16, 1024, 8, 0, 1, 128, 16, None) == _lib.TQ_OK  # empty batch: no-op
+    # ragged step (fake 16-byte aligned addresses: every case fails its checks before a launch)
+    f = 4096
+    sk = _lib.Codec(d=128, bits_hi=4, bits_lo=4, split=128, rotation=f, centroids_hi=f, boundaries_hi=f,
+                    qjl_proj=f, qjl_m=128)
+    nsk = _lib.Codec(d=128, bits_hi=2, bits_lo=2, split=128, rotation=f, centroids_hi=f, boundaries_hi=f)
+    st = _lib.Store(codes_hi=f, norms=f, signs=f, gamma=f)
+    ints = (ctypes.c_int32 * 8)(5, 6, 1, 1, 5, 2, 0, 0)  # batch 2: slots 5 / 6, both drain ring slots 5 / 2
+    rs = lambda kc, vc, dt=_lib.TQ_F16, n=8, i=ints: lib.tq_ragged_step(
+        ctypes.byref(kc), ctypes.byref(vc), f, f, dt, f, f, 129 * 128, 129, ctypes.byref(st), ctypes.byref(st), 2, 8,
+        i, n, f, None)
+    assert rs(sk, nsk) == _lib.TQ_ERR_UNSUPPORTED  # no sketch on the value side: tq_ring_append + tq_compress
+    assert b"no one-launch step" in lib.tq_last_error()
+    assert rs(sk, sk, dt=_lib.TQ_F32) == _lib.TQ_ERR_UNSUPPORTED
+    assert rs(sk, sk, n=7) == _lib.TQ_ERR_INVALID  # fewer than 4 * batch ints
+    assert rs(sk, sk) == _lib.TQ_ERR_INVALID  # sequence 0 drains the slot it appends to
+    assert b"sequence 0 drains ring slot 5" in lib.tq_last_error()
+    bad = (ctypes.c_int32 * 8)(4, 6, 2, 1, 5, 2, 0, 0)  # drain count 2
+    assert rs(sk, sk, i=bad) == _lib.TQ_ERR_INVALID
 
 
 def test_value_table_is_an_exact_fp16_copy_of_the_2bit_codebook():

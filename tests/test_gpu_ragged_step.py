@@ -1,0 +1,86 @@
+"""tq_ragged_step (one launch per decode step of a ragged batch with QJL
+sketches: the ring appends and both sides' one-token drains, cache.py:396-427,
+529-533, 620-706 per sequence) against the two-call path it replaces
+(tq_ring_append, then tq_compress of each side over the rings through the
+drain kernel, itself bit-identical to the general compress kernel in
+test_gpu_drain.py): rings, codes, norms, signs, gamma and the post-step
+length arrays bit for bit, and the attention over the two batches equal, over
+steps that fill sinks, fill rings and drain, for a batch whose ints travel in
+the kernel arguments and one (72 sequences) whose ints take the copy.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+
+
+def _batch(B, H, qjl_m, sink, window, lens, seed, fused):
+    from turboquant_amd.ragged import RaggedKVBatch
+    rb = RaggedKVBatch(B, H, 128, 4, 2, residual_window=window, fp16_sink_size=sink, qjl_n_proj=qjl_m, device=DEV)
+    rb._fused = fused and rb._fused
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    for b, T in enumerate(lens):
+        if T:
+            rb.load(b, torch.randn(H, int(T), 128, generator=g, device=DEV).half(),
+                    torch.randn(H, int(T), 128, generator=g, device=DEV).half())
+    return rb
+
+
+def _state(rb):
+    out = {"ring_k": rb.ring_k, "ring_v": rb.ring_v, "sink_k": rb.sink_k, "sink_v": rb.sink_v}
+    for side, st in (("k", rb.kstore), ("v", rb.vstore)):
+        for name in ("codes_hi", "codes_lo", "norms", "signs", "gamma"):
+            t = getattr(st, name)
+            if t is not None:
+                out[f"{side}.{name}"] = t
+    return {k: v.cpu().numpy().copy() for k, v in out.items()}
+
+
+@pytest.mark.parametrize("B,H,qjl_m,sink,window,lens", [
+    (5, 2, 128, 4, 6, [9, 3, 0, 17, 6]),    # sinks filling, rings filling and draining (ints in the arguments)
+    (16, 8, 128, 0, 128, None),             # the configs[4] shape (window 128, no sink), shorter contexts
+    (72, 1, 64, 2, 5, None),                # 576 ints: the copy path, m = 64
+])
+def test_ragged_step_matches_two_call_path(B, H, qjl_m, sink, window, lens):
+    rng = np.random.RandomState(B + H)
+    if lens is None:
+        lens = rng.randint(window + 3, 3 * window + 40, size=B)
+    lens = [int(x) for x in lens]
+    # sequences start non-empty for attend(); the empty one is loaded with one token
+    lens = [max(x, 1) for x in lens]
+    a = _batch(B, H, qjl_m, sink, window, lens, 7, fused=True)
+    b = _batch(B, H, qjl_m, sink, window, lens, 7, fused=False)
+    assert a._fused and not b._fused
+    g = torch.Generator(device=DEV).manual_seed(11)
+    q = torch.randn(B, 4 * H, 128, generator=g, device=DEV).half()
+    n_steps = window + sink + 3
+    for s in range(n_steps):
+        k = torch.randn(B, H, 128, generator=g, device=DEV).half()
+        v = torch.randn(B, H, 128, generator=g, device=DEV).half()
+        print(f"B={B} H={H} m={qjl_m} step {s}", flush=True)
+        a.step(k, v)
+        b.step(k, v)
+        assert a._fused, "the fused step fell back"
+        for name in ("sink_len", "comp_len", "res_len", "res_start", "offset"):
+            assert np.array_equal(getattr(a, name), getattr(b, name)), name
+        if s % 4 == 3 or s == n_steps - 1:
+            torch.cuda.synchronize()
+            sa, sb = _state(a), _state(b)
+            for name in sa:
+                assert np.array_equal(sa[name], sb[name]), f"step {s}: {name} differs"
+            # the device length arrays the next attention call reads
+            da, db = a._lens_staged, b._lens_staged
+            assert da[0] == a._lens_ver and db[0] == b._lens_ver
+            view = lambda staged, p: staged[(p - staged.data_ptr()) // 4:][:B].cpu().numpy()
+            for name, pa, pb in zip(("comp_len", "sink_len", "res_len", "res_start"), da[1], db[1]):
+                x, y = view(da[2], pa), view(db[2], pb)
+                assert np.array_equal(x, y) and np.array_equal(x, getattr(a, name)), name
+            oa = a.attend(q)
+            ob = b.attend(q)
+            torch.cuda.synchronize()
+            assert torch.equal(oa, ob), f"step {s}: attention differs"
+    assert int(a.comp_len.sum()) > int(sum(max(x - sink - window, 0) for x in lens))  # drains happened

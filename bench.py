@@ -326,13 +326,16 @@ def bench_config4(dev, steps: int = 12):
     """one layer-step of 16 ragged Llama-3.1-8B-shaped sequences
     (lengths ~ U[4096, 32768], seeded), K4/V2, the reference's defaults
     (window 128, no sink): append one token per sequence, drain one per
-    sequence into the packed store (one ragged compress launch per side),
-    fused decode attention over every sequence in one call. With the QJL
-    sketch (m = 128) the K4/V2 kernels run with the sketch's key and value
-    terms around them; without it the K4/V2 kernels alone. Eager launches,
-    events around each step (these include the host's launch overhead when
-    the GPU waits for it); then 8 attention calls back to back between two
-    events, the GPU time of one call with the host running ahead."""
+    sequence into the packed store (with the sketch: appends and both
+    sides' drains in one tq_ragged_step launch; without it the ring append
+    and one ragged compress launch per side), fused decode attention over
+    every sequence in one call. With the QJL sketch (m = 128) the K4/V2
+    kernels run with the sketch's key and value terms around them; without
+    it the K4/V2 kernels alone. Eager launches: one event pair around a
+    layer step (it includes the host's launch overhead when the GPU waits
+    for it), alternating with steps whose attention call alone is timed;
+    then 8 attention calls back to back between two events, the GPU time of
+    one call with the host running ahead."""
     import numpy as np
     import torch
     from turboquant_amd.ragged import RaggedKVBatch
@@ -348,19 +351,25 @@ def bench_config4(dev, steps: int = 12):
         q = torch.randn(16, 32, 128, generator=g, device=dev).half()
         out = torch.empty(16, 32, 128, dtype=torch.float32, device=dev)
         kv = [(torch.randn(16, 8, 128, generator=g, device=dev).half(),
-               torch.randn(16, 8, 128, generator=g, device=dev).half()) for _ in range(steps + 2)]
+               torch.randn(16, 8, 128, generator=g, device=dev).half()) for _ in range(2 * steps + 2)]
         t_step, t_attn = [], []
         for i, (k, v) in enumerate(kv):
-            e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-            e0.record()
-            rb.step(k, v)
-            e1.record()
-            rb.attend(q, out=out)
-            e2.record()
+            # even iterations time the layer step (one event pair around it),
+            # odd ones the attention call alone after an untimed step
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            if i % 2 == 0:
+                e0.record()
+                rb.step(k, v)
+                rb.attend(q, out=out)
+                e1.record()
+            else:
+                rb.step(k, v)
+                e0.record()
+                rb.attend(q, out=out)
+                e1.record()
             torch.cuda.synchronize()
             if i >= 2:
-                t_step.append(e0.elapsed_time(e2))
-                t_attn.append(e1.elapsed_time(e2))
+                (t_step if i % 2 == 0 else t_attn).append(e0.elapsed_time(e1))
         rep = 8
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -374,8 +383,8 @@ def bench_config4(dev, steps: int = 12):
         byt = 8 * (int(rb.comp_len.sum()) * per_tok + int(rb.res_len.sum()) * 512) + 16 * 32 * 128 * 6
         ms_s, ms_a = float(np.median(t_step)), float(np.median(t_attn))
         res["qjl" if qjl_m else "no_qjl"] = {
-            "kernel": ("K4/V2 + sketch (qjl_sq_kernel, decode_partials_kernel computing the key term from the "
-                       "sketch, merge, qjl_value_kernel, qjl_final_kernel)") if qjl_m
+            "kernel": ("K4/V2 + sketch (decode_partials_kernel computing S q and the key term from the sketch, "
+                       "merge, qjl_value_kernel, qjl_final_kernel; the step in one tq_ragged_step launch)") if qjl_m
                       else "K4/V2 (decode_partials_kernel + merge)",
             "layer_step_us": round(ms_s * 1e3, 1), "attend_us": round(ms_a * 1e3, 1),
             "attend_bytes": byt, "attend_GBps": round(byt / (ms_a * 1e-3) / 1e9, 1),

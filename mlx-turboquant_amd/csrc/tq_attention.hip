@@ -1402,8 +1402,7 @@ static bool fill_uniform(UniformArgs& u, const tq_codec* kc, const tq_codec* vc,
 }
 
 static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part, bool qb,
-                       float* qjl_bias, float* scores, int64_t qb_hs, float* ml, int merge, hipStream_t s,
-                       const float* sq = nullptr) {
+                       float* qjl_bias, float* scores, int64_t qb_hs, float* ml, int merge, hipStream_t s) {
   const int G = d->hq / d->hkv;
   UniformArgs u;
   if (fill_uniform(u, kc, vc, d, part)) {
@@ -1413,10 +1412,12 @@ static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_des
   FastArgs f;
   fill_fast(f, kc, vc, d, part);
   f.qjl_bias = qjl_bias; f.scores = scores; f.qb_hs = qb_hs; f.ml = ml;
-  // the persistent kernel computes the QJL key term itself (sketch and S q)
+  // the persistent kernel computes the QJL key term itself (S q at the query
+  // rotation, then the sketch against it)
   f.ksg = d->kstore.signs; f.ksg_hs = d->kstore.sign_head_stride;
   f.kgam = d->kstore.gamma; f.kgam_hs = d->kstore.gamma_head_stride;
-  f.sq = sq;
+  f.sproj = kc->qjl_proj;
+  f.sscale = d->scale;
   f.qm = kc->qjl_m;
   return launch_fast_decode(f, G, qb ? (kc->qjl_m <= 128 ? 1 : 2) : 0, merge, s);
 }
@@ -1538,17 +1539,19 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   qa.qb_hs = QL.qb_hs;
   qa.nvc = QL.nvc;
   qa.qvc = qjl_value_chunks_host(kc->qjl_m);
-  const dim3 sgrid((unsigned)((kc->qjl_m + 63) / 64), d->hkv, d->batch);
-  switch (G) {
-    case 1: hipLaunchKernelGGL((qjl_sq_kernel<1>), sgrid, dim3(256), 0, s, qa); break;
-    case 2: hipLaunchKernelGGL((qjl_sq_kernel<2>), sgrid, dim3(256), 0, s, qa); break;
-    case 4: hipLaunchKernelGGL((qjl_sq_kernel<4>), sgrid, dim3(256), 0, s, qa); break;
-    default: hipLaunchKernelGGL((qjl_sq_kernel<8>), sgrid, dim3(256), 0, s, qa); break;
-  }
-  TQ_LAUNCH_CHECK("tq_decode_attention qjl S q");
-  // the key term: a bias kernel for the uniform-batch kernels; the persistent
-  // kernel computes it from the sketch and S q
+  // the key term: S q and a bias kernel for the uniform-batch kernels; the
+  // persistent kernel computes both from S and the sketch itself
   const bool uniform = k4v2_uniform(kc, vc, d);
+  if (uniform) {
+    const dim3 sgrid((unsigned)((kc->qjl_m + 63) / 64), d->hkv, d->batch);
+    switch (G) {
+      case 1: hipLaunchKernelGGL((qjl_sq_kernel<1>), sgrid, dim3(256), 0, s, qa); break;
+      case 2: hipLaunchKernelGGL((qjl_sq_kernel<2>), sgrid, dim3(256), 0, s, qa); break;
+      case 4: hipLaunchKernelGGL((qjl_sq_kernel<4>), sgrid, dim3(256), 0, s, qa); break;
+      default: hipLaunchKernelGGL((qjl_sq_kernel<8>), sgrid, dim3(256), 0, s, qa); break;
+    }
+    TQ_LAUNCH_CHECK("tq_decode_attention qjl S q");
+  }
   const dim3 bgrid((unsigned)((QL.qb_hs + QBC * QCH - 1) / (QBC * QCH)), d->hkv, d->batch);
   if (uniform) switch (G * 2 + (w8 ? 1 : 0)) {
     case 2: hipLaunchKernelGGL((qjl_bias_kernel<1, 1>), bgrid, dim3(NT), 0, s, qa); break;
@@ -1562,7 +1565,7 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl bias");
   if (launch_k4v2(kc, vc, d, reinterpret_cast<float*>(ws + QL.part), true, qa.bias, const_cast<float*>(qa.scores),
-                  QL.qb_hs, const_cast<float*>(qa.ml), 1, s, qa.sq) != 0)
+                  QL.qb_hs, const_cast<float*>(qa.ml), 1, s) != 0)
     TQ_LAUNCH_CHECK("tq_decode_attention qjl fast");
   const dim3 vgrid((unsigned)QL.nvc, d->hkv, d->batch);
   switch (G * 2 + (w8 ? 1 : 0)) {

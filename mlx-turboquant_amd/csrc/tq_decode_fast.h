@@ -64,12 +64,13 @@ struct FastArgs {
   float* ml;             // merge output: (batch, hq, 2) global max and sum, or NULL
   int32_t* plan_tab;     // (batch, 2): first partial slot N_b and chunks n_b per kv head of each sequence,
                          // written by the partials kernel when uni == 0 (workspace, after the partials)
-  // QJL key term computed in the partials kernel (QB): the keys' 128-projection
-  // sketch (16-byte sign rows, one residual norm per token) and S (scale q)
-  // per query head, (batch, hq, 128) float32
+  // QJL key term computed in the partials kernel (QB): the keys' sketch (sign
+  // rows of qm / 8 bytes, one residual norm per token) against S (scale q) of
+  // the segment's query heads, computed at the query rotation from S
   const uint8_t* ksg; int64_t ksg_hs;  // key sign rows (bytes)
   const float* kgam;  int64_t kgam_hs; // key residual norms (elements)
-  const float* sq;
+  const float* sproj;    // (qm, 128) S float32, row-major (zero rows past the sketch's projections)
+  float sscale;          // scale (S q in natural units)
   int qm;                // projections of the sketch (a multiple of 32, at most 256): sign rows of qm / 8 bytes
 };
 

@@ -96,7 +96,9 @@ constexpr float Q_LOW = 0.25f;
 // of the 16 patterns of 4 sign bits (row n: the halves (bit j of n ? 1 : -1),
 // j < 4, in 32 replicas: its address is a byte permute too), the S q B
 // operands of the segment's heads (zero past the sketch's projections) and
-// their key-term factors; the norm staging also holds the key residual norms.
+// their key-term factors, and, at the query rotation, S (scale q) in float32
+// (computed there on MFMA from S); the norm staging also holds the key
+// residual norms.
 template <int G, int QB = 0>
 struct Lay {
   static constexpr int NCP = G <= 4 ? 32 : 16;
@@ -107,7 +109,10 @@ struct Lay {
   static constexpr uint32_t SQS = 256 * (QB > 1 ? 2 : 1) + 16;       // QB: bytes per (head, part) of sqo
   static constexpr uint32_t sqo = slut + 4096;                        // QB: [G][2 parts][SQS] S q B operands
   static constexpr uint32_t kfx = sqo + G * 2 * SQS;                  // QB: [G] f32 key-term factors
-  static constexpr uint32_t CMB_BYTES = !QB || FW * G * CMS * 4 >= kfx + 64 - cmb ? FW * G * CMS * 4 : kfx + 64 - cmb;
+  static constexpr int SQM = 128 * (QB > 1 ? 2 : 1);                   // QB: projections per head of sqf
+  static constexpr uint32_t sqf = kfx + 64;                           // QB: [G][SQM] f32 S (scale q)
+  static constexpr uint32_t QBEND = sqf + G * SQM * 4;
+  static constexpr uint32_t CMB_BYTES = !QB || FW * G * CMS * 4 >= QBEND - cmb ? FW * G * CMS * 4 : QBEND - cmb;
   static constexpr uint32_t QOPS = 528;                               // bytes per (head, part) of qop (512 + 16)
   static constexpr uint32_t qop = cmb + CMB_BYTES;                    // [G][2 parts][QOPS] rotated-q B operands
   static constexpr uint32_t qfo = qop + G * 2 * QOPS;                 // [G][2 parts][4 q4][4 kb][16 B] original-space q
@@ -502,8 +507,9 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
   // ---- per-segment loads, issued at the end of the previous segment (for
   // the first segment before the lookup tables are built): the query rows,
   // the R rows j0 + n of this wave as MFMA B operands (fp16 high part and
-  // remainder; k-slot (q4, i) of step kb = dim 32 kb + 8 q4 + i), then the
-  // first two packed blocks of the wave.
+  // remainder; k-slot (q4, i) of step kb = dim 32 kb + 8 q4 + i; QB: at the
+  // segment's start instead, with the S rows), then the first two packed
+  // blocks of the wave.
   Seg S{};
   const int qchunks = G * FD * esz / 16;  // 16-byte chunks of the G query rows
   u4 rqh[4], rql[4];
@@ -512,7 +518,6 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
   int nkw = 0;
   const uint8_t *kcodes = nullptr, *vcodes = nullptr, *ksgn = nullptr;
   const float *knorm = nullptr, *vnorm = nullptr, *kgam = nullptr;
-  float sqv[QB > 1 ? 4 : 2] = {};      // QB: S q of head w, projections (QB + 1) lane ..
   auto slot_t0 = [&](int m) { return (S.k0 + w + FW * m) << 5; };
   auto load_slot = [&](Blk& B, int m) {
     const bool live = m < nkw;
@@ -594,10 +599,6 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
     if constexpr (QB) {
       ksgn = a.ksg + (int64_t)S.row * a.ksg_hs;
       kgam = a.kgam + (int64_t)S.row * a.kgam_hs;
-      const float* sp = a.sq + ((int64_t)S.b * a.hq + S.g * G + min(w, G - 1)) * a.qm;
-      constexpr int NQ = QB > 1 ? 4 : 2;
-#pragma unroll
-      for (int i = 0; i < NQ; ++i) sqv[i] = NQ * lane + i < a.qm ? sp[NQ * lane + i] : 0.f;
     }
     // wave WF16 requests its packed blocks after its fp16 tiles (their
     // registers do not overlap)
@@ -748,6 +749,25 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
   for (int v = v0; v < v1;) {
     rederive();
     const bool has16 = S.t1 > S.t0;
+    // QB: the R rows and rows 16 (w + FW c) + r of S, dims 32 kb + 8 q4 .. + 8
+    // at [c][2 kb], [c][2 kb + 1] (opaque addresses: loaded per segment, not
+    // held across the block loop), requested before the barrier; tiles past
+    // the sketch's projections read row r
+    [[maybe_unused]] float4 srow[QB > 1 ? 2 : 1][8];
+    if constexpr (QB) {
+      load_rrows();
+#pragma unroll
+      for (int c = 0; c < QB; ++c) {
+        const int p0 = 16 * (w + FW * c);
+        const float* sp = a.sproj + (int64_t)((p0 < a.qm ? p0 : 0) + r) * FD + 8 * q4;
+        asm volatile("" : "+v"(sp));
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          srow[c][2 * kb] = *reinterpret_cast<const float4*>(sp + 32 * kb);
+          srow[c][2 * kb + 1] = *reinterpret_cast<const float4*>(sp + 32 * kb + 4);
+        }
+      }
+    }
     __syncthreads();
 
     // ---- query rotation: D[h][n] = sum_i q[h][i] R[j0 + n][i] on MFMA (q
@@ -758,7 +778,6 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
     // (e & 1) + 4*(e >> 1) and + 2
     float qe_scale;  // 2^qe of this lane's column head: multiplies its scores
     {
-      if constexpr (QB) load_rrows();
       // dims 32 kb + 8 q4 .. + 8 of query head min(r, G - 1) (the A operand
       // rows), as float
       float x[4][8];
@@ -809,6 +828,49 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
         dq = mfma(qo_hi[kb], as_h8(rql[kb]), dq);
         dq = mfma(qo_lo[kb], as_h8(rqh[kb]), dq);
       }
+      if constexpr (QB) {
+        // S (scale q) of the segment's heads on MFMA: the rotation's A
+        // operands against S rows as B operands (fp16 high part / remainder);
+        // lane (r, q4) ends with projection 16 (w + FW c) + r of heads
+        // 4 q4 + i, times scale 2^qe_h (undoing the query's 2^-qe_h), into sqf
+        float sfac[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          int e = 0;
+#pragma unroll
+          for (int h = 0; h < G; ++h) {
+            const int xh = __builtin_amdgcn_readlane(qe, h);
+            e = 4 * q4 + i == h ? xh : e;
+          }
+          sfac[i] = __builtin_amdgcn_ldexpf(a.sscale, e);
+        }
+#pragma unroll
+        for (int c = 0; c < QB; ++c) {
+          const int p0 = 16 * (w + FW * c);
+          if (p0 >= a.qm) break;  // wave-uniform
+          f4 ds = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) {
+            half8 sh, sl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float4 v4 = srow[c][2 * kb + (e >> 2)];
+              const float v = (e & 3) == 0 ? v4.x : (e & 3) == 1 ? v4.y : (e & 3) == 2 ? v4.z : v4.w;
+              sh[e] = (_Float16)v;
+              sl[e] = (_Float16)(v - (float)sh[e]);
+            }
+            ds = mfma(qo_hi[kb], sh, ds);
+            ds = mfma(qo_hi[kb], sl, ds);
+            ds = mfma(qo_lo[kb], sh, ds);
+          }
+          float* sf = reinterpret_cast<float*>(smem + LY::sqf);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int h = 4 * q4 + i;
+            if (h < G) sf[h * LY::SQM + p0 + r] = ds[i] * sfac[i];
+          }
+        }
+      }
       // the first fp16 tile of wave WF16, requested once the rotation's
       // registers are free (its latency overlaps the barrier)
       if (has16 && w == WF16) load_tile(S.t0);
@@ -858,8 +920,15 @@ __global__ __launch_bounds__(FT) void decode_partials_kernel(FastArgs a) {
         auto hv = [&](int j) { return ((n >> j) & 1u) ? 0x3C00u : 0xBC00u; };
         *reinterpret_cast<u2*>(smem + LY::slut + n * 256 + 8 * (tid & 31)) = u2{hv(0) | hv(1) << 16, hv(2) | hv(3) << 16};
       }
+      __syncthreads();  // every wave's S q is in sqf
       if (w < G) {
         constexpr int NQ = QB > 1 ? 4 : 2;
+        float sqv[NQ];
+        {
+          const float* sf = reinterpret_cast<const float*>(smem + LY::sqf) + w * LY::SQM;
+#pragma unroll
+          for (int i = 0; i < NQ; ++i) sqv[i] = NQ * lane + i < a.qm ? sf[NQ * lane + i] : 0.f;
+        }
         float mx = 0.f;
 #pragma unroll
         for (int i = 0; i < NQ; ++i) mx = fmaxf(mx, fabsf(sqv[i]));

@@ -141,7 +141,16 @@ def require_device(t: torch.Tensor) -> None:
         raise RuntimeError("turboquant_amd runs on the GPU only; got a CPU tensor")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device | None = None) -> int:
+    """The hipStream_t of torch's current stream on ``device`` (the raw
+    handle through torch's direct query where it has one: a decode step's
+    host path calls this per launch)."""
+    if _raw_stream is not None:
+        idx = device.index if device is not None and device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

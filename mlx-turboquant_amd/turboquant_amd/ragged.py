@@ -208,8 +208,10 @@ class RaggedKVBatch:
         stream = _lib.stream_ptr(dev)
         if drain.any():
             need = int(comp_after.max())
-            self.kstore.reserve(need, int(self.comp_len.max()))
-            self.vstore.reserve(need, int(self.comp_len.max()))
+            if need > self.kstore.cap or need > self.vstore.cap:
+                keep = int(self.comp_len.max())
+                self.kstore.reserve(need, keep)
+                self.vstore.reserve(need, keep)
         if self._fused and self._step_fused(lib, keys, values, ints, stream):
             self.comp_len, self.res_start, self.res_len = comp_after, start_after, res_after - drain
             self.offset += 1

@@ -84,3 +84,15 @@ def test_ragged_step_matches_two_call_path(B, H, qjl_m, sink, window, lens):
             torch.cuda.synchronize()
             assert torch.equal(oa, ob), f"step {s}: attention differs"
     assert int(a.comp_len.sum()) > int(sum(max(x - sink - window, 0) for x in lens))  # drains happened
+
+
+def test_stream_handle_is_torch_current_stream():
+    """Launches go to torch's current stream (the raw handle query agrees with
+    torch.cuda.current_stream, also inside a stream context)."""
+    from turboquant_amd import _lib
+    assert _lib.stream_ptr(DEV) == torch.cuda.current_stream(DEV).cuda_stream
+    assert _lib.stream_ptr(torch.device("cuda")) == torch.cuda.current_stream().cuda_stream
+    s = torch.cuda.Stream(device=DEV)
+    with torch.cuda.stream(s):
+        assert _lib.stream_ptr(DEV) == s.cuda_stream != 0
+    assert _lib.stream_ptr(DEV) == torch.cuda.current_stream(DEV).cuda_stream

@@ -790,6 +790,7 @@ struct QjlArgs {
   const float* scores;  // (batch*hkv*G, qb_hs) final base-2 scores
   const float* ml;      // (batch, hq, 2) global max and sum of the merge
   float* upart;         // (batch, hq, nvc, m) value terms, one per value-kernel workgroup
+  float* umax;          // (batch, hq, nvc) each value partial's reference max (value kernel with LOC)
   int64_t qb_hs;
   int nvc;              // value-kernel workgroups per (b, g), one partial each
   int qvc;              // chunks of QCH tokens per value-kernel workgroup
@@ -985,7 +986,12 @@ static int qjl_value_chunks_host(int m) { return m > 128 ? qjl_value_chunks<2>()
 // front; one accumulator per tile runs over the chunks. The weights stay
 // unnormalised (O(gamma), whatever the context length); -2^(E_h - 14) / L_h is
 // applied in float32 to the sums.
-template <int G, int NW4>
+// LOC: M is the workgroup's own max score of head h instead of the merged
+// one (the kernel then runs before the merge, which weights the partial by
+// 2^(M_loc - M) / L: umax holds M_loc), and E_h the exponent of the
+// workgroup's largest residual norm (every weight is at most that norm); the
+// sums are scaled by -2^(E_h - 14) alone.
+template <int G, int NW4, bool LOC = false>
 __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   static_assert(NT == QCH, "thread t = token t of the chunk");
   constexpr int QV = qjl_value_chunks<NW4>();
@@ -999,7 +1005,8 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   // ysm[c][p]: projections 16c .. 16c + 15 of token 2p (low half) and 2p + 1 (high half)
   __shared__ __align__(16) uint32_t ysm[MAXM / 16][YS];
   __shared__ __align__(16) uint32_t aw[QCH / 32 * ASB];
-  __shared__ uint32_t wm[NT / 64][G];  // per wave and head: the max weight (float bits)
+  __shared__ uint32_t wm[NT / 64][G];  // per wave and head: the max weight (float bits); LOC: the max score
+  __shared__ uint32_t wg[NT / 64];     // LOC: per wave the largest residual norm (float bits)
   const int cg = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int row = b * a.d.hkv + g, m = a.m, hq = a.d.hq, nw = m / 32;
   const int comp = seq_comp(a.d, b);
@@ -1012,11 +1019,13 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   uint32_t sw[QV][4 * NW4];
   float gv[QV], sc[QV][G], Mh[G], Lh[G];
   {
-    const float* mlp = a.ml + ((int64_t)b * hq + g * G) * 2;
+    if constexpr (!LOC) {
+      const float* mlp = a.ml + ((int64_t)b * hq + g * G) * 2;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      Mh[h] = mlp[2 * h];
-      Lh[h] = mlp[2 * h + 1];
+      for (int h = 0; h < G; ++h) {
+        Mh[h] = mlp[2 * h];
+        Lh[h] = mlp[2 * h + 1];
+      }
     }
     const uint8_t* srow = vs.signs + (int64_t)row * vs.sign_head_stride + (int64_t)base0 * (m / 8);
     const float* grow = vs.gamma + (int64_t)row * vs.gamma_head_stride + base0;
@@ -1032,27 +1041,67 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   }
   // ---- unnormalised weights and their per-wave max per head over the chunks
   float wt[QV][G];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float mx = 0.f;
-#pragma unroll
-    for (int c = 0; c < QV; ++c) {
-      const float p = c * QCH + t < ntok && Lh[h] > 0.f ? __builtin_amdgcn_exp2f(sc[c][h] - Mh[h]) : 0.f;
-      wt[c][h] = p * gv[c];
-      mx = fmaxf(mx, wt[c][h]);
-    }
-    const uint32_t wmx = wave_max_nonneg(mx);
-    if (lane == 0) wm[w][h] = wmx;
-  }
-  __syncthreads();
-  // E_h: the exponent of the workgroup's max weight (weights are >= 0)
   int eh[G];
+  if constexpr (LOC) {
+    // the workgroup's max score per head and largest residual norm
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    uint32_t mb = wm[0][h];
+    for (int h = 0; h < G; ++h) {
+      float mx = -INFINITY;
 #pragma unroll
-    for (int ww = 1; ww < NT / 64; ++ww) mb = max(mb, wm[ww][h]);
-    eh[h] = mb == 0u ? 0 : max((int)((mb >> 23) & 0xFFu), 1) - 127;
+      for (int c = 0; c < QV; ++c) mx = c * QCH + t < ntok ? fmaxf(mx, sc[c][h]) : mx;
+      const float wmx = wave_max_dpp(mx);
+      if (lane == 0) wm[w][h] = __float_as_uint(wmx);
+    }
+    float gx = 0.f;
+#pragma unroll
+    for (int c = 0; c < QV; ++c) gx = c * QCH + t < ntok ? fmaxf(gx, gv[c]) : gx;
+    const uint32_t gmx = wave_max_nonneg(gx);
+    if (lane == 0) wg[w] = gmx;
+    __syncthreads();
+    uint32_t gb = wg[0];
+#pragma unroll
+    for (int ww = 1; ww < NT / 64; ++ww) gb = max(gb, wg[ww]);
+    const int eg = gb == 0u ? 0 : max((int)((gb >> 23) & 0xFFu), 1) - 127;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float mh = __uint_as_float(wm[0][h]);
+#pragma unroll
+      for (int ww = 1; ww < NT / 64; ++ww) mh = fmaxf(mh, __uint_as_float(wm[ww][h]));
+      Mh[h] = mh;
+      Lh[h] = 1.f;
+      eh[h] = eg;
+#pragma unroll
+      for (int c = 0; c < QV; ++c)
+        wt[c][h] = c * QCH + t < ntok ? __builtin_amdgcn_exp2f(sc[c][h] - mh) * gv[c] : 0.f;
+    }
+    if (tid < G) {
+      float mo = Mh[0];
+#pragma unroll
+      for (int h = 1; h < G; ++h) mo = tid == h ? Mh[h] : mo;
+      a.umax[((int64_t)b * hq + g * G + tid) * a.nvc + cg] = mo;
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float mx = 0.f;
+#pragma unroll
+      for (int c = 0; c < QV; ++c) {
+        const float p = c * QCH + t < ntok && Lh[h] > 0.f ? __builtin_amdgcn_exp2f(sc[c][h] - Mh[h]) : 0.f;
+        wt[c][h] = p * gv[c];
+        mx = fmaxf(mx, wt[c][h]);
+      }
+      const uint32_t wmx = wave_max_nonneg(mx);
+      if (lane == 0) wm[w][h] = wmx;
+    }
+    __syncthreads();
+    // E_h: the exponent of the workgroup's max weight (weights are >= 0)
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      uint32_t mb = wm[0][h];
+#pragma unroll
+      for (int ww = 1; ww < NT / 64; ++ww) mb = max(mb, wm[ww][h]);
+      eh[h] = mb == 0u ? 0 : max((int)((mb >> 23) & 0xFFu), 1) - 127;
+    }
   }
   const bool odd = (t & 1) != 0;
   const uint32_t shl = 15u - (uint32_t)r;
@@ -1124,7 +1173,9 @@ __global__ __launch_bounds__(NT) void qjl_value_kernel(QjlArgs a) {
   // its scale -2^(E_h - 14) / L_h (the B operands hold -z)
   float hsc[G];
 #pragma unroll
-  for (int h = 0; h < G; ++h) hsc[h] = Lh[h] > 0.f ? -__builtin_amdgcn_ldexpf(1.f, eh[h] - 14) / Lh[h] : 0.f;
+  for (int h = 0; h < G; ++h)
+    hsc[h] = LOC ? -__builtin_amdgcn_ldexpf(1.f, eh[h] - 14)
+                 : Lh[h] > 0.f ? -__builtin_amdgcn_ldexpf(1.f, eh[h] - 14) / Lh[h] : 0.f;
   float osc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) osc[i] = q4 == 0 ? hsc[min(i, G - 1)] : hsc[min(4 + i, G - 1)];
@@ -1184,7 +1235,7 @@ __global__ __launch_bounds__(256) void qjl_final_kernel(QjlArgs a) {
 
 // Workspace of the QJL fast route: [fast partials | sq | bias | scores | ml | upart], 256-byte pieces.
 struct QjlLayout {
-  size_t part, pro, bias, scores, ml, upart, total;
+  size_t part, pro, bias, scores, ml, upart, umax, total;
   int64_t qb_hs;
   int nvc;
 };
@@ -1317,6 +1368,7 @@ static QjlLayout qjl_layout(const tq_codec* kc, const tq_attn_desc* d) {
   L.scores = off; off += al256((size_t)d->batch * d->hkv * G * (size_t)L.qb_hs * 4);
   L.ml = off; off += al256(heads * 2 * 4);
   L.upart = off; off += al256(heads * (size_t)L.nvc * m * 4);
+  L.umax = off; off += al256(heads * (size_t)L.nvc * 4);
   L.total = off;
   return L;
 }
@@ -1401,8 +1453,10 @@ static bool fill_uniform(UniformArgs& u, const tq_codec* kc, const tq_codec* vc,
   return true;
 }
 
+// (fout: the persistent kernel's arguments, for a merge launched later)
 static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_desc* d, float* part, bool qb,
-                       float* qjl_bias, float* scores, int64_t qb_hs, float* ml, int merge, hipStream_t s) {
+                       float* qjl_bias, float* scores, int64_t qb_hs, float* ml, int merge, hipStream_t s,
+                       FastArgs* fout = nullptr) {
   const int G = d->hq / d->hkv;
   UniformArgs u;
   if (fill_uniform(u, kc, vc, d, part)) {
@@ -1419,6 +1473,7 @@ static int launch_k4v2(const tq_codec* kc, const tq_codec* vc, const tq_attn_des
   f.sproj = kc->qjl_proj;
   f.sscale = d->scale;
   f.qm = kc->qjl_m;
+  if (fout) *fout = f;
   return launch_fast_decode(f, G, qb ? (kc->qjl_m <= 128 ? 1 : 2) : 0, merge, s);
 }
 
@@ -1536,6 +1591,7 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
   qa.scores = reinterpret_cast<float*>(ws + QL.scores);
   qa.ml = reinterpret_cast<float*>(ws + QL.ml);
   qa.upart = reinterpret_cast<float*>(ws + QL.upart);
+  qa.umax = reinterpret_cast<float*>(ws + QL.umax);
   qa.qb_hs = QL.qb_hs;
   qa.nvc = QL.nvc;
   qa.qvc = qjl_value_chunks_host(kc->qjl_m);
@@ -1564,10 +1620,35 @@ static int qjl_fast_run(const tq_codec* kc, const tq_codec* vc, const tq_attn_de
     default: hipLaunchKernelGGL((qjl_bias_kernel<8, 2>), bgrid, dim3(NT), 0, s, qa); break;
   }
   TQ_LAUNCH_CHECK("tq_decode_attention qjl bias");
+  const dim3 vgrid((unsigned)QL.nvc, d->hkv, d->batch);
+  if (!uniform) {
+    // persistent kernel: partials (key term inside), the value kernel with
+    // each workgroup's own max, then the merge adding the value term
+    FastArgs f;
+    if (launch_k4v2(kc, vc, d, reinterpret_cast<float*>(ws + QL.part), true, nullptr, const_cast<float*>(qa.scores),
+                    QL.qb_hs, nullptr, 0, s, &f) != 0)
+      TQ_LAUNCH_CHECK("tq_decode_attention qjl fast");
+    switch (G * 2 + (w8 ? 1 : 0)) {
+      case 2: hipLaunchKernelGGL((qjl_value_kernel<1, 1, true>), vgrid, dim3(NT), 0, s, qa); break;
+      case 3: hipLaunchKernelGGL((qjl_value_kernel<1, 2, true>), vgrid, dim3(NT), 0, s, qa); break;
+      case 4: hipLaunchKernelGGL((qjl_value_kernel<2, 1, true>), vgrid, dim3(NT), 0, s, qa); break;
+      case 5: hipLaunchKernelGGL((qjl_value_kernel<2, 2, true>), vgrid, dim3(NT), 0, s, qa); break;
+      case 8: hipLaunchKernelGGL((qjl_value_kernel<4, 1, true>), vgrid, dim3(NT), 0, s, qa); break;
+      case 9: hipLaunchKernelGGL((qjl_value_kernel<4, 2, true>), vgrid, dim3(NT), 0, s, qa); break;
+      case 16: hipLaunchKernelGGL((qjl_value_kernel<8, 1, true>), vgrid, dim3(NT), 0, s, qa); break;
+      default: hipLaunchKernelGGL((qjl_value_kernel<8, 2, true>), vgrid, dim3(NT), 0, s, qa); break;
+    }
+    TQ_LAUNCH_CHECK("tq_decode_attention qjl value");
+    f.qjl_up = qa.upart;
+    f.qjl_umax = qa.umax;
+    f.qnvc = QL.nvc;
+    f.qtok = QCH * qa.qvc;
+    if (launch_fast_merge_qjl(f, G, w8 ? 2 : 1, s) != 0) TQ_LAUNCH_CHECK("tq_decode_attention qjl merge");
+    return TQ_OK;
+  }
   if (launch_k4v2(kc, vc, d, reinterpret_cast<float*>(ws + QL.part), true, qa.bias, const_cast<float*>(qa.scores),
                   QL.qb_hs, const_cast<float*>(qa.ml), 1, s) != 0)
     TQ_LAUNCH_CHECK("tq_decode_attention qjl fast");
-  const dim3 vgrid((unsigned)QL.nvc, d->hkv, d->batch);
   switch (G * 2 + (w8 ? 1 : 0)) {
     case 2: hipLaunchKernelGGL((qjl_value_kernel<1, 1>), vgrid, dim3(NT), 0, s, qa); break;
     case 3: hipLaunchKernelGGL((qjl_value_kernel<1, 2>), vgrid, dim3(NT), 0, s, qa); break;

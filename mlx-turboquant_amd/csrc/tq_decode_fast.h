@@ -72,6 +72,14 @@ struct FastArgs {
   const float* sproj;    // (qm, 128) S float32, row-major (zero rows past the sketch's projections)
   float sscale;          // scale (S q in natural units)
   int qm;                // projections of the sketch (a multiple of 32, at most 256): sign rows of qm / 8 bytes
+  // QJL value term added by the merge (decode_merge_kernel with QV): per
+  // (sequence, query head) qnvc value partials of qm floats, each the sum
+  // over its tokens of 2^(s - umax) gamma (-z) times -2^(E - 14), weighted by
+  // 2^(umax - M) / L in the merge, times sqrt(pi / 2) / 128 through S^T
+  const float* qjl_up;   // (batch, hq, qnvc, qm)
+  const float* qjl_umax; // (batch, hq, qnvc)
+  int qnvc;              // value partials per (sequence, query head)
+  int qtok;              // tokens per value partial
 };
 
 // Host-side sizing of the K4/V2 path for a call: workgroups, chunks per
@@ -83,9 +91,12 @@ void fast_uniform_plan(int batch, int hkv, int max_comp, int max_sink, int max_r
                        int& nu, int& V);
 // Launches the partials kernel and, when merge != 0, the merge kernel. G in
 // {1, 2, 4, 8}; qb 1 / 2: with the QJL key term of a sketch of at most 128 /
-// 256 projections computed in the kernel (ksg, kgam, sq, qm), the final scores
-// stored.
+// 256 projections computed in the kernel (ksg, kgam, sproj, sscale, qm), the
+// final scores stored.
 int launch_fast_decode(const FastArgs& a, int G, int qb, int merge, hipStream_t s);
+// The merge kernel alone, with the QJL value term of qjl_up (qv = 1 for
+// sketches of at most 128 projections, 2 for at most 256).
+int launch_fast_merge_qjl(const FastArgs& a, int G, int qv, hipStream_t s);
 
 // Merge of per-workgroup partials in original space ([M, L, pad, pad,
 // out[128] / L] per query head, nwg per (sequence, kv head)) into out

@@ -1224,11 +1224,12 @@ constexpr int MB = 32;   // partials per batch of loads (orig_merge_kernel)
 constexpr int RMB = 16;  // partials per parity per batch of loads (decode_merge_kernel)
 constexpr int RMT = 256; // threads of decode_merge_kernel
 
-template <int G>
+template <int G, int QV = 0>
 __global__ __launch_bounds__(RMT) void decode_merge_kernel(FastArgs a) {
   __shared__ __align__(16) float ys[2][FD];   // the two parities' weighted sums, rotated
   __shared__ __align__(16) float xs[2][FD];   // and original-space
   __shared__ __align__(16) float red[8][FD];  // rotation: sums over the 8 row blocks
+  __shared__ __align__(16) float us[QV ? 2 : 1][QV ? 128 * QV : 1];  // QV: the parities' weighted value partials
   const int hqi = blockIdx.x, b = blockIdx.y;
   const int g = hqi / G, h = hqi % G;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1313,8 +1314,41 @@ __global__ __launch_bounds__(RMT) void decode_merge_kernel(FastArgs a) {
   }
   ys[par][d] = acc;
   xs[par][d] = acco;
+  // QV: S[16 ib + k + 128 c][j4 .. j4 + 3] (rows past the sketch's
+  // projections clamped: their weights are zero), requested with the value
+  // partials
+  [[maybe_unused]] float4 sr[QV ? QV : 1][16];
+  if constexpr (QV) {
+#pragma unroll
+    for (int c = 0; c < QV; ++c)
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        sr[c][k] = *reinterpret_cast<const float4*>(a.sproj + min(16 * ib + k + 128 * c, a.qm - 1) * FD + j4);
+    // value partials of the query head weighted by 2^(umax - M) (the value
+    // kernel's workgroups holding tokens of the sequence; uniform over the
+    // wave), projection d (+ 128) of parity par; zero past the sketch
+    const int comp = a.comp_len_b ? a.comp_len_b[b] : a.max_comp;
+    const int nvb = min(a.qnvc, (comp + a.qtok - 1) / a.qtok);
+    const int64_t hb = (int64_t)b * a.hq + hqi;
+    const float* up = a.qjl_up + hb * a.qnvc * a.qm;
+    const float* um = a.qjl_umax + hb * a.qnvc;
+#pragma unroll
+    for (int c = 0; c < QV; ++c) {
+      const int i = d + 128 * c;
+      const int il = i < a.qm ? i : 0;  // projections past the sketch read projection 0 and store 0
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      int q = upar;
+      for (; q + 6 < nvb; q += 8) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = fmaf(fexp2(um[q + 2 * k] - M), up[(int64_t)(q + 2 * k) * a.qm + il], v[k]);
+      }
+      for (; q < nvb; q += 2) v[0] = fmaf(fexp2(um[q] - M), up[(int64_t)q * a.qm + il], v[0]);
+      us[par][i] = i < a.qm ? (v[0] + v[1]) + (v[2] + v[3]) : 0.f;
+    }
+  }
   __syncthreads();
-  // rotation: rows 16 ib .. + 15 of R times the merged rotated sum
+  // rotation: rows 16 ib .. + 15 of R times the merged rotated sum (QV: and
+  // the value term, sqrt(pi / 2) / 128 S^T u)
   float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
@@ -1324,6 +1358,20 @@ __global__ __launch_bounds__(RMT) void decode_merge_kernel(FastArgs a) {
     o.y = fmaf(y, rr[k].y, o.y);
     o.z = fmaf(y, rr[k].z, o.z);
     o.w = fmaf(y, rr[k].w, o.w);
+  }
+  if constexpr (QV) {
+    constexpr float QJL_C = 1.2533141373155003f / 128.f;  // sqrt(pi / 2) / d
+#pragma unroll
+    for (int c = 0; c < QV; ++c)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int i = 16 * ib + k + 128 * c;
+        const float u = QJL_C * (us[0][i] + us[1][i]);
+        o.x = fmaf(u, sr[c][k].x, o.x);
+        o.y = fmaf(u, sr[c][k].y, o.y);
+        o.z = fmaf(u, sr[c][k].z, o.z);
+        o.w = fmaf(u, sr[c][k].w, o.w);
+      }
   }
   *reinterpret_cast<float4*>(&red[ib][j4]) = o;
   __syncthreads();
@@ -1449,6 +1497,22 @@ int launch_fast_decode(const FastArgs& a, int G, int qb, int merge, hipStream_t 
     case 32: launch_g<8, 0>(a, merge, s); break;
     case 33: launch_g<8, 1>(a, merge, s); break;
     case 34: launch_g<8, 2>(a, merge, s); break;
+    default: return -1;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_fast_merge_qjl(const FastArgs& a, int G, int qv, hipStream_t s) {
+  const dim3 grid(a.hq, a.batch);
+  switch (G * 4 + qv) {
+    case 5: hipLaunchKernelGGL((decode_merge_kernel<1, 1>), grid, dim3(RMT), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((decode_merge_kernel<1, 2>), grid, dim3(RMT), 0, s, a); break;
+    case 9: hipLaunchKernelGGL((decode_merge_kernel<2, 1>), grid, dim3(RMT), 0, s, a); break;
+    case 10: hipLaunchKernelGGL((decode_merge_kernel<2, 2>), grid, dim3(RMT), 0, s, a); break;
+    case 17: hipLaunchKernelGGL((decode_merge_kernel<4, 1>), grid, dim3(RMT), 0, s, a); break;
+    case 18: hipLaunchKernelGGL((decode_merge_kernel<4, 2>), grid, dim3(RMT), 0, s, a); break;
+    case 33: hipLaunchKernelGGL((decode_merge_kernel<8, 1>), grid, dim3(RMT), 0, s, a); break;
+    case 34: hipLaunchKernelGGL((decode_merge_kernel<8, 2>), grid, dim3(RMT), 0, s, a); break;
     default: return -1;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;

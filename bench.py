@@ -326,10 +326,9 @@ def bench_config4(dev, steps: int = 12):
     """one layer-step of 16 ragged Llama-3.1-8B-shaped sequences
     (lengths ~ U[4096, 32768], seeded), K4/V2, the reference's defaults
     (window 128, no sink): append one token per sequence, drain one per
-    sequence into the packed store (with the sketch: appends and both
-    sides' drains in one tq_ragged_step launch; without it the ring append
-    and one ragged compress launch per side), fused decode attention over
-    every sequence in one call. With the QJL sketch (m = 128) the K4/V2
+    sequence into the packed store (appends and both sides' drains in one
+    tq_ragged_step launch), fused decode attention over every sequence in
+    one call. With the QJL sketch (m = 128) the K4/V2
     kernels run with the sketch's key and value terms around them; without
     it the K4/V2 kernels alone. Eager launches: one event pair around a
     layer step (it includes the host's launch overhead when the GPU waits
@@ -384,8 +383,8 @@ def bench_config4(dev, steps: int = 12):
         ms_s, ms_a = float(np.median(t_step)), float(np.median(t_attn))
         res["qjl" if qjl_m else "no_qjl"] = {
             "kernel": ("K4/V2 + sketch (decode_partials_kernel computing S q and the key term from the sketch, "
-                       "merge, qjl_value_kernel, qjl_final_kernel; the step in one tq_ragged_step launch)") if qjl_m
-                      else "K4/V2 (decode_partials_kernel + merge)",
+                       "qjl_value_kernel, merge adding the value term; the step in one tq_ragged_step launch)") if qjl_m
+                      else "K4/V2 (decode_partials_kernel + merge; the step in one tq_ragged_step launch)",
             "layer_step_us": round(ms_s * 1e3, 1), "attend_us": round(ms_a * 1e3, 1),
             "attend_bytes": byt, "attend_GBps": round(byt / (ms_a * 1e-3) / 1e9, 1),
             "attend_back_to_back_us": round(ms_b * 1e3, 1),

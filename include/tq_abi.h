@@ -279,25 +279,27 @@ int tq_ring_append(const void* k, const void* v, int32_t dtype, void* ring_k, vo
                    int64_t ring_head_stride, int32_t ring_cap, int32_t batch, int32_t heads, int32_t d,
                    const int32_t* slot_b, void* stream);
 
-/* One decode step of a ragged batch with QJL sketches in one launch: the
- * tq_ring_append of k / v (batch, heads, 128) at slot_b[b], and the one-token
- * drain of ring position src_b[b] of every sequence with drain_b[b] == 1 into
- * the key and value stores at token dst_b[b] — the results of tq_ring_append
- * followed by tq_compress of each side over the rings (a span of n_tok 1 and
- * n_tok_b / src_tok0_b / dst_tok0_b = drain_b / src_b / dst_b), bit for bit.
+/* One decode step of a ragged batch in one launch: the tq_ring_append of
+ * k / v (batch, heads, 128) at slot_b[b], and the one-token drain of ring
+ * position src_b[b] of every sequence with drain_b[b] == 1 into the key and
+ * value stores at token dst_b[b] — the results of tq_ring_append followed by
+ * tq_compress of each side over the rings (a span of n_tok 1 and n_tok_b /
+ * src_tok0_b / dst_tok0_b = drain_b / src_b / dst_b), bit for bit (without a
+ * sketch: as tq_compress with TQ_CODEC_GENERAL_COMPRESS; the default MFMA
+ * compress kernel agrees with it outside the near-boundary band).
  * `seq_ints` is HOST memory: n_ints >= 4*batch int32 = [slot_b | drain_b |
  * src_b | dst_b | anything the caller adds], each array `batch` long; all
  * n_ints are copied to the device array `seq_ints_dev` in stream order
  * (later calls may read the caller's part there, e.g. an attention
  * descriptor's length arrays); seq_ints may be reused once the call returns.
  * A drained slot must differ from the sequence's append slot. Both codecs
- * head_dim 128 with a sketch of <= 128 projections (the tq_compress drain
- * route), rings fp16 or bf16 (dtype) with head stride ring_head_stride
- * elements, k, v and rings 16-byte aligned; other codecs return
- * TQ_ERR_UNSUPPORTED (use tq_ring_append + tq_compress). Replaces a decode
- * step of update_and_fetch with the chunk_size = 1 drain policy and the QJL
- * sketch of the drained vector (cache.py:396-427, 529-533, 620-706), per
- * sequence of a ragged batch. */
+ * head_dim 128, with a sketch of <= 128 projections (stored where the store
+ * has sign rows) or none, rings fp16 or bf16 (dtype) with head stride
+ * ring_head_stride elements, k, v and rings 16-byte aligned; other codecs
+ * return TQ_ERR_UNSUPPORTED (use tq_ring_append + tq_compress). Replaces a
+ * decode step of update_and_fetch with the chunk_size = 1 drain policy and
+ * the QJL sketch of the drained vector (cache.py:396-427, 529-533, 620-706),
+ * per sequence of a ragged batch. */
 int tq_ragged_step(const tq_codec* kcodec, const tq_codec* vcodec, const void* k, const void* v, int32_t dtype,
                    void* ring_k, void* ring_v, int64_t ring_head_stride, int32_t ring_cap, const tq_store* kstore,
                    const tq_store* vstore, int32_t batch, int32_t heads, const int32_t* seq_ints, int32_t n_ints,

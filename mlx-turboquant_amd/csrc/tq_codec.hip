@@ -826,8 +826,9 @@ __global__ __launch_bounds__(256) void ring_append_kernel(const uint4* k, const 
 // One decode step of a ragged batch in one launch (tq_ragged_step): the
 // step's key and value vectors appended to the residual rings, and the
 // one-token drains of both sides. Workgroups [0, dwg) drain keys, [dwg, 2 dwg)
-// values (the drain workgroup of drain_kernel: the same operations, so the
-// stored codes, norms, signs and gamma are bit-identical to tq_compress's),
+// values (the drain workgroup of drain_kernel: the general compress kernel's
+// operations, so the stored codes, norms, signs and gamma are bit-identical
+// to tq_compress's with a sketch, and to its general kernel without one),
 // the rest append. The per-sequence ints are [slot | drain | src | dst |
 // caller's extra] (batch each); up to STEP_INL of them travel in the kernel
 // arguments and are copied to ints_dev by the first append workgroup,
@@ -926,21 +927,23 @@ int tq_ragged_step(const tq_codec* kcodec, const tq_codec* vcodec, const void* k
       n_ints < 4 * batch || (int64_t)batch * heads >= ((int64_t)1 << 24))
     return set_error(TQ_ERR_INVALID, "ragged_step: bad shape (batch %d heads %d cap %d stride %lld ints %d)", batch, heads,
                      ring_cap, (long long)ring_head_stride, n_ints);
-  // the one-token drain workgroup serves d = 128 with a sketch of <= 128
-  // projections (the tq_compress drain route); other codecs use
-  // tq_ring_append + tq_compress
+  // the one-token drain workgroup serves d = 128, with a sketch of at most
+  // 128 projections or none (the general compress kernel's operations, as in
+  // the tq_compress drain route); other codecs use tq_ring_append + tq_compress
   const tq_codec* cs[2] = {kcodec, vcodec};
   const tq_store* ss[2] = {kstore, vstore};
+  bool sk[2];
   for (int i = 0; i < 2; ++i) {
     const tq_codec* c = cs[i];
-    if (c->d != 128 || !c->qjl_proj || c->qjl_m > 128 || (c->flags & TQ_CODEC_GENERAL_COMPRESS) ||
-        (reinterpret_cast<uintptr_t>(c->rotation) & 15) || (reinterpret_cast<uintptr_t>(c->qjl_proj) & 15))
-      return set_error(TQ_ERR_UNSUPPORTED, "ragged_step: codec (d %d, qjl_m %d) has no one-launch step", c->d, c->qjl_m);
     const tq_store* st = ss[i];
-    if (!st->codes_hi || !st->norms || !st->signs || !st->gamma || (c->split < c->d && !st->codes_lo))
-      return set_error(TQ_ERR_INVALID, "ragged_step: store without codes / norms / signs / gamma");
+    sk[i] = c->qjl_proj && st->signs;  // the sketch is stored where the store has sign rows
+    if (c->d != 128 || (sk[i] && c->qjl_m > 128) || (reinterpret_cast<uintptr_t>(c->rotation) & 15) ||
+        (sk[i] && (reinterpret_cast<uintptr_t>(c->qjl_proj) & 15)))
+      return set_error(TQ_ERR_UNSUPPORTED, "ragged_step: codec (d %d, qjl_m %d) has no one-launch step", c->d, c->qjl_m);
+    if (!st->codes_hi || !st->norms || (sk[i] && !st->gamma) || (c->split < c->d && !st->codes_lo))
+      return set_error(TQ_ERR_INVALID, "ragged_step: store without codes / norms (or gamma with a sketch)");
     if (!aligned4(st->codes_hi) || (st->hi_head_stride & 3) || (st->codes_lo && (!aligned4(st->codes_lo) || (st->lo_head_stride & 3))) ||
-        !aligned4(st->signs) || (st->sign_head_stride & 3))
+        (sk[i] && (!aligned4(st->signs) || (st->sign_head_stride & 3))))
       return set_error(TQ_ERR_INVALID, "ragged_step: packed outputs must be 4-byte aligned");
   }
   const auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -970,8 +973,8 @@ int tq_ragged_step(const tq_codec* kcodec, const tq_codec* vcodec, const void* k
     a.bnd_lo = c->split < c->d ? c->boundaries_lo : c->boundaries_hi;
     a.cen_hi = c->centroids_hi;
     a.cen_lo = c->split < c->d ? c->centroids_lo : c->centroids_hi;
-    a.proj = c->qjl_proj;
-    a.qjl_m = c->qjl_m;
+    a.proj = sk[i] ? c->qjl_proj : nullptr;
+    a.qjl_m = sk[i] ? c->qjl_m : 0;
     a.d = c->d;
     a.bits_hi = c->bits_hi;
     a.bits_lo = c->split < c->d ? c->bits_lo : c->bits_hi;

@@ -114,11 +114,11 @@ class RaggedKVBatch:
         z = lambda: np.zeros(batch, dtype=np.int64)
         self.sink_len, self.comp_len, self.res_len, self.res_start, self.offset = z(), z(), z(), z(), z()
         self._step_ints = _IntStage(8 * batch, dev)   # ring slots / drain arrays / post-step lengths of a step
-        # tq_ragged_step (one launch per step; codecs with a sketch at head_dim
-        # 128): the per-sequence ints of a step from host arrays, two slots
+        # tq_ragged_step (one launch per step at head_dim 128): the
+        # per-sequence ints of a step from host arrays, two slots
         # (pinned, and guarded by an event, when they travel by an
         # asynchronous copy rather than in the kernel arguments)
-        self._fused = self.qjl
+        self._fused = True
         self._seq_async = 8 * batch > _STEP_INLINE_INTS
         self._seq_host = [torch.empty(8 * batch, dtype=torch.int32, pin_memory=self._seq_async).numpy()
                           for _ in range(2)]
@@ -179,9 +179,9 @@ class RaggedKVBatch:
         """Append one token per sequence ((B, H, D) keys / values). Sequences
         still filling their sink write there; the others append to their ring,
         and a sequence whose ring then holds residual_window + 1 tokens drains
-        its oldest one into the store: with QJL sketches at head_dim 128 the
-        appends and both sides' drains are one tq_ragged_step launch, else
-        tq_ring_append and one ragged tq_compress per side."""
+        its oldest one into the store: at head_dim 128 the appends and both
+        sides' drains are one tq_ragged_step launch, else tq_ring_append and
+        one ragged tq_compress per side."""
         B, H, D, dev = self.B, self.H, self.D, self.device
         if keys.shape != (B, H, D) or values.shape != keys.shape:
             raise ValueError("keys / values must be (batch, num_kv_heads, head_dim)")

@@ -115,8 +115,11 @@ def test_host_side_validation_errors():
     rs = lambda kc, vc, dt=_lib.TQ_F16, n=8, i=ints: lib.tq_ragged_step(
         ctypes.byref(kc), ctypes.byref(vc), f, f, dt, f, f, 129 * 128, 129, ctypes.byref(st), ctypes.byref(st), 2, 8,
         i, n, f, None)
-    assert rs(sk, nsk) == _lib.TQ_ERR_UNSUPPORTED  # no sketch on the value side: tq_ring_append + tq_compress
+    d96 = _lib.Codec(d=96, bits_hi=4, bits_lo=4, split=96, rotation=f, centroids_hi=f, boundaries_hi=f)
+    assert rs(sk, d96) == _lib.TQ_ERR_UNSUPPORTED  # head_dim 96: tq_ring_append + tq_compress
     assert b"no one-launch step" in lib.tq_last_error()
+    assert rs(sk, nsk) == _lib.TQ_ERR_INVALID  # a side without a sketch is served: the ints are checked next
+    assert b"sequence 0 drains ring slot 5" in lib.tq_last_error()
     assert rs(sk, sk, dt=_lib.TQ_F32) == _lib.TQ_ERR_UNSUPPORTED
     assert rs(sk, sk, n=7) == _lib.TQ_ERR_INVALID  # fewer than 4 * batch ints
     assert rs(sk, sk) == _lib.TQ_ERR_INVALID  # sequence 0 drains the slot it appends to

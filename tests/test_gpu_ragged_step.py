@@ -1,12 +1,14 @@
-"""tq_ragged_step (one launch per decode step of a ragged batch with QJL
-sketches: the ring appends and both sides' one-token drains, cache.py:396-427,
-529-533, 620-706 per sequence) against the two-call path it replaces
-(tq_ring_append, then tq_compress of each side over the rings through the
-drain kernel, itself bit-identical to the general compress kernel in
-test_gpu_drain.py): rings, codes, norms, signs, gamma and the post-step
-length arrays bit for bit, and the attention over the two batches equal, over
-steps that fill sinks, fill rings and drain, for a batch whose ints travel in
-the kernel arguments and one (72 sequences) whose ints take the copy.
+"""tq_ragged_step (one launch per decode step of a ragged batch: the ring
+appends and both sides' one-token drains, cache.py:396-427, 529-533, 620-706
+per sequence) against the two-call path it replaces (tq_ring_append, then
+tq_compress of each side over the rings: with a sketch through the drain
+kernel, itself bit-identical to the general compress kernel in
+test_gpu_drain.py; without one through the general compress kernel, whose
+operations the step's drain performs): rings, codes, norms, signs, gamma and
+the post-step length arrays bit for bit, and the attention over the two
+batches equal, over steps that fill sinks, fill rings and drain, for a batch
+whose ints travel in the kernel arguments and one (72 sequences) whose ints
+take the copy.
 """
 
 import numpy as np
@@ -18,10 +20,25 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 
 
-def _batch(B, H, qjl_m, sink, window, lens, seed, fused):
+class _GeneralCompress:
+    """A codec whose tq_compress calls take the general kernel."""
+
+    def __init__(self, codec):
+        self._codec = codec
+
+    def ref(self, general_compress: bool = False):
+        return self._codec.ref(True)
+
+    def __getattr__(self, name):
+        return getattr(self._codec, name)
+
+
+def _batch(B, H, qjl_m, sink, window, lens, seed, fused, kb=4, vb=2):
     from turboquant_amd.ragged import RaggedKVBatch
-    rb = RaggedKVBatch(B, H, 128, 4, 2, residual_window=window, fp16_sink_size=sink, qjl_n_proj=qjl_m, device=DEV)
+    rb = RaggedKVBatch(B, H, 128, kb, vb, residual_window=window, fp16_sink_size=sink, qjl_n_proj=qjl_m, device=DEV)
     rb._fused = fused and rb._fused
+    if qjl_m == 0:  # both batches load and (two-call path) drain through the general kernel
+        rb.kc, rb.vc = _GeneralCompress(rb.kc), _GeneralCompress(rb.vc)
     g = torch.Generator(device=DEV).manual_seed(seed)
     for b, T in enumerate(lens):
         if T:
@@ -40,20 +57,22 @@ def _state(rb):
     return {k: v.cpu().numpy().copy() for k, v in out.items()}
 
 
-@pytest.mark.parametrize("B,H,qjl_m,sink,window,lens", [
-    (5, 2, 128, 4, 6, [9, 3, 0, 17, 6]),    # sinks filling, rings filling and draining (ints in the arguments)
-    (16, 8, 128, 0, 128, None),             # the configs[4] shape (window 128, no sink), shorter contexts
-    (72, 1, 64, 2, 5, None),                # 576 ints: the copy path, m = 64
+@pytest.mark.parametrize("B,H,qjl_m,sink,window,lens,kb,vb", [
+    (5, 2, 128, 4, 6, [9, 3, 0, 17, 6], 4, 2),    # sinks filling, rings filling and draining (ints in the arguments)
+    (16, 8, 128, 0, 128, None, 4, 2),             # the configs[4] shape (window 128, no sink), shorter contexts
+    (72, 1, 64, 2, 5, None, 4, 2),                # 576 ints: the copy path, m = 64
+    (16, 8, 0, 0, 128, None, 4, 2),               # configs[4] without a sketch
+    (6, 2, 0, 3, 7, [20, 2, 9, 40, 1, 13], 3.5, 2.5),  # fractional widths without a sketch
 ])
-def test_ragged_step_matches_two_call_path(B, H, qjl_m, sink, window, lens):
+def test_ragged_step_matches_two_call_path(B, H, qjl_m, sink, window, lens, kb, vb):
     rng = np.random.RandomState(B + H)
     if lens is None:
         lens = rng.randint(window + 3, 3 * window + 40, size=B)
     lens = [int(x) for x in lens]
     # sequences start non-empty for attend(); the empty one is loaded with one token
     lens = [max(x, 1) for x in lens]
-    a = _batch(B, H, qjl_m, sink, window, lens, 7, fused=True)
-    b = _batch(B, H, qjl_m, sink, window, lens, 7, fused=False)
+    a = _batch(B, H, qjl_m, sink, window, lens, 7, fused=True, kb=kb, vb=vb)
+    b = _batch(B, H, qjl_m, sink, window, lens, 7, fused=False, kb=kb, vb=vb)
     assert a._fused and not b._fused
     g = torch.Generator(device=DEV).manual_seed(11)
     q = torch.randn(B, 4 * H, 128, generator=g, device=DEV).half()

@@ -376,12 +376,20 @@ struct DrainLds {
   float cen[2][16];
 };
 
-// The drain of vector `vid` (row vid / n_tok, token vid % n_tok) by wave w of
-// a workgroup whose LDS `L` already holds R, S and the codebooks of `a`;
-// seq(b) gives sequence b's {token count, first source token, first
-// destination token}.
+// The drain of vector `vid` (row vid / n_tok, token vid % n_tok) by wave w,
+// in two parts: drain_begin, before the workgroup's barrier (the vector's
+// indices and loads, whose latency then runs under the staging of R and S),
+// and drain_vector after it (R, S and the codebooks of `a` in LDS); seq(b)
+// gives sequence b's {token count, first source token, first destination
+// token}.
+struct DrainIn {
+  int r, dst;
+  float x0, x1;
+  bool ok;  // the wave has a vector
+};
 template <class Seq>
-__device__ __forceinline__ void drain_vector(const CompressArgs& a, DrainLds& L, int vid, int w, int lane, Seq seq);
+__device__ __forceinline__ DrainIn drain_begin(const CompressArgs& a, DrainLds& L, int vid, int w, int lane, Seq seq);
+__device__ __forceinline__ void drain_vector(const CompressArgs& a, DrainLds& L, int w, int lane, const DrainIn& in);
 
 // R, S and the codebooks of `a` into the workgroup's LDS (before a barrier)
 __device__ __forceinline__ void drain_stage(const CompressArgs& a, DrainLds& L, int tid) {
@@ -432,33 +440,43 @@ __global__ __launch_bounds__(DRW * 64) void drain_kernel(CompressArgs a) {
   __shared__ __align__(16) DrainLds L;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  drain_stage(a, L, tid);
-  __syncthreads();  // the only barrier: waves without a vector may leave after it
-  drain_vector(a, L, blockIdx.x * DRW + w, w, lane, [&](int b) {
+  const DrainIn in = drain_begin(a, L, blockIdx.x * DRW + w, w, lane, [&](int b) {
     return SeqRange{a.span.n_tok_b ? a.span.n_tok_b[b] : a.span.n_tok, a.span.src_tok0_b ? a.span.src_tok0_b[b] : 0,
                     a.span.dst_tok0_b ? a.span.dst_tok0_b[b] : 0};
   });
+  drain_stage(a, L, tid);
+  __syncthreads();  // the only barrier: waves without a vector leave after it
+  if (in.ok) drain_vector(a, L, w, lane, in);
 }
 
 template <class Seq>
-__device__ __forceinline__ void drain_vector(const CompressArgs& a, DrainLds& L, int vid, int w, int lane, Seq seq) {
+__device__ __forceinline__ DrainIn drain_begin(const CompressArgs& a, DrainLds& L, int vid, int w, int lane, Seq seq) {
+  DrainIn in{0, 0, 0.f, 0.f, false};
+  const int r = vid / a.span.n_tok, t = vid % a.span.n_tok;
+  if (r >= a.span.rows) return in;
+  const int b = r / a.span.heads;
+  const SeqRange sr = seq(b);
+  if (t >= sr.n_tok) return in;
+  const int src = sr.src0 + t;
+  in.r = r;
+  in.dst = sr.dst0 + t;
+  in.ok = true;
+  const int64_t xrow = (int64_t)r * a.x_hs + (int64_t)src * 128;
+  in.x0 = load_elem(a.x, xrow + lane, a.x_dtype);
+  in.x1 = load_elem(a.x, xrow + 64 + lane, a.x_dtype);
+  return in;
+}
+
+__device__ __forceinline__ void drain_vector(const CompressArgs& a, DrainLds& L, int w, int lane, const DrainIn& in) {
   const float* rt = L.rt;
   const float* st = L.st;
   auto& vec = L.vec;
   auto& cds = L.cds;
   auto& bnd = L.bnd;
   auto& cen = L.cen;
-  const int r = vid / a.span.n_tok, t = vid % a.span.n_tok;
-  if (r >= a.span.rows) return;
-  const int b = r / a.span.heads;
-  const SeqRange sr = seq(b);
-  if (t >= sr.n_tok) return;
-  const int src = sr.src0 + t;
-  const int dst = sr.dst0 + t;
+  const int r = in.r, dst = in.dst;
+  const float x0 = in.x0, x1 = in.x1;
   float* xv = vec[w];
-  const int64_t xrow = (int64_t)r * a.x_hs + (int64_t)src * 128;
-  const float x0 = load_elem(a.x, xrow + lane, a.x_dtype);
-  const float x1 = load_elem(a.x, xrow + 64 + lane, a.x_dtype);
   xv[lane] = x0;
   xv[64 + lane] = x1;
   // norm: float64 block sums (every lane, the same value)
@@ -879,11 +897,12 @@ __global__ __launch_bounds__(DRW * 64) void step_kernel(StepArgs A) {
   const int sd = wg >= A.dwg ? 1 : 0;
   const CompressArgs& a = A.side[sd];
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  drain_stage(a, L, tid);
-  __syncthreads();  // the only barrier: waves without a vector may leave after it
   const int B = A.batch;
-  drain_vector(a, L, (wg - sd * A.dwg) * DRW + w, w, lane,
-               [&](int b) { return SeqRange{seqi[B + b], seqi[2 * B + b], seqi[3 * B + b]}; });
+  const DrainIn in = drain_begin(a, L, (wg - sd * A.dwg) * DRW + w, w, lane,
+                                 [&](int b) { return SeqRange{seqi[B + b], seqi[2 * B + b], seqi[3 * B + b]}; });
+  drain_stage(a, L, tid);
+  __syncthreads();  // the only barrier: waves without a vector leave after it
+  if (in.ok) drain_vector(a, L, w, lane, in);
 }
 }  // namespace tq
 

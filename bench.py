@@ -334,7 +334,10 @@ def bench_config4(dev, steps: int = 12):
     layer step (it includes the host's launch overhead when the GPU waits
     for it), alternating with steps whose attention call alone is timed;
     then 8 attention calls back to back between two events, the GPU time of
-    one call with the host running ahead."""
+    one call with the host running ahead; then 8 layer steps back to back
+    between two events (a decode loop's steady state: the host prepares
+    step n + 1 while the GPU runs step n; the stores' capacity is reserved
+    beforehand, as their geometric growth leaves it on almost every step)."""
     import numpy as np
     import torch
     from turboquant_amd.ragged import RaggedKVBatch
@@ -378,6 +381,20 @@ def bench_config4(dev, steps: int = 12):
         e1.record()
         torch.cuda.synchronize()
         ms_b = e0.elapsed_time(e1) / rep
+        kv = [(torch.randn(16, 8, 128, generator=g, device=dev).half(),
+               torch.randn(16, 8, 128, generator=g, device=dev).half()) for _ in range(rep + 1)]
+        for st in (rb.kstore, rb.vstore):
+            st.reserve(int(rb.comp_len.max()) + rep + 2, int(rb.comp_len.max()))
+        rb.step(*kv[0])
+        rb.attend(q, out=out)
+        torch.cuda.synchronize()
+        e0.record()
+        for k, v in kv[1:]:
+            rb.step(k, v)
+            rb.attend(q, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_lb = e0.elapsed_time(e1) / rep
         per_tok = sum(c.row_hi + c.row_lo + 4 + (c.row_sign + 4 if qjl_m else 0) for c in (rb.kc, rb.vc))
         byt = 8 * (int(rb.comp_len.sum()) * per_tok + int(rb.res_len.sum()) * 512) + 16 * 32 * 128 * 6
         ms_s, ms_a = float(np.median(t_step)), float(np.median(t_attn))
@@ -385,7 +402,8 @@ def bench_config4(dev, steps: int = 12):
             "kernel": ("K4/V2 + sketch (decode_partials_kernel computing S q and the key term from the sketch, "
                        "qjl_value_kernel, merge adding the value term; the step in one tq_ragged_step launch)") if qjl_m
                       else "K4/V2 (decode_partials_kernel + merge; the step in one tq_ragged_step launch)",
-            "layer_step_us": round(ms_s * 1e3, 1), "attend_us": round(ms_a * 1e3, 1),
+            "layer_step_us": round(ms_s * 1e3, 1), "layer_step_back_to_back_us": round(ms_lb * 1e3, 1),
+            "attend_us": round(ms_a * 1e3, 1),
             "attend_bytes": byt, "attend_GBps": round(byt / (ms_a * 1e-3) / 1e9, 1),
             "attend_back_to_back_us": round(ms_b * 1e3, 1),
             "attend_back_to_back_GBps": round(byt / (ms_b * 1e-3) / 1e9, 1)}

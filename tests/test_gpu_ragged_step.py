@@ -105,6 +105,36 @@ def test_ragged_step_matches_two_call_path(B, H, qjl_m, sink, window, lens, kb, 
     assert int(a.comp_len.sum()) > int(sum(max(x - sink - window, 0) for x in lens))  # drains happened
 
 
+@pytest.mark.parametrize("qjl_m", [128, 0])
+def test_back_to_back_steps_match_synchronised_steps(qjl_m):
+    """A decode loop with the host running ahead (step + attention per step,
+    no synchronisation between steps, as the benchmark's back-to-back layer
+    steps): every step's attention output equals that of a batch that
+    synchronises after each step, bit for bit (the device length slots the
+    step kernel writes alternate between steps and are read in stream order)."""
+    B, H, window = 16, 8, 128
+    lens = [int(x) for x in np.random.RandomState(5).randint(window + 3, 3 * window + 40, size=B)]
+    a = _batch(B, H, qjl_m, 0, window, lens, 9, fused=True)
+    b = _batch(B, H, qjl_m, 0, window, lens, 9, fused=True)
+    g = torch.Generator(device=DEV).manual_seed(13)
+    q = torch.randn(B, 4 * H, 128, generator=g, device=DEV).half()
+    kv = [(torch.randn(B, H, 128, generator=g, device=DEV).half(), torch.randn(B, H, 128, generator=g, device=DEV).half())
+          for _ in range(12)]
+    torch.cuda.synchronize()
+    print(f"m={qjl_m} back-to-back steps", flush=True)
+    outs = []
+    for k, v in kv:
+        a.step(k, v)
+        outs.append(a.attend(q))
+    torch.cuda.synchronize()
+    for s, (k, v) in enumerate(kv):
+        b.step(k, v)
+        ob = b.attend(q)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[s], ob), f"step {s}: attention differs"
+    assert a._fused and b._fused
+
+
 def test_stream_handle_is_torch_current_stream():
     """Launches go to torch's current stream (the raw handle query agrees with
     torch.cuda.current_stream, also inside a stream context)."""

@@ -11,6 +11,8 @@ whose ints travel in the kernel arguments and one (72 sequences) whose ints
 take the copy.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -133,6 +135,62 @@ def test_back_to_back_steps_match_synchronised_steps(qjl_m):
         torch.cuda.synchronize()
         assert torch.equal(outs[s], ob), f"step {s}: attention differs"
     assert a._fused and b._fused
+
+
+@pytest.mark.parametrize("qjl_m", [128, 0])
+def test_ragged_step_bf16_rings_through_the_abi(qjl_m):
+    """tq_ragged_step called through the C ABI with bf16 keys, values and
+    rings (RaggedKVBatch keeps fp16 ones): the rings equal a torch append
+    (a token going to the sink, slot -1, is not appended), and the stores
+    equal the general compress kernel's drain of the same ring slots, bit for
+    bit (sequences without a drain write nothing)."""
+    from test_gpu_drain import drain
+    from turboquant_amd import _codec, _lib
+    B, H, cap, D = 5, 3, 12, 128
+    g = torch.Generator(device=DEV).manual_seed(23)
+    rk = (torch.randn(B, H, cap, D, generator=g, device=DEV) * 2.0).bfloat16()
+    rv = torch.randn(B, H, cap, D, generator=g, device=DEV).bfloat16()
+    k = torch.randn(B, H, D, generator=g, device=DEV).bfloat16()
+    v = torch.randn(B, H, D, generator=g, device=DEV).bfloat16()
+    slot = np.array([3, -1, 0, 11, 7], np.int32)
+    dr = np.array([1, 1, 0, 1, 1], np.int32)
+    src = np.array([4, 9, 0, 2, 6], np.int32)
+    dst = np.array([0, 5, 0, 17, 33], np.int32)
+    ints = np.ascontiguousarray(np.concatenate([slot, dr, src, dst]))
+    ints_dev = torch.zeros(ints.size, dtype=torch.int32, device=DEV)
+    kc = _codec.get_codec(D, 4, 42, qjl_m, DEV)
+    vc = _codec.get_codec(D, 2, 42, qjl_m, DEV)
+    stores = []
+    for c in (kc, vc):
+        st = _codec.PackedStore(c, B, H, qjl=qjl_m > 0)
+        st.reserve(64, 0)
+        for name in ("codes_hi", "codes_lo", "norms", "signs", "gamma"):
+            t = getattr(st, name)
+            if t is not None:
+                t.zero_()
+        stores.append(st)
+    ref_k = drain(kc, rk, dr, src, dst, H, general=True)
+    ref_v = drain(vc, rv, dr, src, dst, H, general=True)
+    exp_k, exp_v = rk.clone(), rv.clone()
+    for b in range(B):
+        if slot[b] >= 0:
+            exp_k[b, :, slot[b]] = k[b]
+            exp_v[b, :, slot[b]] = v[b]
+    lib = _lib.load()
+    kst, vst = stores[0].struct(0), stores[1].struct(0)
+    print(f"m={qjl_m} bf16 ragged step", flush=True)
+    _lib.check(lib.tq_ragged_step(kc.ref(), vc.ref(), k.data_ptr(), v.data_ptr(), _lib.TQ_BF16, rk.data_ptr(),
+                                  rv.data_ptr(), cap * D, cap, ctypes.byref(kst), ctypes.byref(vst), B, H,
+                                  ints.ctypes.data, ints.size, ints_dev.data_ptr(), _lib.stream_ptr(DEV)),
+               "tq_ragged_step")
+    torch.cuda.synchronize()
+    assert torch.equal(rk, exp_k) and torch.equal(rv, exp_v)
+    assert np.array_equal(ints_dev.cpu().numpy(), ints)
+    for st, ref in zip(stores, (ref_k, ref_v)):
+        for name in ("codes_hi", "codes_lo", "norms", "signs", "gamma"):
+            t = getattr(st, name)
+            if t is not None and t.numel():
+                assert np.array_equal(t.cpu().numpy(), ref[name]), name
 
 
 def test_stream_handle_is_torch_current_stream():
